@@ -1,0 +1,849 @@
+// fmx_api.cpp -- the C-ABI of libfmx.so: argument checks with MLX's shape
+// rules, workspace layout, and the launch sequence of each entry point.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fmx.h"
+#include "fmx_kernels.hpp"
+
+using namespace fmx;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int ok() {
+  g_last_error.clear();
+  return FMX_OK;
+}
+
+#define FMX_HIP(expr)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (expr);                                                        \
+    if (e_ != hipSuccess)                                                          \
+      return fail(FMX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));            \
+  } while (0)
+
+int64_t numel(const fmx_array& a) {
+  int64_t n = 1;
+  for (int i = 0; i < a.ndim; ++i) n *= a.shape[i];
+  return n;
+}
+
+int64_t prod(const int64_t* s, int n) {
+  int64_t p = 1;
+  for (int i = 0; i < n; ++i) p *= s[i];
+  return p;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_array(const fmx_array* a, const char* name, int dtype, int min_ndim) {
+  if (!a) return fail(FMX_ERR_ARG, "%s is NULL", name);
+  if (a->ndim < min_ndim || a->ndim > FMX_MAX_NDIM)
+    return fail(FMX_ERR_SHAPE, "%s: ndim %d (need %d..%d)", name, a->ndim, min_ndim, FMX_MAX_NDIM);
+  for (int i = 0; i < a->ndim; ++i)
+    if (a->shape[i] < 0) return fail(FMX_ERR_SHAPE, "%s: negative dim", name);
+  if (dtype >= 0 && a->dtype != dtype)
+    return fail(FMX_ERR_DTYPE, "%s: dtype %d, expected %d", name, a->dtype, dtype);
+  if (!a->data && numel(*a) > 0) return fail(FMX_ERR_ARG, "%s: data is NULL", name);
+  if (a->data && !aligned(a->data, 16)) return fail(FMX_ERR_ARG, "%s: data not 16-byte aligned", name);
+  return FMX_OK;
+}
+
+int check_quant_args(int transpose, int group_size, int bits, const char* mode) {
+  if (mode && std::strcmp(mode, "affine") != 0)
+    return fail(FMX_ERR_UNSUPPORTED, "mode '%s' (only \"affine\")", mode);
+  if (bits != 4) return fail(FMX_ERR_UNSUPPORTED, "bits=%d (only 4)", bits);
+  if (group_size != 64) return fail(FMX_ERR_UNSUPPORTED, "group_size=%d (only 64)", group_size);
+  if (!transpose) return fail(FMX_ERR_UNSUPPORTED, "transpose=false");
+  return FMX_OK;
+}
+
+// Scratch arena over the caller's workspace (or a stream-ordered allocation).
+struct Arena {
+  char* base = nullptr;
+  size_t cap = 0, used = 0;
+  bool owned = false;
+  hipStream_t stream = nullptr;
+  void* take(size_t bytes) {
+    void* p = base ? base + used : nullptr;
+    used = static_cast<size_t>(align_up(static_cast<int64_t>(used + bytes), 256));
+    return p;
+  }
+};
+
+// Sizes a plan by running it against a null arena, then binds the real one.
+struct WsGuard {
+  Arena& a;
+  explicit WsGuard(Arena& ar) : a(ar) {}
+  ~WsGuard() {
+    if (a.owned && a.base) (void)hipFreeAsync(a.base, a.stream);
+  }
+};
+
+int bind_workspace(Arena& ar, void* ws, size_t ws_bytes, size_t need, hipStream_t stream) {
+  ar.stream = stream;
+  ar.used = 0;
+  if (ws) {
+    if (ws_bytes < need)
+      return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes, need %zu", ws_bytes, need);
+    if (!aligned(ws, 256)) return fail(FMX_ERR_ARG, "workspace not 256-byte aligned");
+    ar.base = static_cast<char*>(ws);
+    ar.cap = ws_bytes;
+    return FMX_OK;
+  }
+  if (need == 0) return FMX_OK;
+  void* p = nullptr;
+  FMX_HIP(hipMallocAsync(&p, need, stream));
+  ar.base = static_cast<char*>(p);
+  ar.cap = need;
+  ar.owned = true;
+  return FMX_OK;
+}
+
+// ---------------------------------------------------------------- MoE layout
+
+constexpr int64_t kMoEMaxTokens = 65536;
+constexpr size_t kCounterBytes = (kMoEMaxTokens / kRouterTok + 64) * sizeof(uint32_t);
+
+struct MoELayout {
+  uint32_t* counters;
+  uint16_t* logits;
+  uint16_t* probs;
+  uint32_t* inds;
+  uint16_t* scores;
+  uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base;
+  float* sgate;
+  uint16_t *xp, *h, *hs, *d, *sd;
+  size_t total;
+};
+
+MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
+  Arena ar;
+  ar.base = base;
+  MoELayout L{};
+  const int64_t E = c.num_experts, k = c.num_experts_per_tok, H = c.hidden_size;
+  const int64_t I = c.moe_intermediate_size, Is = c.shared_expert_intermediate_size;
+  const int64_t n = T * k;
+  L.counters = static_cast<uint32_t*>(ar.take(kCounterBytes));
+  L.logits = static_cast<uint16_t*>(ar.take(T * (E + 1) * 2));
+  L.probs = static_cast<uint16_t*>(ar.take(T * E * 2));
+  L.inds = static_cast<uint32_t*>(ar.take(n * 4));
+  L.scores = static_cast<uint16_t*>(ar.take(n * 2));
+  L.order = static_cast<uint32_t*>(ar.take(n * 4));
+  L.inv = static_cast<uint32_t*>(ar.take(n * 4));
+  L.src = static_cast<uint32_t*>(ar.take(n * 4));
+  L.idx = static_cast<uint32_t*>(ar.take(n * 4));
+  L.offsets = static_cast<uint32_t*>(ar.take((E + 1) * 4));
+  L.seg_n = static_cast<uint32_t*>(ar.take(4));
+  L.seg_exp = static_cast<uint32_t*>(ar.take(E * 4));
+  L.seg_off = static_cast<uint32_t*>(ar.take((E + 1) * 4));
+  L.sort_base = static_cast<uint32_t*>(ar.take(E * ((n + 63) / 64) * 4));
+  L.sgate = static_cast<float*>(ar.take(T * 4));
+  L.xp = static_cast<uint16_t*>(ar.take(T * H * 2));
+  L.h = static_cast<uint16_t*>(ar.take(n * I * 2));
+  L.hs = static_cast<uint16_t*>(ar.take(T * Is * 2));
+  L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
+  L.sd = static_cast<uint16_t*>(ar.take(T * H * 2));
+  L.total = ar.used;
+  return L;
+}
+
+int check_moe_config(const fmx_moe_config* c) {
+  if (!c) return fail(FMX_ERR_ARG, "cfg is NULL");
+  if (c->quant_bits != 4) return fail(FMX_ERR_UNSUPPORTED, "quant_bits=%d (only 4)", c->quant_bits);
+  if (c->quant_group_size != 64)
+    return fail(FMX_ERR_UNSUPPORTED, "quant_group_size=%d (only 64)", c->quant_group_size);
+  if (c->hidden_size <= 0 || c->hidden_size % 64)
+    return fail(FMX_ERR_SHAPE, "hidden_size=%lld must be a positive multiple of 64",
+                static_cast<long long>(c->hidden_size));
+  if (c->moe_intermediate_size <= 0 || c->moe_intermediate_size % 64)
+    return fail(FMX_ERR_SHAPE, "moe_intermediate_size=%lld must be a positive multiple of 64",
+                static_cast<long long>(c->moe_intermediate_size));
+  if (c->shared_expert_intermediate_size < 0 || c->shared_expert_intermediate_size % 64)
+    return fail(FMX_ERR_SHAPE, "shared_expert_intermediate_size=%lld must be a multiple of 64",
+                static_cast<long long>(c->shared_expert_intermediate_size));
+  if (c->num_experts < 1 || c->num_experts > 1024)
+    return fail(FMX_ERR_UNSUPPORTED, "num_experts=%lld (1..1024)", static_cast<long long>(c->num_experts));
+  if (c->num_experts_per_tok < 1 || c->num_experts_per_tok > 16 ||
+      c->num_experts_per_tok > c->num_experts)
+    return fail(FMX_ERR_UNSUPPORTED, "num_experts_per_tok=%d (1..min(16, E))", c->num_experts_per_tok);
+  return FMX_OK;
+}
+
+bool qw_ok(const fmx_qweight& q) {
+  return q.w && q.scales && q.biases && aligned(q.w, 16) && aligned(q.scales, 2) &&
+         aligned(q.biases, 2);
+}
+
+// Router launch shared by the block forward and fmx_moe_router_topk.
+int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64_t T,
+               const void* router_w, const void* lbias, const void* wsg, uint32_t* inds,
+               uint16_t* scores, uint16_t* probs, float* sgate, uint16_t* xp, bool want_sort,
+               bool* sorted_in_router, hipStream_t stream) {
+  RouterArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.wr = static_cast<const uint16_t*>(router_w);
+  a.lbias = static_cast<const uint16_t*>(lbias);
+  a.wsg = static_cast<const uint16_t*>(wsg);
+  a.T = static_cast<int>(T);
+  a.H = static_cast<int>(c.hidden_size);
+  a.E = static_cast<int>(c.num_experts);
+  a.k = c.num_experts_per_tok;
+  a.norm = c.norm_topk_prob ? 1 : 0;
+  a.logits = L.logits;
+  a.probs = probs;
+  a.inds = inds;
+  a.scores = scores;
+  a.sgate = sgate;
+  a.xp = xp;
+  a.counters = L.counters;
+  a.n_tt = static_cast<int>((T + kRouterTok - 1) / kRouterTok);
+  a.n_ct = static_cast<int>((c.num_experts + (wsg ? 1 : 0) + kRouterCols - 1) / kRouterCols);
+  const int64_t n = T * c.num_experts_per_tok;
+  a.fuse_sort = want_sort && router_sort_fits(n, c.num_experts) ? 1 : 0;
+  a.sort.order = L.order;
+  a.sort.inv = L.inv;
+  a.sort.src = L.src;
+  a.sort.idx = L.idx;
+  a.sort.offsets = L.offsets;
+  a.sort.seg_n = L.seg_n;
+  a.sort.seg_exp = L.seg_exp;
+  a.sort.seg_off = L.seg_off;
+  a.sort.base = L.sort_base;
+  if (sorted_in_router) *sorted_in_router = a.fuse_sort != 0;
+  FMX_HIP(launch_router(a, stream));
+  return FMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmx_abi_version(void) { return FMX_ABI_VERSION; }
+
+const char* fmx_status_string(int s) {
+  switch (s) {
+    case FMX_OK: return "FMX_OK";
+    case FMX_ERR_ARG: return "FMX_ERR_ARG";
+    case FMX_ERR_SHAPE: return "FMX_ERR_SHAPE";
+    case FMX_ERR_DTYPE: return "FMX_ERR_DTYPE";
+    case FMX_ERR_UNSUPPORTED: return "FMX_ERR_UNSUPPORTED";
+    case FMX_ERR_WORKSPACE: return "FMX_ERR_WORKSPACE";
+    case FMX_ERR_HIP: return "FMX_ERR_HIP";
+    default: return "FMX_ERR_UNKNOWN";
+  }
+}
+
+const char* fmx_last_error(void) { return g_last_error.c_str(); }
+
+// ---------------------------------------------------------------- quantized_matmul
+
+int fmx_quantized_matmul_out_shape(const fmx_array* x, const fmx_array* w, int transpose,
+                                   int group_size, int bits, fmx_array* out) {
+  int rc;
+  if ((rc = check_quant_args(transpose, group_size, bits, nullptr))) return rc;
+  if (!x || !w || !out) return fail(FMX_ERR_ARG, "NULL argument");
+  if (x->ndim < 2 || w->ndim != 2) return fail(FMX_ERR_SHAPE, "x.ndim >= 2 and w.ndim == 2 required");
+  const int64_t K = x->shape[x->ndim - 1];
+  if (w->shape[1] * 8 != K)
+    return fail(FMX_ERR_SHAPE, "x K=%lld does not match w [%lld, %lld]", static_cast<long long>(K),
+                static_cast<long long>(w->shape[0]), static_cast<long long>(w->shape[1]));
+  out->ndim = x->ndim;
+  for (int i = 0; i < x->ndim - 1; ++i) out->shape[i] = x->shape[i];
+  out->shape[x->ndim - 1] = w->shape[0];
+  out->dtype = FMX_BF16;
+  return ok();
+}
+
+size_t fmx_quantized_matmul_workspace_size(const fmx_array* x, const fmx_array* w) {
+  (void)w;
+  if (!x) return 0;
+  return static_cast<size_t>(align_up(numel(*x) * 2, 256));
+}
+
+int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
+                         const fmx_array* biases, int transpose, int group_size, int bits,
+                         const char* mode, fmx_array* out, void* workspace,
+                         size_t workspace_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_quant_args(transpose, group_size, bits, mode))) return rc;
+  if ((rc = check_array(x, "x", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(w, "w", FMX_U32, 2))) return rc;
+  if ((rc = check_array(scales, "scales", FMX_BF16, 2))) return rc;
+  if (!biases) return fail(FMX_ERR_ARG, "affine mode requires biases");
+  if ((rc = check_array(biases, "biases", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(out, "out", FMX_BF16, 2))) return rc;
+  if (w->ndim != 2) return fail(FMX_ERR_UNSUPPORTED, "w with batch dims (use gather_qmm)");
+  const int64_t K = x->shape[x->ndim - 1], N = w->shape[0];
+  if (K % 64) return fail(FMX_ERR_SHAPE, "K=%lld not a multiple of 64", static_cast<long long>(K));
+  if (w->shape[1] * 8 != K) return fail(FMX_ERR_SHAPE, "w.shape[1]*8 != K");
+  if (scales->ndim != 2 || scales->shape[0] != N || scales->shape[1] != K / 64 ||
+      biases->ndim != 2 || biases->shape[0] != N || biases->shape[1] != K / 64)
+    return fail(FMX_ERR_SHAPE, "scales/biases must be [N, K/64]");
+  fmx_array expect{};
+  if ((rc = fmx_quantized_matmul_out_shape(x, w, transpose, group_size, bits, &expect))) return rc;
+  if (out->ndim != expect.ndim || std::memcmp(out->shape, expect.shape, sizeof(int64_t) * out->ndim))
+    return fail(FMX_ERR_SHAPE, "out shape mismatch");
+  const int64_t rows = numel(*x) / K;
+  if (rows == 0 || N == 0) return ok();
+  if (rows > (1ll << 30)) return fail(FMX_ERR_UNSUPPORTED, "too many rows");
+
+  Arena ar;
+  WsGuard guard(ar);
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes,
+                           fmx_quantized_matmul_workspace_size(x, w), stream)))
+    return rc;
+  uint16_t* xp = static_cast<uint16_t*>(ar.take(rows * K * 2));
+  FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), rows, K, xp, stream));
+  QGemmProblem p{};
+  p.x = xp;
+  p.ldx = K;
+  p.rows_static = static_cast<int>(rows);
+  p.max_seg = 1;
+  p.w0 = static_cast<const uint32_t*>(w->data);
+  p.s0 = static_cast<const uint16_t*>(scales->data);
+  p.b0 = static_cast<const uint16_t*>(biases->data);
+  p.N = static_cast<int>(N);
+  p.K = static_cast<int>(K);
+  p.out = static_cast<uint16_t*>(out->data);
+  p.ldo = N;
+  p.n_tiles = static_cast<int>((N + 15) / 16);
+  p.n_exp = 1;
+  p.rows_max = p.x_rows = p.out_rows = static_cast<int>(rows);
+  FMX_HIP(launch_qgemm(p, nullptr, stream));
+  return ok();
+}
+
+// ---------------------------------------------------------------- gather_qmm
+
+namespace {
+
+struct GatherPlan {
+  int64_t K, N, M, E, n_x;
+  int ndim;  // batch ndim
+  int64_t batch[FMX_MAX_NDIM];
+  int64_t nb;
+};
+
+// MLX: batch(x) = x.shape[:-2], batch(w) = w.shape[:-2]; default lhs/rhs are
+// arange(prod(batch)).reshape(batch); out = broadcast(lhs, rhs) + [M, N].
+int gather_plan(const fmx_array* x, const fmx_array* w, const fmx_array* lhs,
+                const fmx_array* rhs, GatherPlan* p) {
+  if (!x || !w) return fail(FMX_ERR_ARG, "NULL argument");
+  if (x->ndim < 2 || w->ndim < 2) return fail(FMX_ERR_SHAPE, "x and w need ndim >= 2");
+  p->K = x->shape[x->ndim - 1];
+  p->M = x->shape[x->ndim - 2];
+  p->N = w->shape[w->ndim - 2];
+  if (w->shape[w->ndim - 1] * 8 != p->K) return fail(FMX_ERR_SHAPE, "w.shape[-1]*8 != K");
+  p->E = prod(w->shape, w->ndim - 2);
+  p->n_x = prod(x->shape, x->ndim - 2);
+  const int64_t* ls = lhs ? lhs->shape : x->shape;
+  const int ln = lhs ? lhs->ndim : x->ndim - 2;
+  const int64_t* rs = rhs ? rhs->shape : w->shape;
+  const int rn = rhs ? rhs->ndim : w->ndim - 2;
+  const int nd = std::max(ln, rn);
+  if (nd > FMX_MAX_NDIM - 2) return fail(FMX_ERR_SHAPE, "too many batch dims");
+  for (int i = 0; i < nd; ++i) {
+    const int li = i - (nd - ln), ri = i - (nd - rn);
+    const int64_t a = li >= 0 ? ls[li] : 1, b = ri >= 0 ? rs[ri] : 1;
+    if (a != b && a != 1 && b != 1)
+      return fail(FMX_ERR_SHAPE, "lhs/rhs index shapes do not broadcast");
+    p->batch[i] = (a == 1) ? b : a;
+  }
+  p->ndim = nd;
+  p->nb = prod(p->batch, nd);
+  return FMX_OK;
+}
+
+void fill_bcast(const GatherPlan& p, const fmx_array* idx, const int64_t* dflt_shape,
+                int dflt_ndim, BcastArgs* b) {
+  const int64_t* s = idx ? idx->shape : dflt_shape;
+  const int n = idx ? idx->ndim : dflt_ndim;
+  b->src = idx ? idx->data : nullptr;
+  b->is_i32 = idx && idx->dtype == FMX_I32;
+  b->ndim = p.ndim;
+  b->n = p.nb;
+  int64_t stride = 1;
+  for (int i = p.ndim - 1; i >= 0; --i) {
+    const int si = i - (p.ndim - n);
+    b->out_shape[i] = p.batch[i];
+    const int64_t dim = si >= 0 ? s[si] : 1;
+    b->src_stride[i] = (dim == 1) ? 0 : stride;
+    stride *= dim;
+  }
+}
+
+size_t gather_ws(const GatherPlan& p) {
+  const int64_t rows = p.nb * p.M;
+  Arena ar;
+  ar.take(p.n_x * p.M * p.K * 2);      // xp
+  ar.take(p.nb * 4);                   // lhs flat
+  ar.take(p.nb * 4);                   // rhs flat
+  ar.take(rows * 4);                   // row keys
+  ar.take(rows * 4);                   // order
+  ar.take((p.E + 1) * 4);              // offsets
+  ar.take(4);                          // seg_n
+  ar.take(p.E * 4);                    // seg_exp
+  ar.take((p.E + 1) * 4);              // seg_off
+  ar.take(p.E * ((rows + 63) / 64) * 4);  // sort base
+  ar.take(rows * 4);                   // row_map
+  return ar.used;
+}
+
+}  // namespace
+
+int fmx_gather_qmm_out_shape(const fmx_array* x, const fmx_array* w, const fmx_array* lhs,
+                             const fmx_array* rhs, int transpose, int group_size, int bits,
+                             fmx_array* out) {
+  int rc;
+  if ((rc = check_quant_args(transpose, group_size, bits, nullptr))) return rc;
+  if (!out) return fail(FMX_ERR_ARG, "out is NULL");
+  GatherPlan p;
+  if ((rc = gather_plan(x, w, lhs, rhs, &p))) return rc;
+  out->ndim = p.ndim + 2;
+  for (int i = 0; i < p.ndim; ++i) out->shape[i] = p.batch[i];
+  out->shape[p.ndim] = p.M;
+  out->shape[p.ndim + 1] = p.N;
+  out->dtype = FMX_BF16;
+  return ok();
+}
+
+size_t fmx_gather_qmm_workspace_size(const fmx_array* x, const fmx_array* w,
+                                     const fmx_array* lhs, const fmx_array* rhs) {
+  GatherPlan p;
+  if (gather_plan(x, w, lhs, rhs, &p)) return 0;
+  return gather_ws(p);
+}
+
+int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
+                   const fmx_array* biases, const fmx_array* lhs, const fmx_array* rhs,
+                   int transpose, int group_size, int bits, const char* mode,
+                   int sorted_indices, fmx_array* out, void* workspace, size_t workspace_bytes,
+                   fmx_stream stream_) {
+  (void)sorted_indices;  // a hint; the rows are always grouped by expert
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_quant_args(transpose, group_size, bits, mode))) return rc;
+  if ((rc = check_array(x, "x", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(w, "w", FMX_U32, 2))) return rc;
+  if ((rc = check_array(scales, "scales", FMX_BF16, 2))) return rc;
+  if (!biases) return fail(FMX_ERR_ARG, "affine mode requires biases");
+  if ((rc = check_array(biases, "biases", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(out, "out", FMX_BF16, 2))) return rc;
+  if (lhs) {
+    if ((rc = check_array(lhs, "lhs_indices", -1, 0))) return rc;
+    if (lhs->dtype != FMX_U32 && lhs->dtype != FMX_I32)
+      return fail(FMX_ERR_DTYPE, "lhs_indices must be uint32 or int32");
+  }
+  if (rhs) {
+    if ((rc = check_array(rhs, "rhs_indices", -1, 0))) return rc;
+    if (rhs->dtype != FMX_U32 && rhs->dtype != FMX_I32)
+      return fail(FMX_ERR_DTYPE, "rhs_indices must be uint32 or int32");
+  }
+  GatherPlan p;
+  if ((rc = gather_plan(x, w, lhs, rhs, &p))) return rc;
+  if (p.K % 64) return fail(FMX_ERR_SHAPE, "K=%lld not a multiple of 64", static_cast<long long>(p.K));
+  if (scales->ndim != w->ndim || biases->ndim != w->ndim)
+    return fail(FMX_ERR_SHAPE, "scales/biases must have w's batch dims");
+  for (int i = 0; i < w->ndim - 1; ++i)
+    if (scales->shape[i] != w->shape[i] || biases->shape[i] != w->shape[i])
+      return fail(FMX_ERR_SHAPE, "scales/biases batch dims differ from w");
+  if (scales->shape[w->ndim - 1] != p.K / 64 || biases->shape[w->ndim - 1] != p.K / 64)
+    return fail(FMX_ERR_SHAPE, "scales/biases last dim must be K/64");
+  fmx_array expect{};
+  if ((rc = fmx_gather_qmm_out_shape(x, w, lhs, rhs, transpose, group_size, bits, &expect)))
+    return rc;
+  if (out->ndim != expect.ndim || std::memcmp(out->shape, expect.shape, sizeof(int64_t) * out->ndim))
+    return fail(FMX_ERR_SHAPE, "out shape mismatch");
+  const int64_t rows = p.nb * p.M;
+  if (rows == 0 || p.N == 0) return ok();
+  if (p.E == 0 || p.n_x == 0) return fail(FMX_ERR_SHAPE, "empty w or x batch with non-empty output");
+  if (!sort_fits(rows, p.E))
+    return fail(FMX_ERR_UNSUPPORTED, "rows=%lld x experts=%lld exceed the one-workgroup sort",
+                static_cast<long long>(rows), static_cast<long long>(p.E));
+
+  Arena ar;
+  WsGuard guard(ar);
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, gather_ws(p), stream))) return rc;
+  uint16_t* xp = static_cast<uint16_t*>(ar.take(p.n_x * p.M * p.K * 2));
+  uint32_t* lhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
+  uint32_t* rhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
+  uint32_t* keys = static_cast<uint32_t*>(ar.take(rows * 4));
+  uint32_t* order = static_cast<uint32_t*>(ar.take(rows * 4));
+  uint32_t* offsets = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
+  uint32_t* seg_n = static_cast<uint32_t*>(ar.take(4));
+  uint32_t* seg_exp = static_cast<uint32_t*>(ar.take(p.E * 4));
+  uint32_t* seg_off = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
+  uint32_t* sbase = static_cast<uint32_t*>(ar.take(p.E * ((rows + 63) / 64) * 4));
+  uint32_t* row_map = static_cast<uint32_t*>(ar.take(rows * 4));
+
+  FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, stream));
+  BcastArgs bl{}, br{};
+  fill_bcast(p, lhs, x->shape, x->ndim - 2, &bl);
+  bl.dst = lhs_flat;
+  fill_bcast(p, rhs, w->shape, w->ndim - 2, &br);
+  br.dst = rhs_flat;
+  br.M = static_cast<int>(p.M);
+  br.dst_rows = keys;
+  FMX_HIP(launch_bcast_indices(bl, stream));
+  FMX_HIP(launch_bcast_indices(br, stream));
+  SortOut so{};
+  so.order = order;
+  so.offsets = offsets;
+  so.seg_n = seg_n;
+  so.seg_exp = seg_exp;
+  so.seg_off = seg_off;
+  so.base = sbase;
+  FMX_HIP(launch_sort(keys, static_cast<int>(rows), 1, static_cast<int>(p.E), so, stream));
+  FMX_HIP(launch_gather_maps(order, lhs_flat, rows, static_cast<int>(p.M), p.n_x, row_map, stream));
+
+  QGemmProblem q{};
+  q.x = xp;
+  q.ldx = p.K;
+  q.row_map = row_map;
+  q.out_map = order;
+  q.seg_n = seg_n;
+  q.seg_exp = seg_exp;
+  q.seg_off = seg_off;
+  q.max_seg = static_cast<int>(std::min<int64_t>(p.E, rows));
+  q.w0 = static_cast<const uint32_t*>(w->data);
+  q.s0 = static_cast<const uint16_t*>(scales->data);
+  q.b0 = static_cast<const uint16_t*>(biases->data);
+  q.ew = p.N * (p.K / 8);
+  q.es = p.N * (p.K / 64);
+  q.N = static_cast<int>(p.N);
+  q.K = static_cast<int>(p.K);
+  q.out = static_cast<uint16_t*>(out->data);
+  q.ldo = p.N;
+  q.n_tiles = static_cast<int>((p.N + 15) / 16);
+  q.n_exp = static_cast<int>(p.E);
+  q.rows_max = q.out_rows = static_cast<int>(rows);
+  q.x_rows = static_cast<int>(p.n_x * p.M);
+  FMX_HIP(launch_qgemm(q, nullptr, stream));
+  return ok();
+}
+
+// ---------------------------------------------------------------- quantize
+
+int fmx_quantize(const fmx_array* w, int group_size, int bits, const char* mode, fmx_array* wq,
+                 fmx_array* scales, fmx_array* biases, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_quant_args(1, group_size, bits, mode))) return rc;
+  if ((rc = check_array(w, "w", FMX_BF16, 1))) return rc;
+  if ((rc = check_array(wq, "wq", FMX_U32, 1))) return rc;
+  if ((rc = check_array(scales, "scales", FMX_BF16, 1))) return rc;
+  if ((rc = check_array(biases, "biases", FMX_BF16, 1))) return rc;
+  const int nd = w->ndim;
+  const int64_t K = w->shape[nd - 1];
+  if (K % 64) return fail(FMX_ERR_SHAPE, "last dim %lld not a multiple of 64", static_cast<long long>(K));
+  if (wq->ndim != nd || scales->ndim != nd || biases->ndim != nd)
+    return fail(FMX_ERR_SHAPE, "outputs must have w's ndim");
+  for (int i = 0; i < nd - 1; ++i)
+    if (wq->shape[i] != w->shape[i] || scales->shape[i] != w->shape[i] || biases->shape[i] != w->shape[i])
+      return fail(FMX_ERR_SHAPE, "output leading dims differ from w");
+  if (wq->shape[nd - 1] != K / 8 || scales->shape[nd - 1] != K / 64 || biases->shape[nd - 1] != K / 64)
+    return fail(FMX_ERR_SHAPE, "wq last dim must be K/8, scales/biases K/64");
+  FMX_HIP(launch_quantize(static_cast<const uint16_t*>(w->data), numel(*w) / 64,
+                          static_cast<uint32_t*>(wq->data), static_cast<uint16_t*>(scales->data),
+                          static_cast<uint16_t*>(biases->data), stream));
+  return ok();
+}
+
+int fmx_dequantize(const fmx_array* wq, const fmx_array* scales, const fmx_array* biases,
+                   int group_size, int bits, const char* mode, fmx_array* out, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_quant_args(1, group_size, bits, mode))) return rc;
+  if ((rc = check_array(wq, "wq", FMX_U32, 1))) return rc;
+  if ((rc = check_array(scales, "scales", FMX_BF16, 1))) return rc;
+  if (!biases) return fail(FMX_ERR_ARG, "affine mode requires biases");
+  if ((rc = check_array(biases, "biases", FMX_BF16, 1))) return rc;
+  if ((rc = check_array(out, "out", FMX_BF16, 1))) return rc;
+  const int nd = wq->ndim;
+  const int64_t K = wq->shape[nd - 1] * 8;
+  if (out->ndim != nd || scales->ndim != nd || biases->ndim != nd)
+    return fail(FMX_ERR_SHAPE, "ndim mismatch");
+  for (int i = 0; i < nd - 1; ++i)
+    if (out->shape[i] != wq->shape[i] || scales->shape[i] != wq->shape[i] || biases->shape[i] != wq->shape[i])
+      return fail(FMX_ERR_SHAPE, "leading dims differ");
+  if (out->shape[nd - 1] != K || scales->shape[nd - 1] != K / 64 || biases->shape[nd - 1] != K / 64)
+    return fail(FMX_ERR_SHAPE, "last dims inconsistent");
+  if (K % 64) return fail(FMX_ERR_SHAPE, "K not a multiple of 64");
+  FMX_HIP(launch_dequantize(static_cast<const uint32_t*>(wq->data),
+                            static_cast<const uint16_t*>(scales->data),
+                            static_cast<const uint16_t*>(biases->data), numel(*out) / 64,
+                            static_cast<uint16_t*>(out->data), stream));
+  return ok();
+}
+
+int fmx_stack_experts(const void* const* src, int64_t n_experts, size_t bytes, void* dst,
+                      fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!src || !dst || n_experts < 0) return fail(FMX_ERR_ARG, "NULL argument");
+  for (int64_t e = 0; e < n_experts; ++e) {
+    if (!src[e]) return fail(FMX_ERR_ARG, "expert %lld source is NULL", static_cast<long long>(e));
+    FMX_HIP(hipMemcpyAsync(static_cast<char*>(dst) + e * bytes, src[e], bytes,
+                           hipMemcpyDeviceToDevice, stream));
+  }
+  return ok();
+}
+
+// ---------------------------------------------------------------- MoE block
+
+size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens) {
+  if (check_moe_config(cfg) || max_tokens < 0 || max_tokens > kMoEMaxTokens) return 0;
+  return moe_layout(*cfg, max_tokens, nullptr).total;
+}
+
+int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
+  if (workspace_bytes < kCounterBytes)
+    return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, kCounterBytes);
+  FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(workspace), kCounterBytes / 4, 0u, stream));
+  return ok();
+}
+
+int fmx_moe_workspace_routing(const fmx_moe_config* cfg, int64_t n_tokens, const void* workspace,
+                              const uint32_t** inds, const void** scores, const void** probs,
+                              const uint32_t** order, const uint32_t** inv,
+                              const uint32_t** src, const uint32_t** idx,
+                              const uint32_t** expert_offsets) {
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
+  if (n_tokens < 0 || n_tokens > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  const MoELayout L = moe_layout(*cfg, n_tokens, static_cast<char*>(const_cast<void*>(workspace)));
+  if (inds) *inds = L.inds;
+  if (scores) *scores = L.scores;
+  if (probs) *probs = L.probs;
+  if (order) *order = L.order;
+  if (inv) *inv = L.inv;
+  if (src) *src = L.src;
+  if (idx) *idx = L.idx;
+  if (expert_offsets) *expert_offsets = L.offsets;
+  return ok();
+}
+
+int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x,
+                          int64_t T, void* y, void* workspace, size_t workspace_bytes,
+                          fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  if (!w || !x || !y) return fail(FMX_ERR_ARG, "NULL argument");
+  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens=%lld out of range", static_cast<long long>(T));
+  if (T == 0) return ok();
+  const fmx_moe_config& c = *cfg;
+  const bool has_sh = c.shared_expert_intermediate_size > 0;
+  if (!w->router_w || !aligned(w->router_w, 16)) return fail(FMX_ERR_ARG, "router_w NULL or misaligned");
+  if (!qw_ok(w->gate) || !qw_ok(w->up) || !qw_ok(w->down))
+    return fail(FMX_ERR_ARG, "expert weights NULL or misaligned");
+  if (has_sh && (!qw_ok(w->shared_gate) || !qw_ok(w->shared_up) || !qw_ok(w->shared_down) ||
+                 !w->shared_expert_gate_w || !aligned(w->shared_expert_gate_w, 16)))
+    return fail(FMX_ERR_ARG, "shared expert weights NULL or misaligned");
+  if (!aligned(x, 16) || !aligned(y, 16)) return fail(FMX_ERR_ARG, "x/y not 16-byte aligned");
+  const int64_t H = c.hidden_size, E = c.num_experts, k = c.num_experts_per_tok;
+  const int64_t I = c.moe_intermediate_size, Is = c.shared_expert_intermediate_size;
+  const int64_t n = T * k;
+  if (!sort_fits(n, E))
+    return fail(FMX_ERR_UNSUPPORTED, "T*k=%lld with E=%lld exceeds the one-workgroup sort",
+                static_cast<long long>(n), static_cast<long long>(E));
+
+  Arena ar;
+  WsGuard guard(ar);
+  const size_t need = moe_layout(c, T, nullptr).total;
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
+  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  const MoELayout L = moe_layout(c, T, ar.base);
+
+  // 1. router + top-k (+ sort when it fits in the router's last workgroup)
+  bool sorted = false;
+  if ((rc = run_router(c, L, x, T, w->router_w, w->router_logit_bias,
+                       has_sh ? w->shared_expert_gate_w : nullptr, L.inds, L.scores, L.probs,
+                       has_sh ? L.sgate : nullptr, L.xp, true, &sorted, stream)))
+    return rc;
+  if (!sorted) {
+    SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base};
+    FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
+  }
+
+  // 2. gate/up + SwiGLU: routed experts over the sorted rows, and the shared expert
+  QGemmProblem gu{};
+  gu.x = L.xp;
+  gu.ldx = H;
+  gu.row_map = L.src;
+  gu.seg_n = L.seg_n;
+  gu.seg_exp = L.seg_exp;
+  gu.seg_off = L.seg_off;
+  gu.max_seg = static_cast<int>(std::min(E, n));
+  gu.w0 = static_cast<const uint32_t*>(w->gate.w);
+  gu.s0 = static_cast<const uint16_t*>(w->gate.scales);
+  gu.b0 = static_cast<const uint16_t*>(w->gate.biases);
+  gu.w1 = static_cast<const uint32_t*>(w->up.w);
+  gu.s1 = static_cast<const uint16_t*>(w->up.scales);
+  gu.b1 = static_cast<const uint16_t*>(w->up.biases);
+  gu.ew = I * (H / 8);
+  gu.es = I * (H / 64);
+  gu.N = static_cast<int>(I);
+  gu.K = static_cast<int>(H);
+  gu.out = L.h;
+  gu.ldo = I;
+  gu.dual = 1;
+  gu.out_p8 = 1;
+  gu.n_tiles = static_cast<int>((I + 15) / 16);
+  gu.n_exp = static_cast<int>(E);
+  gu.rows_max = gu.out_rows = static_cast<int>(n);
+  gu.x_rows = static_cast<int>(T);
+  QGemmProblem sgu{};
+  if (has_sh) {
+    sgu.x = L.xp;
+    sgu.ldx = H;
+    sgu.rows_static = static_cast<int>(T);
+    sgu.max_seg = 1;
+    sgu.w0 = static_cast<const uint32_t*>(w->shared_gate.w);
+    sgu.s0 = static_cast<const uint16_t*>(w->shared_gate.scales);
+    sgu.b0 = static_cast<const uint16_t*>(w->shared_gate.biases);
+    sgu.w1 = static_cast<const uint32_t*>(w->shared_up.w);
+    sgu.s1 = static_cast<const uint16_t*>(w->shared_up.scales);
+    sgu.b1 = static_cast<const uint16_t*>(w->shared_up.biases);
+    sgu.N = static_cast<int>(Is);
+    sgu.K = static_cast<int>(H);
+    sgu.out = L.hs;
+    sgu.ldo = Is;
+    sgu.dual = 1;
+    sgu.out_p8 = 1;
+    sgu.n_tiles = static_cast<int>((Is + 15) / 16);
+    sgu.n_exp = 1;
+    sgu.rows_max = sgu.x_rows = sgu.out_rows = static_cast<int>(T);
+  }
+  FMX_HIP(launch_qgemm(gu, has_sh ? &sgu : nullptr, stream));
+
+  // 3. down: routed rows (sorted order) and the shared expert
+  QGemmProblem dn{};
+  dn.x = L.h;
+  dn.ldx = I;
+  dn.seg_n = L.seg_n;
+  dn.seg_exp = L.seg_exp;
+  dn.seg_off = L.seg_off;
+  dn.max_seg = gu.max_seg;
+  dn.w0 = static_cast<const uint32_t*>(w->down.w);
+  dn.s0 = static_cast<const uint16_t*>(w->down.scales);
+  dn.b0 = static_cast<const uint16_t*>(w->down.biases);
+  dn.ew = H * (I / 8);
+  dn.es = H * (I / 64);
+  dn.N = static_cast<int>(H);
+  dn.K = static_cast<int>(I);
+  dn.out = L.d;
+  dn.ldo = H;
+  dn.n_tiles = static_cast<int>((H + 15) / 16);
+  dn.n_exp = static_cast<int>(E);
+  dn.rows_max = dn.x_rows = dn.out_rows = static_cast<int>(n);
+  QGemmProblem sdn{};
+  if (has_sh) {
+    sdn.x = L.hs;
+    sdn.ldx = Is;
+    sdn.rows_static = static_cast<int>(T);
+    sdn.max_seg = 1;
+    sdn.w0 = static_cast<const uint32_t*>(w->shared_down.w);
+    sdn.s0 = static_cast<const uint16_t*>(w->shared_down.scales);
+    sdn.b0 = static_cast<const uint16_t*>(w->shared_down.biases);
+    sdn.N = static_cast<int>(H);
+    sdn.K = static_cast<int>(Is);
+    sdn.out = L.sd;
+    sdn.ldo = H;
+    sdn.n_tiles = static_cast<int>((H + 15) / 16);
+    sdn.n_exp = 1;
+    sdn.rows_max = sdn.x_rows = sdn.out_rows = static_cast<int>(T);
+  }
+  FMX_HIP(launch_qgemm(dn, has_sh ? &sdn : nullptr, stream));
+
+  // 4. top-k weighted combine + gated shared expert
+  CombineArgs cb{};
+  cb.d = L.d;
+  cb.inv = L.inv;
+  cb.scores = L.scores;
+  cb.sd = has_sh ? L.sd : nullptr;
+  cb.sgate = has_sh ? L.sgate : nullptr;
+  cb.y = static_cast<uint16_t*>(y);
+  cb.T = static_cast<int>(T);
+  cb.k = static_cast<int>(k);
+  cb.H = static_cast<int>(H);
+  FMX_HIP(launch_combine(cb, stream));
+  return ok();
+}
+
+int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, const void* router_w,
+                        const void* lbias, uint32_t* inds, void* scores, void* probs,
+                        void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  if (!x || !router_w || !inds || !scores) return fail(FMX_ERR_ARG, "NULL argument");
+  if (!aligned(x, 16) || !aligned(router_w, 16)) return fail(FMX_ERR_ARG, "x/router_w not 16-byte aligned");
+  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  if (T == 0) return ok();
+  Arena ar;
+  WsGuard guard(ar);
+  const size_t need = moe_layout(*cfg, T, nullptr).total;
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
+  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  const MoELayout L = moe_layout(*cfg, T, ar.base);
+  return run_router(*cfg, L, x, T, router_w, lbias, nullptr, inds, static_cast<uint16_t*>(scores),
+                    static_cast<uint16_t*>(probs), nullptr, nullptr, false, nullptr, stream);
+}
+
+size_t fmx_moe_sort_workspace_size(int64_t T, int32_t k, int64_t E) {
+  if (T < 0 || k < 1 || E < 1) return 0;
+  const int64_t n = T * k;
+  Arena sizer;
+  sizer.take((E + 1) * 4);
+  sizer.take(E * ((n + 63) / 64) * 4);
+  return sizer.used;
+}
+
+int fmx_moe_sort(const uint32_t* inds, int64_t T, int32_t k, int64_t E, uint32_t* order,
+                 uint32_t* inv, uint32_t* src, uint32_t* idx, uint32_t* expert_offsets,
+                 void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!inds && T > 0) return fail(FMX_ERR_ARG, "inds is NULL");
+  if (T < 0 || k < 1 || E < 1) return fail(FMX_ERR_SHAPE, "bad sizes");
+  const int64_t n = T * k;
+  if (n == 0) return ok();
+  if (!sort_fits(n, E)) return fail(FMX_ERR_UNSUPPORTED, "n=%lld, E=%lld exceed the one-workgroup sort",
+                                    static_cast<long long>(n), static_cast<long long>(E));
+  Arena ar;
+  WsGuard guard(ar);
+  int rc;
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, fmx_moe_sort_workspace_size(T, k, E),
+                           stream)))
+    return rc;
+  uint32_t* off_scratch = static_cast<uint32_t*>(ar.take((E + 1) * 4));
+  uint32_t* base = static_cast<uint32_t*>(ar.take(E * ((n + 63) / 64) * 4));
+  SortOut so{order, inv, src, idx, expert_offsets ? expert_offsets : off_scratch,
+             nullptr, nullptr, nullptr, base};
+  FMX_HIP(launch_sort(inds, static_cast<int>(n), k, static_cast<int>(E), so, stream));
+  return ok();
+}
+
+}  // extern "C"

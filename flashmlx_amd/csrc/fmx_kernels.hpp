@@ -1,0 +1,136 @@
+// fmx_kernels.hpp -- kernel argument blocks and launchers (library-internal).
+#pragma once
+
+#include "fmx_common.hpp"
+
+namespace fmx {
+
+// ---------------------------------------------------------------- sorting
+// Stable counting sort of n keys (< E) by key: the permutation MLX's
+// argsort(flatten(inds)) produces in switch_mlp (server/src/model.cpp:686-699)
+// plus the non-empty-expert segment table the grouped GEMMs walk.
+struct SortOut {
+  uint32_t* order;    // [n]   sorted position -> entry           (nullable)
+  uint32_t* inv;      // [n]   entry -> sorted position           (nullable)
+  uint32_t* src;      // [n]   sorted position -> entry / k       (nullable)
+  uint32_t* idx;      // [n]   sorted position -> key             (nullable)
+  uint32_t* offsets;  // [E+1] first sorted position of each key  (required)
+  uint32_t* seg_n;    // [1]   number of non-empty keys U         (nullable)
+  uint32_t* seg_exp;  // [E]   u -> key of the u-th non-empty key (nullable)
+  uint32_t* seg_off;  // [E+1] u -> first sorted position         (nullable)
+  uint32_t* base;     // [E * ceil(n/64)] scratch
+};
+
+// Sort in one workgroup of 1024 threads (separate launch).
+constexpr int kSortThreads = 1024;
+constexpr int kSortCntBytes = 64 * 1024;   // LDS for the [E][tiles] count table
+constexpr int kSortMaxN = 32 * 1024;       // LDS for the per-entry ranks
+bool sort_fits(int64_t n, int64_t E);
+hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
+                       hipStream_t stream);
+
+// ---------------------------------------------------------------- router
+// logits = x . [Wr; wsg]^T in fp64 (exact bf16 products), rounded once to
+// bf16; per token: softmax in fp64 with exp_det, top-k, scores, renorm;
+// optionally the sort of all tokens' indices in the last workgroup.
+constexpr int kRouterTok = 8;      // tokens per tile
+constexpr int kRouterCols = 8;     // logit columns per tile
+constexpr int kRouterThreads = 256;
+constexpr int kRouterSortCnt = 16 * 1024;  // LDS bytes for a fused sort's count table
+constexpr int kRouterSortMaxN = 2048;
+
+struct RouterArgs {
+  const uint16_t* x;       // [T, H] bf16
+  const uint16_t* wr;      // [E, H] bf16
+  const uint16_t* lbias;   // [E] bf16 or null
+  const uint16_t* wsg;     // [H] bf16 shared-expert gate or null
+  int T, H, E, k, norm;
+  uint16_t* logits;        // [T, E+1] bf16 scratch (column E: shared gate logit)
+  uint16_t* probs;         // [T, E] bf16 or null
+  uint32_t* inds;          // [T, k]
+  uint16_t* scores;        // [T, k] bf16
+  float* sgate;            // [T] sigmoid(shared gate logit) (bf16 value) or null
+  uint16_t* xp;            // [T, H] P8 copy of x or null
+  uint32_t* counters;      // [n_tt + 1], zero on entry, zero on exit
+  int n_tt, n_ct;          // token tiles, column tiles
+  int fuse_sort;           // last workgroup sorts inds (needs router_sort_fits)
+  SortOut sort;
+};
+bool router_sort_fits(int64_t n, int64_t E);
+hipError_t launch_router(const RouterArgs& a, hipStream_t stream);
+
+// ---------------------------------------------------------------- grouped GEMM
+// One problem: rows grouped in segments that share one expert's packed
+// weights. out[row] = x[row_map[row]] . deq(W[e])^T  (or SwiGLU of two).
+struct QGemmProblem {
+  const uint16_t* x;        // activation rows in P8 layout
+  int64_t ldx;              // elements between x rows
+  const uint32_t* row_map;  // sorted row -> x row (null: identity)
+  const uint32_t* out_map;  // sorted row -> out row (null: identity)
+  const uint32_t* seg_n;    // device segment count (null: 1 static segment)
+  const uint32_t* seg_exp;  // device expert per segment (null: expert 0)
+  const uint32_t* seg_off;  // device [n+1] row offsets (null: [0, rows_static))
+  int rows_static;
+  int max_seg;              // segments the grid covers
+  const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // gate (or the matrix)
+  const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // up (dual only)
+  int64_t ew, es;           // per-expert strides: u32 words, bf16 elements
+  int N, K;
+  uint16_t* out;
+  int64_t ldo;
+  int dual;                 // out = swiglu(x.W0^T, x.W1^T)
+  int out_p8;               // write out rows in P8 layout (needs N % 8 == 0)
+  int n_tiles;              // ceil(N / 16)
+  // bounds the device-side tables are clamped to, so that stale or invalid
+  // routing state can never address memory outside the arrays
+  int n_exp;                // experts in w (seg_exp values clamp to n_exp-1)
+  int rows_max;             // sorted rows (seg_off values clamp to it)
+  int x_rows;               // rows of x (row_map values clamp to x_rows-1)
+  int out_rows;             // rows of out (out_map values clamp to out_rows-1)
+};
+// Launch one or two independent problems in one grid (p1 may be null).
+hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStream_t stream);
+
+// ---------------------------------------------------------------- elementwise
+struct CombineArgs {
+  const uint16_t* d;       // [T*k, H] bf16, sorted rows
+  const uint32_t* inv;     // [T*k] entry -> sorted row
+  const uint16_t* scores;  // [T, k] bf16
+  const uint16_t* sd;      // [T, H] bf16 shared-expert output or null
+  const float* sgate;      // [T] or null
+  uint16_t* y;             // [T, H] bf16
+  int T, k, H;
+};
+hipError_t launch_combine(const CombineArgs& a, hipStream_t stream);
+
+hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
+                             hipStream_t stream);
+hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
+
+// gather_qmm row maps: for sorted row r (of nb*M rows, sorted by rhs key),
+// x row = lhs[b]*M + m where b*M + m = order[r]; lhs values >= n_x are
+// clamped to n_x - 1.
+hipError_t launch_gather_maps(const uint32_t* order, const uint32_t* lhs, int64_t rows,
+                              int M, int64_t n_x, uint32_t* row_map, hipStream_t stream);
+
+// MLX broadcasting of index arrays to the common batch shape (up to 8 dims).
+struct BcastArgs {
+  const void* src; int is_i32;  // null: arange over the flattened batch
+  int ndim;
+  int64_t out_shape[8];
+  int64_t src_stride[8];        // 0 on broadcast dims
+  int64_t n;
+  uint32_t* dst;
+  // M > 1: also emit the per-row key expansion: dst_rows[b*M + m] = dst[b]
+  int M;
+  uint32_t* dst_rows;           // nullable
+};
+hipError_t launch_bcast_indices(const BcastArgs& a, hipStream_t stream);
+
+// ---------------------------------------------------------------- quantization
+hipError_t launch_quantize(const uint16_t* w, int64_t n_groups, uint32_t* wq, uint16_t* s,
+                           uint16_t* b, hipStream_t stream);
+hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* s, const uint16_t* b,
+                             int64_t n_groups, uint16_t* out, hipStream_t stream);
+
+}  // namespace fmx

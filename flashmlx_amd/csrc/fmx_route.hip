@@ -1,0 +1,337 @@
+// fmx_route.hip -- router (logits, softmax, top-k, scores) and the
+// token->expert stable counting sort.
+//
+// Reference: server/src/model.cpp:757-775 (router, softmax, argpartition
+// top-k, take_along_axis), :682-700 (switch_mlp's argsort-based sort), and
+// the renormalisation of docs/superpowers/plans/2026-04-01-moe-support-plan.md:319-322.
+#include "fmx_kernels.hpp"
+
+namespace fmx {
+
+// ------------------------------------------------------------------ helpers
+
+__device__ inline uint64_t lanes_below(int lane) {
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+template <int NT>
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == kWave - 1) s_tmp[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t t = s_tmp[w];
+      s_tmp[w] = run;
+      run += t;
+    }
+    s_tmp[NW] = run;
+  }
+  __syncthreads();
+  const uint32_t r = s_tmp[wave] + x - v;
+  if (total) *total = s_tmp[NW];
+  __syncthreads();
+  return r;
+}
+
+// Stable counting sort of n keys by value, by one workgroup of NT threads.
+// Entries are cut into tiles of 64 (one per lane of a wave). Within a tile,
+// the lanes holding an equal key are found with one ballot per key bit; a
+// lane's rank among them is the popcount of the equal lanes below it. The
+// per-(key, tile) counts, scanned in key-major order, give every (key, tile)
+// its first output position, so position = base[key][tile] + rank.
+// s_cnt: E * n_tiles bytes of LDS; s_rank: n bytes; s_tmp: NT/64 + 1 words.
+template <int NT>
+__device__ void sort_block(const uint32_t* __restrict__ keys, int n, int k, int E,
+                           const SortOut& o, uint8_t* s_cnt, uint8_t* s_rank,
+                           uint32_t* s_tmp) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_tiles = (n + 63) / 64;
+  const int total = E * n_tiles;
+  const int nbits = E <= 1 ? 1 : 32 - __builtin_clz(static_cast<uint32_t>(E - 1));
+
+  for (int i = tid; i < total; i += NT) s_cnt[i] = 0;
+  __syncthreads();
+
+  for (int tile = wave; tile < n_tiles; tile += NW) {
+    const int i = tile * 64 + lane;
+    const bool valid = i < n;
+    uint32_t key = valid ? keys[i] : 0u;
+    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
+    uint64_t eq = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      eq &= bit ? m : ~m;
+    }
+    if (valid) {
+      const int rank = __popcll(eq & lanes_below(lane));
+      s_rank[i] = static_cast<uint8_t>(rank);
+      if (rank == 0) s_cnt[key * n_tiles + tile] = static_cast<uint8_t>(__popcll(eq));
+    }
+  }
+  __syncthreads();
+
+  // key-major exclusive scan of the count table
+  const int per = (total + NT - 1) / NT;
+  const int beg = tid * per;
+  const int end = min(beg + per, total);
+  uint32_t local = 0;
+  for (int j = beg; j < end; ++j) local += s_cnt[j];
+  uint32_t run = block_exclusive_scan<NT>(local, s_tmp, nullptr);
+  for (int j = beg; j < end; ++j) {
+    o.base[j] = run;
+    if (j % n_tiles == 0) o.offsets[j / n_tiles] = run;
+    run += s_cnt[j];
+  }
+  if (tid == 0) o.offsets[E] = static_cast<uint32_t>(n);
+  __syncthreads();
+
+  for (int i = tid; i < n; i += NT) {
+    uint32_t key = keys[i];
+    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
+    const uint32_t pos = o.base[key * n_tiles + i / 64] + s_rank[i];
+    if (o.order) o.order[pos] = static_cast<uint32_t>(i);
+    if (o.inv) o.inv[i] = pos;
+    if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
+    if (o.idx) o.idx[pos] = key;
+  }
+
+  // segment table of the non-empty keys, ascending
+  if (o.seg_off) {
+    const int eper = (E + NT - 1) / NT;
+    const int eb = tid * eper, ee = min(eb + eper, E);
+    uint32_t cnt = 0;
+    for (int e = eb; e < ee; ++e) cnt += (o.offsets[e + 1] > o.offsets[e]) ? 1u : 0u;
+    uint32_t U = 0;
+    uint32_t u = block_exclusive_scan<NT>(cnt, s_tmp, &U);
+    for (int e = eb; e < ee; ++e) {
+      if (o.offsets[e + 1] > o.offsets[e]) {
+        if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
+        o.seg_off[u] = o.offsets[e];
+        ++u;
+      }
+    }
+    if (tid == 0) {
+      o.seg_off[U] = static_cast<uint32_t>(n);
+      if (o.seg_n) *o.seg_n = U;
+    }
+  }
+}
+
+bool sort_fits(int64_t n, int64_t E) {
+  const int64_t tiles = (n + 63) / 64;
+  return n >= 0 && n <= kSortMaxN && E >= 1 && E * tiles <= kSortCntBytes;
+}
+
+__global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys, int n, int k,
+                                                            int E, SortOut o) {
+  __shared__ uint8_t s_cnt[kSortCntBytes];
+  __shared__ uint8_t s_rank[kSortMaxN];
+  __shared__ uint32_t s_tmp[kSortThreads / kWave + 1];
+  sort_block<kSortThreads>(keys, n, k, E, o, s_cnt, s_rank, s_tmp);
+}
+
+hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
+                       hipStream_t stream) {
+  hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, keys, n, k, E, o);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ router
+
+bool router_sort_fits(int64_t n, int64_t E) {
+  const int64_t tiles = (n + 63) / 64;
+  return n <= kRouterSortMaxN && E * tiles <= kRouterSortCnt;
+}
+
+__device__ inline double warp_max_f64(double v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fmax(v, __shfl_xor(v, d));
+  return v;
+}
+
+__device__ inline uint32_t warp_max_u32(uint32_t v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(v, d)));
+  return v;
+}
+
+// Release this workgroup's global writes and count it in; true in exactly
+// one workgroup: the last of `expected` to arrive, which then sees all of
+// their writes. Every thread fences its own stores before the barrier.
+__device__ inline bool arrive_last(uint32_t* counter, uint32_t expected, int* s_flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = atomicAdd(counter, 1u);
+    *s_flag = (prev == expected - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  const bool last = *s_flag != 0;
+  if (last) __threadfence();
+  return last;
+}
+
+constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
+
+__global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
+  __shared__ uint8_t s_cnt[kRouterSortCnt];
+  __shared__ uint8_t s_rank[kRouterSortMaxN];
+  __shared__ uint32_t s_tmp[kRouterThreads / kWave + 1];
+  __shared__ int s_flag;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ct = blockIdx.x, tt = blockIdx.y;
+  const int H = a.H, E = a.E;
+  const int ncols = E + (a.wsg ? 1 : 0);
+
+  // ---- phase 1: one 8x8 tile of logits; 4 threads per dot product
+  {
+    const int pair = tid >> 2, q = tid & 3;
+    const int t = tt * kRouterTok + (pair >> 3);
+    const int c = ct * kRouterCols + (pair & 7);
+    const bool valid = t < a.T && c < ncols;
+    double acc = 0.0;
+    if (valid) {
+      const uint16_t* xr = a.x + static_cast<int64_t>(t) * H;
+      const uint16_t* wrow = c < E ? a.wr + static_cast<int64_t>(c) * H : a.wsg;
+      const int h0 = q * (H / 4), h1 = h0 + H / 4;
+      for (int h = h0; h < h1; h += 8) {
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xr + h);
+        const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(wrow + h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const double x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+          const double w0 = __uint_as_float(wv[i] << 16), w1 = __uint_as_float(wv[i] & 0xffff0000u);
+          acc = __builtin_fma(x0, w0, acc);
+          acc = __builtin_fma(x1, w1, acc);
+        }
+      }
+    }
+    acc += __shfl_xor(acc, 1);
+    acc += __shfl_xor(acc, 2);
+    if (valid && q == 0) {
+      uint16_t l = f64_to_bf16(acc);
+      if (c < E && a.lbias)
+        l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) +
+                        static_cast<double>(bf16_to_f32(a.lbias[c])));
+      a.logits[static_cast<int64_t>(t) * (E + 1) + c] = l;
+    }
+    // P8 copy of the tile's x rows, once per token tile
+    if (ct == 0 && a.xp) {
+      const int oct = H / 8;
+      for (int o = tid; o < kRouterTok * oct; o += kRouterThreads) {
+        const int tl = o / oct, oc = o % oct;
+        const int tok = tt * kRouterTok + tl;
+        if (tok >= a.T) continue;
+        const u32x4_t v =
+            *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(tok) * H + oc * 8);
+        // elements e0..e7 -> slots 0,2,4,6 (e0..e3) and 1,3,5,7 (e4..e7)
+        u32x4_t p;
+        p[0] = (v[0] & 0xffffu) | (v[2] << 16);
+        p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+        p[2] = (v[1] & 0xffffu) | (v[3] << 16);
+        p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+        *reinterpret_cast<u32x4_t*>(a.xp + static_cast<int64_t>(tok) * H + oc * 8) = p;
+      }
+    }
+  }
+  if (!arrive_last(&a.counters[tt], static_cast<uint32_t>(a.n_ct), &s_flag)) return;
+
+  // ---- phase 2 (last column tile of this token tile): softmax and top-k
+  for (int tl = wave; tl < kRouterTok; tl += kRouterThreads / kWave) {
+    const int t = tt * kRouterTok + tl;
+    if (t >= a.T) break;
+    const uint16_t* lrow = a.logits + static_cast<int64_t>(t) * (E + 1);
+    double lv[kMaxExpertsPerLane];
+    double m = -__builtin_huge_val();
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      const int e = lane + 64 * i;
+      lv[i] = e < E ? static_cast<double>(bf16_to_f32(lrow[e])) : -__builtin_huge_val();
+      m = fmax(m, lv[i]);
+    }
+    m = warp_max_f64(m);
+    double ex[kMaxExpertsPerLane];
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      const int e = lane + 64 * i;
+      ex[i] = e < E ? exp_det(lv[i] - m) : 0.0;
+    }
+    // sequential sum in expert order: e = 64*i + l
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      if (64 * i >= E) break;
+      const int lim = min(64, E - 64 * i);
+      for (int l = 0; l < lim; ++l) sum += __shfl(ex[i], l);
+    }
+    uint32_t key[kMaxExpertsPerLane];
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) {
+        const uint16_t p = f64_to_bf16(ex[i] / sum);
+        if (a.probs) a.probs[static_cast<int64_t>(t) * E + e] = p;
+        key[i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
+      } else {
+        key[i] = 0u;
+      }
+    }
+    // top-k: (prob desc, expert asc); probabilities are >= 0 so their bf16
+    // bit patterns order like their values
+    float sc_sum = 0.0f;
+    uint16_t sc[16];
+    for (int j = 0; j < a.k; ++j) {
+      uint32_t best = 0u;
+#pragma unroll
+      for (int i = 0; i < kMaxExpertsPerLane; ++i) best = max(best, key[i]);
+      best = warp_max_u32(best);
+      const uint32_t e = 0xffffu - (best & 0xffffu);
+#pragma unroll
+      for (int i = 0; i < kMaxExpertsPerLane; ++i)
+        if (key[i] == best) key[i] = 0u;
+      sc[j] = static_cast<uint16_t>(best >> 16);
+      sc_sum += bf16_to_f32(sc[j]);
+      if (lane == 0) a.inds[static_cast<int64_t>(t) * a.k + j] = e;
+    }
+    if (lane == 0) {
+      if (a.norm) {
+        const double den = static_cast<double>(round_bf16(sc_sum));
+        for (int j = 0; j < a.k; ++j) {
+          const float qv =
+              static_cast<float>(static_cast<double>(bf16_to_f32(sc[j])) / den);
+          a.scores[static_cast<int64_t>(t) * a.k + j] = f32_to_bf16(qv);
+        }
+      } else {
+        for (int j = 0; j < a.k; ++j) a.scores[static_cast<int64_t>(t) * a.k + j] = sc[j];
+      }
+      if (a.wsg && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
+    }
+  }
+  if (tid == 0) a.counters[tt] = 0u;  // every column tile of this token tile has arrived
+
+  if (!a.fuse_sort) return;
+  if (!arrive_last(&a.counters[a.n_tt], static_cast<uint32_t>(a.n_tt), &s_flag)) return;
+
+  // ---- phase 3 (last token tile): sort all tokens' expert indices
+  sort_block<kRouterThreads>(a.inds, a.T * a.k, a.k, E, a.sort, s_cnt, s_rank, s_tmp);
+  if (tid == 0) a.counters[a.n_tt] = 0u;
+}
+
+hipError_t launch_router(const RouterArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(router_kernel, dim3(a.n_ct, a.n_tt), dim3(kRouterThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace fmx

@@ -1,0 +1,172 @@
+"""MoE-layer workloads: model shapes, token counts, seeds, synthetic inputs.
+
+Shapes follow the two MoE families the reference serves through
+LlamaModel::moe_block (server/src/model.cpp:750-807; config fields
+server/include/flashmlx/model.h:40-53):
+  Qwen1.5-MoE-A2.7B: H 2048, 60 experts, top-4, I 1408, shared expert 5632
+                     with a sigmoid gate, no top-k renormalisation;
+  Qwen3-30B-A3B:     H 2048, 128 experts, top-8, I 768, no shared expert,
+                     renormalised top-k scores.
+Inputs are drawn from fmx_synth_normal_bf16 (one counter-based stream per
+tensor), so every byte is a pure function of (seed, tensor, index).
+"""
+from __future__ import annotations
+
+import hashlib
+from dataclasses import dataclass, field
+from typing import Dict, Optional
+
+import numpy as np
+
+QWEN15 = dict(name="qwen1.5-moe-a2.7b", hidden=2048, n_experts=60, top_k=4, inter=1408,
+              shared_inter=5632, norm_topk=False)
+QWEN3 = dict(name="qwen3-30b-a3b", hidden=2048, n_experts=128, top_k=8, inter=768,
+             shared_inter=0, norm_topk=True)
+# small shapes with the same structure, for tests that the CPU oracle must finish fast
+TINY = dict(name="tiny", hidden=256, n_experts=8, top_k=2, inter=128, shared_inter=192,
+            norm_topk=False)
+TINY_NORM = dict(name="tiny-norm", hidden=320, n_experts=12, top_k=3, inter=192, shared_inter=0,
+                 norm_topk=True)
+
+# synth stream ids, one per tensor
+S_X, S_ROUTER, S_RBIAS = 1, 2, 3
+S_GATE, S_UP, S_DOWN = 10, 11, 12
+S_SH_GATE, S_SH_UP, S_SH_DOWN, S_SH_EGATE = 20, 21, 22, 23
+
+W_STD = 0.02
+
+
+@dataclass(frozen=True)
+class Workload:
+    key: str
+    model: dict
+    tokens: int
+    seed: int
+    router_bias: bool = False
+    note: str = ""
+
+
+WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
+    Workload("qwen15_decode_b1", QWEN15, 1, 0, note="decode batch 1"),
+    Workload("qwen15_decode_b4", QWEN15, 4, 1, note="decode batch 4"),
+    Workload("qwen15_decode_b8", QWEN15, 8, 2, note="decode batch 8"),
+    Workload("qwen15_prefill_512", QWEN15, 512, 3, router_bias=True,
+             note="prefill 512 tokens, per-expert router logit bias ~ N(0,1)"),
+    Workload("qwen3_decode_b1", QWEN3, 1, 4, note="decode batch 1"),
+    Workload("qwen3_decode_b8", QWEN3, 8, 4, note="decode batch 8"),
+    Workload("qwen3_prefill_1024", QWEN3, 1024, 4, note="prefill 1024 tokens"),
+    Workload("tiny_t5", TINY, 5, 11, note="tiny shapes, 5 tokens"),
+    Workload("tiny_t40", TINY, 40, 12, router_bias=True, note="tiny shapes, 40 tokens, skewed"),
+    Workload("tiny_norm_t33", TINY_NORM, 33, 13, note="tiny shapes, renormalised top-3"),
+]}
+
+
+def _synth(n: int, seed: int, stream: int, std: float) -> np.ndarray:
+    from .moe import synth_normal_bf16
+    return synth_normal_bf16(n, seed, stream, 0.0, std)
+
+
+@dataclass
+class HostInputs:
+    """bf16 bit patterns (uint16) of every input of one MoE-layer call."""
+    x: np.ndarray                      # [T, H]
+    router_w: np.ndarray               # [E, H]
+    router_bias: Optional[np.ndarray]  # [E]
+    gate: np.ndarray                   # [E, I, H]
+    up: np.ndarray                     # [E, I, H]
+    down: np.ndarray                   # [E, H, I]
+    shared_gate: Optional[np.ndarray] = None   # [Is, H]
+    shared_up: Optional[np.ndarray] = None     # [Is, H]
+    shared_down: Optional[np.ndarray] = None   # [H, Is]
+    shared_expert_gate_w: Optional[np.ndarray] = None  # [1, H]
+    meta: dict = field(default_factory=dict)
+
+    def sha256(self) -> str:
+        h = hashlib.sha256()
+        for name in ("x", "router_w", "router_bias", "gate", "up", "down", "shared_gate",
+                     "shared_up", "shared_down", "shared_expert_gate_w"):
+            a = getattr(self, name)
+            if a is not None:
+                h.update(name.encode())
+                h.update(np.ascontiguousarray(a).tobytes())
+        return h.hexdigest()
+
+
+def host_inputs(wl: Workload, tokens: Optional[int] = None) -> HostInputs:
+    m = wl.model
+    T = wl.tokens if tokens is None else tokens
+    H, E, I, Is = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"]
+    s = wl.seed
+    hi = HostInputs(
+        x=_synth(T * H, s, S_X, 1.0).reshape(T, H),
+        router_w=_synth(E * H, s, S_ROUTER, W_STD).reshape(E, H),
+        router_bias=_synth(E, s, S_RBIAS, 1.0) if wl.router_bias else None,
+        gate=_synth(E * I * H, s, S_GATE, W_STD).reshape(E, I, H),
+        up=_synth(E * I * H, s, S_UP, W_STD).reshape(E, I, H),
+        down=_synth(E * H * I, s, S_DOWN, W_STD).reshape(E, H, I),
+    )
+    if Is:
+        hi.shared_gate = _synth(Is * H, s, S_SH_GATE, W_STD).reshape(Is, H)
+        hi.shared_up = _synth(Is * H, s, S_SH_UP, W_STD).reshape(Is, H)
+        hi.shared_down = _synth(H * Is, s, S_SH_DOWN, W_STD).reshape(H, Is)
+        hi.shared_expert_gate_w = _synth(H, s, S_SH_EGATE, W_STD).reshape(1, H)
+    hi.meta = dict(workload=wl.key, model=m["name"], tokens=T, seed=s)
+    return hi
+
+
+# ------------------------------------------------------------------ device side
+
+def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None, device="cuda"):
+    """Uploads the inputs, quantizes the weights on the GPU (fmx_quantize) and
+    returns (MoEBlock, x_device, quantized weights dict)."""
+    import torch
+
+    from .moe import MoEBlock, MoEConfig, MoEWeights, QWeight, quantize
+
+    m = wl.model
+
+    def up(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(device).view(torch.bfloat16)
+
+    def q(a):
+        t = up(a)
+        wq, s, b = quantize(t)
+        del t
+        return QWeight(wq, s, b)
+
+    cfg = MoEConfig(hidden_size=m["hidden"], num_experts=m["n_experts"],
+                    num_experts_per_tok=m["top_k"], moe_intermediate_size=m["inter"],
+                    shared_expert_intermediate_size=m["shared_inter"],
+                    norm_topk_prob=m["norm_topk"])
+    w = MoEWeights(router_w=up(hi.router_w), gate=q(hi.gate), up=q(hi.up), down=q(hi.down))
+    if hi.router_bias is not None:
+        w.router_logit_bias = up(hi.router_bias)
+    if m["shared_inter"]:
+        w.shared_gate, w.shared_up, w.shared_down = q(hi.shared_gate), q(hi.shared_up), q(hi.shared_down)
+        w.shared_expert_gate_w = up(hi.shared_expert_gate_w)
+    block = MoEBlock(cfg, w, max_tokens=max_tokens or hi.x.shape[0])
+    return block, up(hi.x)
+
+
+def algorithmic_bytes(m: dict, tokens: int, unique_experts: int, router_bias: bool = False) -> int:
+    """HBM bytes one MoE-layer call must move at minimum: the packed weights
+    of every routed (unique) expert, the shared expert, the bf16 router and
+    shared-gate rows, and the bf16 activations in and out."""
+    H, E, I, Is = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"]
+    per_w = lambda n, k: n * k // 2 + 2 * 2 * n * (k // 64)  # noqa: E731
+    expert = 2 * per_w(I, H) + per_w(H, I)
+    shared = (2 * per_w(Is, H) + per_w(H, Is)) if Is else 0
+    router = E * H * 2 + (E * 2 if router_bias else 0)
+    sgate = H * 2 if Is else 0
+    act = 2 * tokens * H * 2
+    return unique_experts * expert + shared + router + sgate + act
+
+
+def flops(m: dict, tokens: int) -> int:
+    """Useful FLOPs of one call: routed experts (k per token), shared expert,
+    router and shared-gate dot products."""
+    H, E, I, Is, k = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"], m["top_k"]
+    f = 2 * tokens * k * 3 * H * I + 2 * tokens * H * E
+    if Is:
+        f += 2 * tokens * 3 * H * Is + 2 * tokens * H
+    return f

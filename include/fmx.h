@@ -1,0 +1,241 @@
+/*
+ * fmx.h -- C-ABI of the MI355X-native MoE hot path (libfmx.so).
+ *
+ * The reference (FlashMLX) runs its MoE block through MLX C++ ops on Apple
+ * GPUs. This library replaces the ops on that path with HIP kernels for
+ * gfx950 behind a plain C interface: device pointers and sizes in, status
+ * codes out, no C++ or torch types in any signature.
+ *
+ * Conventions
+ *   - Every pointer named `data`, `x`, `y`, weights, indices, outputs and
+ *     `workspace` is DEVICE memory on the current HIP device. Arrays are
+ *     row-major and contiguous.
+ *   - Calls are asynchronous on `stream` (a hipStream_t; NULL = null
+ *     stream). The caller synchronises.
+ *   - Ownership: the library never frees caller memory and keeps no pointer
+ *     past a call. Scratch memory comes from the caller's `workspace`; when
+ *     `workspace` is NULL the call allocates it stream-ordered
+ *     (hipMallocAsync) and frees it before returning.
+ *   - Errors: every entry point returns an fmx_status. MLX raises C++
+ *     exceptions (std::invalid_argument) for the same conditions; none
+ *     crosses this boundary. fmx_last_error() gives the thread's last message.
+ *   - Concurrency: calls are re-entrant for distinct (stream, workspace)
+ *     pairs. Two calls sharing one workspace must be ordered on one stream.
+ *   - Scope: affine mode, bits = 4, group_size = 64, transpose = true, bf16
+ *     activations and bf16 scales/biases. Any other valid MLX argument returns
+ *     FMX_ERR_UNSUPPORTED and computes nothing.
+ *
+ * Packed weight layout (MLX's, unchanged): for a logical [N, K] matrix
+ *   w       uint32 [..., N, K/8]   element k of a row is nibble k%8 (bits
+ *                                   4*(k%8)..+3) of word k/8
+ *   scales  bf16   [..., N, K/64]
+ *   biases  bf16   [..., N, K/64]  dequantised value = scale * q + bias
+ */
+#ifndef FMX_H
+#define FMX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMX_ABI_VERSION 1
+
+typedef enum fmx_status {
+  FMX_OK = 0,
+  FMX_ERR_ARG = 1,         /* null pointer or bad enum value                 */
+  FMX_ERR_SHAPE = 2,       /* shapes/sizes inconsistent                      */
+  FMX_ERR_DTYPE = 3,       /* dtype not the one the argument requires       */
+  FMX_ERR_UNSUPPORTED = 4, /* valid MLX call outside this library's scope    */
+  FMX_ERR_WORKSPACE = 5,   /* workspace smaller than the size query returned */
+  FMX_ERR_HIP = 6          /* HIP runtime error (launch, allocation)         */
+} fmx_status;
+
+typedef enum fmx_dtype { FMX_BF16 = 0, FMX_F32 = 1, FMX_U32 = 2, FMX_I32 = 3 } fmx_dtype;
+
+#define FMX_MAX_NDIM 8
+
+/* Non-owning view of a contiguous device array. */
+typedef struct fmx_array {
+  void* data;
+  int32_t dtype; /* fmx_dtype */
+  int32_t ndim;
+  int64_t shape[FMX_MAX_NDIM];
+} fmx_array;
+
+typedef void* fmx_stream; /* hipStream_t */
+
+int fmx_abi_version(void);
+const char* fmx_status_string(int status);
+const char* fmx_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * quantized_matmul
+ * Replaces mx::quantized_matmul(x, w, scales, biases, transpose, group_size,
+ * bits) as called by LlamaModel::linear_fast (server/src/model.cpp:476-480)
+ * and LlamaModel::shared_expert_mlp (server/src/model.cpp:741-747).
+ *   x [..., M, K] bf16, w [N, K/8] u32, scales/biases [N, K/64] bf16
+ *   out [..., M, N] bf16 (caller-allocated; shape from the _out_shape query)
+ * `mode` must be "affine" (or NULL, which means "affine").
+ * --------------------------------------------------------------------- */
+int fmx_quantized_matmul_out_shape(const fmx_array* x, const fmx_array* w, int transpose,
+                                   int group_size, int bits, fmx_array* out);
+size_t fmx_quantized_matmul_workspace_size(const fmx_array* x, const fmx_array* w);
+int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
+                         const fmx_array* biases, int transpose, int group_size, int bits,
+                         const char* mode, fmx_array* out, void* workspace,
+                         size_t workspace_bytes, fmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * gather_qmm
+ * Replaces mx::gather_qmm(x, w, scales, biases, lhs_indices, rhs_indices,
+ * transpose, group_size, bits, mode, sorted_indices) as called by
+ * LlamaModel::switch_mlp (server/src/model.cpp:703-721).
+ *   x [..., M, K] bf16; w [E..., N, K/8] u32; scales/biases [E..., N, K/64]
+ *   lhs_indices / rhs_indices: u32 or i32 arrays, or NULL for MLX's defaults
+ *     (arange over the flattened batch dims of x / of w)
+ *   out: broadcast(lhs.shape, rhs.shape) + [M, N], bf16
+ * Out-of-range index values (undefined behaviour in MLX) are clamped to the
+ * last valid row / expert on the device, so they never address memory
+ * outside the arrays.
+ * `sorted_indices` is a hint only: results never depend on it.
+ * --------------------------------------------------------------------- */
+int fmx_gather_qmm_out_shape(const fmx_array* x, const fmx_array* w,
+                             const fmx_array* lhs_indices, const fmx_array* rhs_indices,
+                             int transpose, int group_size, int bits, fmx_array* out);
+size_t fmx_gather_qmm_workspace_size(const fmx_array* x, const fmx_array* w,
+                                     const fmx_array* lhs_indices,
+                                     const fmx_array* rhs_indices);
+int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
+                   const fmx_array* biases, const fmx_array* lhs_indices,
+                   const fmx_array* rhs_indices, int transpose, int group_size, int bits,
+                   const char* mode, int sorted_indices, fmx_array* out, void* workspace,
+                   size_t workspace_bytes, fmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * quantize / dequantize
+ * Replace mx::quantize / mx::dequantize (affine, bits 4, group 64): the
+ * format the reference's checkpoints are stored in and that
+ * LlamaModel::build_moe_weight_cache stacks (server/src/model.cpp:368-470).
+ *   w [..., N, K] bf16 -> wq [..., N, K/8] u32, scales/biases [..., N, K/64] bf16
+ * --------------------------------------------------------------------- */
+int fmx_quantize(const fmx_array* w, int group_size, int bits, const char* mode,
+                 fmx_array* wq, fmx_array* scales, fmx_array* biases, fmx_stream stream);
+int fmx_dequantize(const fmx_array* wq, const fmx_array* scales, const fmx_array* biases,
+                   int group_size, int bits, const char* mode, fmx_array* out,
+                   fmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Expert stacking: mx::stack of per-expert arrays into [E, ...]
+ * (server/src/model.cpp:396-404). Copies n_experts device buffers of `bytes`
+ * each into dst (device), expert e at dst + e*bytes.
+ * --------------------------------------------------------------------- */
+int fmx_stack_experts(const void* const* src_per_expert, int64_t n_experts, size_t bytes,
+                      void* dst, fmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * MoE block
+ * Replaces LlamaModel::moe_block (server/src/model.cpp:750-807) together with
+ * switch_mlp (:673-734) and shared_expert_mlp (:736-748):
+ *   gates  = softmax(x . router_w^T [+ logit_bias], precise)
+ *   inds   = top-k of gates (ties: lower expert index; slots ordered by
+ *            probability descending, then index ascending)
+ *   scores = gates[inds]   (divided by their sum when norm_topk_prob)
+ *   y      = sum_k scores_k * down_e(swiglu(gate_e(x), up_e(x)))
+ *          + sigmoid(x . shared_expert_gate_w^T) * shared_expert(x)
+ * --------------------------------------------------------------------- */
+
+/* ModelConfig's MoE fields (server/include/flashmlx/model.h:20-54). */
+typedef struct fmx_moe_config {
+  int64_t hidden_size;                     /* H                          */
+  int64_t num_experts;                     /* E  (<= 1024)               */
+  int32_t num_experts_per_tok;             /* k  (<= 16, <= E)           */
+  int32_t norm_topk_prob;                  /* 0 / 1                      */
+  int64_t moe_intermediate_size;           /* I                          */
+  int64_t shared_expert_intermediate_size; /* Is; 0 = no shared expert   */
+  int32_t quant_bits;                      /* 4                          */
+  int32_t quant_group_size;                /* 64                         */
+} fmx_moe_config;
+
+typedef struct fmx_qweight {
+  const void* w;      /* u32  [.., N, K/8]  */
+  const void* scales; /* bf16 [.., N, K/64] */
+  const void* biases; /* bf16 [.., N, K/64] */
+} fmx_qweight;
+
+/* MoEWeights (server/include/flashmlx/model.h:58-72), stacked layout. */
+typedef struct fmx_moe_weights {
+  const void* router_w;          /* bf16 [E, H] (unquantised router, model.cpp:762) */
+  const void* router_logit_bias; /* bf16 [E] added to the logits before softmax, or
+                                    NULL. No counterpart in the reference: lets a
+                                    caller skew expert loads (benchmarks).        */
+  fmx_qweight gate;              /* [E, I, H/8] ...                                */
+  fmx_qweight up;                /* [E, I, H/8] ...                                */
+  fmx_qweight down;              /* [E, H, I/8] ...                                */
+  fmx_qweight shared_gate;       /* [Is, H/8] ... (ignored when Is == 0)           */
+  fmx_qweight shared_up;         /* [Is, H/8] ...                                  */
+  fmx_qweight shared_down;       /* [H, Is/8] ...                                  */
+  const void* shared_expert_gate_w; /* bf16 [1, H]                                 */
+} fmx_moe_weights;
+
+/* Bytes of workspace one forward of up to max_tokens tokens needs
+ * (max_tokens <= 65536). */
+size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens);
+
+/* Prepares a fresh workspace: clears the completion counters kept in its
+ * first bytes. Call once after allocating; every forward leaves them
+ * cleared again, so a workspace is reusable across calls and sizes. */
+int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream);
+
+/* y [T, H] bf16 = moe_block(x [T, H] bf16), T = B*L tokens. The workspace
+ * must hold fmx_moe_workspace_size(cfg, T) bytes and have been initialised
+ * once with fmx_moe_workspace_init. */
+int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                          const void* x, int64_t n_tokens, void* y, void* workspace,
+                          size_t workspace_bytes, fmx_stream stream);
+
+/* Device views of the routing state a forward of n_tokens tokens left in
+ * the workspace (valid until the next call on that workspace). Any out
+ * pointer may be NULL.
+ *   inds [T,k] u32, scores [T,k] bf16, probs [T,E] bf16,
+ *   order/inv/src/idx [T*k] u32 (switch_mlp's sort, model.cpp:682-700),
+ *   expert_offsets [E+1] u32 (rows of expert e are [off[e], off[e+1]) ). */
+int fmx_moe_workspace_routing(const fmx_moe_config* cfg, int64_t n_tokens,
+                              const void* workspace, const uint32_t** inds,
+                              const void** scores, const void** probs,
+                              const uint32_t** order, const uint32_t** inv,
+                              const uint32_t** src, const uint32_t** idx,
+                              const uint32_t** expert_offsets);
+
+/* Router alone (model.cpp:757-775 + renorm): inds [T,k] u32, scores [T,k]
+ * bf16, probs [T,E] bf16 (may be NULL). */
+int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t n_tokens,
+                        const void* router_w, const void* router_logit_bias,
+                        uint32_t* inds, void* scores, void* probs, void* workspace,
+                        size_t workspace_bytes, fmx_stream stream);
+
+/* Sort / permutation alone (model.cpp:682-700): order = stable argsort of the
+ * flattened inds, inv = argsort(order), src = order / k, idx = flat[order],
+ * expert_offsets [E+1]. Any output may be NULL. Index values >= E are
+ * treated as E-1. Workspace: fmx_moe_sort_workspace_size bytes (or NULL). */
+size_t fmx_moe_sort_workspace_size(int64_t n_tokens, int32_t k, int64_t num_experts);
+int fmx_moe_sort(const uint32_t* inds, int64_t n_tokens, int32_t k, int64_t num_experts,
+                 uint32_t* order, uint32_t* inv, uint32_t* src, uint32_t* idx,
+                 uint32_t* expert_offsets, void* workspace, size_t workspace_bytes,
+                 fmx_stream stream);
+
+/* ------------------------------------------------------------------------
+ * Synthetic inputs (host memory; no counterpart in the reference, which
+ * loads checkpoints). Counter-based: element i of (seed, stream) is a pure
+ * function of (seed, stream, i), so any slice can be regenerated alone.
+ *   out[i] = bf16(mean + std * N(0,1)), Box-Muller on splitmix64 counters.
+ * --------------------------------------------------------------------- */
+int fmx_synth_normal_bf16(uint16_t* host_out, int64_t n, uint64_t seed, uint64_t stream,
+                          double mean, double std_dev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMX_H */

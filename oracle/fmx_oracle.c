@@ -1,0 +1,495 @@
+/*
+ * fmx_oracle.c -- CPU restatement of FlashMLX's MoE hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP library, and the CPU
+ * baseline that bench.py times beside it. Nothing in the product links it.
+ * Build: oracle/Makefile (gcc, -ffp-contract=off so that every a*b+c below is
+ * two roundings exactly as written, never a contracted fma).
+ *
+ * Every function cites the reference line it restates; see fmx_oracle.h for
+ * which MLX op each one stands for and how it is pinned by the tests.
+ */
+#include "fmx_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* numerics                                                                  */
+/* ------------------------------------------------------------------------ */
+
+float orc_bf16_to_f32(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u); /* quiet NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* One rounding from fp64 to bf16 (nearest even). Implemented as round-to-odd
+ * into fp32 followed by nearest-even into bf16: with 16 spare bits the odd
+ * sticky bit makes the second rounding equal to a single direct rounding. */
+uint16_t orc_f64_to_bf16(double d) {
+  if (d != d) return 0x7fc0u;
+  float f = (float)d;
+  if ((double)f != d && !isinf(f)) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if (fabs((double)f) > fabs(d)) u -= 1u; /* rounded away from zero: step back */
+    u |= 1u;                                /* sticky */
+    memcpy(&f, &u, 4);
+  }
+  return orc_f32_to_bf16(f);
+}
+
+/* exp for the router softmax, deterministic across machines: Cody-Waite
+ * reduction by ln2 (fdlibm's split constants) and the degree-13 Taylor
+ * polynomial of e^t on |t| <= ln2/2 evaluated by Horner with explicit fma.
+ * Only IEEE basic operations are used, so any conforming machine computes
+ * the same bits. Results below 2^-1000 are returned as 0 (they round to 0
+ * in bf16 after normalisation anyway). */
+double orc_exp(double r) {
+  if (r != r) return r;
+  if (r > 709.0) return INFINITY;
+  if (r < -690.0) return 0.0;
+  const double log2e = 1.4426950408889634074;
+  const double ln2_hi = 6.93147180369123816490e-01;
+  const double ln2_lo = 1.90821492927058770002e-10;
+  double n = rint(r * log2e);
+  double t = fma(-n, ln2_hi, r);
+  t = fma(-n, ln2_lo, t);
+  double p = 1.0 / 6227020800.0;         /* 1/13! */
+  p = fma(p, t, 1.0 / 479001600.0);      /* 1/12! */
+  p = fma(p, t, 1.0 / 39916800.0);       /* 1/11! */
+  p = fma(p, t, 1.0 / 3628800.0);        /* 1/10! */
+  p = fma(p, t, 1.0 / 362880.0);         /* 1/9!  */
+  p = fma(p, t, 1.0 / 40320.0);          /* 1/8!  */
+  p = fma(p, t, 1.0 / 5040.0);           /* 1/7!  */
+  p = fma(p, t, 1.0 / 720.0);            /* 1/6!  */
+  p = fma(p, t, 1.0 / 120.0);            /* 1/5!  */
+  p = fma(p, t, 1.0 / 24.0);             /* 1/4!  */
+  p = fma(p, t, 1.0 / 6.0);              /* 1/3!  */
+  p = fma(p, t, 0.5);                    /* 1/2!  */
+  p = fma(p, t, 1.0);
+  p = fma(p, t, 1.0);
+  return ldexp(p, (int)n);
+}
+
+/* bf16(sigmoid(g)): MLX's sigmoid on a bf16 array returns bf16
+ * (model.cpp:17, :802). Computed in fp64 and rounded once. */
+float orc_sigmoid_bf16(uint16_t g) {
+  double v = (double)orc_bf16_to_f32(g);
+  return orc_bf16_to_f32(orc_f64_to_bf16(1.0 / (1.0 + exp(-v))));
+}
+
+static inline float bf(uint16_t h) { return orc_bf16_to_f32(h); }
+static inline uint16_t rb(float f) { return orc_f32_to_bf16(f); }
+
+static int g_threads = 0;
+void orc_set_threads(int n) {
+  g_threads = n;
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#endif
+}
+int orc_get_threads(void) {
+#ifdef _OPENMP
+  return g_threads > 0 ? g_threads : omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* affine quantization                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Restates MLX's CPU affine quantizer (mx::quantize, mode "affine") as
+ * recalled: per group, scale = max((max-min)/15, 1e-7), signed toward the
+ * larger-magnitude edge; q0 = rint(edge/scale); if q0 != 0 the scale is
+ * snapped to edge/q0 and the bias is the edge (so the edge is a level);
+ * q = clamp(rint((w - bias)/scale), 0, 15); scale and bias stored as bf16.
+ * The reference consumes checkpoints quantized this way
+ * (docs/superpowers/specs/2026-04-01-moe-support-design.md:138-151). */
+int orc_quantize(const uint16_t* w, int64_t N, int64_t K, int group_size, int bits,
+                 uint32_t* wq, uint16_t* scales, uint16_t* biases) {
+  if (bits != 4 || group_size != 64 || K % group_size != 0) return -1;
+  const float n_bins = 15.0f;
+  const float eps = 1e-7f;
+  const int64_t groups = N * (K / group_size);
+#pragma omp parallel for schedule(static)
+  for (int64_t gi = 0; gi < groups; ++gi) {
+    const uint16_t* src = w + gi * group_size;
+    float w_min = INFINITY, w_max = -INFINITY;
+    for (int j = 0; j < group_size; ++j) {
+      float v = bf(src[j]);
+      w_max = fmaxf(w_max, v);
+      w_min = fminf(w_min, v);
+    }
+    int mask = fabsf(w_min) > fabsf(w_max);
+    float scale = fmaxf((w_max - w_min) / n_bins, eps);
+    scale = mask ? scale : -scale;
+    float edge = mask ? w_min : w_max;
+    float q0 = rintf(edge / scale);
+    float bias = 0.0f;
+    if (q0 != 0.0f) {
+      scale = edge / q0;
+      bias = edge;
+    }
+    uint32_t* dst = wq + gi * (group_size / 8);
+    for (int p = 0; p < group_size / 8; ++p) {
+      uint32_t word = 0;
+      for (int j = 0; j < 8; ++j) {
+        float v = bf(src[p * 8 + j]);
+        float q = rintf((v - bias) / scale);
+        q = fminf(fmaxf(q, 0.0f), n_bins);
+        word |= (uint32_t)q << (4 * j);
+      }
+      dst[p] = word;
+    }
+    scales[gi] = rb(scale);
+    biases[gi] = rb(bias);
+  }
+  return 0;
+}
+
+int orc_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                   int64_t N, int64_t K, int group_size, int bits, float* out) {
+  if (bits != 4 || group_size != 64 || K % group_size != 0) return -1;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k) {
+      uint32_t word = wq[n * (K / 8) + k / 8];
+      float q = (float)((word >> (4 * (k % 8))) & 15u);
+      int64_t g = n * (K / group_size) + k / group_size;
+      out[n * K + k] = bf(scales[g]) * q + bf(biases[g]);
+    }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* quantized products                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* One output element: x[K] (bf16) . deq(w row)[K], returned as bf16.
+ * This is the inner loop of MLX's CPU quantized matmul with transpose=true
+ * (the `_qmm_t` family), in one of four accumulation modes. */
+static uint16_t qdot_row(const uint16_t* x, const uint32_t* wrow, const uint16_t* srow,
+                         const uint16_t* brow, int64_t K, int mode) {
+  const int64_t G = K / 64;
+  if (mode == ORC_ACC_F64) {
+    double acc = 0.0;
+    for (int64_t g = 0; g < G; ++g) {
+      double s = bf(srow[g]), b = bf(brow[g]);
+      for (int p = 0; p < 8; ++p) {
+        uint32_t word = wrow[g * 8 + p];
+        for (int j = 0; j < 8; ++j) {
+          double q = (double)((word >> (4 * j)) & 15u);
+          acc += (double)bf(x[g * 64 + p * 8 + j]) * (s * q + b);
+        }
+      }
+    }
+    return orc_f64_to_bf16(acc);
+  }
+  if (mode == ORC_ACC_A) {
+    float acc = 0.0f;
+    for (int64_t g = 0; g < G; ++g) {
+      float s = bf(srow[g]), b = bf(brow[g]);
+      for (int p = 0; p < 8; ++p) {
+        uint32_t word = wrow[g * 8 + p];
+        for (int j = 0; j < 8; ++j) {
+          float q = (float)((word >> (4 * j)) & 15u);
+          float wv = s * q + b;
+          acc += bf(x[g * 64 + p * 8 + j]) * wv;
+        }
+      }
+    }
+    return rb(acc);
+  }
+  if (mode == ORC_ACC_B) {
+    uint16_t sum = 0;
+    for (int64_t g = 0; g < G; ++g) {
+      uint16_t s = srow[g], b = brow[g];
+      for (int p = 0; p < 8; ++p) {
+        uint32_t word = wrow[g * 8 + p];
+        for (int j = 0; j < 8; ++j) {
+          uint16_t q = rb((float)((word >> (4 * j)) & 15u));
+          uint16_t sq = rb(bf(s) * bf(q));
+          uint16_t wv = rb(bf(sq) + bf(b));
+          uint16_t pr = rb(bf(x[g * 64 + p * 8 + j]) * bf(wv));
+          sum = rb(bf(sum) + bf(pr));
+        }
+      }
+    }
+    return sum;
+  }
+  /* ORC_ACC_C: 8 fp32 lanes over k mod 8, then a pairwise lane sum */
+  float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t g = 0; g < G; ++g) {
+    float s = bf(srow[g]), b = bf(brow[g]);
+    for (int p = 0; p < 8; ++p) {
+      uint32_t word = wrow[g * 8 + p];
+      for (int j = 0; j < 8; ++j) {
+        float q = (float)((word >> (4 * j)) & 15u);
+        float wv = q * s;
+        wv = wv + b;
+        lane[j] = lane[j] + bf(x[g * 64 + p * 8 + j]) * wv;
+      }
+    }
+  }
+  float a0 = lane[0] + lane[4], a1 = lane[1] + lane[5], a2 = lane[2] + lane[6], a3 = lane[3] + lane[7];
+  float b0 = a0 + a2, b1 = a1 + a3;
+  return rb(b0 + b1);
+}
+
+/* quantized_matmul(x, w, scales, biases, transpose=true, 64, 4):
+ * model.cpp:476-480 (linear_fast), :741-747 (shared expert). */
+int orc_qmm_t(const uint16_t* x, int64_t M, int64_t K,
+              const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+              int64_t N, int mode, uint16_t* out) {
+  if (K % 64 != 0 || mode < 0 || mode > 3) return -1;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n)
+      out[m * N + n] = qdot_row(x + m * K, w + n * (K / 8), scales + n * (K / 64),
+                                biases + n * (K / 64), K, mode);
+  return 0;
+}
+
+/* gather_qmm(x, w, scales, biases, lhs, rhs, transpose=true, 64, 4, "affine"):
+ * model.cpp:703-721. Index lists are already broadcast to a common length. */
+int orc_gather_qmm(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
+                   const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                   int64_t E, int64_t N,
+                   const uint32_t* lhs, const uint32_t* rhs, int64_t nb,
+                   int mode, uint16_t* out) {
+  if (K % 64 != 0 || mode < 0 || mode > 3) return -1;
+  for (int64_t b = 0; b < nb; ++b)
+    if ((int64_t)lhs[b] >= n_x || (int64_t)rhs[b] >= E) return -2;
+  const int64_t wstride = N * (K / 8), sstride = N * (K / 64);
+#pragma omp parallel for schedule(static) collapse(3)
+  for (int64_t b = 0; b < nb; ++b)
+    for (int64_t m = 0; m < M; ++m)
+      for (int64_t n = 0; n < N; ++n) {
+        const uint32_t e = rhs[b];
+        out[(b * M + m) * N + n] =
+            qdot_row(x + ((int64_t)lhs[b] * M + m) * K, w + e * wstride + n * (K / 8),
+                     scales + e * sstride + n * (K / 64), biases + e * sstride + n * (K / 64),
+                     K, mode);
+      }
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* router                                                                    */
+/* ------------------------------------------------------------------------ */
+
+/* x . w^T of bf16 vectors: the products of two bf16 values are exact in
+ * fp64 and so, except in cases far below any bf16 rounding boundary, are
+ * all partial sums; the result is therefore independent of summation order
+ * and is rounded once to bf16 (MLX: bf16 matmul with fp32 accumulate,
+ * model.cpp:762). */
+static uint16_t bf16_dot_exact(const uint16_t* a, const uint16_t* b, int64_t n) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) acc += (double)bf(a[i]) * (double)bf(b[i]);
+  return orc_f64_to_bf16(acc);
+}
+
+/* model.cpp:757-775: gates = x.Wr^T; softmax(precise=true); top-k by
+ * argpartition(-gates, k-1)[..., :k]; scores = take_along_axis.
+ * The selected set is the k largest bf16 probabilities with ties going to
+ * the lower expert index; slots are ordered (prob desc, index asc).
+ * norm_topk: s / sum(s) (moe-support-plan.md:319-322; nemotron_h.cpp:1045). */
+int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
+                    const uint16_t* wr, int64_t E, const uint16_t* logit_bias,
+                    int k, int norm_topk,
+                    uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores) {
+  if (k <= 0 || k > E || E > 65535) return -1;
+  int rc = 0;
+#pragma omp parallel
+  {
+    uint16_t* lg = (uint16_t*)malloc(sizeof(uint16_t) * E);
+    uint16_t* pb = (uint16_t*)malloc(sizeof(uint16_t) * E);
+    double* ex = (double*)malloc(sizeof(double) * E);
+    unsigned char* taken = (unsigned char*)malloc(E);
+    if (!lg || !pb || !ex || !taken) {
+#pragma omp atomic write
+      rc = -3;
+    } else {
+#pragma omp for schedule(static)
+      for (int64_t t = 0; t < T; ++t) {
+        for (int64_t e = 0; e < E; ++e) {
+          uint16_t l = bf16_dot_exact(x + t * H, wr + e * H, H);
+          if (logit_bias) l = orc_f64_to_bf16((double)bf(l) + (double)bf(logit_bias[e]));
+          lg[e] = l;
+        }
+        double m = -INFINITY;
+        for (int64_t e = 0; e < E; ++e) m = fmax(m, (double)bf(lg[e]));
+        double sum = 0.0;
+        for (int64_t e = 0; e < E; ++e) {
+          ex[e] = orc_exp((double)bf(lg[e]) - m);
+          sum += ex[e];
+        }
+        for (int64_t e = 0; e < E; ++e) pb[e] = orc_f64_to_bf16(ex[e] / sum);
+        memset(taken, 0, E);
+        for (int j = 0; j < k; ++j) {
+          int64_t best = -1;
+          for (int64_t e = 0; e < E; ++e) {
+            if (taken[e]) continue;
+            if (best < 0 || bf(pb[e]) > bf(pb[best])) best = e; /* strict: ties keep lower index */
+          }
+          taken[best] = 1;
+          inds[t * k + j] = (uint32_t)best;
+          scores[t * k + j] = pb[best];
+        }
+        if (norm_topk) {
+          float s = 0.0f;
+          for (int j = 0; j < k; ++j) s += bf(scores[t * k + j]);
+          uint16_t sb = rb(s);
+          for (int j = 0; j < k; ++j) {
+            float q = (float)((double)bf(scores[t * k + j]) / (double)bf(sb));
+            scores[t * k + j] = rb(q);
+          }
+        }
+        if (logits) memcpy(logits + t * E, lg, sizeof(uint16_t) * E);
+        if (probs) memcpy(probs + t * E, pb, sizeof(uint16_t) * E);
+      }
+    }
+    free(lg);
+    free(pb);
+    free(ex);
+    free(taken);
+  }
+  return rc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* sort / permutation                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* model.cpp:682-700: stable counting sort by expert, which equals MLX's
+ * stable argsort of the flattened indices. */
+int orc_moe_sort(const uint32_t* inds, int64_t T, int k, int64_t E,
+                 uint32_t* order, uint32_t* inv, uint32_t* src, uint32_t* idx,
+                 uint32_t* offsets) {
+  const int64_t n = T * (int64_t)k;
+  uint32_t* cursor = (uint32_t*)calloc((size_t)E + 1, sizeof(uint32_t));
+  if (!cursor) return -3;
+  for (int64_t i = 0; i < n; ++i) {
+    if ((int64_t)inds[i] >= E) {
+      free(cursor);
+      return -2;
+    }
+    cursor[inds[i] + 1]++;
+  }
+  for (int64_t e = 0; e < E; ++e) cursor[e + 1] += cursor[e];
+  if (offsets) memcpy(offsets, cursor, sizeof(uint32_t) * (E + 1));
+  for (int64_t i = 0; i < n; ++i) {
+    uint32_t e = inds[i];
+    uint32_t pos = cursor[e]++;
+    if (order) order[pos] = (uint32_t)i;
+    if (inv) inv[i] = pos;
+    if (src) src[pos] = (uint32_t)(i / k);
+    if (idx) idx[pos] = e;
+  }
+  free(cursor);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* full block                                                                */
+/* ------------------------------------------------------------------------ */
+
+/* compiled SwiGLU (model.cpp:14-25): multiply(multiply(g, sigmoid(g)), u),
+ * each op producing bf16. */
+static uint16_t swiglu_bf16(uint16_t g, uint16_t u) {
+  float sg = orc_sigmoid_bf16(g);
+  uint16_t t = rb(bf(g) * sg);
+  return rb(bf(t) * bf(u));
+}
+
+/* dense out[n] = x . deq(W[n]) for n < N, bf16 */
+static void qmv(const uint16_t* x, int64_t K, const uint32_t* w, const uint16_t* s,
+                const uint16_t* b, int64_t N, int mode, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n)
+    out[n] = qdot_row(x, w + n * (K / 8), s + n * (K / 64), b + n * (K / 64), K, mode);
+}
+
+int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                  const uint16_t* x, int64_t T, int mode,
+                  const int64_t* token_subset, int64_t n_subset,
+                  uint16_t* y, uint32_t* inds_out, uint16_t* scores_out) {
+  const int64_t H = cfg->hidden, E = cfg->n_experts, I = cfg->inter, Is = cfg->shared_inter;
+  const int k = cfg->top_k;
+  if (cfg->group_size != 64 || cfg->bits != 4 || H % 64 || I % 64 || (Is && Is % 64)) return -1;
+  uint32_t* inds = (uint32_t*)malloc(sizeof(uint32_t) * T * k);
+  uint16_t* scores = (uint16_t*)malloc(sizeof(uint16_t) * T * k);
+  int64_t Imax = I > Is ? I : Is;
+  uint16_t* g = (uint16_t*)malloc(sizeof(uint16_t) * Imax);
+  uint16_t* u = (uint16_t*)malloc(sizeof(uint16_t) * Imax);
+  uint16_t* a = (uint16_t*)malloc(sizeof(uint16_t) * Imax);
+  uint16_t* d = (uint16_t*)malloc(sizeof(uint16_t) * H);
+  float* acc = (float*)malloc(sizeof(float) * H);
+  if (!inds || !scores || !g || !u || !a || !d || !acc) return -3;
+
+  int rc = orc_router_topk(x, T, H, w->router_w, E, w->router_bias, k, cfg->norm_topk,
+                           NULL, NULL, inds, scores);
+  if (rc) return rc;
+
+  const int64_t n_tok = token_subset ? n_subset : T;
+  const int64_t wst_gu = I * (H / 8), sst_gu = I * (H / 64);
+  const int64_t wst_d = H * (I / 8), sst_d = H * (I / 64);
+  for (int64_t ti = 0; ti < n_tok; ++ti) {
+    const int64_t t = token_subset ? token_subset[ti] : ti;
+    const uint16_t* xt = x + t * H;
+    for (int64_t h = 0; h < H; ++h) acc[h] = 0.0f;
+    /* switch_mlp, one (token, slot) row at a time: gather_qmm gate/up,
+     * SwiGLU, gather_qmm down (model.cpp:703-721) */
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = inds[t * k + j];
+      qmv(xt, H, w->gate_w + e * wst_gu, w->gate_s + e * sst_gu, w->gate_b + e * sst_gu, I, mode, g);
+      qmv(xt, H, w->up_w + e * wst_gu, w->up_s + e * sst_gu, w->up_b + e * sst_gu, I, mode, u);
+      for (int64_t i = 0; i < I; ++i) a[i] = swiglu_bf16(g[i], u[i]);
+      qmv(a, I, w->down_w + e * wst_d, w->down_s + e * sst_d, w->down_b + e * sst_d, H, mode, d);
+      /* y = sum(y * scores[..., None], -2) (model.cpp:782-784): the product
+       * is bf16, the k-sum accumulates in fp32 in slot order */
+      const float sc = bf(scores[t * k + j]);
+      for (int64_t h = 0; h < H; ++h) acc[h] += bf(rb(bf(d[h]) * sc));
+    }
+    for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(acc[h]);
+    if (Is > 0) {
+      /* shared_expert_mlp (model.cpp:736-748) and its sigmoid gate (:787-803) */
+      uint16_t gl = bf16_dot_exact(xt, w->sh_expert_gate_w, H);
+      float gv = orc_sigmoid_bf16(gl);
+      qmv(xt, H, w->sh_gate_w, w->sh_gate_s, w->sh_gate_b, Is, mode, g);
+      qmv(xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, u);
+      for (int64_t i = 0; i < Is; ++i) a[i] = swiglu_bf16(g[i], u[i]);
+      qmv(a, Is, w->sh_down_w, w->sh_down_s, w->sh_down_b, H, mode, d);
+      for (int64_t h = 0; h < H; ++h) {
+        uint16_t sh = rb(gv * bf(d[h]));
+        y[t * H + h] = rb(bf(y[t * H + h]) + bf(sh));
+      }
+    }
+  }
+  if (inds_out) memcpy(inds_out, inds, sizeof(uint32_t) * T * k);
+  if (scores_out) memcpy(scores_out, scores, sizeof(uint16_t) * T * k);
+  free(inds);
+  free(scores);
+  free(g);
+  free(u);
+  free(a);
+  free(d);
+  free(acc);
+  return 0;
+}

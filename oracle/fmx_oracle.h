@@ -1,0 +1,143 @@
+/*
+ * fmx_oracle.h -- CPU restatement of FlashMLX's MoE hot path (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker, never the product. Only tests/, the smoke
+ * entry point and bench.py's CPU-baseline leg may load it. It restates, in
+ * plain C, what the reference's MoE block computes through MLX ops:
+ *
+ *   server/src/model.cpp:750-807  LlamaModel::moe_block
+ *   server/src/model.cpp:673-734  LlamaModel::switch_mlp   (sort / gather_qmm / unsort)
+ *   server/src/model.cpp:736-748  LlamaModel::shared_expert_mlp
+ *   server/src/model.cpp:14-25    compiled SwiGLU  g * sigmoid(g) * u
+ *   server/src/model.cpp:476-480  linear_fast = quantized_matmul(transpose=true)
+ *   server/include/flashmlx/model.h:20-72  ModelConfig / MoEWeights layout
+ *
+ * The arithmetic of those ops lives in MLX (third-party, pinned only as
+ * mlx>=0.22.0 in pyproject.toml:7, not vendored, not installed here).
+ * Each function below names which MLX op it restates and how it is pinned.
+ *
+ * Data conventions (all row-major, little-endian):
+ *   bf16          uint16_t bit pattern
+ *   packed weight w      uint32 [N, K/8]   nibble j of a word = element 8*word+j,
+ *                                           stored at bits 4j..4j+3
+ *                 scales bf16   [N, K/64]
+ *                 biases bf16   [N, K/64]   dequant: s*q + b
+ *   stacked experts: a leading [E] dimension on all three.
+ *
+ * Parity status per function (how each is pinned; see tests/test_oracle_*.py):
+ *   orc_f32_to_bf16 / orc_f64_to_bf16   exact rational rounding (Python Fraction)
+ *   orc_exp                              libm exp within 2 ulp + exact powers
+ *   orc_quantize                         KAT grids, nearest-level property,
+ *                                        nibble order, |deq-w| bound.  The MLX
+ *                                        edge/q0 snap rule itself is recalled
+ *                                        from MLX's CPU quantizer: parity of
+ *                                        that rule against MLX is UNPINNED.
+ *   orc_qmm_t / orc_gather_qmm (mode 0)  fp64 dequant + numpy matmul, one-hot
+ *                                        reduction, brute force on tiny shapes
+ *   orc_qmm_t modes A/B/C                recalled MLX CPU accumulators; which
+ *                                        one MLX uses is UNPINNED (reported only)
+ *   orc_router_topk                      numpy fp64 logits, numpy softmax,
+ *                                        full sort with (p desc, idx asc)
+ *   orc_moe_sort                         numpy stable argsort + invariants
+ *   orc_moe_block                        dense fp64 formula on tiny shapes
+ */
+#ifndef FMX_ORACLE_H
+#define FMX_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* accumulation modes of the quantized products */
+enum {
+  ORC_ACC_F64 = 0,  /* fp64 dequant + fp64 accumulate: the mathematical value */
+  ORC_ACC_A = 1,    /* fp32 dequant (s*q then +b) + sequential fp32 accumulate: parity gate */
+  ORC_ACC_B = 2,    /* every op rounded to bf16 (MLX scalar `T sum` loop, recalled) */
+  ORC_ACC_C = 3     /* 8 fp32 lanes over k mod 8 + lane sum (MLX simd loop, recalled) */
+};
+
+/* ---- numerics ---------------------------------------------------------- */
+float    orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_bf16(float f);   /* round to nearest even */
+uint16_t orc_f64_to_bf16(double d);  /* single round to nearest even from fp64 */
+double   orc_exp(double r);          /* deterministic exp used by the router softmax */
+float    orc_sigmoid_bf16(uint16_t g); /* bf16(sigmoid(g)) as float */
+
+/* ---- affine quantization (mx::quantize, bits=4, group_size=64) -------- */
+int  orc_quantize(const uint16_t* w, int64_t N, int64_t K, int group_size, int bits,
+                  uint32_t* wq, uint16_t* scales, uint16_t* biases);
+int  orc_dequantize(const uint32_t* wq, const uint16_t* scales, const uint16_t* biases,
+                    int64_t N, int64_t K, int group_size, int bits, float* out);
+
+/* ---- quantized matmul, transpose=true --------------------------------- */
+/* out[M,N] = x[M,K] . deq(w)[N,K]^T, output rounded to bf16. */
+int orc_qmm_t(const uint16_t* x, int64_t M, int64_t K,
+              const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+              int64_t N, int mode, uint16_t* out);
+
+/* gather_qmm over already-broadcast index lists of length nb:
+ *   out[b, M, N] = x[lhs[b], M, K] . deq(w[rhs[b]])^T                        */
+int orc_gather_qmm(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
+                   const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                   int64_t E, int64_t N,
+                   const uint32_t* lhs, const uint32_t* rhs, int64_t nb,
+                   int mode, uint16_t* out);
+
+/* ---- router (model.cpp:757-775; renorm per moe-support-plan.md:319-322) -- */
+/* logits/probs [T,E] may be NULL. logit_bias [E] may be NULL (harness-only
+ * extension: a per-expert logit offset added before softmax). */
+int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
+                    const uint16_t* wr, int64_t E, const uint16_t* logit_bias,
+                    int k, int norm_topk,
+                    uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores);
+
+/* ---- sort / permutation (model.cpp:682-700) ---------------------------- */
+/* order = stable argsort(flat inds); inv = argsort(order); src = order / k;
+ * idx = flat[order]; offsets[e] = #entries with expert < e (E+1 entries). */
+int orc_moe_sort(const uint32_t* inds, int64_t T, int k, int64_t E,
+                 uint32_t* order, uint32_t* inv, uint32_t* src, uint32_t* idx,
+                 uint32_t* offsets);
+
+/* ---- full MoE block (model.cpp:750-807) -------------------------------- */
+typedef struct {
+  int64_t hidden;        /* H */
+  int64_t n_experts;     /* E */
+  int     top_k;         /* k */
+  int64_t inter;         /* I  (moe_intermediate_size) */
+  int64_t shared_inter;  /* Is (shared_expert_intermediate_size), 0 = none */
+  int     norm_topk;     /* renormalise the k scores */
+  int     group_size;    /* 64 */
+  int     bits;          /* 4 */
+} orc_moe_cfg;
+
+typedef struct {
+  const uint16_t* router_w;      /* [E, H] bf16 */
+  const uint16_t* router_bias;   /* [E] bf16 or NULL (harness extension) */
+  const uint32_t* gate_w;  const uint16_t* gate_s;  const uint16_t* gate_b;   /* [E, I, ..] */
+  const uint32_t* up_w;    const uint16_t* up_s;    const uint16_t* up_b;     /* [E, I, ..] */
+  const uint32_t* down_w;  const uint16_t* down_s;  const uint16_t* down_b;   /* [E, H, ..] */
+  const uint32_t* sh_gate_w; const uint16_t* sh_gate_s; const uint16_t* sh_gate_b; /* [Is, ..] */
+  const uint32_t* sh_up_w;   const uint16_t* sh_up_s;   const uint16_t* sh_up_b;
+  const uint32_t* sh_down_w; const uint16_t* sh_down_s; const uint16_t* sh_down_b; /* [H, ..] */
+  const uint16_t* sh_expert_gate_w; /* [1, H] bf16 */
+} orc_moe_weights;
+
+/* y [T, H] bf16. inds/scores [T,k] may be NULL. token_subset (may be NULL):
+ * compute y only for these n_subset tokens (routing still uses all tokens;
+ * rows of y for other tokens are left untouched). */
+int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                  const uint16_t* x, int64_t T, int mode,
+                  const int64_t* token_subset, int64_t n_subset,
+                  uint16_t* y, uint32_t* inds, uint16_t* scores);
+
+/* threads used by the OpenMP loops (0 = leave the runtime default) */
+void orc_set_threads(int n);
+int  orc_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

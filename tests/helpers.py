@@ -1,0 +1,66 @@
+"""Test helpers: host<->device bf16 moves, error metrics, oracle argument packs."""
+from __future__ import annotations
+
+import numpy as np
+
+# Parity bar for bf16 outputs, plus a tight relative
+# bound that makes small-magnitude outputs meaningful.
+RTOL = 2e-2
+ATOL = 1e-2
+REL_L2_MAX = 1e-2
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def to_dev(a_u16, device="cuda"):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a_u16).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def to_dev_u32(a, device="cuda"):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(device)
+
+
+def from_dev_bf16(t):
+    return t.contiguous().view(dtype=__import__("torch").int16).cpu().numpy().view(np.uint16)
+
+
+def from_dev_u32(t):
+    return t.contiguous().cpu().numpy().view(np.uint32)
+
+
+def errors(got_u16, ref_u16):
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    r = bf16_to_f32(ref_u16).astype(np.float64)
+    d = np.abs(g - r)
+    max_abs = float(d.max()) if d.size else 0.0
+    mean_rel = float((d / np.maximum(np.abs(r), 1e-6)).mean()) if d.size else 0.0
+    rel_l2 = float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30))
+    return dict(max_abs=max_abs, mean_rel=mean_rel, rel_l2=rel_l2)
+
+
+def assert_close(got_u16, ref_u16, what="", rtol=RTOL, atol=ATOL, rel_l2=REL_L2_MAX):
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    r = bf16_to_f32(ref_u16).astype(np.float64)
+    assert g.shape == r.shape, (what, g.shape, r.shape)
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    bad = np.abs(g - r) > atol + rtol * np.abs(r)
+    e = errors(got_u16, ref_u16)
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements outside rtol/atol; {e}"
+    assert e["rel_l2"] <= rel_l2, f"{what}: relative L2 error {e['rel_l2']:.3g} > {rel_l2}; {e}"
+    return e
+
+
+def oracle_args(hi, model, quant):
+    """(cfg, weights) for oracle.moe_block from HostInputs and a quantizer."""
+    cfg = dict(hidden=model["hidden"], n_experts=model["n_experts"], top_k=model["top_k"],
+               inter=model["inter"], shared_inter=model["shared_inter"], norm_topk=model["norm_topk"])
+    w = dict(router_w=hi.router_w, router_bias=hi.router_bias,
+             gate=quant(hi.gate), up=quant(hi.up), down=quant(hi.down))
+    if model["shared_inter"]:
+        w.update(shared_gate=quant(hi.shared_gate), shared_up=quant(hi.shared_up),
+                 shared_down=quant(hi.shared_down), shared_expert_gate_w=hi.shared_expert_gate_w)
+    return cfg, w

@@ -1,0 +1,180 @@
+"""GPU parity of the single ops behind the C-ABI against the CPU oracle:
+quantize/dequantize (bit-exact), quantized_matmul and gather_qmm (bf16
+tolerance), router top-k and the expert sort (bit-exact)."""
+import numpy as np
+import pytest
+
+from helpers import (assert_close, bf16_to_f32, from_dev_bf16, from_dev_u32, to_dev,
+                     to_dev_u32)
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_bf16(rng, shape, std=1.0):
+    from oracle import oracle as O
+    return O.f32_to_bf16_array(rng.standard_normal(shape).astype(np.float32) * std)
+
+
+@pytest.mark.parametrize("shape", [(4, 128), (3, 5, 256), (1408, 2048)])
+def test_quantize_bitexact(gpu, fmx, oracle, shape):
+    rng = np.random.default_rng(7)
+    w = _rand_bf16(rng, shape, 0.02)
+    if shape == (4, 128):  # edge groups: constant, all-negative, tiny range, zeros
+        w[0, :64] = w[0, 0]
+        w[1, :64] = np.abs(w[1, :64]) | 0x8000
+        w[2, 64:] = 0
+        w[3, :64] = 0x3f80  # 1.0
+    wq, s, b = fmx.quantize(to_dev(w))
+    rq, rs, rb = oracle.quantize(w)
+    np.testing.assert_array_equal(from_dev_u32(wq), rq)
+    np.testing.assert_array_equal(from_dev_bf16(s), rs)
+    np.testing.assert_array_equal(from_dev_bf16(b), rb)
+
+
+def test_dequantize_matches_oracle(gpu, fmx, oracle):
+    rng = np.random.default_rng(8)
+    w = _rand_bf16(rng, (64, 512), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    out = fmx.dequantize(to_dev_u32(rq), to_dev(rs), to_dev(rb))
+    ref = oracle.f32_to_bf16_array(oracle.dequantize(rq, rs, rb))
+    np.testing.assert_array_equal(from_dev_bf16(out), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (3, 200, 1408), (16, 128, 2048),
+                                   (37, 96, 768), (5, 2048, 5632)])
+def test_quantized_matmul(gpu, fmx, oracle, M, N, K):
+    rng = np.random.default_rng(M * 1000 + N + K)
+    x = _rand_bf16(rng, (M, K))
+    w = _rand_bf16(rng, (N, K), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    out = fmx.quantized_matmul(to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb))
+    got = from_dev_bf16(out)
+    ref = oracle.qmm_t(x, rq, rs, rb, oracle.ACC_A)
+    e = assert_close(got, ref, f"qmm M={M} N={N} K={K}")
+    # also against the exact (fp64) value: the GPU dequantises exactly
+    ref64 = oracle.qmm_t(x, rq, rs, rb, oracle.ACC_F64)
+    e64 = assert_close(got, ref64, "qmm vs fp64")
+    assert e64["max_abs"] <= 2 * np.abs(bf16_to_f32(ref64)).max() * 2 ** -8 + 1e-6, e64
+    print(f"qmm M={M} N={N} K={K}: vs A {e}, vs f64 {e64}")
+
+
+def test_quantized_matmul_batch_dims(gpu, fmx, oracle):
+    rng = np.random.default_rng(3)
+    x = _rand_bf16(rng, (2, 3, 1, 256))
+    w = _rand_bf16(rng, (64, 256), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    out = fmx.quantized_matmul(to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb))
+    assert tuple(out.shape) == (2, 3, 1, 64)
+    ref = oracle.qmm_t(x.reshape(-1, 256), rq, rs, rb, oracle.ACC_A).reshape(2, 3, 1, 64)
+    assert_close(from_dev_bf16(out), ref, "qmm batch dims")
+
+
+def _gather_case(rng, oracle, E, N, K, n_x, M):
+    x = _rand_bf16(rng, (n_x, M, K))
+    w = _rand_bf16(rng, (E, N, K), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    return x, rq, rs, rb
+
+
+def test_gather_qmm_unsorted_decode_layout(gpu, fmx, oracle):
+    """switch_mlp's unsorted call: x [B,L,1,1,H], rhs = inds [B,L,k] (model.cpp:681, :703)."""
+    rng = np.random.default_rng(11)
+    B, L, k, E, N, K = 2, 3, 4, 8, 128, 512
+    x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, B * L, 1)
+    inds = np.stack([rng.permutation(E)[:k] for _ in range(B * L)]).astype(np.uint32).reshape(B, L, k)
+    xd = to_dev(x.reshape(B, L, 1, 1, K))
+    out = fmx.gather_qmm(xd, to_dev_u32(rq), to_dev(rs), to_dev(rb), rhs_indices=to_dev_u32(inds))
+    assert tuple(out.shape) == (B, L, k, 1, N)
+    lhs = np.repeat(np.arange(B * L, dtype=np.uint32), k)
+    ref = oracle.gather_qmm(x, rq, rs, rb, lhs, inds.reshape(-1), oracle.ACC_A)
+    assert_close(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather unsorted")
+
+
+def test_gather_qmm_sorted_layout(gpu, fmx, oracle):
+    """switch_mlp's sorted call: x [Tk,1,H] gathered, rhs [Tk] (model.cpp:686-699)."""
+    rng = np.random.default_rng(12)
+    n, E, N, K = 70, 6, 96, 256
+    x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, n, 1)
+    idx = np.sort(rng.integers(0, E, n)).astype(np.uint32)
+    out = fmx.gather_qmm(to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb),
+                         rhs_indices=to_dev_u32(idx), sorted_indices=True)
+    assert tuple(out.shape) == (n, 1, N)
+    ref = oracle.gather_qmm(x, rq, rs, rb, np.arange(n, dtype=np.uint32), idx, oracle.ACC_A)
+    assert_close(from_dev_bf16(out), ref, "gather sorted")
+
+
+def test_gather_qmm_broadcast_and_m_rows(gpu, fmx, oracle):
+    rng = np.random.default_rng(13)
+    E, N, K, n_x, M = 5, 64, 256, 4, 3
+    x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, n_x, M)
+    lhs = np.array([[3], [0]], dtype=np.int32)          # [2,1]
+    rhs = np.array([[4, 1, 1]], dtype=np.uint32)         # [1,3]
+    import torch
+    out = fmx.gather_qmm(to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb),
+                         lhs_indices=torch.from_numpy(lhs).cuda(), rhs_indices=to_dev_u32(rhs))
+    assert tuple(out.shape) == (2, 3, M, N)
+    L = np.broadcast_to(lhs, (2, 3)).reshape(-1).astype(np.uint32)
+    R = np.broadcast_to(rhs, (2, 3)).reshape(-1)
+    ref = oracle.gather_qmm(x, rq, rs, rb, L, R, oracle.ACC_A)
+    assert_close(from_dev_bf16(out).reshape(6, M, N), ref, "gather broadcast")
+
+
+def test_gather_qmm_defaults_one_hot(gpu, fmx, oracle):
+    """No index arrays: out[e] = x[e] . W[e]^T, i.e. E independent quantized_matmuls."""
+    rng = np.random.default_rng(14)
+    E, N, K, M = 3, 48, 128, 2
+    x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, E, M)
+    out = from_dev_bf16(fmx.gather_qmm(to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb)))
+    for e in range(E):
+        assert_close(out[e], oracle.qmm_t(x[e], rq[e], rs[e], rb[e], oracle.ACC_A), f"one-hot {e}")
+
+
+def test_unsupported_arguments(gpu, fmx, oracle):
+    rng = np.random.default_rng(15)
+    x = _rand_bf16(rng, (1, 128))
+    w = _rand_bf16(rng, (16, 128), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    args = (to_dev(x), to_dev_u32(rq), to_dev(rs), to_dev(rb))
+    for kw in (dict(bits=8), dict(group_size=32), dict(transpose=False), dict(mode="mxfp4")):
+        with pytest.raises(fmx.FmxError, match="UNSUPPORTED"):
+            fmx.quantized_matmul(*args, **kw)
+
+
+@pytest.mark.parametrize("T,E,k,norm,H,bias", [(1, 60, 4, False, 2048, False),
+                                                (8, 128, 8, True, 2048, False),
+                                                (77, 60, 4, False, 2048, True),
+                                                (300, 128, 8, True, 512, False),
+                                                (5, 1024, 16, True, 128, False)])
+def test_router_bitexact(gpu, fmx, oracle, T, E, k, norm, H, bias):
+    rng = np.random.default_rng(T + E + k)
+    x = _rand_bf16(rng, (T, H))
+    wr = _rand_bf16(rng, (E, H), 0.02)
+    lb = _rand_bf16(rng, (E,)) if bias else None
+    cfg = fmx.MoEConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k,
+                        moe_intermediate_size=64, norm_topk_prob=norm)
+    inds, scores, probs = fmx.router_topk(cfg, to_dev(x), to_dev(wr),
+                                          None if lb is None else to_dev(lb))
+    _, rp, ri, rsc = oracle.router_topk(x, wr, k, norm, lb)
+    np.testing.assert_array_equal(from_dev_bf16(probs), rp)
+    np.testing.assert_array_equal(from_dev_u32(inds), ri)
+    np.testing.assert_array_equal(from_dev_bf16(scores), rsc)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 4, 60), (8, 8, 128), (512, 4, 60), (1024, 8, 128),
+                                   (33, 3, 5), (4096, 8, 128)])
+def test_sort_bitexact(gpu, fmx, oracle, T, k, E):
+    rng = np.random.default_rng(T * k + E)
+    if T % 2:  # arbitrary keys, repeats allowed within a row
+        inds = rng.integers(0, E, (T, k)).astype(np.uint32)
+    else:      # distinct experts per token, skewed toward low ids
+        p = np.exp(-np.arange(E) / (E / 6.0))
+        p /= p.sum()
+        inds = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.uint32)
+    order, inv, src, idx, offs = fmx.moe_sort(to_dev_u32(inds), E)
+    ro, ri, rsrc, ridx, roff = oracle.moe_sort(inds, E)
+    np.testing.assert_array_equal(from_dev_u32(order), ro)
+    np.testing.assert_array_equal(from_dev_u32(inv), ri)
+    np.testing.assert_array_equal(from_dev_u32(src), rsrc)
+    np.testing.assert_array_equal(from_dev_u32(idx), ridx)
+    np.testing.assert_array_equal(from_dev_u32(offs), roff)
+    np.testing.assert_array_equal(ro, np.argsort(inds.reshape(-1), kind="stable"))
