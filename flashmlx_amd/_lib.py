@@ -108,6 +108,11 @@ _SIGS = {
         [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
          C.c_size_t, C.c_void_p],
     ),
+    "fmx_moe_block_forward_profiled": (
+        C.c_int,
+        [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+         C.c_size_t, C.c_void_p, P(C.c_void_p)],
+    ),
     "fmx_moe_workspace_routing": (
         C.c_int,
         [P(FmxMoEConfig), C.c_int64, C.c_void_p] + [P(C.c_void_p)] * 8,

@@ -121,6 +121,8 @@ int bind_workspace(Arena& ar, void* ws, size_t ws_bytes, size_t need, hipStream_
 // ---------------------------------------------------------------- MoE layout
 
 constexpr int64_t kMoEMaxTokens = 65536;
+// K slices of the shared expert's down projection (K = Is is long, N = H short)
+constexpr int kSharedDownSplit = 4;
 constexpr size_t kCounterBytes = (kMoEMaxTokens / kRouterTok + 64) * sizeof(uint32_t);
 
 struct MoELayout {
@@ -131,7 +133,8 @@ struct MoELayout {
   uint16_t* scores;
   uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base;
   float* sgate;
-  uint16_t *xp, *h, *hs, *d, *sd;
+  uint16_t *xp, *h, *hs, *d;
+  float* sd_part;
   size_t total;
 };
 
@@ -161,7 +164,7 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.h = static_cast<uint16_t*>(ar.take(n * I * 2));
   L.hs = static_cast<uint16_t*>(ar.take(T * Is * 2));
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
-  L.sd = static_cast<uint16_t*>(ar.take(T * H * 2));
+  L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
   L.total = ar.used;
   return L;
 }
@@ -189,8 +192,8 @@ int check_moe_config(const fmx_moe_config* c) {
 }
 
 bool qw_ok(const fmx_qweight& q) {
-  return q.w && q.scales && q.biases && aligned(q.w, 16) && aligned(q.scales, 2) &&
-         aligned(q.biases, 2);
+  return q.w && q.scales && q.biases && aligned(q.w, 16) && aligned(q.scales, 4) &&
+         aligned(q.biases, 4);
 }
 
 // Router launch shared by the block forward and fmx_moe_router_topk.
@@ -216,7 +219,11 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.xp = xp;
   a.counters = L.counters;
   a.n_tt = static_cast<int>((T + kRouterTok - 1) / kRouterTok);
-  a.n_ct = static_cast<int>((c.num_experts + (wsg ? 1 : 0) + kRouterCols - 1) / kRouterCols);
+  // one token tile: a wave per column spreads the router weights over the
+  // most CUs; many token tiles: 4 columns per wave re-read x 4x less
+  a.cols_per_wave = a.n_tt > 1 ? 4 : 1;
+  const int64_t cols_per_tile = 4 * a.cols_per_wave;
+  a.n_ct = static_cast<int>((c.num_experts + (wsg ? 1 : 0) + cols_per_tile - 1) / cols_per_tile);
   const int64_t n = T * c.num_experts_per_tok;
   a.fuse_sort = want_sort && router_sort_fits(n, c.num_experts) ? 1 : 0;
   a.sort.order = L.order;
@@ -326,9 +333,9 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
   p.K = static_cast<int>(K);
   p.out = static_cast<uint16_t*>(out->data);
   p.ldo = N;
-  p.n_tiles = static_cast<int>((N + 15) / 16);
   p.n_exp = 1;
   p.rows_max = p.x_rows = p.out_rows = static_cast<int>(rows);
+  p.max_rows_per_seg = static_cast<int>(rows);
   FMX_HIP(launch_qgemm(p, nullptr, stream));
   return ok();
 }
@@ -534,10 +541,10 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   q.K = static_cast<int>(p.K);
   q.out = static_cast<uint16_t*>(out->data);
   q.ldo = p.N;
-  q.n_tiles = static_cast<int>((p.N + 15) / 16);
   q.n_exp = static_cast<int>(p.E);
   q.rows_max = q.out_rows = static_cast<int>(rows);
   q.x_rows = static_cast<int>(p.n_x * p.M);
+  q.max_rows_per_seg = static_cast<int>(rows);
   FMX_HIP(launch_qgemm(q, nullptr, stream));
   return ok();
 }
@@ -648,7 +655,19 @@ int fmx_moe_workspace_routing(const fmx_moe_config* cfg, int64_t n_tokens, const
 int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x,
                           int64_t T, void* y, void* workspace, size_t workspace_bytes,
                           fmx_stream stream_) {
+  return fmx_moe_block_forward_profiled(cfg, w, x, T, y, workspace, workspace_bytes, stream_,
+                                        nullptr);
+}
+
+int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                   const void* x, int64_t T, void* y, void* workspace,
+                                   size_t workspace_bytes, fmx_stream stream_,
+                                   void* const* stage_events) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  auto mark = [&](int i) -> hipError_t {
+    return stage_events ? hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream)
+                        : hipSuccess;
+  };
   int rc;
   if ((rc = check_moe_config(cfg))) return rc;
   if (!w || !x || !y) return fail(FMX_ERR_ARG, "NULL argument");
@@ -678,6 +697,7 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
   const MoELayout L = moe_layout(c, T, ar.base);
 
   // 1. router + top-k (+ sort when it fits in the router's last workgroup)
+  FMX_HIP(mark(0));
   bool sorted = false;
   if ((rc = run_router(c, L, x, T, w->router_w, w->router_logit_bias,
                        has_sh ? w->shared_expert_gate_w : nullptr, L.inds, L.scores, L.probs,
@@ -687,6 +707,7 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
     SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base};
     FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
   }
+  FMX_HIP(mark(1));
 
   // 2. gate/up + SwiGLU: routed experts over the sorted rows, and the shared expert
   QGemmProblem gu{};
@@ -711,10 +732,10 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
   gu.ldo = I;
   gu.dual = 1;
   gu.out_p8 = 1;
-  gu.n_tiles = static_cast<int>((I + 15) / 16);
   gu.n_exp = static_cast<int>(E);
   gu.rows_max = gu.out_rows = static_cast<int>(n);
   gu.x_rows = static_cast<int>(T);
+  gu.max_rows_per_seg = static_cast<int>(T);  // a token picks an expert at most once
   QGemmProblem sgu{};
   if (has_sh) {
     sgu.x = L.xp;
@@ -733,11 +754,12 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
     sgu.ldo = Is;
     sgu.dual = 1;
     sgu.out_p8 = 1;
-    sgu.n_tiles = static_cast<int>((Is + 15) / 16);
     sgu.n_exp = 1;
     sgu.rows_max = sgu.x_rows = sgu.out_rows = static_cast<int>(T);
+    sgu.max_rows_per_seg = static_cast<int>(T);
   }
   FMX_HIP(launch_qgemm(gu, has_sh ? &sgu : nullptr, stream));
+  FMX_HIP(mark(2));
 
   // 3. down: routed rows (sorted order) and the shared expert
   QGemmProblem dn{};
@@ -756,9 +778,9 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
   dn.K = static_cast<int>(I);
   dn.out = L.d;
   dn.ldo = H;
-  dn.n_tiles = static_cast<int>((H + 15) / 16);
   dn.n_exp = static_cast<int>(E);
   dn.rows_max = dn.x_rows = dn.out_rows = static_cast<int>(n);
+  dn.max_rows_per_seg = static_cast<int>(T);
   QGemmProblem sdn{};
   if (has_sh) {
     sdn.x = L.hs;
@@ -770,26 +792,31 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, c
     sdn.b0 = static_cast<const uint16_t*>(w->shared_down.biases);
     sdn.N = static_cast<int>(H);
     sdn.K = static_cast<int>(Is);
-    sdn.out = L.sd;
     sdn.ldo = H;
-    sdn.n_tiles = static_cast<int>((H + 15) / 16);
     sdn.n_exp = 1;
     sdn.rows_max = sdn.x_rows = sdn.out_rows = static_cast<int>(T);
+    sdn.max_rows_per_seg = static_cast<int>(T);
+    sdn.ksplit = kSharedDownSplit;
+    sdn.out_part = L.sd_part;
   }
   FMX_HIP(launch_qgemm(dn, has_sh ? &sdn : nullptr, stream));
+  FMX_HIP(mark(3));
 
   // 4. top-k weighted combine + gated shared expert
   CombineArgs cb{};
   cb.d = L.d;
   cb.inv = L.inv;
   cb.scores = L.scores;
-  cb.sd = has_sh ? L.sd : nullptr;
+  cb.sd = nullptr;
+  cb.sd_part = has_sh ? L.sd_part : nullptr;
+  cb.sd_ksplit = kSharedDownSplit;
   cb.sgate = has_sh ? L.sgate : nullptr;
   cb.y = static_cast<uint16_t*>(y);
   cb.T = static_cast<int>(T);
   cb.k = static_cast<int>(k);
   cb.H = static_cast<int>(H);
   FMX_HIP(launch_combine(cb, stream));
+  FMX_HIP(mark(4));
   return ok();
 }
 

@@ -81,10 +81,17 @@ __device__ inline float sigmoid_bf16(float v) {
   return bf16_to_f32(f64_to_bf16(s));
 }
 
+// bf16(sigmoid(v)) from fp32 hardware exp2 and reciprocal (a few ulp of
+// fp32, far below the bf16 rounding step).
+__device__ inline float sigmoid_bf16_fast(float v) {
+  const float e = __builtin_amdgcn_exp2f(-v * 1.4426950408889634f);
+  return round_bf16(__builtin_amdgcn_rcpf(1.0f + e));
+}
+
 // MLX's compiled SwiGLU on bf16 arrays: multiply(multiply(g, sigmoid(g)), u),
 // every op rounded to bf16 (server/src/model.cpp:14-25).
 __device__ inline uint16_t swiglu_bf16(float g_bf, float u_bf) {
-  const float sg = sigmoid_bf16(g_bf);
+  const float sg = sigmoid_bf16_fast(g_bf);
   const float t = round_bf16(g_bf * sg);
   return f32_to_bf16(t * u_bf);
 }

@@ -36,15 +36,37 @@ __global__ __launch_bounds__(kElemThreads) void combine_kernel(CombineArgs a) {
   uint16_t outv[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) outv[i] = f32_to_bf16(acc[i]);
-  if (a.sd) {
+  if (a.sd || a.sd_part) {
     const float g = a.sgate[t];
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.sd + static_cast<int64_t>(t) * a.H + o * 8);
+    float sdv[8];
+    if (a.sd_part) {
+      // shared down projection from its split-K partial sums, in slice order
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float sh0 = round_bf16(g * __uint_as_float(v[i] << 16));
-      const float sh1 = round_bf16(g * __uint_as_float(v[i] & 0xffff0000u));
-      outv[2 * i] = f32_to_bf16(bf16_to_f32(outv[2 * i]) + sh0);
-      outv[2 * i + 1] = f32_to_bf16(bf16_to_f32(outv[2 * i + 1]) + sh1);
+      for (int i = 0; i < 8; ++i) sdv[i] = 0.0f;
+      for (int ks = 0; ks < a.sd_ksplit; ++ks) {
+        const float* p = a.sd_part + (static_cast<int64_t>(ks) * a.T + t) * a.H + o * 8;
+        const f32x4_t lo = *reinterpret_cast<const f32x4_t*>(p);
+        const f32x4_t hi = *reinterpret_cast<const f32x4_t*>(p + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sdv[i] += lo[i];
+          sdv[4 + i] += hi[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sdv[i] = round_bf16(sdv[i]);
+    } else {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.sd + static_cast<int64_t>(t) * a.H + o * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sdv[2 * i] = __uint_as_float(v[i] << 16);
+        sdv[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float sh = round_bf16(g * sdv[i]);
+      outv[i] = f32_to_bf16(bf16_to_f32(outv[i]) + sh);
     }
   }
   u32x4_t w;

@@ -34,8 +34,7 @@ hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut&
 // bf16; per token: softmax in fp64 with exp_det, top-k, scores, renorm;
 // optionally the sort of all tokens' indices in the last workgroup.
 constexpr int kRouterTok = 8;      // tokens per tile
-constexpr int kRouterCols = 8;     // logit columns per tile
-constexpr int kRouterThreads = 256;
+constexpr int kRouterThreads = 256;  // 4 waves; each wave forms 8 tokens x cols_per_wave logits
 constexpr int kRouterSortCnt = 16 * 1024;  // LDS bytes for a fused sort's count table
 constexpr int kRouterSortMaxN = 2048;
 
@@ -52,7 +51,8 @@ struct RouterArgs {
   float* sgate;            // [T] sigmoid(shared gate logit) (bf16 value) or null
   uint16_t* xp;            // [T, H] P8 copy of x or null
   uint32_t* counters;      // [n_tt + 1], zero on entry, zero on exit
-  int n_tt, n_ct;          // token tiles, column tiles
+  int n_tt, n_ct;          // token tiles, column tiles (4 * cols_per_wave columns each)
+  int cols_per_wave;       // 1 (one token tile: decode) or 4 (prefill)
   int fuse_sort;           // last workgroup sorts inds (needs router_sort_fits)
   SortOut sort;
 };
@@ -80,13 +80,21 @@ struct QGemmProblem {
   int64_t ldo;
   int dual;                 // out = swiglu(x.W0^T, x.W1^T)
   int out_p8;               // write out rows in P8 layout (needs N % 8 == 0)
-  int n_tiles;              // ceil(N / 16)
+  int n_tiles;              // output tiles of 32 rows (set by launch_qgemm)
   // bounds the device-side tables are clamped to, so that stale or invalid
   // routing state can never address memory outside the arrays
   int n_exp;                // experts in w (seg_exp values clamp to n_exp-1)
   int rows_max;             // sorted rows (seg_off values clamp to it)
   int x_rows;               // rows of x (row_map values clamp to x_rows-1)
   int out_rows;             // rows of out (out_map values clamp to out_rows-1)
+  // split-K over workgroups: ksplit > 1 writes fp32 partial sums of each K
+  // slice to out_part[ks][out_rows][N] (not with dual) instead of `out`
+  int ksplit;
+  float* out_part;
+  // activation rows are staged in LDS in passes of rows_per_pass rows (set
+  // by launch_qgemm from max_rows_per_seg, the most rows a segment can hold)
+  int max_rows_per_seg;
+  int rows_per_pass;
 };
 // Launch one or two independent problems in one grid (p1 may be null).
 hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStream_t stream);
@@ -97,6 +105,8 @@ struct CombineArgs {
   const uint32_t* inv;     // [T*k] entry -> sorted row
   const uint16_t* scores;  // [T, k] bf16
   const uint16_t* sd;      // [T, H] bf16 shared-expert output or null
+  const float* sd_part;    // or [sd_ksplit, T, H] fp32 partial sums of it (added in order)
+  int sd_ksplit;
   const float* sgate;      // [T] or null
   uint16_t* y;             // [T, H] bf16
   int T, k, H;

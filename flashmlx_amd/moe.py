@@ -248,6 +248,16 @@ class MoEBlock:
             self.workspace.data_ptr(), self.ws_bytes, _stream()))
         self._last_T = T
 
+    def forward_profiled(self, x: torch.Tensor, y: torch.Tensor, events) -> None:
+        """forward_into that records 5 torch.cuda.Events at the stage
+        boundaries (router | gate/up | down | combine)."""
+        T = x.numel() // self.cfg.hidden_size
+        arr = (C.c_void_p * 5)(*[ev.cuda_event for ev in events])
+        _lib.check(self.lib.fmx_moe_block_forward_profiled(
+            C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),
+            self.workspace.data_ptr(), self.ws_bytes, _stream(), arr))
+        self._last_T = T
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         if x.dtype != torch.bfloat16 or not x.is_contiguous():
             raise ValueError("x must be a contiguous bf16 tensor [..., H]")

@@ -196,6 +196,18 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
                           const void* x, int64_t n_tokens, void* y, void* workspace,
                           size_t workspace_bytes, fmx_stream stream);
 
+/* fmx_moe_block_forward that also records caller-created HIP events
+ * (hipEvent_t, as void*) on `stream` at its stage boundaries:
+ *   stage_events[0] before the router, [1] after routing and sort,
+ *   [2] after the gate/up GEMMs, [3] after the down GEMMs, [4] after the
+ *   combine. Used to time each stage's kernels; no counterpart in the
+ *   reference. */
+#define FMX_MOE_STAGE_EVENTS 5
+int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                   const void* x, int64_t n_tokens, void* y, void* workspace,
+                                   size_t workspace_bytes, fmx_stream stream,
+                                   void* const* stage_events);
+
 /* Device views of the routing state a forward of n_tokens tokens left in
  * the workspace (valid until the next call on that workspace). Any out
  * pointer may be NULL.

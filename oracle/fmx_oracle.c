@@ -305,6 +305,23 @@ static uint16_t bf16_dot_exact(const uint16_t* a, const uint16_t* b, int64_t n) 
   return orc_f64_to_bf16(acc);
 }
 
+/* Softmax normaliser in a fixed summation order (MLX's own order is an
+ * implementation detail of its CPU kernel): 64 partial sums, partial l
+ * taking ex[l], ex[l+64], ... in turn, then six butterfly rounds
+ * s_l <- s_l + s_{l xor w} for w = 32, 16, ..., 1; the result is s_0. */
+static double softmax_den(const double* ex, int64_t E) {
+  double s[64], t[64];
+  for (int l = 0; l < 64; ++l) {
+    s[l] = 0.0;
+    for (int64_t e = l; e < E; e += 64) s[l] += ex[e];
+  }
+  for (int w = 32; w >= 1; w >>= 1) {
+    for (int l = 0; l < 64; ++l) t[l] = s[l] + s[l ^ w];
+    memcpy(s, t, sizeof s);
+  }
+  return s[0];
+}
+
 /* model.cpp:757-775: gates = x.Wr^T; softmax(precise=true); top-k by
  * argpartition(-gates, k-1)[..., :k]; scores = take_along_axis.
  * The selected set is the k largest bf16 probabilities with ties going to
@@ -335,11 +352,8 @@ int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
         }
         double m = -INFINITY;
         for (int64_t e = 0; e < E; ++e) m = fmax(m, (double)bf(lg[e]));
-        double sum = 0.0;
-        for (int64_t e = 0; e < E; ++e) {
-          ex[e] = orc_exp((double)bf(lg[e]) - m);
-          sum += ex[e];
-        }
+        for (int64_t e = 0; e < E; ++e) ex[e] = orc_exp((double)bf(lg[e]) - m);
+        const double sum = softmax_den(ex, E);
         for (int64_t e = 0; e < E; ++e) pb[e] = orc_f64_to_bf16(ex[e] / sum);
         memset(taken, 0, E);
         for (int j = 0; j < k; ++j) {
