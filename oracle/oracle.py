@@ -21,8 +21,12 @@ ACC_F64, ACC_A, ACC_B, ACC_C = 0, 1, 2, 3
 _lib = None
 
 
-def build() -> pathlib.Path:
-    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+def build(force: bool = False) -> pathlib.Path:
+    """make in oracle/ (recompiles always with force=True)."""
+    args = ["make", "-s", "-C", str(HERE)]
+    if force:
+        args.insert(2, "-B")
+    subprocess.run(args, check=True)
     return LIB_PATH
 
 

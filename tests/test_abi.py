@@ -1,0 +1,140 @@
+"""The C-ABI library without a GPU: it loads, exports every entry point that
+include/fmx.h declares, and its host-side logic (size queries, argument
+validation, status strings, the seeded generator) behaves. No call here
+launches a kernel."""
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def header_functions() -> list[str]:
+    text = (ROOT / "include" / "fmx.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fmx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(fmx):
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding declares a signature for each of them
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from flashmlx_amd import _lib
+    with pytest.raises(ImportError):
+        _lib.load(tmp_path / "libfmx.so")
+
+
+def test_status_strings_and_version(fmx):
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    assert lib.fmx_abi_version() >= 1
+    for code, name in _lib.STATUS_NAMES.items():
+        assert lib.fmx_status_string(code).decode() == name
+    assert lib.fmx_status_string(99).decode() == "FMX_ERR_UNKNOWN"
+
+
+def _arr(shape, dtype, data=None):
+    from flashmlx_amd import _lib
+    a = _lib.FmxArray()
+    a.data = data
+    a.dtype = dtype
+    a.ndim = len(shape)
+    for i, s in enumerate(shape):
+        a.shape[i] = s
+    return a
+
+
+def test_quantized_matmul_validation(fmx):
+    """Arguments outside scope or inconsistent are rejected before any HIP call."""
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    buf = np.zeros(1 << 16, np.uint8)
+    p = (buf.ctypes.data + 255) // 256 * 256     # aligned host address; never dereferenced
+    x, w = _arr([4, 256], _lib.FMX_BF16, p), _arr([64, 32], _lib.FMX_U32, p)
+    s, b = _arr([64, 4], _lib.FMX_BF16, p), _arr([64, 4], _lib.FMX_BF16, p)
+    out = _arr([4, 64], _lib.FMX_BF16, p)
+    R = C.byref
+    call = lambda **kw: lib.fmx_quantized_matmul(  # noqa: E731
+        R(kw.get("x", x)), R(w), R(s), R(b), kw.get("t", 1), kw.get("g", 64), kw.get("bits", 4),
+        kw.get("mode", b"affine"), R(out), None, 0, None)
+    assert call(bits=8) == _lib.FMX_ERR_UNSUPPORTED
+    assert b"bits=8" in lib.fmx_last_error()
+    assert call(g=32) == _lib.FMX_ERR_UNSUPPORTED
+    assert call(t=0) == _lib.FMX_ERR_UNSUPPORTED
+    assert call(mode=b"mxfp4") == _lib.FMX_ERR_UNSUPPORTED
+    assert call(x=_arr([4, 256], _lib.FMX_F32, p)) == _lib.FMX_ERR_DTYPE
+    assert call(x=_arr([4, 128], _lib.FMX_BF16, p)) == _lib.FMX_ERR_SHAPE
+    assert call(x=_arr([4, 256], _lib.FMX_BF16, p + 2)) == _lib.FMX_ERR_ARG
+    o = _lib.FmxArray()
+    assert lib.fmx_quantized_matmul_out_shape(R(_arr([2, 3, 256], 0, p)), R(w), 1, 64, 4, R(o)) == 0
+    assert o.ndim == 3 and list(o.shape[:3]) == [2, 3, 64]
+
+
+def test_gather_qmm_out_shape_broadcasts(fmx):
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    x = _arr([5, 1, 1, 256], _lib.FMX_BF16)     # batch (5, 1), M = 1
+    w = _arr([8, 96, 32], _lib.FMX_U32)
+    rhs = _arr([5, 4], _lib.FMX_U32)
+    o = _lib.FmxArray()
+    rc = lib.fmx_gather_qmm_out_shape(C.byref(x), C.byref(w), None, C.byref(rhs), 1, 64, 4, C.byref(o))
+    assert rc == 0, lib.fmx_last_error()
+    assert list(o.shape[:o.ndim]) == [5, 4, 1, 96]
+
+
+def test_moe_workspace_sizes(fmx):
+    from flashmlx_amd import MoEConfig
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    q15 = MoEConfig(2048, 60, 4, 1408, 5632, False).to_c()
+    q3 = MoEConfig(2048, 128, 8, 768, 0, True).to_c()
+    s1 = lib.fmx_moe_workspace_size(C.byref(q15), 1)
+    s512 = lib.fmx_moe_workspace_size(C.byref(q15), 512)
+    assert 0 < s1 < s512 < (1 << 31)
+    assert lib.fmx_moe_workspace_size(C.byref(q3), 1024) > 0
+    assert lib.fmx_moe_workspace_size(C.byref(q3), 65537) == 0        # above the token limit
+    bad = MoEConfig(2048, 60, 4, 1408, 5632, False, quant_bits=8).to_c()
+    assert lib.fmx_moe_workspace_size(C.byref(bad), 8) == 0
+    odd = MoEConfig(2000, 60, 4, 1408, 5632, False).to_c()             # H not a multiple of 64
+    assert lib.fmx_moe_workspace_size(C.byref(odd), 8) == 0
+    topk = MoEConfig(2048, 8, 9, 1408, 0, False).to_c()                # k > E
+    assert lib.fmx_moe_workspace_size(C.byref(topk), 8) == 0
+
+
+def test_synth_is_counter_based(fmx):
+    """Each value is a pure function of (seed, stream, index): prefixes agree,
+    streams and seeds differ, moments are those of N(mean, std)."""
+    from flashmlx_amd import synth_normal_bf16
+    a = synth_normal_bf16(1 << 20, 7, 3)
+    b = synth_normal_bf16(1000, 7, 3)
+    np.testing.assert_array_equal(a[:1000], b)
+    assert not np.array_equal(synth_normal_bf16(1000, 7, 4), b)
+    assert not np.array_equal(synth_normal_bf16(1000, 8, 3), b)
+    f = (a.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    assert abs(f.mean()) < 5e-3 and abs(f.std() - 1) < 5e-3
+    assert abs((np.abs(f) < 1).mean() - 0.6827) < 3e-3
+    g = (synth_normal_bf16(1 << 18, 1, 1, 0.5, 0.02).astype(np.uint32) << 16).view(np.float32)
+    assert abs(g.mean() - 0.5) < 1e-3 and abs(g.std() - 0.02) < 1e-3
+
+
+def test_workload_bytes_match_published_figure():
+    """Algorithmic bytes of one Qwen1.5 decode B=1 call with 4 unique experts:
+    4 x 4,866,048 + 19,464,192 + 245,760 + 4,096 + 8,192 = 39,186,432."""
+    from flashmlx_amd import workloads as W
+    assert W.algorithmic_bytes(W.QWEN15, 1, 4) == 39_186_432
+    assert W.algorithmic_bytes(W.QWEN3, 1, 8) == 21_766_144
+    assert W.flops(W.QWEN15, 512) == 70_994_886_656
+    assert W.flops(W.QWEN3, 1024) == 77_846_282_240
