@@ -124,6 +124,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--eager", action="store_true", help="no HIP graph")
+    ap.add_argument("--no-pack", action="store_true",
+                    help="MLX-layout weights only (no fmx_pack_expert_weights re-layout)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -147,7 +149,7 @@ def main():
 
     log(f"workload {wl.key}: generating inputs")
     hi = W.host_inputs(wl)
-    block0, x = W.device_block(wl, hi)
+    block0, x = W.device_block(wl, hi, pack=not args.no_pack)
     del hi
 
     def clone_q(q):
@@ -163,7 +165,9 @@ def main():
             nw.shared_gate, nw.shared_up, nw.shared_down = (clone_q(w.shared_gate), clone_q(w.shared_up),
                                                             clone_q(w.shared_down))
             nw.shared_expert_gate_w = w.shared_expert_gate_w.clone()
-        return MoEBlock(b.cfg, nw, max_tokens=T)
+        if w.packed is not None:
+            nw.packed = w.packed.clone()
+        return MoEBlock(b.cfg, nw, max_tokens=T, pack=False)
 
     R = max(1, args.layers)
     blocks = [block0] + [clone_block(block0) for _ in range(R - 1)]

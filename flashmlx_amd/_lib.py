@@ -60,6 +60,7 @@ class FmxMoEWeights(C.Structure):
         ("shared_up", FmxQWeight),
         ("shared_down", FmxQWeight),
         ("shared_expert_gate_w", C.c_void_p),
+        ("packed", C.c_void_p),
     ]
 
 
@@ -101,6 +102,9 @@ _SIGS = {
     "fmx_quantize": (C.c_int, [_A, C.c_int, C.c_int, C.c_char_p, _A, _A, _A, C.c_void_p]),
     "fmx_dequantize": (C.c_int, [_A, _A, _A, C.c_int, C.c_int, C.c_char_p, _A, C.c_void_p]),
     "fmx_stack_experts": (C.c_int, [P(C.c_void_p), C.c_int64, C.c_size_t, C.c_void_p, C.c_void_p]),
+    "fmx_moe_packed_size": (C.c_size_t, [P(FmxMoEConfig)]),
+    "fmx_pack_expert_weights": (
+        C.c_int, [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_size_t, C.c_void_p]),
     "fmx_moe_workspace_size": (C.c_size_t, [P(FmxMoEConfig), C.c_int64]),
     "fmx_moe_workspace_init": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
     "fmx_moe_block_forward": (

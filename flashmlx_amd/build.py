@@ -20,6 +20,7 @@ OBJDIR = HERE / "_build"
 SOURCES = [
     "csrc/fmx_route.hip",
     "csrc/fmx_qgemm.hip",
+    "csrc/fmx_qgemv.hip",
     "csrc/fmx_elem.hip",
     "csrc/fmx_api.cpp",
     "csrc/fmx_synth.cpp",

@@ -131,7 +131,7 @@ struct MoELayout {
   uint16_t* probs;
   uint32_t* inds;
   uint16_t* scores;
-  uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base;
+  uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base, *recs;
   float* sgate;
   uint16_t *xp, *h, *hs, *d;
   float* sd_part;
@@ -159,6 +159,7 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.seg_exp = static_cast<uint32_t*>(ar.take(E * 4));
   L.seg_off = static_cast<uint32_t*>(ar.take((E + 1) * 4));
   L.sort_base = static_cast<uint32_t*>(ar.take(E * ((n + 63) / 64) * 4));
+  L.recs = static_cast<uint32_t*>(ar.take(E * kSegRecWords * 4));
   L.sgate = static_cast<float*>(ar.take(T * 4));
   L.xp = static_cast<uint16_t*>(ar.take(T * H * 2));
   L.h = static_cast<uint16_t*>(ar.take(n * I * 2));
@@ -194,6 +195,31 @@ int check_moe_config(const fmx_moe_config* c) {
 bool qw_ok(const fmx_qweight& q) {
   return q.w && q.scales && q.biases && aligned(q.w, 16) && aligned(q.scales, 4) &&
          aligned(q.biases, 4);
+}
+
+// Offsets (bytes) of the parts of a packed layer (fmx_pack_expert_weights).
+struct PackedLayout {
+  int64_t gu_es, dn_es;           // bytes per routed expert: gate+up pair, down
+  size_t gu, dn, sgu, sdn, total;
+};
+
+bool packable(const fmx_moe_config& c) {
+  return c.hidden_size % 128 == 0 && c.moe_intermediate_size % 128 == 0 &&
+         c.shared_expert_intermediate_size % 128 == 0;
+}
+
+PackedLayout packed_layout(const fmx_moe_config& c) {
+  const int64_t H = c.hidden_size, E = c.num_experts, I = c.moe_intermediate_size;
+  const int64_t Is = c.shared_expert_intermediate_size;
+  PackedLayout P{};
+  P.gu_es = (I / 16) * (H / 128) * kPackedBlockPair;
+  P.dn_es = (H / 16) * (I / 128) * kPackedBlockSingle;
+  P.gu = 0;
+  P.dn = P.gu + static_cast<size_t>(align_up(E * P.gu_es, 256));
+  P.sgu = P.dn + static_cast<size_t>(align_up(E * P.dn_es, 256));
+  P.sdn = P.sgu + static_cast<size_t>(align_up((Is / 16) * (H / 128) * kPackedBlockPair, 256));
+  P.total = P.sdn + static_cast<size_t>(align_up((H / 16) * (Is / 128) * kPackedBlockSingle, 256));
+  return P;
 }
 
 // Router launch shared by the block forward and fmx_moe_router_topk.
@@ -235,6 +261,7 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.seg_exp = L.seg_exp;
   a.sort.seg_off = L.seg_off;
   a.sort.base = L.sort_base;
+  a.sort.recs = L.recs;
   if (sorted_in_router) *sorted_in_router = a.fuse_sort != 0;
   FMX_HIP(launch_router(a, stream));
   return FMX_OK;
@@ -622,6 +649,60 @@ size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens) {
   return moe_layout(*cfg, max_tokens, nullptr).total;
 }
 
+size_t fmx_moe_packed_size(const fmx_moe_config* cfg) {
+  if (check_moe_config(cfg) || !packable(*cfg)) return 0;
+  return packed_layout(*cfg).total;
+}
+
+int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* src, void* packed,
+                            size_t packed_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  const fmx_moe_config& c = *cfg;
+  if (!packable(c))
+    return fail(FMX_ERR_UNSUPPORTED, "packing needs H, I and Is to be multiples of 128");
+  if (!src || !packed) return fail(FMX_ERR_ARG, "NULL argument");
+  if (!aligned(packed, 256)) return fail(FMX_ERR_ARG, "packed not 256-byte aligned");
+  const PackedLayout PL = packed_layout(c);
+  if (packed_bytes < PL.total)
+    return fail(FMX_ERR_WORKSPACE, "packed buffer %zu bytes, need %zu", packed_bytes, PL.total);
+  const bool has_sh = c.shared_expert_intermediate_size > 0;
+  if (!qw_ok(src->gate) || !qw_ok(src->up) || !qw_ok(src->down))
+    return fail(FMX_ERR_ARG, "expert weights NULL or misaligned");
+  if (has_sh && (!qw_ok(src->shared_gate) || !qw_ok(src->shared_up) || !qw_ok(src->shared_down)))
+    return fail(FMX_ERR_ARG, "shared expert weights NULL or misaligned");
+  const int64_t H = c.hidden_size, E = c.num_experts, I = c.moe_intermediate_size;
+  const int64_t Is = c.shared_expert_intermediate_size;
+  uint8_t* dst = static_cast<uint8_t*>(packed);
+  auto pack = [&](const fmx_qweight& a, const fmx_qweight* b, int64_t n_exp, int64_t N, int64_t K,
+                  size_t off, int64_t es) -> hipError_t {
+    PackArgs pa{};
+    pa.w0 = static_cast<const uint32_t*>(a.w);
+    pa.s0 = static_cast<const uint16_t*>(a.scales);
+    pa.b0 = static_cast<const uint16_t*>(a.biases);
+    if (b) {
+      pa.w1 = static_cast<const uint32_t*>(b->w);
+      pa.s1 = static_cast<const uint16_t*>(b->scales);
+      pa.b1 = static_cast<const uint16_t*>(b->biases);
+    }
+    pa.n_exp = n_exp;
+    pa.N = static_cast<int>(N);
+    pa.nt = static_cast<int>(N / 16);
+    pa.nu = static_cast<int>(K / 128);
+    pa.dst = dst + off;
+    pa.dst_estride = es;
+    return launch_pack(pa, stream);
+  };
+  FMX_HIP(pack(src->gate, &src->up, E, I, H, PL.gu, PL.gu_es));
+  FMX_HIP(pack(src->down, nullptr, E, H, I, PL.dn, PL.dn_es));
+  if (has_sh) {
+    FMX_HIP(pack(src->shared_gate, &src->shared_up, 1, Is, H, PL.sgu, 0));
+    FMX_HIP(pack(src->shared_down, nullptr, 1, H, Is, PL.sdn, 0));
+  }
+  return ok();
+}
+
 int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream_) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
@@ -704,11 +785,104 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
                        has_sh ? L.sgate : nullptr, L.xp, true, &sorted, stream)))
     return rc;
   if (!sorted) {
-    SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base};
+    SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base,
+               L.recs};
     FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
   }
   FMX_HIP(mark(1));
 
+  // decode shapes (at most 16 tokens, so at most 16 rows per expert) on packed weights
+  int gu_ks = 0, dn_upw = 0, dn_ks = 0, sd_split = kSharedDownSplit;
+  if (w->packed && T <= 16 && packable(c) && aligned(w->packed, 256)) {
+    const int64_t nu_h = H / 128, nu_i = I / 128, nu_s = Is / 128;
+    if (nu_h <= 64) gu_ks = static_cast<int>((nu_h + 7) / 8);
+    for (int upw : {4, 8}) {
+      for (int ks = 1; ks <= 8 && !dn_ks; ++ks) {
+        const int64_t span = static_cast<int64_t>(upw) * ks;
+        if (span < nu_i) continue;
+        const int64_t split = has_sh ? (nu_s + span - 1) / span : 1;
+        if (split > kSharedDownSplit) continue;
+        dn_upw = upw;
+        dn_ks = ks;
+        if (has_sh) sd_split = static_cast<int>(split);
+      }
+      if (dn_ks) break;
+    }
+  }
+  if (gu_ks && dn_ks) {
+    const PackedLayout PL = packed_layout(c);
+    const uint8_t* pk = static_cast<const uint8_t*>(w->packed);
+    // 2. gate/up + SwiGLU
+    GemvProblem g{};
+    g.wpk = pk + PL.gu;
+    g.estride = PL.gu_es;
+    g.nt = static_cast<int>(I / 16);
+    g.nu = static_cast<int>(H / 128);
+    g.n_exp = static_cast<int>(E);
+    g.recs = L.recs;
+    g.seg_n = L.seg_n;
+    g.max_seg = static_cast<int>(std::min(E, n));
+    g.gather = 1;
+    g.max_rows = static_cast<int>(T);  // a token picks an expert at most once
+    g.x = L.xp;
+    g.ldx = H;
+    g.x_rows = static_cast<int>(T);
+    g.out = L.h;
+    g.ldo = I;
+    g.out_p8 = 1;
+    g.out_rows = static_cast<int>(n);
+    GemvProblem sg{};
+    if (has_sh) {
+      sg.wpk = pk + PL.sgu;
+      sg.nt = static_cast<int>(Is / 16);
+      sg.nu = static_cast<int>(H / 128);
+      sg.n_exp = 1;
+      sg.max_seg = 1;
+      sg.rows_static = sg.max_rows = static_cast<int>(T);
+      sg.x = L.xp;
+      sg.ldx = H;
+      sg.x_rows = static_cast<int>(T);
+      sg.out = L.hs;
+      sg.ldo = Is;
+      sg.out_p8 = 1;
+      sg.out_rows = static_cast<int>(T);
+    }
+    FMX_HIP(launch_qgemv(g, has_sh ? &sg : nullptr, 1, 8, gu_ks, stream));
+    FMX_HIP(mark(2));
+    // 3. down: routed rows (sorted order) and the shared expert (fp32 K slices)
+    GemvProblem d{};
+    d.wpk = pk + PL.dn;
+    d.estride = PL.dn_es;
+    d.nt = static_cast<int>(H / 16);
+    d.nu = static_cast<int>(I / 128);
+    d.n_exp = static_cast<int>(E);
+    d.recs = L.recs;
+    d.seg_n = L.seg_n;
+    d.max_seg = g.max_seg;
+    d.max_rows = static_cast<int>(T);
+    d.x = L.h;
+    d.ldx = I;
+    d.x_rows = static_cast<int>(n);
+    d.out = L.d;
+    d.ldo = H;
+    d.out_rows = static_cast<int>(n);
+    GemvProblem sd{};
+    if (has_sh) {
+      sd.wpk = pk + PL.sdn;
+      sd.nt = static_cast<int>(H / 16);
+      sd.nu = static_cast<int>(Is / 128);
+      sd.n_exp = 1;
+      sd.max_seg = 1;
+      sd.rows_static = sd.max_rows = static_cast<int>(T);
+      sd.x = L.hs;
+      sd.ldx = Is;
+      sd.x_rows = static_cast<int>(T);
+      sd.out_rows = static_cast<int>(T);
+      sd.part = L.sd_part;
+    }
+    FMX_HIP(launch_qgemv(d, has_sh ? &sd : nullptr, 0, dn_upw, dn_ks, stream));
+    FMX_HIP(mark(3));
+  } else {
   // 2. gate/up + SwiGLU: routed experts over the sorted rows, and the shared expert
   QGemmProblem gu{};
   gu.x = L.xp;
@@ -801,6 +975,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   }
   FMX_HIP(launch_qgemm(dn, has_sh ? &sdn : nullptr, stream));
   FMX_HIP(mark(3));
+  }
 
   // 4. top-k weighted combine + gated shared expert
   CombineArgs cb{};
@@ -809,7 +984,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   cb.scores = L.scores;
   cb.sd = nullptr;
   cb.sd_part = has_sh ? L.sd_part : nullptr;
-  cb.sd_ksplit = kSharedDownSplit;
+  cb.sd_ksplit = sd_split;
   cb.sgate = has_sh ? L.sgate : nullptr;
   cb.y = static_cast<uint16_t*>(y);
   cb.T = static_cast<int>(T);

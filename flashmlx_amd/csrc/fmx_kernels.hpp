@@ -19,7 +19,11 @@ struct SortOut {
   uint32_t* seg_exp;  // [E]   u -> key of the u-th non-empty key (nullable)
   uint32_t* seg_off;  // [E+1] u -> first sorted position         (nullable)
   uint32_t* base;     // [E * ceil(n/64)] scratch
+  // [E][kSegRecWords] per non-empty key u: {entry/k of the first min(count,
+  // 16) positions (last repeated), key, first position, count, 0} (nullable)
+  uint32_t* recs;
 };
+constexpr int kSegRecWords = 32;
 
 // Sort in one workgroup of 1024 threads (separate launch).
 constexpr int kSortThreads = 1024;
@@ -98,6 +102,47 @@ struct QGemmProblem {
 };
 // Launch one or two independent problems in one grid (p1 may be null).
 hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStream_t stream);
+
+// ---------------------------------------------------------------- packed decode GEMM
+// Segments of at most 16 rows over weights packed by launch_pack (layout in
+// fmx_qgemv.hip). out[r0 + i] = x[row(i)] . W[e]^T, or SwiGLU of a pair.
+constexpr int kGemvMaxThreads = 512;
+constexpr int kPackedBlockSingle = 1152;  // bytes of one (16-row tile, 128-k unit) block
+constexpr int kPackedBlockPair = 2304;    // gate + up
+struct GemvProblem {
+  const uint8_t* wpk;       // packed weights of expert 0
+  int64_t estride;          // bytes per expert
+  int nt, nu;               // 16-row tiles (N/16), 128-k units (K/128)
+  int n_exp;                // experts (record keys clamp to n_exp-1)
+  const uint32_t* recs;     // segment records (SortOut::recs); null: one static segment
+  const uint32_t* seg_n;    // number of records (device)
+  int max_seg;              // segments the grid covers
+  int rows_static;          // rows of the static segment (<= 16)
+  int max_rows;             // most rows a segment holds (<= 16; sizes LDS, clamps records)
+  int gather;               // x row of segment row i = record entry i (else first + i)
+  const uint16_t* x;        // activation rows, P8 layout
+  int64_t ldx;
+  int x_rows;               // x row indices clamp to x_rows-1
+  uint16_t* out;            // bf16 rows (row = first position + i)
+  int64_t ldo;
+  int out_p8;               // write rows in P8 layout
+  int out_rows;             // rows of out
+  float* part;              // non-null: fp32 partial sums [ks_wg][out_rows][N] instead of out
+  int ks_wg;                // K slices over workgroups (set by launch_qgemv)
+};
+// dual: SwiGLU pair; upw: units per wave (4 or 8); ks: waves per workgroup.
+hipError_t launch_qgemv(const GemvProblem& p0, const GemvProblem* p1, int dual, int upw, int ks,
+                        hipStream_t stream);
+
+struct PackArgs {
+  const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // MLX layout [n_exp][N][..]
+  const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // second matrix of a pair or null
+  int64_t n_exp;
+  int N, nt, nu;
+  uint8_t* dst;
+  int64_t dst_estride;      // bytes per expert in dst
+};
+hipError_t launch_pack(const PackArgs& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- elementwise
 struct CombineArgs {

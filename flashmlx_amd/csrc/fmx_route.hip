@@ -128,6 +128,32 @@ __device__ void sort_block(const uint32_t* __restrict__ keys, int n, int k, int 
   }
 }
 
+// Segment records for the decode GEMM (SortOut::recs): once the segment
+// table and src are complete, record u = {src of the first min(count, 16)
+// positions (the last one repeated), key, first position, count}.
+__device__ void write_seg_recs(const SortOut& o, int nthreads) {
+  if (!o.recs || !o.seg_n || !o.seg_exp || !o.seg_off || !o.src) return;
+  __syncthreads();
+  const uint32_t U = *o.seg_n;
+  constexpr int F = 4 + 16;
+  for (uint32_t i = threadIdx.x; i < U * F; i += nthreads) {
+    const uint32_t u = i / F, f = i - u * F;
+    const uint32_t r0 = o.seg_off[u], r1 = o.seg_off[u + 1];
+    uint32_t v;
+    if (f < 16)
+      v = o.src[min(r0 + f, r1 - 1)];
+    else if (f == 16)
+      v = o.seg_exp[u];
+    else if (f == 17)
+      v = r0;
+    else if (f == 18)
+      v = r1 - r0;
+    else
+      v = 0u;
+    o.recs[u * kSegRecWords + f] = v;
+  }
+}
+
 bool sort_fits(int64_t n, int64_t E) {
   const int64_t tiles = (n + 63) / 64;
   return n >= 0 && n <= kSortMaxN && E >= 1 && E * tiles <= kSortCntBytes;
@@ -139,6 +165,7 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
   __shared__ uint8_t s_rank[kSortMaxN];
   __shared__ uint32_t s_tmp[kSortThreads / kWave + 1];
   sort_block<kSortThreads>(keys, n, k, E, o, s_cnt, s_rank, s_tmp);
+  write_seg_recs(o, kSortThreads);
 }
 
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
@@ -470,6 +497,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     sort_small(a.inds, n, a.k, a.E, a.sort, reinterpret_cast<uint32_t*>(s_cnt), s_idx);
   else
     sort_block<kRouterThreads>(a.inds, n, a.k, a.E, a.sort, s_cnt, s_rank, s_tmp);
+  write_seg_recs(a.sort, kRouterThreads);
   if (tid == 0 && a.n_tt > 1) a.counters[a.n_tt] = 0u;
 }
 

@@ -203,6 +203,7 @@ class MoEWeights:
     shared_down: Optional[QWeight] = None
     shared_expert_gate_w: Optional[torch.Tensor] = None  # bf16 [1, H]
     router_logit_bias: Optional[torch.Tensor] = None     # bf16 [E] (no reference counterpart)
+    packed: Optional[torch.Tensor] = None  # uint8 blob from pack() (no reference counterpart)
 
     def to_c(self) -> FmxMoEWeights:
         w = FmxMoEWeights()
@@ -214,7 +215,23 @@ class MoEWeights:
             w.shared_up = self.shared_up.to_c()
             w.shared_down = self.shared_down.to_c()
             w.shared_expert_gate_w = self.shared_expert_gate_w.data_ptr()
+        w.packed = self.packed.data_ptr() if self.packed is not None else None
         return w
+
+    def pack(self, cfg: "MoEConfig") -> None:
+        """fmx_pack_expert_weights: adds the load-time re-layout that forwards
+        of at most 16 tokens read (the MLX-layout arrays stay in use)."""
+        lib = _lib.load()
+        c = cfg.to_c()
+        nbytes = lib.fmx_moe_packed_size(C.byref(c))
+        if nbytes == 0:
+            raise _lib.FmxError(_lib.FMX_ERR_UNSUPPORTED, "config cannot be packed")
+        self.packed = None
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=self.router_w.device)
+        w = self.to_c()
+        _lib.check(lib.fmx_pack_expert_weights(C.byref(c), C.byref(w), buf.data_ptr(), nbytes,
+                                               _stream()))
+        self.packed = buf
 
 
 class MoEBlock:
@@ -225,10 +242,12 @@ class MoEBlock:
     """
 
     def __init__(self, cfg: MoEConfig, weights: MoEWeights, max_tokens: int = 1024,
-                 device: Optional[torch.device] = None):
+                 device: Optional[torch.device] = None, pack: bool = True):
         self.lib = _lib.load()
         self.cfg = cfg
         self.weights = weights
+        if pack and weights.packed is None and self.lib.fmx_moe_packed_size(C.byref(cfg.to_c())):
+            weights.pack(cfg)
         self._c_cfg = cfg.to_c()
         self._c_w = weights.to_c()
         self.max_tokens = max_tokens

@@ -116,9 +116,11 @@ def host_inputs(wl: Workload, tokens: Optional[int] = None) -> HostInputs:
 
 # ------------------------------------------------------------------ device side
 
-def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None, device="cuda"):
-    """Uploads the inputs, quantizes the weights on the GPU (fmx_quantize) and
-    returns (MoEBlock, x_device, quantized weights dict)."""
+def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None, device="cuda",
+                 pack: bool = True):
+    """Uploads the inputs, quantizes the weights on the GPU (fmx_quantize),
+    packs them (fmx_pack_expert_weights) unless pack=False, and returns
+    (MoEBlock, x_device)."""
     import torch
 
     from .moe import MoEBlock, MoEConfig, MoEWeights, QWeight, quantize
@@ -144,7 +146,7 @@ def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None,
     if m["shared_inter"]:
         w.shared_gate, w.shared_up, w.shared_down = q(hi.shared_gate), q(hi.shared_up), q(hi.shared_down)
         w.shared_expert_gate_w = up(hi.shared_expert_gate_w)
-    block = MoEBlock(cfg, w, max_tokens=max_tokens or hi.x.shape[0])
+    block = MoEBlock(cfg, w, max_tokens=max_tokens or hi.x.shape[0], pack=pack)
     return block, up(hi.x)
 
 

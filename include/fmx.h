@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMX_ABI_VERSION 1
+#define FMX_ABI_VERSION 2
 
 typedef enum fmx_status {
   FMX_OK = 0,
@@ -178,7 +178,22 @@ typedef struct fmx_moe_weights {
   fmx_qweight shared_up;         /* [Is, H/8] ...                                  */
   fmx_qweight shared_down;       /* [H, Is/8] ...                                  */
   const void* shared_expert_gate_w; /* bf16 [1, H]                                 */
+  const void* packed;            /* NULL, or the same expert weights re-laid out by
+                                    fmx_pack_expert_weights; forwards of at most 16
+                                    tokens then read them from here. No
+                                    counterpart in the reference.                 */
 } fmx_moe_weights;
+
+/* Load-time re-layout of a layer's expert weights (replaces the stacking
+ * step of model.cpp:368-470 as the last load-time transform; the MLX-layout
+ * arrays stay valid and are still read by forwards of more than 16 tokens).
+ * Packs gate+up of every routed expert as interleaved pairs, down per
+ * expert, and the shared expert the same way, into `packed` (device memory
+ * of fmx_moe_packed_size(cfg) bytes, 256-byte aligned). Returns 0 bytes /
+ * FMX_ERR_UNSUPPORTED when H, I or Is is not a multiple of 128. */
+size_t fmx_moe_packed_size(const fmx_moe_config* cfg);
+int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* src, void* packed,
+                            size_t packed_bytes, fmx_stream stream);
 
 /* Bytes of workspace one forward of up to max_tokens tokens needs
  * (max_tokens <= 65536). */
