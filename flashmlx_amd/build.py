@@ -20,7 +20,8 @@ OBJDIR = HERE / "_build"
 SOURCES = [
     "csrc/fmx_route.hip",
     "csrc/fmx_qgemm.hip",
-    "csrc/fmx_qgemv.hip",
+    "csrc/fmx_pack.hip",
+    "csrc/fmx_decode.hip",
     "csrc/fmx_elem.hip",
     "csrc/fmx_api.cpp",
     "csrc/fmx_synth.cpp",

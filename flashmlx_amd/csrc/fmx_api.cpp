@@ -122,7 +122,7 @@ int bind_workspace(Arena& ar, void* ws, size_t ws_bytes, size_t need, hipStream_
 
 constexpr int64_t kMoEMaxTokens = 65536;
 // K slices of the shared expert's down projection (K = Is is long, N = H short)
-constexpr int kSharedDownSplit = 4;
+constexpr int kSharedDownSplit = kDecSdSplit;
 constexpr size_t kCounterBytes = (kMoEMaxTokens / kRouterTok + 64) * sizeof(uint32_t);
 
 struct MoELayout {
@@ -131,7 +131,8 @@ struct MoELayout {
   uint16_t* probs;
   uint32_t* inds;
   uint16_t* scores;
-  uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base, *recs;
+  uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base, *seg;
+  uint8_t* slots;
   float* sgate;
   uint16_t *xp, *h, *hs, *d;
   float* sd_part;
@@ -159,7 +160,8 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.seg_exp = static_cast<uint32_t*>(ar.take(E * 4));
   L.seg_off = static_cast<uint32_t*>(ar.take((E + 1) * 4));
   L.sort_base = static_cast<uint32_t*>(ar.take(E * ((n + 63) / 64) * 4));
-  L.recs = static_cast<uint32_t*>(ar.take(E * kSegRecWords * 4));
+  L.seg = static_cast<uint32_t*>(ar.take((E + 1) * 4));
+  L.slots = static_cast<uint8_t*>(ar.take(E * 16));
   L.sgate = static_cast<float*>(ar.take(T * 4));
   L.xp = static_cast<uint16_t*>(ar.take(T * H * 2));
   L.h = static_cast<uint16_t*>(ar.take(n * I * 2));
@@ -261,7 +263,6 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.seg_exp = L.seg_exp;
   a.sort.seg_off = L.seg_off;
   a.sort.base = L.sort_base;
-  a.sort.recs = L.recs;
   if (sorted_in_router) *sorted_in_router = a.fuse_sort != 0;
   FMX_HIP(launch_router(a, stream));
   return FMX_OK;
@@ -777,6 +778,56 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
   const MoELayout L = moe_layout(c, T, ar.base);
 
+  // decode batches (T <= 16) on packed weights: three kernels, combine included
+  if (w->packed && packable(c) && aligned(w->packed, 256)) {
+    const PackedLayout PL = packed_layout(c);
+    const uint8_t* pk = static_cast<const uint8_t*>(w->packed);
+    DecodeArgs da{};
+    da.T = static_cast<int>(T);
+    da.H = static_cast<int>(H);
+    da.E = static_cast<int>(E);
+    da.k = static_cast<int>(k);
+    da.I = static_cast<int>(I);
+    da.Is = static_cast<int>(Is);
+    da.norm = c.norm_topk_prob ? 1 : 0;
+    da.x = static_cast<const uint16_t*>(x);
+    da.wr = static_cast<const uint16_t*>(w->router_w);
+    da.lbias = static_cast<const uint16_t*>(w->router_logit_bias);
+    da.wsg = has_sh ? static_cast<const uint16_t*>(w->shared_expert_gate_w) : nullptr;
+    da.gu = pk + PL.gu;
+    da.gu_es = PL.gu_es;
+    da.dn = pk + PL.dn;
+    da.dn_es = PL.dn_es;
+    da.sgu = pk + PL.sgu;
+    da.sdn = pk + PL.sdn;
+    da.logits = L.logits;
+    da.hs = L.hs;
+    da.h = L.h;
+    da.d = L.d;
+    da.sd_part = L.sd_part;
+    da.inds = L.inds;
+    da.scores = L.scores;
+    da.probs = L.probs;
+    da.sgate = has_sh ? L.sgate : nullptr;
+    da.sort = SortOut{L.order, L.inv, L.src, L.idx, L.offsets, nullptr, nullptr, nullptr, L.sort_base};
+    da.seg = L.seg;
+    da.slots = L.slots;
+    da.counter = L.counters;
+    da.y = static_cast<uint16_t*>(y);
+    if (decode_plan(da)) {
+      FMX_HIP(mark(0));
+      FMX_HIP(launch_decode_k1(da, stream));
+      FMX_HIP(mark(1));
+      FMX_HIP(launch_decode_k2(da, stream));
+      FMX_HIP(mark(2));
+      FMX_HIP(launch_decode_k3(da, stream));
+      FMX_HIP(mark(3));
+      FMX_HIP(launch_decode_k4(da, stream));
+      FMX_HIP(mark(4));
+      return ok();
+    }
+  }
+
   // 1. router + top-k (+ sort when it fits in the router's last workgroup)
   FMX_HIP(mark(0));
   bool sorted = false;
@@ -785,104 +836,12 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
                        has_sh ? L.sgate : nullptr, L.xp, true, &sorted, stream)))
     return rc;
   if (!sorted) {
-    SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base,
-               L.recs};
+    SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off, L.sort_base};
     FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
   }
   FMX_HIP(mark(1));
 
-  // decode shapes (at most 16 tokens, so at most 16 rows per expert) on packed weights
-  int gu_ks = 0, dn_upw = 0, dn_ks = 0, sd_split = kSharedDownSplit;
-  if (w->packed && T <= 16 && packable(c) && aligned(w->packed, 256)) {
-    const int64_t nu_h = H / 128, nu_i = I / 128, nu_s = Is / 128;
-    if (nu_h <= 64) gu_ks = static_cast<int>((nu_h + 7) / 8);
-    for (int upw : {4, 8}) {
-      for (int ks = 1; ks <= 8 && !dn_ks; ++ks) {
-        const int64_t span = static_cast<int64_t>(upw) * ks;
-        if (span < nu_i) continue;
-        const int64_t split = has_sh ? (nu_s + span - 1) / span : 1;
-        if (split > kSharedDownSplit) continue;
-        dn_upw = upw;
-        dn_ks = ks;
-        if (has_sh) sd_split = static_cast<int>(split);
-      }
-      if (dn_ks) break;
-    }
-  }
-  if (gu_ks && dn_ks) {
-    const PackedLayout PL = packed_layout(c);
-    const uint8_t* pk = static_cast<const uint8_t*>(w->packed);
-    // 2. gate/up + SwiGLU
-    GemvProblem g{};
-    g.wpk = pk + PL.gu;
-    g.estride = PL.gu_es;
-    g.nt = static_cast<int>(I / 16);
-    g.nu = static_cast<int>(H / 128);
-    g.n_exp = static_cast<int>(E);
-    g.recs = L.recs;
-    g.seg_n = L.seg_n;
-    g.max_seg = static_cast<int>(std::min(E, n));
-    g.gather = 1;
-    g.max_rows = static_cast<int>(T);  // a token picks an expert at most once
-    g.x = L.xp;
-    g.ldx = H;
-    g.x_rows = static_cast<int>(T);
-    g.out = L.h;
-    g.ldo = I;
-    g.out_p8 = 1;
-    g.out_rows = static_cast<int>(n);
-    GemvProblem sg{};
-    if (has_sh) {
-      sg.wpk = pk + PL.sgu;
-      sg.nt = static_cast<int>(Is / 16);
-      sg.nu = static_cast<int>(H / 128);
-      sg.n_exp = 1;
-      sg.max_seg = 1;
-      sg.rows_static = sg.max_rows = static_cast<int>(T);
-      sg.x = L.xp;
-      sg.ldx = H;
-      sg.x_rows = static_cast<int>(T);
-      sg.out = L.hs;
-      sg.ldo = Is;
-      sg.out_p8 = 1;
-      sg.out_rows = static_cast<int>(T);
-    }
-    FMX_HIP(launch_qgemv(g, has_sh ? &sg : nullptr, 1, 8, gu_ks, stream));
-    FMX_HIP(mark(2));
-    // 3. down: routed rows (sorted order) and the shared expert (fp32 K slices)
-    GemvProblem d{};
-    d.wpk = pk + PL.dn;
-    d.estride = PL.dn_es;
-    d.nt = static_cast<int>(H / 16);
-    d.nu = static_cast<int>(I / 128);
-    d.n_exp = static_cast<int>(E);
-    d.recs = L.recs;
-    d.seg_n = L.seg_n;
-    d.max_seg = g.max_seg;
-    d.max_rows = static_cast<int>(T);
-    d.x = L.h;
-    d.ldx = I;
-    d.x_rows = static_cast<int>(n);
-    d.out = L.d;
-    d.ldo = H;
-    d.out_rows = static_cast<int>(n);
-    GemvProblem sd{};
-    if (has_sh) {
-      sd.wpk = pk + PL.sdn;
-      sd.nt = static_cast<int>(H / 16);
-      sd.nu = static_cast<int>(Is / 128);
-      sd.n_exp = 1;
-      sd.max_seg = 1;
-      sd.rows_static = sd.max_rows = static_cast<int>(T);
-      sd.x = L.hs;
-      sd.ldx = Is;
-      sd.x_rows = static_cast<int>(T);
-      sd.out_rows = static_cast<int>(T);
-      sd.part = L.sd_part;
-    }
-    FMX_HIP(launch_qgemv(d, has_sh ? &sd : nullptr, 0, dn_upw, dn_ks, stream));
-    FMX_HIP(mark(3));
-  } else {
+  {
   // 2. gate/up + SwiGLU: routed experts over the sorted rows, and the shared expert
   QGemmProblem gu{};
   gu.x = L.xp;
@@ -984,7 +943,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   cb.scores = L.scores;
   cb.sd = nullptr;
   cb.sd_part = has_sh ? L.sd_part : nullptr;
-  cb.sd_ksplit = sd_split;
+  cb.sd_ksplit = kSharedDownSplit;
   cb.sgate = has_sh ? L.sgate : nullptr;
   cb.y = static_cast<uint16_t*>(y);
   cb.T = static_cast<int>(T);

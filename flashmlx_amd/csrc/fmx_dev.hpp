@@ -1,0 +1,323 @@
+// fmx_dev.hpp -- device helpers shared by the router, sort and GEMM kernels
+// (library-internal).
+#pragma once
+
+#include "fmx_kernels.hpp"
+
+extern "C" __device__ __attribute__((const)) double __ockl_wfred_max_f64(double);
+
+namespace fmx {
+
+// ------------------------------------------------------------------ lanes, scans
+
+__device__ inline uint64_t lanes_below(int lane) {
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Exclusive scan of one value per thread over a workgroup of NT threads.
+template <int NT>
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
+  constexpr int NW = NT / kWave;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const uint32_t y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (lane == kWave - 1) s_tmp[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t t = s_tmp[w];
+      s_tmp[w] = run;
+      run += t;
+    }
+    s_tmp[NW] = run;
+  }
+  __syncthreads();
+  const uint32_t r = s_tmp[wave] + x - v;
+  if (total) *total = s_tmp[NW];
+  __syncthreads();
+  return r;
+}
+
+// Stable counting sort of n keys by value, by one workgroup of NT threads
+// (every thread calls). Entries are cut into tiles of 64 (one per lane of a
+// wave). Within a tile, the lanes holding an equal key are found with one
+// ballot per key bit; a lane's rank among them is the popcount of the equal
+// lanes below it. The per-(key, tile) counts, scanned in key-major order,
+// give every (key, tile) its first output position, so
+// position = base[key][tile] + rank. Keys >= E are treated as E - 1.
+// `keys` may point to LDS or global memory.
+// s_cnt: E * ceil(n/64) bytes of LDS; s_rank: n bytes; s_tmp: NT/64 + 1 words.
+template <int NT>
+__device__ void sort_block(const uint32_t* keys, int n, int k, int E, const SortOut& o,
+                           uint8_t* s_cnt, uint8_t* s_rank, uint32_t* s_tmp) {
+  constexpr int NW = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_tiles = (n + 63) / 64;
+  const int total = E * n_tiles;
+  const int nbits = E <= 1 ? 1 : 32 - __builtin_clz(static_cast<uint32_t>(E - 1));
+
+  for (int i = tid; i < total; i += NT) s_cnt[i] = 0;
+  __syncthreads();
+
+  for (int tile = wave; tile < n_tiles; tile += NW) {
+    const int i = tile * 64 + lane;
+    const bool valid = i < n;
+    uint32_t key = valid ? keys[i] : 0u;
+    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
+    uint64_t eq = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      eq &= bit ? m : ~m;
+    }
+    if (valid) {
+      const int rank = __popcll(eq & lanes_below(lane));
+      s_rank[i] = static_cast<uint8_t>(rank);
+      if (rank == 0) s_cnt[key * n_tiles + tile] = static_cast<uint8_t>(__popcll(eq));
+    }
+  }
+  __syncthreads();
+
+  // key-major exclusive scan of the count table
+  const int per = (total + NT - 1) / NT;
+  const int beg = tid * per;
+  const int end = min(beg + per, total);
+  uint32_t local = 0;
+  for (int j = beg; j < end; ++j) local += s_cnt[j];
+  uint32_t run = block_exclusive_scan<NT>(local, s_tmp, nullptr);
+  for (int j = beg; j < end; ++j) {
+    o.base[j] = run;
+    if (j % n_tiles == 0) o.offsets[j / n_tiles] = run;
+    run += s_cnt[j];
+  }
+  if (tid == 0) o.offsets[E] = static_cast<uint32_t>(n);
+  __syncthreads();
+
+  for (int i = tid; i < n; i += NT) {
+    uint32_t key = keys[i];
+    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
+    const uint32_t pos = o.base[key * n_tiles + i / 64] + s_rank[i];
+    if (o.order) o.order[pos] = static_cast<uint32_t>(i);
+    if (o.inv) o.inv[i] = pos;
+    if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
+    if (o.idx) o.idx[pos] = key;
+  }
+
+  // segment table of the non-empty keys, ascending
+  if (o.seg_off) {
+    const int eper = (E + NT - 1) / NT;
+    const int eb = tid * eper, ee = min(eb + eper, E);
+    uint32_t cnt = 0;
+    for (int e = eb; e < ee; ++e) cnt += (o.offsets[e + 1] > o.offsets[e]) ? 1u : 0u;
+    uint32_t U = 0;
+    uint32_t u = block_exclusive_scan<NT>(cnt, s_tmp, &U);
+    for (int e = eb; e < ee; ++e) {
+      if (o.offsets[e + 1] > o.offsets[e]) {
+        if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
+        o.seg_off[u] = o.offsets[e];
+        ++u;
+      }
+    }
+    if (tid == 0) {
+      o.seg_off[U] = static_cast<uint32_t>(n);
+      if (o.seg_n) *o.seg_n = U;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ exact dot products
+
+// Butterfly reduce-scatter of N = 2^P doubles over the 64 lanes of a wave:
+// afterwards lane l holds the wave-wide total of value index l >> (6 - P).
+// The router's partial sums are exact, so the association order is free.
+template <int N>
+__device__ inline double reduce_scatter64(double (&v)[N], int lane) {
+  constexpr int P = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
+  static_assert((1 << P) == N && P <= 6, "N must be a power of two <= 64");
+#pragma unroll
+  for (int s = 0; s < P; ++s) {
+    const int w = 32 >> s;
+    const bool up = (lane & w) != 0;
+    const int half = N >> (s + 1);
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      if (i < half) {
+        // bitwise select of two loaded values: a lane-dependent array index
+        // would move v[] to scratch memory
+        const uint64_t lo = __double_as_longlong(v[i]);
+        const uint64_t hi = __double_as_longlong(v[i + half]);
+        const uint64_t m = up ? ~0ull : 0ull;
+        const double send = __longlong_as_double((lo & m) | (hi & ~m));
+        const double keep = __longlong_as_double((hi & m) | (lo & ~m));
+        v[i] = keep + __shfl_xor(send, w);
+      }
+    }
+  }
+  double r = v[0];
+#pragma unroll
+  for (int w = 32 >> P; w >= 1; w >>= 1) r += __shfl_xor(r, w);
+  return r;
+}
+
+// ------------------------------------------------------------------ LDS staging
+
+// One row of K bf16 (K a multiple of 8) -> LDS by LDS DMA: each
+// global_load_lds_dwordx4 moves a wave's 64 x 16 bytes (a 1 KB piece of the
+// row) straight into LDS, with no registers and no wait at the issuing point;
+// in a last, partial piece the lanes past the row's end do not take part.
+// Called by one whole wave (dst must be wave-uniform).
+__device__ inline void dma_row(const uint16_t* src, int K, uint16_t* s_dst, int lane) {
+  for (int pc = 0; pc * 512 < K; ++pc) {
+    if (pc * 512 + 8 * lane < K)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + pc * 512 + 8 * lane),
+                                       (__attribute__((address_space(3))) void*)(s_dst + pc * 512),
+                                       16, 0, 0);
+  }
+}
+
+// Rows [T][K] of bf16 (row stride ld elements) -> LDS rows of stride xs
+// elements: waves wave, wave + nw, ... take the rows in turn (wave must be
+// wave-uniform). The caller waits (wait_vmcnt0) and barriers before any wave
+// reads the rows.
+__device__ inline void dma_rows(const uint16_t* src, int64_t ld, int T, int K, uint16_t* s_dst, int xs,
+                                int wave, int nw, int lane) {
+  for (int t = wave; t < T; t += nw) dma_row(src + t * ld, K, s_dst + t * xs, lane);
+}
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt[3:0] |
+// expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]). Vector memory loads
+// complete in issue order, so vmcnt(N) right after N loads means that every
+// older load, e.g. an LDS DMA issued before them, has landed.
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ inline void wait_vmcnt0() { wait_vmcnt<0>(); }
+
+// Workgroup barrier for LDS written by LDS DMA that every wave has already
+// waited for (wait_vmcnt): s_barrier alone, with compiler-level memory
+// barriers around it, so that no fence adds a wait for the loads still in
+// flight (the fences of __syncthreads drain vmcnt to 0).
+__device__ inline void lds_dma_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ------------------------------------------------------------------ packed 4-bit tiles
+//
+// Packed layout (fmx_pack_expert_weights). A matrix [N, K] is cut into tiles
+// of 16 rows and units of 128 k (two quantisation groups). Block (tile, unit)
+// holds, for lane l = 16*j + c of a wave, the 16 bytes of row 16*tile + c
+// that the lane feeds to four v_mfma_f32_16x16x32_bf16 as its B operand:
+// words 4a + j (a = 0..3) of the unit, i.e. k = 32a + 8j .. 32a + 8j + 7.
+// MFMAs a = 0, 1 then cover group 0 of the unit and a = 2, 3 group 1, so
+// every group's partial sum is formed without masking. Within each word the
+// nibbles are re-ordered (element 2i at position i, element 2i + 1 at
+// position i + 4) so that nib8 below yields the elements in natural order and
+// activation rows are used exactly as stored. After the 1024 weight
+// bytes come 16 x 8 bytes of (scale g0 | scale g1 << 16, bias g0 | bias g1 <<
+// 16) per row. A SwiGLU pair stores gate and up blocks side by side:
+// [gate w | up w | gate sb | up sb], 2304 bytes. The blocks of a tile are
+// consecutive (unit-major within the tile), tiles follow each other, and
+// experts follow each other.
+//
+// Exact dequantisation: nibbles become the bf16 values 128 + q (exact); per
+// group the products P = x.(128+q) and X = x.1 (an all-ones operand) are
+// formed in fp32 by the MFMA, and acc += s * P + (b - 128 s) * X is the
+// fp32 value of x.(s*q + b): weights are never rounded to bf16.
+
+constexpr int kBlockSingle = 1152;
+constexpr int kBlockPair = 2304;
+
+__device__ inline f32x4_t mfma_bf16(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8 nibbles -> bf16 pairs (128 + p_i, 128 + p_{i+4}), i = 0..3, where p_i is
+// the nibble at position i (for a packed word: elements 2i and 2i + 1)
+__device__ inline bf16x8_t nib8(uint32_t w) {
+  u32x4_t d;
+  d[0] = (w & 0x000f000fu) | 0x43004300u;
+  d[1] = ((w >> 4) & 0x000f000fu) | 0x43004300u;
+  d[2] = ((w >> 8) & 0x000f000fu) | 0x43004300u;
+  d[3] = ((w >> 12) & 0x000f000fu) | 0x43004300u;
+  return __builtin_bit_cast(bf16x8_t, d);
+}
+
+template <bool DUAL>
+struct PkUnit {
+  u32x4_t w0, w1;    // packed words (gate / up)
+  u32x2_t sb0, sb1;  // (s g0 | s g1 << 16, b g0 | b g1 << 16)
+};
+
+// vector memory instructions one pk_load issues
+template <bool DUAL>
+constexpr int pk_load_insts() { return DUAL ? 4 : 2; }
+
+template <bool DUAL>
+__device__ inline PkUnit<DUAL> pk_load(const uint8_t* blk, int lane) {
+  PkUnit<DUAL> L;
+  const int col = lane & 15;
+  L.w0 = *reinterpret_cast<const u32x4_t*>(blk + 16 * lane);
+  if (DUAL) {
+    L.w1 = *reinterpret_cast<const u32x4_t*>(blk + 1024 + 16 * lane);
+    L.sb0 = *reinterpret_cast<const u32x2_t*>(blk + 2048 + 8 * col);
+    L.sb1 = *reinterpret_cast<const u32x2_t*>(blk + 2048 + 128 + 8 * col);
+  } else {
+    L.sb0 = *reinterpret_cast<const u32x2_t*>(blk + 1024 + 8 * col);
+  }
+  return L;
+}
+
+// acc[i] += s0 P0 + (b0 - 128 s0) X0 + s1 P1 + (b1 - 128 s1) X1
+__device__ inline void pk_epi(f32x4_t& acc, const u32x2_t& sb, const f32x4_t& P0, const f32x4_t& P1,
+                              const f32x4_t& X0, const f32x4_t& X1) {
+  const float s0 = __uint_as_float(sb[0] << 16), s1 = __uint_as_float(sb[0] & 0xffff0000u);
+  const float c0 = __builtin_fmaf(-128.0f, s0, __uint_as_float(sb[1] << 16));
+  const float c1 = __builtin_fmaf(-128.0f, s1, __uint_as_float(sb[1] & 0xffff0000u));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[i] = __builtin_fmaf(s0, P0[i], acc[i]);
+    acc[i] = __builtin_fmaf(c0, X0[i], acc[i]);
+    acc[i] = __builtin_fmaf(s1, P1[i], acc[i]);
+    acc[i] = __builtin_fmaf(c1, X1[i], acc[i]);
+  }
+}
+
+// One unit: A[a] (a = 0..3) are the lane's activation operands for k =
+// 32a + 8j .. +7 (P8 order); accumulates into acc0 (and acc1 for a pair).
+template <bool DUAL>
+__device__ inline void pk_unit(const PkUnit<DUAL>& L, const bf16x8_t (&A)[4], f32x4_t& acc0,
+                               f32x4_t& acc1) {
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+  const f32x4_t X0 = mfma_bf16(A[1], ones, mfma_bf16(A[0], ones, zero));
+  const f32x4_t X1 = mfma_bf16(A[3], ones, mfma_bf16(A[2], ones, zero));
+  {
+    const f32x4_t P0 = mfma_bf16(A[1], nib8(L.w0[1]), mfma_bf16(A[0], nib8(L.w0[0]), zero));
+    const f32x4_t P1 = mfma_bf16(A[3], nib8(L.w0[3]), mfma_bf16(A[2], nib8(L.w0[2]), zero));
+    pk_epi(acc0, L.sb0, P0, P1, X0, X1);
+  }
+  if (DUAL) {
+    const f32x4_t P0 = mfma_bf16(A[1], nib8(L.w1[1]), mfma_bf16(A[0], nib8(L.w1[0]), zero));
+    const f32x4_t P1 = mfma_bf16(A[3], nib8(L.w1[3]), mfma_bf16(A[2], nib8(L.w1[2]), zero));
+    pk_epi(acc1, L.sb1, P0, P1, X0, X1);
+  }
+}
+
+// The four A operands of one unit from an LDS row (P8 layout): xu points at
+// the unit's first element of the lane's row, plus 8*j.
+__device__ inline void lds_a(const uint16_t* xu, bf16x8_t (&A)[4]) {
+#pragma unroll
+  for (int a = 0; a < 4; ++a) A[a] = *reinterpret_cast<const bf16x8_t*>(xu + 32 * a);
+}
+
+}  // namespace fmx

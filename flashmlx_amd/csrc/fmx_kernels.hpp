@@ -19,11 +19,7 @@ struct SortOut {
   uint32_t* seg_exp;  // [E]   u -> key of the u-th non-empty key (nullable)
   uint32_t* seg_off;  // [E+1] u -> first sorted position         (nullable)
   uint32_t* base;     // [E * ceil(n/64)] scratch
-  // [E][kSegRecWords] per non-empty key u: {entry/k of the first min(count,
-  // 16) positions (last repeated), key, first position, count, 0} (nullable)
-  uint32_t* recs;
 };
-constexpr int kSegRecWords = 32;
 
 // Sort in one workgroup of 1024 threads (separate launch).
 constexpr int kSortThreads = 1024;
@@ -103,36 +99,57 @@ struct QGemmProblem {
 // Launch one or two independent problems in one grid (p1 may be null).
 hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStream_t stream);
 
-// ---------------------------------------------------------------- packed decode GEMM
-// Segments of at most 16 rows over weights packed by launch_pack (layout in
-// fmx_qgemv.hip). out[r0 + i] = x[row(i)] . W[e]^T, or SwiGLU of a pair.
-constexpr int kGemvMaxThreads = 512;
+// ---------------------------------------------------------------- decode (T <= 16)
+// The MoE block for decode batches on packed weights (fmx_decode.hip):
+// K1 router + shared gate/up, K2 routed gate/up, K3 down projections,
+// K4 combine.
+constexpr int kDecMaxT = 16;            // tokens
+constexpr int kDecMaxK = 16;            // top-k
+constexpr int kDecMaxE = 256;           // experts
+constexpr int kDecThreads = 256;        // K1, K2 workgroups
+constexpr int kDecSdSplit = 4;         // K slices of the shared expert's down projection
+constexpr int kDecRouterLpBytes = kDecMaxT * 4 * 64 * 8;  // K1/K2 LDS ahead of the staged rows
+                                        // (router lane partials; pair reductions)
+constexpr int kDecRouterChunks = 2;     // 16-byte chunks per lane of half a router row (H <= 2048)
 constexpr int kPackedBlockSingle = 1152;  // bytes of one (16-row tile, 128-k unit) block
 constexpr int kPackedBlockPair = 2304;    // gate + up
-struct GemvProblem {
-  const uint8_t* wpk;       // packed weights of expert 0
-  int64_t estride;          // bytes per expert
-  int nt, nu;               // 16-row tiles (N/16), 128-k units (K/128)
-  int n_exp;                // experts (record keys clamp to n_exp-1)
-  const uint32_t* recs;     // segment records (SortOut::recs); null: one static segment
-  const uint32_t* seg_n;    // number of records (device)
-  int max_seg;              // segments the grid covers
-  int rows_static;          // rows of the static segment (<= 16)
-  int max_rows;             // most rows a segment holds (<= 16; sizes LDS, clamps records)
-  int gather;               // x row of segment row i = record entry i (else first + i)
-  const uint16_t* x;        // activation rows, P8 layout
-  int64_t ldx;
-  int x_rows;               // x row indices clamp to x_rows-1
-  uint16_t* out;            // bf16 rows (row = first position + i)
-  int64_t ldo;
-  int out_p8;               // write rows in P8 layout
-  int out_rows;             // rows of out
-  float* part;              // non-null: fp32 partial sums [ks_wg][out_rows][N] instead of out
-  int ks_wg;                // K slices over workgroups (set by launch_qgemv)
+
+struct DecodeArgs {
+  int T, H, E, k, I, Is, norm;
+  const uint16_t* x;        // [T, H] bf16
+  const uint16_t* wr;       // [E, H] bf16 router
+  const uint16_t* lbias;    // [E] bf16 router logit bias or null
+  const uint16_t* wsg;      // [H] bf16 shared-expert gate row, null when Is == 0
+  const uint8_t* gu;        // packed gate/up pairs of the routed experts
+  int64_t gu_es;            //   bytes per expert
+  const uint8_t* dn;        // packed down projections of the routed experts
+  int64_t dn_es;
+  const uint8_t* sgu;       // packed shared gate/up pair
+  const uint8_t* sdn;       // packed shared down
+  uint16_t* logits;         // [T, E+1] bf16 (column E: shared gate logit)
+  uint16_t* hs;             // [T, Is] shared SwiGLU output
+  uint16_t* h;              // [T*k, I] routed SwiGLU output, entry order
+  uint16_t* d;              // [T*k, H] routed down projections, entry order
+  float* sd_part;           // [kDecSdSplit, T, H] shared down projection, fp32 K-slice sums
+  uint32_t* inds;           // [T, k]
+  uint16_t* scores;         // [T, k] bf16
+  uint16_t* probs;          // [T, E] bf16 or null
+  float* sgate;             // [T] bf16-valued sigmoid of the shared gate logit, or null
+  SortOut sort;             // order/inv/src/idx/offsets (+ base scratch)
+  uint32_t* seg;            // [1 + max_seg]: U, then the routed experts ascending
+  uint8_t* slots;           // [max_seg][16]: slot of token t for routed expert u, or 0xff
+  uint32_t* counter;        // router arrival counter: zero on entry, zero on exit
+  uint16_t* y;              // [T, H] bf16
+  // launch shape (decode_plan)
+  int n_rt, n_sgu;          // K1: router workgroups (one per column), shared gate/up pairs
+  int max_seg, gu_pairs;    // K2: expert slots x tile pairs
 };
-// dual: SwiGLU pair; upw: units per wave (4 or 8); ks: waves per workgroup.
-hipError_t launch_qgemv(const GemvProblem& p0, const GemvProblem* p1, int dual, int upw, int ks,
-                        hipStream_t stream);
+// Fills the launch shape; false when the shapes are outside the decode path.
+bool decode_plan(DecodeArgs& a);
+hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_k4(const DecodeArgs& a, hipStream_t stream);
 
 struct PackArgs {
   const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // MLX layout [n_exp][N][..]

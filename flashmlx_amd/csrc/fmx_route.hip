@@ -4,155 +4,9 @@
 // Reference: server/src/model.cpp:757-775 (router, softmax, argpartition
 // top-k, take_along_axis), :682-700 (switch_mlp's argsort-based sort), and
 // the renormalisation of docs/superpowers/plans/2026-04-01-moe-support-plan.md:319-322.
-#include "fmx_kernels.hpp"
+#include "fmx_dev.hpp"
 
 namespace fmx {
-
-// ------------------------------------------------------------------ helpers
-
-__device__ inline uint64_t lanes_below(int lane) {
-  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
-}
-
-template <int NT>
-__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
-  constexpr int NW = NT / kWave;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const uint32_t y = __shfl_up(x, d);
-    if (lane >= d) x += y;
-  }
-  if (lane == kWave - 1) s_tmp[wave] = x;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t run = 0;
-    for (int w = 0; w < NW; ++w) {
-      const uint32_t t = s_tmp[w];
-      s_tmp[w] = run;
-      run += t;
-    }
-    s_tmp[NW] = run;
-  }
-  __syncthreads();
-  const uint32_t r = s_tmp[wave] + x - v;
-  if (total) *total = s_tmp[NW];
-  __syncthreads();
-  return r;
-}
-
-// Stable counting sort of n keys by value, by one workgroup of NT threads.
-// Entries are cut into tiles of 64 (one per lane of a wave). Within a tile,
-// the lanes holding an equal key are found with one ballot per key bit; a
-// lane's rank among them is the popcount of the equal lanes below it. The
-// per-(key, tile) counts, scanned in key-major order, give every (key, tile)
-// its first output position, so position = base[key][tile] + rank.
-// s_cnt: E * n_tiles bytes of LDS; s_rank: n bytes; s_tmp: NT/64 + 1 words.
-template <int NT>
-__device__ void sort_block(const uint32_t* __restrict__ keys, int n, int k, int E,
-                           const SortOut& o, uint8_t* s_cnt, uint8_t* s_rank,
-                           uint32_t* s_tmp) {
-  constexpr int NW = NT / kWave;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n_tiles = (n + 63) / 64;
-  const int total = E * n_tiles;
-  const int nbits = E <= 1 ? 1 : 32 - __builtin_clz(static_cast<uint32_t>(E - 1));
-
-  for (int i = tid; i < total; i += NT) s_cnt[i] = 0;
-  __syncthreads();
-
-  for (int tile = wave; tile < n_tiles; tile += NW) {
-    const int i = tile * 64 + lane;
-    const bool valid = i < n;
-    uint32_t key = valid ? keys[i] : 0u;
-    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
-    uint64_t eq = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (key >> b) & 1u;
-      const uint64_t m = __ballot(bit);
-      eq &= bit ? m : ~m;
-    }
-    if (valid) {
-      const int rank = __popcll(eq & lanes_below(lane));
-      s_rank[i] = static_cast<uint8_t>(rank);
-      if (rank == 0) s_cnt[key * n_tiles + tile] = static_cast<uint8_t>(__popcll(eq));
-    }
-  }
-  __syncthreads();
-
-  // key-major exclusive scan of the count table
-  const int per = (total + NT - 1) / NT;
-  const int beg = tid * per;
-  const int end = min(beg + per, total);
-  uint32_t local = 0;
-  for (int j = beg; j < end; ++j) local += s_cnt[j];
-  uint32_t run = block_exclusive_scan<NT>(local, s_tmp, nullptr);
-  for (int j = beg; j < end; ++j) {
-    o.base[j] = run;
-    if (j % n_tiles == 0) o.offsets[j / n_tiles] = run;
-    run += s_cnt[j];
-  }
-  if (tid == 0) o.offsets[E] = static_cast<uint32_t>(n);
-  __syncthreads();
-
-  for (int i = tid; i < n; i += NT) {
-    uint32_t key = keys[i];
-    key = key < static_cast<uint32_t>(E) ? key : static_cast<uint32_t>(E - 1);
-    const uint32_t pos = o.base[key * n_tiles + i / 64] + s_rank[i];
-    if (o.order) o.order[pos] = static_cast<uint32_t>(i);
-    if (o.inv) o.inv[i] = pos;
-    if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
-    if (o.idx) o.idx[pos] = key;
-  }
-
-  // segment table of the non-empty keys, ascending
-  if (o.seg_off) {
-    const int eper = (E + NT - 1) / NT;
-    const int eb = tid * eper, ee = min(eb + eper, E);
-    uint32_t cnt = 0;
-    for (int e = eb; e < ee; ++e) cnt += (o.offsets[e + 1] > o.offsets[e]) ? 1u : 0u;
-    uint32_t U = 0;
-    uint32_t u = block_exclusive_scan<NT>(cnt, s_tmp, &U);
-    for (int e = eb; e < ee; ++e) {
-      if (o.offsets[e + 1] > o.offsets[e]) {
-        if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
-        o.seg_off[u] = o.offsets[e];
-        ++u;
-      }
-    }
-    if (tid == 0) {
-      o.seg_off[U] = static_cast<uint32_t>(n);
-      if (o.seg_n) *o.seg_n = U;
-    }
-  }
-}
-
-// Segment records for the decode GEMM (SortOut::recs): once the segment
-// table and src are complete, record u = {src of the first min(count, 16)
-// positions (the last one repeated), key, first position, count}.
-__device__ void write_seg_recs(const SortOut& o, int nthreads) {
-  if (!o.recs || !o.seg_n || !o.seg_exp || !o.seg_off || !o.src) return;
-  __syncthreads();
-  const uint32_t U = *o.seg_n;
-  constexpr int F = 4 + 16;
-  for (uint32_t i = threadIdx.x; i < U * F; i += nthreads) {
-    const uint32_t u = i / F, f = i - u * F;
-    const uint32_t r0 = o.seg_off[u], r1 = o.seg_off[u + 1];
-    uint32_t v;
-    if (f < 16)
-      v = o.src[min(r0 + f, r1 - 1)];
-    else if (f == 16)
-      v = o.seg_exp[u];
-    else if (f == 17)
-      v = r0;
-    else if (f == 18)
-      v = r1 - r0;
-    else
-      v = 0u;
-    o.recs[u * kSegRecWords + f] = v;
-  }
-}
 
 bool sort_fits(int64_t n, int64_t E) {
   const int64_t tiles = (n + 63) / 64;
@@ -165,7 +19,6 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
   __shared__ uint8_t s_rank[kSortMaxN];
   __shared__ uint32_t s_tmp[kSortThreads / kWave + 1];
   sort_block<kSortThreads>(keys, n, k, E, o, s_cnt, s_rank, s_tmp);
-  write_seg_recs(o, kSortThreads);
 }
 
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
@@ -181,7 +34,6 @@ bool router_sort_fits(int64_t n, int64_t E) {
   return n <= kRouterSortMaxN && E * tiles <= kRouterSortCnt && E * 4 <= kRouterSortCnt;
 }
 
-extern "C" __device__ __attribute__((const)) double __ockl_wfred_max_f64(double);
 
 // Release this workgroup's global writes and count it in; true in exactly
 // one workgroup: the last of `expected` to arrive, which then sees all of
@@ -201,38 +53,6 @@ __device__ inline bool arrive_last(uint32_t* counter, uint32_t expected, int* s_
 
 constexpr int kMaxExpertsPerLane = 16;  // E <= 1024
 constexpr int kRouterWaves = kRouterThreads / kWave;
-
-// Butterfly reduce-scatter of N = 2^P doubles over the 64 lanes of a wave:
-// afterwards lane l holds the wave-wide total of value index l >> (6 - P).
-// The router's partial sums are exact, so the association order is free.
-template <int N>
-__device__ inline double reduce_scatter64(double (&v)[N], int lane) {
-  constexpr int P = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
-  static_assert((1 << P) == N && P <= 6, "N must be a power of two <= 64");
-#pragma unroll
-  for (int s = 0; s < P; ++s) {
-    const int w = 32 >> s;
-    const bool up = (lane & w) != 0;
-    const int half = N >> (s + 1);
-#pragma unroll
-    for (int i = 0; i < N / 2; ++i) {
-      if (i < half) {
-        // bitwise select of two loaded values: a lane-dependent array index
-        // would move v[] to scratch memory
-        const uint64_t lo = __double_as_longlong(v[i]);
-        const uint64_t hi = __double_as_longlong(v[i + half]);
-        const uint64_t m = up ? ~0ull : 0ull;
-        const double send = __longlong_as_double((lo & m) | (hi & ~m));
-        const double keep = __longlong_as_double((hi & m) | (lo & ~m));
-        v[i] = keep + __shfl_xor(send, w);
-      }
-    }
-  }
-  double r = v[0];
-#pragma unroll
-  for (int w = 32 >> P; w >= 1; w >>= 1) r += __shfl_xor(r, w);
-  return r;
-}
 
 // Phase 1 of the router: each wave forms the logits of TT tokens x CE
 // consecutive columns. Lanes take interleaved 8-element chunks of H
@@ -497,7 +317,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     sort_small(a.inds, n, a.k, a.E, a.sort, reinterpret_cast<uint32_t*>(s_cnt), s_idx);
   else
     sort_block<kRouterThreads>(a.inds, n, a.k, a.E, a.sort, s_cnt, s_rank, s_tmp);
-  write_seg_recs(a.sort, kRouterThreads);
   if (tid == 0 && a.n_tt > 1) a.counters[a.n_tt] = 0u;
 }
 
