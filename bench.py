@@ -1,21 +1,29 @@
 #!/usr/bin/env python3
 """MoE-layer benchmark of libfmx on one MI355X.
 
-A step is one MoE-layer forward (router, sort, gate/up + SwiGLU, down,
-top-k combine, gated shared expert) over one batch of tokens already
-resident in HBM. Steps cycle over `--layers` copies of the layer's weights
-(distinct HBM addresses, 24 by default like a 24-layer model) so that the
-weights stream from HBM rather than the 256 MB last-level cache, and run as
-a captured HIP graph. Prints ONE JSON line.
+A step is one MoE-layer forward (router, top-k, gate/up + SwiGLU, down,
+top-k weighted combine, gated shared expert) over one batch of tokens
+already resident in HBM. Steps cycle over `--layers` copies of the layer's
+weights (distinct HBM addresses, 24 by default like a 24-layer model) so that
+the weights stream from HBM rather than the 256 MB last-level cache, and run
+as a captured HIP graph. Prints ONE JSON line.
 
-Default workload: Qwen1.5-MoE-A2.7B-shape MoE block, decode batch 8
-(seed 2). Other workloads: --workload (see flashmlx_amd/workloads.py).
+Default workload: Qwen1.5-MoE-A2.7B-shape MoE block, decode batch 8 (seed 2).
+Other workloads: --workload (flashmlx_amd/workloads.py).
+
+Per-stage timing: a second graph records a HIP event at every kernel-stage
+boundary of every layer (events on the stream the kernels run on); the
+dominant stage's average duration gives the roofline figure. The same
+command under `rocprofv3 --kernel-trace --stats` gives the per-kernel
+averages that the summaries under profiles/ quote.
+
+`--copy-calibration MIB` instead runs a plain device copy of MIB MiB five
+times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import platform
 import subprocess
@@ -25,6 +33,7 @@ import time
 METRIC = "MoE-layer tok/s; decode HBM GB/s and prefill MFMA % on 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
 
 
 def log(*a):
@@ -42,39 +51,23 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def stage_bytes_flops(m, wl, U):
-    """Algorithmic HBM bytes and FLOPs of each stage for one call."""
-    H, E, I, Is, k = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"], m["top_k"]
-    T = wl.tokens
-    pw = lambda n, kk: n * kk // 2 + 4 * n * (kk // 64)  # noqa: E731  packed weight bytes
-    gu_b = U * 2 * pw(I, H) + (2 * pw(Is, H) if Is else 0) + T * H * 2 + T * k * I * 2 + T * Is * 2
-    dn_b = U * pw(H, I) + (pw(H, Is) if Is else 0) + T * k * I * 2 + T * Is * 2 + T * k * H * 2 + T * H * 2
-    rt_b = E * H * 2 + T * H * 2 + (H * 2 if Is else 0)
-    cb_b = T * k * H * 2 + (T * H * 2 if Is else 0) + T * H * 2
-    gu_f = 2 * T * k * 2 * H * I + (2 * T * 2 * H * Is if Is else 0)
-    dn_f = 2 * T * k * H * I + (2 * T * H * Is if Is else 0)
-    rt_f = 2 * T * H * (E + (1 if Is else 0))
-    return {"router": (rt_b, rt_f), "gate_up": (gu_b, gu_f), "down": (dn_b, dn_f),
-            "combine": (cb_b, 0)}
-
-
-def load_traffic(workload: str, kernel_stage: str):
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 --pmc summary (profiles/traffic_<workload>.json), if present."""
-    p = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                     f"traffic_{workload}.json")
+def load_traffic(workload: str, stage: str):
+    """HBM bytes per launch of a stage's kernel from the committed rocprofv3
+    --pmc summary (profiles/traffic_<workload>.json), if there is one."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     try:
         with open(p) as f:
             d = json.load(f)
-        return d.get(kernel_stage)
+        return d.get("stages", {}).get(stage)
     except (OSError, ValueError):
         return None
 
 
 def cpu_baseline(wl, seconds: float):
     """The CPU oracle (C restatement of the reference's MLX CPU semantics,
-    fp32 accumulation) timed on this host on the same workload."""
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    fp32 accumulation) timed on this host on a bounded sample of the same
+    workload."""
+    sys.path.insert(0, ROOT)
     from flashmlx_amd import workloads as W
     from oracle import oracle as O
 
@@ -113,6 +106,19 @@ def cpu_baseline(wl, seconds: float):
     }
 
 
+def copy_calibration(mib: int) -> None:
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,9 +129,9 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=480, help="steps of the per-stage timing pass")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="no HIP graph")
     ap.add_argument("--no-pack", action="store_true",
                     help="MLX-layout weights only (no fmx_pack_expert_weights re-layout)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -134,8 +140,11 @@ def main():
                                    "run bench.py with --gpus 1",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, ROOT)
     import torch
 
     from flashmlx_amd import workloads as W
@@ -144,8 +153,7 @@ def main():
     wl = W.WORKLOADS[args.workload]
     m = wl.model
     T = wl.tokens
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+    torch.cuda.set_device(0)
 
     log(f"workload {wl.key}: generating inputs")
     hi = W.host_inputs(wl)
@@ -173,10 +181,8 @@ def main():
     blocks = [block0] + [clone_block(block0) for _ in range(R - 1)]
     y = torch.empty_like(x)
     torch.cuda.synchronize()
-    layer_bytes = sum(t.numel() * t.element_size() for q in (block0.weights.gate, block0.weights.up,
-                                                            block0.weights.down)
-                      for t in (q.w, q.scales, q.biases))
-    log(f"{R} layer copies, {R * layer_bytes / 2**30:.2f} GiB of expert weights")
+    per_layer = sum(t.numel() * t.element_size() for t in blocks[0].weight_tensors())
+    log(f"{R} layer copies, {R * per_layer / 2**30:.2f} GiB of weights")
 
     # reference output (eager) and routing statistics
     blocks[0].forward_into(x, y)
@@ -186,121 +192,111 @@ def main():
     offs = r["expert_offsets"].cpu().numpy().astype("int64")
     U = int((offs[1:] > offs[:-1]).sum())
 
-    def run_layers(n0, n):
-        for i in range(n0, n0 + n):
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+
+    def capture(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+        return g
+
+    with torch.cuda.stream(stream):
+        for b in blocks:  # warm every layer eagerly before capture
+            b.forward_into(x, y)
+    torch.cuda.synchronize()
+
+    def run_layers(n):
+        for i in range(n):
             blocks[i % R].forward_into(x, y)
 
     K, Wm = args.steps, args.warmup
-    graphs = {}
-    use_graph = not args.eager
-    if use_graph:
-        try:
-            s = torch.cuda.Stream()
-            s.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(s):
-                run_layers(0, R)  # warm the stream before capture
-            torch.cuda.current_stream().wait_stream(s)
-            torch.cuda.synchronize()
-
-            def capture(n):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    run_layers(0, n)
-                return g
-
-            graphs[R] = capture(R)
-            if K % R:
-                graphs[K % R] = capture(K % R)
-            # every replay must equal the eager result
-            for _ in range(3):
-                graphs[R].replay()
-                torch.cuda.synchronize()
-                if not torch.equal(y, y_ref):
-                    raise RuntimeError("graph replay output differs from eager output")
-                blocks[0].forward_into(x, y)
-                torch.cuda.synchronize()
-        except Exception as e:  # noqa: BLE001
-            log(f"graph capture unavailable ({e}); timing eager launches")
-            use_graph = False
-            graphs = {}
+    graphs = {R: capture(lambda: run_layers(R))}
+    if K % R:
+        graphs[K % R] = capture(lambda: run_layers(K % R))
+    # every replay must reproduce the eager result
+    for _ in range(3):
+        graphs[R].replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, y_ref):
+            raise RuntimeError("graph replay output differs from the eager output")
+        with torch.cuda.stream(stream):
+            blocks[0].forward_into(x, y)
+        torch.cuda.synchronize()
 
     def run_steps(n):
-        if use_graph:
+        with torch.cuda.stream(stream):
             for _ in range(n // R):
                 graphs[R].replay()
             if n % R:
-                g = graphs.get(n % R)
-                if g is None:
-                    run_layers(0, n % R)
-                else:
-                    g.replay()
-        else:
-            run_layers(0, n)
+                graphs[n % R].replay()
 
     run_steps(Wm)
     torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0.record()
+    ev0.record(stream)
     run_steps(K)
-    ev1.record()
+    ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_total = ev0.elapsed_time(ev1)
     ms_step = ms_total / K
     tok_s = T * K / (ms_total / 1e3)
 
-    # ---- per-stage timing pass (events between the kernels of each layer)
-    stages = ["router", "gate_up", "down", "combine"]
-    P = max(R, (args.profile_steps // R) * R)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(P)]
-    for e5 in evs:
-        for ev in e5:
-            ev.record()
-    torch.cuda.synchronize()
-    # queue GPU work ahead so the profiled launches never wait for the host
-    run_steps(K)
-    th0 = time.perf_counter()
-    for i in range(P):
-        blocks[i % R].forward_profiled(x, y, evs[i])
-    host_ms = (time.perf_counter() - th0) * 1e3
-    torch.cuda.synchronize()
-    dur = {s: 0.0 for s in stages}
-    for e5 in evs:
-        for j, s in enumerate(stages):
-            dur[s] += e5[j].elapsed_time(e5[j + 1]) / P
-    stage_us = {s: round(dur[s] * 1e3, 2) for s in stages}
+    # ---- per-stage timing: graphs of R layers that run only the first j
+    # kernel stages (j = 1..4); stage j's marginal time inside the layer is
+    # the difference of consecutive graphs' times (HIP events on the kernels'
+    # stream around each replay)
+    work = W.stage_work(m, T, U, wl.router_bias, packed=not args.no_pack)
+    stages = [s[0] for s in work]
+    reps = max(1, args.profile_steps // R)
+    cum = [0.0]
+    for j in range(1, 5):
+        gj = capture(lambda j=j: [blocks[i].forward_partial(x, y, j) for i in range(R)])
+        with torch.cuda.stream(stream):
+            gj.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for _ in range(reps):
+                gj.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        cum.append(e0.elapsed_time(e1) / (R * reps))
+        del gj
+    dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(4)]
+    stage_us = {s: round(dur[j] * 1e3, 2) for j, s in enumerate(stages)}
 
-    bf = stage_bytes_flops(m, wl, U)
-    dom = max(("gate_up", "down"), key=lambda s: dur[s])
-    prefill = T * m["top_k"] / m["n_experts"] >= 8
+    dom = max(range(4), key=lambda j: dur[j])
+    name, sbytes, sflops = work[dom]
+    prefill = not W.decode_path(m, T, packed=not args.no_pack)
     if prefill:
-        achieved = bf[dom][1] / (dur[dom] * 1e-3) / 1e12
+        achieved = sflops / (dur[dom] * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4)}
     else:
-        achieved = bf[dom][0] / (dur[dom] * 1e-3) / 1e9
+        achieved = sbytes / (dur[dom] * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4)}
-    roof["kernel"] = f"qgemm_kernel ({dom})"
-    roof["algorithmic_per_launch"] = bf[dom][1] if prefill else bf[dom][0]
+    roof["traffic"] = load_traffic(wl.key, name)
+    roof["stage"] = name
+    roof["algorithmic_per_launch"] = sflops if prefill else sbytes
     roof["avg_launch_us"] = round(dur[dom] * 1e3, 2)
-    roof["traffic"] = load_traffic(wl.key, dom)
 
-    layer_bytes_alg = W.algorithmic_bytes(m, T, U, wl.router_bias)
+    layer_bytes = W.algorithmic_bytes(m, T, U, wl.router_bias)
     layer_flops = W.flops(m, T)
     layer = {
         "unique_experts": U,
-        "algorithmic_bytes": layer_bytes_alg,
-        "hbm_gbps": round(layer_bytes_alg / (ms_step * 1e-3) / 1e9, 1),
-        "hbm_frac": round(layer_bytes_alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": layer_bytes,
+        "hbm_gbps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+        "hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "tflops": round(layer_flops / (ms_step * 1e-3) / 1e12, 2),
         "mfma_frac": round(layer_flops / (ms_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "kernel_path": "general" if prefill else "decode",
         "stage_us": stage_us,
-        # true when the host could not enqueue the profiled layers faster than
-        # the queued work drained (stage times may then include idle gaps)
-        "stage_timing_host_bound": bool(host_ms > ms_total + sum(dur.values()) * P),
+        "stage_bytes": {s: b for s, b, _ in work},
     }
 
     cpu = None
@@ -335,7 +331,7 @@ def main():
             "shared_intermediate": m["shared_inter"],
             "seed": wl.seed,
             "layer_copies": R,
-            "hip_graph": use_graph,
+            "hip_graph": True,
             "parallelism": "single GPU",
         },
         "roofline": roof,

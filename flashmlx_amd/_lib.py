@@ -105,6 +105,7 @@ _SIGS = {
     "fmx_moe_packed_size": (C.c_size_t, [P(FmxMoEConfig)]),
     "fmx_pack_expert_weights": (
         C.c_int, [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "fmx_moe_forward_path": (C.c_int, [P(FmxMoEConfig), C.c_int64, C.c_int]),
     "fmx_moe_workspace_size": (C.c_size_t, [P(FmxMoEConfig), C.c_int64]),
     "fmx_moe_workspace_init": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
     "fmx_moe_block_forward": (
@@ -116,6 +117,11 @@ _SIGS = {
         C.c_int,
         [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
          C.c_size_t, C.c_void_p, P(C.c_void_p)],
+    ),
+    "fmx_moe_block_forward_partial": (
+        C.c_int,
+        [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+         C.c_size_t, C.c_void_p, C.c_int],
     ),
     "fmx_moe_workspace_routing": (
         C.c_int,

@@ -734,17 +734,54 @@ int fmx_moe_workspace_routing(const fmx_moe_config* cfg, int64_t n_tokens, const
   return ok();
 }
 
+int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t T, int has_packed) {
+  int rc;
+  if ((rc = check_moe_config(cfg))) return -rc;
+  if (T < 0 || T > kMoEMaxTokens) return -fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  if (!has_packed || !packable(*cfg)) return 0;
+  DecodeArgs da{};
+  da.T = static_cast<int>(T);
+  da.H = static_cast<int>(cfg->hidden_size);
+  da.E = static_cast<int>(cfg->num_experts);
+  da.k = cfg->num_experts_per_tok;
+  da.I = static_cast<int>(cfg->moe_intermediate_size);
+  da.Is = static_cast<int>(cfg->shared_expert_intermediate_size);
+  return decode_plan(da) ? 1 : 0;
+}
+
+namespace {
+int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x, int64_t T,
+                void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_,
+                void* const* stage_events, int n_stages);
+}  // namespace
+
 int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x,
                           int64_t T, void* y, void* workspace, size_t workspace_bytes,
                           fmx_stream stream_) {
-  return fmx_moe_block_forward_profiled(cfg, w, x, T, y, workspace, workspace_bytes, stream_,
-                                        nullptr);
+  return moe_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr, 4);
 }
 
 int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weights* w,
                                    const void* x, int64_t T, void* y, void* workspace,
                                    size_t workspace_bytes, fmx_stream stream_,
                                    void* const* stage_events) {
+  return moe_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, stage_events, 4);
+}
+
+int fmx_moe_block_forward_partial(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                  const void* x, int64_t T, void* y, void* workspace,
+                                  size_t workspace_bytes, fmx_stream stream_, int n_stages) {
+  if (n_stages < 1 || n_stages > 4) return fail(FMX_ERR_ARG, "n_stages=%d (1..4)", n_stages);
+  return moe_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr, n_stages);
+}
+
+}  // extern "C"
+
+namespace {
+
+int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x, int64_t T,
+                void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_,
+                void* const* stage_events, int n_stages) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   auto mark = [&](int i) -> hipError_t {
     return stage_events ? hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream)
@@ -818,10 +855,13 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
       FMX_HIP(mark(0));
       FMX_HIP(launch_decode_k1(da, stream));
       FMX_HIP(mark(1));
+      if (n_stages < 2) return ok();
       FMX_HIP(launch_decode_k2(da, stream));
       FMX_HIP(mark(2));
+      if (n_stages < 3) return ok();
       FMX_HIP(launch_decode_k3(da, stream));
       FMX_HIP(mark(3));
+      if (n_stages < 4) return ok();
       FMX_HIP(launch_decode_k4(da, stream));
       FMX_HIP(mark(4));
       return ok();
@@ -840,6 +880,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
     FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
   }
   FMX_HIP(mark(1));
+  if (n_stages < 2) return ok();
 
   {
   // 2. gate/up + SwiGLU: routed experts over the sorted rows, and the shared expert
@@ -893,6 +934,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   }
   FMX_HIP(launch_qgemm(gu, has_sh ? &sgu : nullptr, stream));
   FMX_HIP(mark(2));
+  if (n_stages < 3) return ok();
 
   // 3. down: routed rows (sorted order) and the shared expert
   QGemmProblem dn{};
@@ -934,6 +976,7 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   }
   FMX_HIP(launch_qgemm(dn, has_sh ? &sdn : nullptr, stream));
   FMX_HIP(mark(3));
+  if (n_stages < 4) return ok();
   }
 
   // 4. top-k weighted combine + gated shared expert
@@ -953,6 +996,10 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
   FMX_HIP(mark(4));
   return ok();
 }
+
+}  // namespace
+
+extern "C" {
 
 int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, const void* router_w,
                         const void* lbias, uint32_t* inds, void* scores, void* probs,

@@ -259,6 +259,18 @@ class MoEBlock:
         _lib.check(self.lib.fmx_moe_workspace_init(self.workspace.data_ptr(), self.ws_bytes, _stream()))
         self._last_T = 0
 
+    def weight_tensors(self) -> list:
+        """Every device tensor of the layer's weights (MLX layout and packed)."""
+        w = self.weights
+        ts = [w.router_w]
+        for q in (w.gate, w.up, w.down, w.shared_gate, w.shared_up, w.shared_down):
+            if q is not None:
+                ts += [q.w, q.scales, q.biases]
+        for t in (w.shared_expert_gate_w, w.router_logit_bias, w.packed):
+            if t is not None:
+                ts.append(t)
+        return ts
+
     def forward_into(self, x: torch.Tensor, y: torch.Tensor) -> None:
         """y[T, H] = moe_block(x[T, H]) without allocating (graph-capturable)."""
         T = x.numel() // self.cfg.hidden_size
@@ -267,9 +279,19 @@ class MoEBlock:
             self.workspace.data_ptr(), self.ws_bytes, _stream()))
         self._last_T = T
 
+    def forward_partial(self, x: torch.Tensor, y: torch.Tensor, n_stages: int) -> None:
+        """forward_into that launches only the first n_stages (1..4) kernel
+        stages: router, gate/up, down, combine (for per-stage timing)."""
+        T = x.numel() // self.cfg.hidden_size
+        _lib.check(self.lib.fmx_moe_block_forward_partial(
+            C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),
+            self.workspace.data_ptr(), self.ws_bytes, _stream(), n_stages))
+        self._last_T = T
+
     def forward_profiled(self, x: torch.Tensor, y: torch.Tensor, events) -> None:
         """forward_into that records 5 torch.cuda.Events at the stage
-        boundaries (router | gate/up | down | combine)."""
+        boundaries (before the first kernel and after each of the four
+        kernel stages)."""
         T = x.numel() // self.cfg.hidden_size
         arr = (C.c_void_p * 5)(*[ev.cuda_event for ev in events])
         _lib.check(self.lib.fmx_moe_block_forward_profiled(

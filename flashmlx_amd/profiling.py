@@ -1,0 +1,118 @@
+"""Summaries of rocprofv3 output for libfmx kernels.
+
+  python -m flashmlx_amd.profiling trace  <kernel_stats.csv> --cmd "<command>"
+      -> markdown table of per-kernel calls / average / min / max durations
+  python -m flashmlx_amd.profiling traffic --fetch <csv> --write <csv>
+         --copy-fetch <csv> --copy-write <csv> --copy-bytes N --workload KEY
+      -> JSON of HBM bytes per launch of each MoE stage's kernel
+
+FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what the same
+counter reads for a plain device copy of known size (the factor that makes
+the copy's reading equal its bytes), measured in the same pass.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import json
+import re
+import sys
+
+# kernel name -> MoE stage (the four kernel stages of fmx_moe_block_forward)
+STAGE_OF = [
+    (r"dec_k1", "router+shared_gate_up"),
+    (r"dec_k2", "gate_up"),
+    (r"dec_k3", "down"),
+    (r"dec_k4", "combine"),
+    (r"router_kernel|sort_kernel", "router+sort"),
+    (r"qgemm_kernel<true", "gate_up"),
+    (r"qgemm_kernel<false", "down"),
+    (r"combine_kernel", "combine"),
+]
+
+
+def short_name(kernel: str) -> str:
+    k = kernel.replace("(anonymous namespace)::", "")
+    return re.sub(r"\(.*", "", k).replace("void ", "")
+
+
+def stage_of(kernel: str):
+    for pat, st in STAGE_OF:
+        if re.search(pat, kernel):
+            return st
+    return None
+
+
+def kernel_stats_md(path: str, cmd: str, top: int = 12) -> str:
+    rows = list(csv.DictReader(open(path)))
+    out = [f"Command: `{cmd}`", "",
+           "| kernel | stage | calls | avg us | min us | max us |",
+           "|---|---|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        name = r["Name"]
+        short = short_name(name)[:60]
+        out.append(f"| `{short}` | {stage_of(name) or '-'} | {r['Calls']} | "
+                   f"{float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                   f"{float(r['MaxNs']) / 1e3:.2f} |")
+    return "\n".join(out) + "\n"
+
+
+def counter_avgs(path: str) -> dict:
+    d = collections.defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        d[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in d.items()}
+
+
+def copy_factor(path: str, copy_bytes: int) -> float:
+    """bytes / (KiB reading x 1024) for the largest copy-kernel dispatch."""
+    vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path))
+            if "copy" in r["Kernel_Name"].lower()]
+    if not vals:
+        raise ValueError(f"no copy kernel in {path}")
+    return copy_bytes / (max(vals) * 1024.0)
+
+
+def traffic(fetch: str, write: str, copy_fetch: str, copy_write: str, copy_bytes: int,
+            workload: str, cmds: dict) -> dict:
+    ff = copy_factor(copy_fetch, copy_bytes)
+    fw = copy_factor(copy_write, copy_bytes)
+    fa, wa = counter_avgs(fetch), counter_avgs(write)
+    stages = {}
+    kernels = {}
+    for k in fa:
+        st = stage_of(k)
+        if st is None:
+            continue
+        fb = fa[k] * 1024.0 * ff
+        wb = wa.get(k, 0.0) * 1024.0 * fw
+        kernels[short_name(k)] = {"fetch_bytes": round(fb), "write_bytes": round(wb)}
+        stages[st] = stages.get(st, 0) + round(fb + wb)
+    return {"workload": workload, "unit": "HBM bytes per launch", "fetch_scale": round(ff, 4),
+            "write_scale": round(fw, 4), "stages": stages, "kernels": kernels, "commands": cmds}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest="what", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("stats")
+    t.add_argument("--cmd", required=True)
+    c = sub.add_parser("traffic")
+    for a in ("fetch", "write", "copy_fetch", "copy_write"):
+        c.add_argument("--" + a.replace("_", "-"), required=True)
+    c.add_argument("--copy-bytes", type=int, required=True)
+    c.add_argument("--workload", required=True)
+    c.add_argument("--cmd", action="append", default=[], help="name=command of a pass")
+    a = ap.parse_args(argv)
+    if a.what == "trace":
+        sys.stdout.write(kernel_stats_md(a.stats, a.cmd))
+    else:
+        cmds = dict(s.split("=", 1) for s in a.cmd)
+        print(json.dumps(traffic(a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes,
+                                 a.workload, cmds), indent=1))
+
+
+if __name__ == "__main__":
+    main()

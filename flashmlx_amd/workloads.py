@@ -172,3 +172,65 @@ def flops(m: dict, tokens: int) -> int:
     if Is:
         f += 2 * tokens * 3 * H * Is + 2 * tokens * H
     return f
+
+
+def packed_bytes(n: int, k: int) -> int:
+    """Bytes of an [n, k] weight at 4 bits per weight with a bf16 scale and
+    bias per 64-group (0.5625 B per weight)."""
+    return n * k // 2 + 2 * 2 * n * (k // 64)
+
+
+def decode_path(m: dict, tokens: int, packed: bool = True) -> bool:
+    """Whether fmx_moe_block_forward runs the decode kernels for this shape
+    (asks the library: fmx_moe_forward_path)."""
+    import ctypes as C
+
+    from . import _lib
+    from ._lib import FmxMoEConfig
+
+    c = FmxMoEConfig()
+    c.hidden_size, c.num_experts = m["hidden"], m["n_experts"]
+    c.num_experts_per_tok, c.norm_topk_prob = m["top_k"], int(bool(m["norm_topk"]))
+    c.moe_intermediate_size, c.shared_expert_intermediate_size = m["inter"], m["shared_inter"]
+    c.quant_bits, c.quant_group_size = 4, 64
+    r = _lib.load().fmx_moe_forward_path(C.byref(c), tokens, int(packed))
+    if r < 0:
+        _lib.check(-r)
+    return r == 1
+
+
+def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = False,
+               packed: bool = True) -> list:
+    """Algorithmic work of each kernel stage of one MoE-layer call, in launch
+    order: [(name, hbm_bytes, flops)]. Bytes are the weights the stage must
+    read plus the activations it must read and write in HBM (the smallest
+    traffic the stage's kernel can have); flops count the useful MACs x 2."""
+    H, E, I, Is, k = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"], m["top_k"]
+    T, U = tokens, unique_experts
+    pw = packed_bytes
+    router_b = E * H * 2 + (E * 2 if router_bias else 0) + (H * 2 if Is else 0)
+    router_f = 2 * T * H * (E + (1 if Is else 0))
+    x_b = T * H * 2
+    h_b = T * k * I * 2
+    hs_b = T * Is * 2
+    d_b = T * k * H * 2
+    sd_b = 4 * T * H * 4 if Is else 0
+    y_b = T * H * 2
+    gu_f = 2 * T * k * 2 * H * I
+    sgu_f = 2 * T * 2 * H * Is
+    dn_f = 2 * T * k * H * I
+    sdn_f = 2 * T * H * Is
+    if decode_path(m, T, packed):
+        return [
+            ("router+shared_gate_up", router_b + 2 * pw(Is, H) + x_b + T * (E + 1) * 2 + hs_b,
+             router_f + sgu_f),
+            ("gate_up", U * 2 * pw(I, H) + x_b + h_b, gu_f),
+            ("down", U * pw(H, I) + (pw(H, Is) if Is else 0) + h_b + hs_b + d_b + sd_b, dn_f + sdn_f),
+            ("combine", d_b + sd_b + y_b, 0),
+        ]
+    return [
+        ("router+sort", router_b + x_b + x_b, router_f),
+        ("gate_up", U * 2 * pw(I, H) + 2 * pw(Is, H) + x_b + h_b + hs_b, gu_f + sgu_f),
+        ("down", U * pw(H, I) + (pw(H, Is) if Is else 0) + h_b + hs_b + d_b + sd_b, dn_f + sdn_f),
+        ("combine", d_b + sd_b + y_b, 0),
+    ]

@@ -195,6 +195,12 @@ size_t fmx_moe_packed_size(const fmx_moe_config* cfg);
 int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* src, void* packed,
                             size_t packed_bytes, fmx_stream stream);
 
+/* Which kernels fmx_moe_block_forward runs for n_tokens tokens: 1 = the
+ * decode kernels (packed weights given, at most 16 tokens, shapes within their
+ * limits), 0 = the general ones, < 0 = an fmx_status error (negated). No
+ * counterpart in the reference; for callers that size work per path. */
+int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t n_tokens, int has_packed);
+
 /* Bytes of workspace one forward of up to max_tokens tokens needs
  * (max_tokens <= 65536). */
 size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens);
@@ -222,6 +228,14 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
                                    const void* x, int64_t n_tokens, void* y, void* workspace,
                                    size_t workspace_bytes, fmx_stream stream,
                                    void* const* stage_events);
+
+/* fmx_moe_block_forward that launches only its first n_stages kernel stages
+ * (1..4: router, gate/up, down, combine; 4 = the whole forward, y complete).
+ * Timing graphs of 1, 2, 3 and 4 stages gives each stage's marginal time
+ * inside the layer. No counterpart in the reference (a measurement aid). */
+int fmx_moe_block_forward_partial(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                  const void* x, int64_t n_tokens, void* y, void* workspace,
+                                  size_t workspace_bytes, fmx_stream stream, int n_stages);
 
 /* Device views of the routing state a forward of n_tokens tokens left in
  * the workspace (valid until the next call on that workspace). Any out
