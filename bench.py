@@ -212,8 +212,8 @@ def main():
 
     K, Wm = args.steps, args.warmup
     graphs = {R: capture(lambda: run_layers(R))}
-    if K % R:
-        graphs[K % R] = capture(lambda: run_layers(K % R))
+    for rem in {K % R, Wm % R} - {0}:
+        graphs[rem] = capture(lambda rem=rem: run_layers(rem))
     # every replay must reproduce the eager result
     for _ in range(3):
         graphs[R].replay()
@@ -271,7 +271,8 @@ def main():
 
     dom = max(range(4), key=lambda j: dur[j])
     name, sbytes, sflops = work[dom]
-    prefill = not W.decode_path(m, T, packed=not args.no_pack)
+    path = W.forward_path(m, T, packed=not args.no_pack)
+    prefill = path != "decode"
     if prefill:
         achieved = sflops / (dur[dom] * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
@@ -294,7 +295,7 @@ def main():
         "hbm_frac": round(layer_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "tflops": round(layer_flops / (ms_step * 1e-3) / 1e12, 2),
         "mfma_frac": round(layer_flops / (ms_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        "kernel_path": "general" if prefill else "decode",
+        "kernel_path": path,
         "stage_us": stage_us,
         "stage_bytes": {s: b for s, b, _ in work},
     }

@@ -22,6 +22,7 @@ SOURCES = [
     "csrc/fmx_qgemm.hip",
     "csrc/fmx_pack.hip",
     "csrc/fmx_decode.hip",
+    "csrc/fmx_prefill.hip",
     "csrc/fmx_elem.hip",
     "csrc/fmx_api.cpp",
     "csrc/fmx_synth.cpp",

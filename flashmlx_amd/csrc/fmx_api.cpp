@@ -132,9 +132,10 @@ struct MoELayout {
   uint32_t* inds;
   uint16_t* scores;
   uint32_t *order, *inv, *src, *idx, *offsets, *seg_n, *seg_exp, *seg_off, *sort_base, *seg;
+  uint32_t *pass_n, *pass_tab;
   uint8_t* slots;
   float* sgate;
-  uint16_t *xp, *h, *hs, *d;
+  uint16_t *xp, *h, *hs, *d, *sd;
   float* sd_part;
   size_t total;
 };
@@ -161,6 +162,8 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.seg_off = static_cast<uint32_t*>(ar.take((E + 1) * 4));
   L.sort_base = static_cast<uint32_t*>(ar.take(E * ((n + 63) / 64) * 4));
   L.seg = static_cast<uint32_t*>(ar.take((E + 1) * 4));
+  L.pass_n = static_cast<uint32_t*>(ar.take(4));
+  L.pass_tab = static_cast<uint32_t*>(ar.take(static_cast<int64_t>(max_passes(n, E)) * 8));
   L.slots = static_cast<uint8_t*>(ar.take(E * 16));
   L.sgate = static_cast<float*>(ar.take(T * 4));
   L.xp = static_cast<uint16_t*>(ar.take(T * H * 2));
@@ -168,6 +171,7 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.hs = static_cast<uint16_t*>(ar.take(T * Is * 2));
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
+  L.sd = static_cast<uint16_t*>(ar.take(Is ? T * H * 2 : 0));
   L.total = ar.used;
   return L;
 }
@@ -263,6 +267,8 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.seg_exp = L.seg_exp;
   a.sort.seg_off = L.seg_off;
   a.sort.base = L.sort_base;
+  a.sort.pass_n = L.pass_n;
+  a.sort.pass_tab = L.pass_tab;
   if (sorted_in_router) *sorted_in_router = a.fuse_sort != 0;
   FMX_HIP(launch_router(a, stream));
   return FMX_OK;
@@ -746,7 +752,7 @@ int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t T, int has_packed) {
   da.k = cfg->num_experts_per_tok;
   da.I = static_cast<int>(cfg->moe_intermediate_size);
   da.Is = static_cast<int>(cfg->shared_expert_intermediate_size);
-  return decode_plan(da) ? 1 : 0;
+  return decode_plan(da) ? 1 : 2;
 }
 
 namespace {
@@ -866,6 +872,96 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       FMX_HIP(mark(4));
       return ok();
     }
+
+    // prefill batches: router (+ sort and pass table), gate/up grid, down
+    // grid, combine
+    FMX_HIP(mark(0));
+    bool sorted = false;
+    if ((rc = run_router(c, L, x, T, w->router_w, w->router_logit_bias,
+                         has_sh ? w->shared_expert_gate_w : nullptr, L.inds, L.scores, L.probs,
+                         has_sh ? L.sgate : nullptr, nullptr, true, &sorted, stream)))
+      return rc;
+    if (!sorted) {
+      SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off,
+                 L.sort_base, L.pass_n, L.pass_tab};
+      FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
+    }
+    FMX_HIP(mark(1));
+    if (n_stages < 2) return ok();
+
+    const int mp = max_passes(n, E);
+    auto routed = [&](const uint8_t* wp, int64_t es, const uint16_t* xr, int64_t ldx,
+                      const uint32_t* row_map, uint16_t* out, int64_t ldo, int64_t N, int64_t K) {
+      PfSet s{};
+      s.w = wp;
+      s.es = es;
+      s.x = xr;
+      s.ldx = ldx;
+      s.row_map = row_map;
+      s.out = out;
+      s.ldo = ldo;
+      s.nt = static_cast<int>(N / 16);
+      s.nu = static_cast<int>(K / 128);
+      s.pass_n = L.pass_n;
+      s.pass_tab = L.pass_tab;
+      s.max_pass = mp;
+      s.n_exp = static_cast<int>(E);
+      s.rows_max = static_cast<int>(n);
+      s.x_rows = static_cast<int>(row_map ? T : n);
+      return s;
+    };
+    auto shared = [&](const uint8_t* wp, const uint16_t* xr, int64_t ldx, uint16_t* out,
+                      int64_t ldo, int64_t N, int64_t K) {
+      PfSet s{};
+      s.w = wp;
+      s.x = xr;
+      s.ldx = ldx;
+      s.out = out;
+      s.ldo = ldo;
+      s.nt = static_cast<int>(N / 16);
+      s.nu = static_cast<int>(K / 128);
+      s.rows_static = s.rows_max = s.x_rows = static_cast<int>(T);
+      s.n_exp = 1;
+      return s;
+    };
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    {
+      PfArgs pa{};
+      pa.s1 = routed(pk + PL.gu, PL.gu_es, xb, H, L.src, L.h, I, I, H);
+      pa.n_items1 = pf_items(pa.s1, true);
+      if (has_sh) {
+        pa.s0 = shared(pk + PL.sgu, xb, H, L.hs, Is, Is, H);
+        pa.n_items0 = pf_items(pa.s0, true);
+      }
+      FMX_HIP(launch_pf(pa, true, stream));
+    }
+    FMX_HIP(mark(2));
+    if (n_stages < 3) return ok();
+    {
+      PfArgs pa{};
+      pa.s1 = routed(pk + PL.dn, PL.dn_es, L.h, I, nullptr, L.d, H, H, I);
+      pa.n_items1 = pf_items(pa.s1, false);
+      if (has_sh) {
+        pa.s0 = shared(pk + PL.sdn, L.hs, Is, L.sd, H, H, Is);
+        pa.n_items0 = pf_items(pa.s0, false);
+      }
+      FMX_HIP(launch_pf(pa, false, stream));
+    }
+    FMX_HIP(mark(3));
+    if (n_stages < 4) return ok();
+    CombineArgs cb{};
+    cb.d = L.d;
+    cb.inv = L.inv;
+    cb.scores = L.scores;
+    cb.sd = has_sh ? L.sd : nullptr;
+    cb.sgate = has_sh ? L.sgate : nullptr;
+    cb.y = static_cast<uint16_t*>(y);
+    cb.T = static_cast<int>(T);
+    cb.k = static_cast<int>(k);
+    cb.H = static_cast<int>(H);
+    FMX_HIP(launch_combine(cb, stream));
+    FMX_HIP(mark(4));
+    return ok();
   }
 
   // 1. router + top-k (+ sort when it fits in the router's last workgroup)

@@ -108,24 +108,38 @@ __device__ void sort_block(const uint32_t* keys, int n, int k, int E, const Sort
     if (o.idx) o.idx[pos] = key;
   }
 
-  // segment table of the non-empty keys, ascending
+  // segment table of the non-empty keys, ascending, and the pass table
+  // (each segment cut into passes of at most kPassRows rows)
   if (o.seg_off) {
     const int eper = (E + NT - 1) / NT;
     const int eb = tid * eper, ee = min(eb + eper, E);
-    uint32_t cnt = 0;
-    for (int e = eb; e < ee; ++e) cnt += (o.offsets[e + 1] > o.offsets[e]) ? 1u : 0u;
-    uint32_t U = 0;
-    uint32_t u = block_exclusive_scan<NT>(cnt, s_tmp, &U);
+    uint32_t cnt = 0, pcnt = 0;
     for (int e = eb; e < ee; ++e) {
-      if (o.offsets[e + 1] > o.offsets[e]) {
+      const uint32_t c = o.offsets[e + 1] - o.offsets[e];
+      cnt += c ? 1u : 0u;
+      pcnt += (c + kPassRows - 1) / kPassRows;
+    }
+    uint32_t U = 0, NP = 0;
+    uint32_t u = block_exclusive_scan<NT>(cnt, s_tmp, &U);
+    uint32_t p = block_exclusive_scan<NT>(pcnt, s_tmp, &NP);
+    for (int e = eb; e < ee; ++e) {
+      const uint32_t off = o.offsets[e], c = o.offsets[e + 1] - off;
+      if (c) {
         if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
-        o.seg_off[u] = o.offsets[e];
+        o.seg_off[u] = off;
         ++u;
+        if (o.pass_tab) {
+          for (uint32_t r = 0; r < c; r += kPassRows, ++p) {
+            o.pass_tab[2 * p] = off + r;
+            o.pass_tab[2 * p + 1] = static_cast<uint32_t>(e) | (min(c - r, static_cast<uint32_t>(kPassRows)) << 16);
+          }
+        }
       }
     }
     if (tid == 0) {
       o.seg_off[U] = static_cast<uint32_t>(n);
       if (o.seg_n) *o.seg_n = U;
+      if (o.pass_n) *o.pass_n = NP;
     }
   }
 }

@@ -19,7 +19,17 @@ struct SortOut {
   uint32_t* seg_exp;  // [E]   u -> key of the u-th non-empty key (nullable)
   uint32_t* seg_off;  // [E+1] u -> first sorted position         (nullable)
   uint32_t* base;     // [E * ceil(n/64)] scratch
+  // pass table of the prefill GEMMs: each segment cut into passes of at
+  // most kPassRows rows, in segment order (both nullable)
+  uint32_t* pass_n;   // [1]   number of passes
+  uint32_t* pass_tab; // [max_passes(n, E)][2]: first sorted row, key | rows << 16
 };
+
+constexpr int kPassRows = 64;
+// most passes n sorted rows over at most E keys can need
+__host__ __device__ inline int max_passes(int64_t n, int64_t E) {
+  return static_cast<int>((n < E ? n : E) + (n + kPassRows - 1) / kPassRows);
+}
 
 // Sort in one workgroup of 1024 threads (separate launch).
 constexpr int kSortThreads = 1024;
@@ -150,6 +160,38 @@ hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k4(const DecodeArgs& a, hipStream_t stream);
+
+// ---------------------------------------------------------------- prefill (T > 16)
+// The expert GEMMs of the MoE block for prefill on packed weights
+// (fmx_prefill.hip): one grid for gate/up + SwiGLU, one for down, each over
+// the routed experts' passes and the shared expert's.
+struct PfSet {
+  const uint8_t* w;          // packed blocks of expert 0 (pairs for gate/up)
+  int64_t es;                // bytes per expert
+  const uint16_t* x;         // activation rows, bf16
+  int64_t ldx;               // elements between rows
+  const uint32_t* row_map;   // pass row -> x row (null: identity)
+  uint16_t* out;             // output rows (indexed like the pass rows), bf16
+  int64_t ldo;
+  int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
+  int nu;                    // 128-k units of K
+  int ng;                    // column groups (kPfWaves * blocks per wave tiles each)
+  const uint32_t* pass_n;    // device pass count (null: static passes over rows_static)
+  const uint32_t* pass_tab;  // [max_pass][2] (see SortOut)
+  int max_pass;              // passes the grid covers
+  int rows_static;           // rows of the static passes
+  int n_exp;                 // experts in w (table values clamp to n_exp - 1)
+  int rows_max;              // pass rows (table rows clamp to it)
+  int x_rows;                // rows of x (row_map values clamp to x_rows - 1)
+};
+struct PfArgs {
+  PfSet s0, s1;              // work items [0, n_items0) serve s0, the rest s1
+  int n_items0, n_items1;
+};
+// Fills ng / max_pass of a set; items of it.
+int pf_items(PfSet& s, bool dual);
+size_t pf_lds_bytes();
+hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream);
 
 struct PackArgs {
   const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // MLX layout [n_exp][N][..]

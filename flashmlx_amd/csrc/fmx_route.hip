@@ -189,6 +189,8 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
   if (lane == 0 && a.wsg && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
 }
 
+static_assert(kPassRows >= kWave, "a segment of at most 64 rows is one pass");
+
 // Stable sort of n <= 64 keys by wave 0 of the workgroup (all threads call).
 // s_hist: E words, s_idx: 64 words of LDS.
 __device__ void sort_small(const uint32_t* keys, int n, int k, int E, const SortOut& o,
@@ -250,11 +252,18 @@ __device__ void sort_small(const uint32_t* keys, int n, int k, int E, const Sort
     if (start) {
       if (o.seg_exp) o.seg_exp[u] = s_idx[lane];
       o.seg_off[u] = static_cast<uint32_t>(lane);
+      if (o.pass_tab) {  // n <= 64 = kPassRows: one pass per segment
+        const uint64_t above = b & ~((2ull << lane) - 1ull);
+        const int next = above ? __ffsll(static_cast<unsigned long long>(above)) - 1 : n;
+        o.pass_tab[2 * u] = static_cast<uint32_t>(lane);
+        o.pass_tab[2 * u + 1] = s_idx[lane] | (static_cast<uint32_t>(next - lane) << 16);
+      }
     }
     if (lane == 0) {
       const int U = __popcll(b);
       o.seg_off[U] = static_cast<uint32_t>(n);
       if (o.seg_n) *o.seg_n = static_cast<uint32_t>(U);
+      if (o.pass_n) *o.pass_n = static_cast<uint32_t>(U);
     }
   }
 }

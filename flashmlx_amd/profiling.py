@@ -26,6 +26,8 @@ STAGE_OF = [
     (r"dec_k3", "down"),
     (r"dec_k4", "combine"),
     (r"router_kernel|sort_kernel", "router+sort"),
+    (r"pf_gemm<true", "gate_up"),
+    (r"pf_gemm<false", "down"),
     (r"qgemm_kernel<true", "gate_up"),
     (r"qgemm_kernel<false", "down"),
     (r"combine_kernel", "combine"),

@@ -27,6 +27,10 @@ TINY = dict(name="tiny", hidden=256, n_experts=8, top_k=2, inter=128, shared_int
             norm_topk=False)
 TINY_NORM = dict(name="tiny-norm", hidden=320, n_experts=12, top_k=3, inter=192, shared_inter=0,
                  norm_topk=True)
+# small shapes that the packed-weight kernels take (every K a multiple of 128);
+# H = 384 leaves the down projection's last column group part-filled
+SMALL = dict(name="small", hidden=384, n_experts=6, top_k=2, inter=256, shared_inter=256,
+             norm_topk=False)
 
 # synth stream ids, one per tensor
 S_X, S_ROUTER, S_RBIAS = 1, 2, 3
@@ -58,6 +62,10 @@ WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
     Workload("tiny_t5", TINY, 5, 11, note="tiny shapes, 5 tokens"),
     Workload("tiny_t40", TINY, 40, 12, router_bias=True, note="tiny shapes, 40 tokens, skewed"),
     Workload("tiny_norm_t33", TINY_NORM, 33, 13, note="tiny shapes, renormalised top-3"),
+    Workload("small_t23", SMALL, 23, 14, router_bias=True,
+             note="packable small shapes, 23 tokens (one pass per expert)"),
+    Workload("small_t200", SMALL, 200, 15,
+             note="packable small shapes, 200 tokens (experts over several passes)"),
 ]}
 
 
@@ -180,9 +188,10 @@ def packed_bytes(n: int, k: int) -> int:
     return n * k // 2 + 2 * 2 * n * (k // 64)
 
 
-def decode_path(m: dict, tokens: int, packed: bool = True) -> bool:
-    """Whether fmx_moe_block_forward runs the decode kernels for this shape
-    (asks the library: fmx_moe_forward_path)."""
+def forward_path(m: dict, tokens: int, packed: bool = True) -> str:
+    """The kernels fmx_moe_block_forward runs for this shape: "decode",
+    "prefill" (packed-weight GEMMs) or "general" (asks the library:
+    fmx_moe_forward_path)."""
     import ctypes as C
 
     from . import _lib
@@ -196,7 +205,12 @@ def decode_path(m: dict, tokens: int, packed: bool = True) -> bool:
     r = _lib.load().fmx_moe_forward_path(C.byref(c), tokens, int(packed))
     if r < 0:
         _lib.check(-r)
-    return r == 1
+    return {0: "general", 1: "decode", 2: "prefill"}[r]
+
+
+def decode_path(m: dict, tokens: int, packed: bool = True) -> bool:
+    """Whether fmx_moe_block_forward runs the decode kernels for this shape."""
+    return forward_path(m, tokens, packed) == "decode"
 
 
 def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = False,

@@ -197,8 +197,10 @@ int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* sr
 
 /* Which kernels fmx_moe_block_forward runs for n_tokens tokens: 1 = the
  * decode kernels (packed weights given, at most 16 tokens, shapes within their
- * limits), 0 = the general ones, < 0 = an fmx_status error (negated). No
- * counterpart in the reference; for callers that size work per path. */
+ * limits), 2 = the prefill GEMMs on packed weights (packed weights given, more
+ * tokens or shapes outside the decode limits), 0 = the general ones on the
+ * MLX layout, < 0 = an fmx_status error (negated). No counterpart in the
+ * reference; for callers that size work per path. */
 int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t n_tokens, int has_packed);
 
 /* Bytes of workspace one forward of up to max_tokens tokens needs

@@ -114,6 +114,23 @@ def test_moe_workspace_sizes(fmx):
     assert lib.fmx_moe_workspace_size(C.byref(topk), 8) == 0
 
 
+def test_forward_path_per_shape(fmx):
+    """Decode kernels up to 16 tokens on packed weights, the packed prefill
+    GEMMs above, the MLX-layout GEMMs without packing or for shapes the
+    packed layout cannot hold (a K that is not a multiple of 128)."""
+    from flashmlx_amd import workloads as W
+    assert W.forward_path(W.QWEN15, 1) == "decode"
+    assert W.forward_path(W.QWEN15, 16) == "decode"
+    assert W.forward_path(W.QWEN15, 17) == "prefill"
+    assert W.forward_path(W.QWEN15, 512) == "prefill"
+    assert W.forward_path(W.QWEN15, 512, packed=False) == "general"
+    assert W.forward_path(W.QWEN3, 8) == "decode"
+    assert W.forward_path(W.QWEN3, 1024) == "prefill"
+    assert W.forward_path(W.SMALL, 23) == "prefill"
+    assert W.forward_path(W.TINY, 40) == "general"        # shared_inter 192
+    assert W.forward_path(W.TINY_NORM, 33) == "general"   # hidden 320
+
+
 def test_synth_is_counter_based(fmx):
     """Each value is a pure function of (seed, stream, index): prefixes agree,
     streams and seeds differ, moments are those of N(mean, std)."""

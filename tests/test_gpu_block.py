@@ -30,13 +30,16 @@ def _run(wl_key, fmx, oracle, tokens=None, pack=True):
 
 CASES = [("tiny_t5", True), ("tiny_t5", False), ("tiny_t40", True), ("tiny_norm_t33", True),
          ("qwen15_decode_b1", True), ("qwen15_decode_b1", False), ("qwen15_decode_b4", True),
+         ("small_t23", True), ("small_t200", True), ("small_t200", False),
          ("qwen15_decode_b8", True), ("qwen15_decode_b8", False), ("qwen15_prefill_512", True),
+         ("qwen15_prefill_512", False),
          ("qwen3_decode_b1", True), ("qwen3_decode_b8", True), ("qwen3_decode_b8", False),
          ("qwen3_prefill_1024", True)]
 
 
 # pack=True: forwards of at most 16 tokens run the packed-weight decode
-# kernels; pack=False keeps them on the MLX-layout grouped GEMM
+# kernels, longer ones the packed-weight prefill GEMMs; pack=False keeps
+# both on the MLX-layout grouped GEMM
 @pytest.mark.parametrize("wl_key,pack", CASES)
 def test_block_parity(gpu, fmx, oracle, wl_key, pack):
     wl, hi, block, xd, y = _run(wl_key, fmx, oracle, pack=pack)
