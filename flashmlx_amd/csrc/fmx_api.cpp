@@ -269,6 +269,12 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.base = L.sort_base;
   a.sort.pass_n = L.pass_n;
   a.sort.pass_tab = L.pass_tab;
+  if (T > kRouterManyMin) {
+    if (sorted_in_router) *sorted_in_router = false;
+    FMX_HIP(launch_router_many(a, stream));
+    if (xp) FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x), T, c.hidden_size, xp, stream));
+    return FMX_OK;
+  }
   if (sorted_in_router) *sorted_in_router = a.fuse_sort != 0;
   FMX_HIP(launch_router(a, stream));
   return FMX_OK;

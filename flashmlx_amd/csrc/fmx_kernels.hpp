@@ -31,10 +31,10 @@ __host__ __device__ inline int max_passes(int64_t n, int64_t E) {
   return static_cast<int>((n < E ? n : E) + (n + kPassRows - 1) / kPassRows);
 }
 
-// Sort in one workgroup of 1024 threads (separate launch).
+// Sort in one workgroup of 1024 threads (separate launch), LDS-resident.
 constexpr int kSortThreads = 1024;
-constexpr int kSortCntBytes = 64 * 1024;   // LDS for the [E][tiles] count table
-constexpr int kSortMaxN = 32 * 1024;       // LDS for the per-entry ranks
+constexpr int kSortMaxN = 32 * 1024;       // keys held in LDS (16 bits each)
+constexpr int kSortMaxE = 1024;            // per-wave key counters in LDS
 bool sort_fits(int64_t n, int64_t E);
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
                        hipStream_t stream);
@@ -68,6 +68,10 @@ struct RouterArgs {
 };
 bool router_sort_fits(int64_t n, int64_t E);
 hipError_t launch_router(const RouterArgs& a, hipStream_t stream);
+// Forwards of more than kRouterManyMin tokens: logits on fp64 MFMA tiles,
+// then softmax/top-k per token, in two launches (no xp copy, no sort).
+constexpr int kRouterManyMin = 16;
+hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- grouped GEMM
 // One problem: rows grouped in segments that share one expert's packed

@@ -9,16 +9,130 @@
 namespace fmx {
 
 bool sort_fits(int64_t n, int64_t E) {
-  const int64_t tiles = (n + 63) / 64;
-  return n >= 0 && n <= kSortMaxN && E >= 1 && E * tiles <= kSortCntBytes;
+  return n >= 0 && n <= kSortMaxN && E >= 1 && E <= kSortMaxE;
 }
 
+namespace {
+
+constexpr int kSortWaves = kSortThreads / kWave;
+
+// One walk over wave `wave`'s contiguous range of entries [r0, r1), in tiles
+// of 64: within a tile the lanes holding an equal key are found with one
+// ballot per key bit; the lowest of them (the leader) reads the wave's
+// running count of that key, hands it to the others and adds the group's
+// size. An entry's rank among the equal keys of its wave's range is then
+// running count + rank in the tile. With SCATTER, position = base[key][wave]
+// + that rank, written to the outputs.
+template <bool SCATTER>
+__device__ void sort_walk(const uint16_t* s_key, uint16_t* s_run, const uint16_t* s_base, int r0,
+                          int r1, int k, int nbits, int wave, int lane, const SortOut& o) {
+  uint16_t* run = s_run + wave * kSortMaxE;
+  for (int t0 = r0; t0 < r1; t0 += kWave) {
+    const int i = t0 + lane;
+    const bool valid = i < r1;
+    const uint32_t key = valid ? s_key[i] : 0u;
+    uint64_t eq = __ballot(valid);
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (key >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      eq &= bit ? m : ~m;
+    }
+    const int leader = valid ? __ffsll(static_cast<unsigned long long>(eq)) - 1 : lane;
+    const bool lead = valid && leader == lane;
+    uint32_t v = lead ? run[key] : 0u;
+    v = __shfl(v, leader);
+    if (lead) run[key] = static_cast<uint16_t>(v + __popcll(eq));
+    if (SCATTER && valid) {
+      const uint32_t pos = s_base[key * kSortWaves + wave] + v + __popcll(eq & lanes_below(lane));
+      if (o.order) o.order[pos] = static_cast<uint32_t>(i);
+      if (o.inv) o.inv[i] = pos;
+      if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
+      if (o.idx) o.idx[pos] = key;
+    }
+  }
+}
+
+}  // namespace
+
+// Stable counting sort of n keys (< E; larger ones count as E - 1) by one
+// workgroup, in LDS: keys are read once (batched), wave w owns the entry
+// range [w * span, (w + 1) * span), a walk counts each key per wave, the
+// (key-major, wave-minor) scan of the counts gives base[key][wave], and a
+// second walk scatters. Then offsets and the segment and pass tables.
 __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys, int n, int k,
                                                             int E, SortOut o) {
-  __shared__ uint8_t s_cnt[kSortCntBytes];
-  __shared__ uint8_t s_rank[kSortMaxN];
-  __shared__ uint32_t s_tmp[kSortThreads / kWave + 1];
-  sort_block<kSortThreads>(keys, n, k, E, o, s_cnt, s_rank, s_tmp);
+  __shared__ uint16_t s_key[kSortMaxN];
+  __shared__ uint16_t s_run[kSortWaves * kSortMaxE];
+  __shared__ uint16_t s_base[kSortMaxE * kSortWaves];
+  __shared__ uint32_t s_off[kSortMaxE + 1];
+  __shared__ uint32_t s_tmp[kSortWaves + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nbits = E <= 1 ? 1 : 32 - __builtin_clz(static_cast<uint32_t>(E - 1));
+  const uint32_t emax = static_cast<uint32_t>(E - 1);
+
+#pragma unroll 8
+  for (int i = tid; i < n; i += kSortThreads) s_key[i] = static_cast<uint16_t>(min(keys[i], emax));
+  for (int i = tid; i < kSortWaves * E; i += kSortThreads) s_run[(i / E) * kSortMaxE + i % E] = 0;
+  __syncthreads();
+
+  const int span = ((n + kSortWaves - 1) / kSortWaves + kWave - 1) / kWave * kWave;
+  const int r0 = min(wave * span, n), r1 = min(r0 + span, n);
+  sort_walk<false>(s_key, s_run, nullptr, r0, r1, k, nbits, wave, lane, o);
+  __syncthreads();
+
+  // key-major exclusive scan of the per-wave counts
+  const int total = E * kSortWaves;
+  const int per = (total + kSortThreads - 1) / kSortThreads;
+  const int beg = min(tid * per, total), end = min(beg + per, total);
+  uint32_t local = 0;
+  for (int j = beg; j < end; ++j) local += s_run[(j % kSortWaves) * kSortMaxE + j / kSortWaves];
+  uint32_t runv = block_exclusive_scan<kSortThreads>(local, s_tmp, nullptr);
+  for (int j = beg; j < end; ++j) {
+    const int e = j / kSortWaves, w = j % kSortWaves;
+    s_base[j] = static_cast<uint16_t>(runv);
+    if (w == 0) s_off[e] = runv;
+    runv += s_run[w * kSortMaxE + e];
+  }
+  if (tid == 0) s_off[E] = static_cast<uint32_t>(n);
+  __syncthreads();
+  for (int e = lane; e < E; e += kWave) s_run[wave * kSortMaxE + e] = 0;  // each wave clears its row
+  for (int e = tid; e <= E; e += kSortThreads) o.offsets[e] = s_off[e];
+  __syncthreads();
+  sort_walk<true>(s_key, s_run, s_base, r0, r1, k, nbits, wave, lane, o);
+
+  // segment table of the non-empty keys, ascending, and the pass table
+  if (o.seg_off) {
+    const int eper = (E + kSortThreads - 1) / kSortThreads;
+    const int eb = min(tid * eper, E), ee = min(eb + eper, E);
+    uint32_t cnt = 0, pcnt = 0;
+    for (int e = eb; e < ee; ++e) {
+      const uint32_t c = s_off[e + 1] - s_off[e];
+      cnt += c ? 1u : 0u;
+      pcnt += (c + kPassRows - 1) / kPassRows;
+    }
+    uint32_t U = 0, NP = 0;
+    uint32_t u = block_exclusive_scan<kSortThreads>(cnt, s_tmp, &U);
+    uint32_t p = block_exclusive_scan<kSortThreads>(pcnt, s_tmp, &NP);
+    for (int e = eb; e < ee; ++e) {
+      const uint32_t off = s_off[e], c = s_off[e + 1] - off;
+      if (c) {
+        if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
+        o.seg_off[u] = off;
+        ++u;
+        if (o.pass_tab) {
+          for (uint32_t r = 0; r < c; r += kPassRows, ++p) {
+            o.pass_tab[2 * p] = off + r;
+            o.pass_tab[2 * p + 1] = static_cast<uint32_t>(e) | (min(c - r, static_cast<uint32_t>(kPassRows)) << 16);
+          }
+        }
+      }
+    }
+    if (tid == 0) {
+      o.seg_off[U] = static_cast<uint32_t>(n);
+      if (o.seg_n) *o.seg_n = U;
+      if (o.pass_n) *o.pass_n = NP;
+    }
+  }
 }
 
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
@@ -126,14 +240,18 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
 // same total in every lane.
 __device__ void router_token(const RouterArgs& a, int t, int lane) {
   const int E = a.E;
+  const int nblk = (E + kWave - 1) / kWave;  // 64-expert blocks (wave-uniform)
   const uint16_t* lrow = a.logits + static_cast<int64_t>(t) * (E + 1);
   double lv[kMaxExpertsPerLane];
   double m = -__builtin_huge_val();
 #pragma unroll
   for (int i = 0; i < kMaxExpertsPerLane; ++i) {
     const int e = lane + 64 * i;
-    lv[i] = e < E ? static_cast<double>(bf16_to_f32(lrow[e])) : -__builtin_huge_val();
-    m = fmax(m, lv[i]);
+    lv[i] = -__builtin_huge_val();
+    if (i < nblk) {
+      if (e < E) lv[i] = static_cast<double>(bf16_to_f32(lrow[e]));
+      m = fmax(m, lv[i]);
+    }
   }
   m = __ockl_wfred_max_f64(m);
   double ex[kMaxExpertsPerLane];
@@ -141,8 +259,11 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
 #pragma unroll
   for (int i = 0; i < kMaxExpertsPerLane; ++i) {
     const int e = lane + 64 * i;
-    ex[i] = e < E ? exp_det(lv[i] - m) : 0.0;
-    s += ex[i];
+    ex[i] = 0.0;
+    if (i < nblk) {
+      if (e < E) ex[i] = exp_det(lv[i] - m);
+      s += ex[i];
+    }
   }
 #pragma unroll
   for (int w = 32; w >= 1; w >>= 1) s += __shfl_xor(s, w);
@@ -150,7 +271,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
 #pragma unroll
   for (int i = 0; i < kMaxExpertsPerLane; ++i) {
     const int e = lane + 64 * i;
-    if (e < E) {
+    if (i < nblk && e < E) {
       const uint16_t p = f64_to_bf16(ex[i] / s);
       if (a.probs) a.probs[static_cast<int64_t>(t) * E + e] = p;
       key[i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
@@ -165,12 +286,13 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
   for (int j = 0; j < a.k; ++j) {
     uint32_t best = 0u;
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) best = max(best, key[i]);
+    for (int i = 0; i < kMaxExpertsPerLane; ++i)
+      if (i < nblk) best = max(best, key[i]);
     best = __ockl_wfred_max_u32(best);
     const uint32_t e = 0xffffu - (best & 0xffffu);
 #pragma unroll
     for (int i = 0; i < kMaxExpertsPerLane; ++i)
-      if (key[i] == best) key[i] = 0u;
+      if (i < nblk && key[i] == best) key[i] = 0u;
     const uint16_t p = static_cast<uint16_t>(best >> 16);
     sc_sum += bf16_to_f32(p);  // fp32, slot order
     if (lane == j) {
@@ -266,6 +388,96 @@ __device__ void sort_small(const uint32_t* keys, int n, int k, int E, const Sort
       if (o.pass_n) *o.pass_n = static_cast<uint32_t>(U);
     }
   }
+}
+
+// ------------------------------------------------------------------ router, many tokens
+//
+// Forwards of more than a few token tiles route in two kernels with no
+// cross-workgroup handoff inside either:
+//   logits_kernel  16 tokens x 16 columns per workgroup on v_mfma_f64_16x16x4f64:
+//                  the bf16 operands are exact in fp64 and so are their
+//                  products; 8 waves take interleaved 32-element slices of H
+//                  and their partial tiles are added in wave order, the sum
+//                  rounded once to bf16 (then the logit bias, as in phase 1
+//                  of router_kernel)
+//   topk_kernel    softmax and top-k, one wave per token (router_token)
+// The sort follows as its own launch.
+
+constexpr int kLgWaves = 8;
+constexpr int kLgThreads = kLgWaves * kWave;
+
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
+  __shared__ double s_red[(kLgWaves - 1) * 4 * kWave];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i16 = lane & 15, kk = lane >> 4;
+  const int H = a.H, E = a.E;
+  const int ncols = E + (a.wsg ? 1 : 0);
+  const int t0 = blockIdx.y * 16, c0 = blockIdx.x * 16;
+  // MFMA operands: lane (i16, kk) feeds token row i16 (A) and column i16 (B)
+  // at k = 8 * chunk + m for the m-th of 8 MFMAs per 16-byte chunk
+  const uint16_t* xrow = a.x + static_cast<int64_t>(min(t0 + i16, a.T - 1)) * H;
+  const int col = min(c0 + i16, ncols - 1);
+  const uint16_t* wrow = col < E ? a.wr + static_cast<int64_t>(col) * H : a.wsg;
+  const int nch = H / 8;
+  f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+  for (int base = 0; base < nch; base += 4 * kLgWaves) {
+    const int ch = base + 4 * wave + kk;
+    u32x4_t xv = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
+    if (ch < nch) {  // chunks past H contribute exact zeros
+      xv = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
+      wv = *reinterpret_cast<const u32x4_t*>(wrow + ch * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const double x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+      const double w0 = __uint_as_float(wv[i] << 16), w1 = __uint_as_float(wv[i] & 0xffff0000u);
+      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
+    }
+  }
+  f64x4_t acc = acc0 + acc1;
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_red[((wave - 1) * 4 + r) * kWave + lane] = acc[r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < kLgWaves - 1; ++w)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += s_red[(w * 4 + r) * kWave + lane];
+  // the f64 MFMA's result layout: lane (i16, kk) holds rows kk + 4 r
+  // (tokens t0 + kk + 4 r) of column i16 (column c0 + i16)
+  const int c = c0 + i16;
+  if (c >= ncols) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + kk + 4 * r;
+    if (t >= a.T) continue;
+    uint16_t l = f64_to_bf16(acc[r]);
+    if (c < E && a.lbias)
+      l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(a.lbias[c])));
+    a.logits[static_cast<int64_t>(t) * (E + 1) + c] = l;
+  }
+}
+
+__global__ __launch_bounds__(kRouterThreads) void topk_kernel(RouterArgs a) {
+  const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
+  if (t < a.T) router_token(a, t, threadIdx.x & 63);
+}
+
+hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream) {
+  const int ncols = a.E + (a.wsg ? 1 : 0);
+  hipLaunchKernelGGL(logits_kernel, dim3((ncols + 15) / 16, (a.T + 15) / 16), dim3(kLgThreads), 0,
+                     stream, a);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(topk_kernel, dim3((a.T + kRouterWaves - 1) / kRouterWaves), dim3(kRouterThreads),
+                     0, stream, a);
+  return hipGetLastError();
 }
 
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
