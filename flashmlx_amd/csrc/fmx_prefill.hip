@@ -14,13 +14,15 @@
 // sorted rows into passes; the shared expert's passes are 64 consecutive
 // tokens). A column group is 4 waves x 4 weight tiles of 16 rows: 128
 // SwiGLU columns (2 gate/up tile pairs per wave) or 256 down columns. The
-// workgroup walks K in 128-k units through a three-stage LDS ring that LDS
+// workgroup walks K in 128-k units through a ring of LDS stages that LDS
 // DMA fills, with no registers held for loads in flight: per unit, the
-// pass's activation rows (64 x 256 bytes, gathered through the row map) and
-// each wave's four packed blocks (weight words, then all four blocks'
-// scale/bias words in one piece). One barrier per unit; after it the unit
-// two ahead is issued into the buffer that every wave finished with in the
-// previous iteration.
+// pass's activation rows (its 16-row tiles x 256 bytes, gathered through
+// the row map) and each wave's four packed blocks (weight words, then all
+// four blocks' scale/bias words in one piece). One barrier per unit; after
+// it the unit kPfStages - 1 ahead is issued into the buffer that every wave
+// finished with in the previous iteration. Two stages (72 KB) let two
+// workgroups share a CU, so one's dequantisation overlaps the other's
+// MFMAs and loads.
 //
 // Activation rows sit in LDS as 16-byte chunks XOR-swizzled by row (chunk c
 // of row r at slot c ^ (r & 15)), so the 16 lanes that read one k-slice of
@@ -50,17 +52,16 @@ constexpr int kPfABytes = kPassRows * 256;                   // a pass's rows, o
 // that the idle half of the DMA wave writes
 constexpr int kPfWaveBBytes = 4096 + 1024;
 constexpr int kPfStageBytes = kPfABytes + kPfWaves * kPfWaveBBytes;
-constexpr int kPfStages = 3;
+constexpr int kPfStages = 2;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
 template <bool DUAL>
 constexpr int pf_nb() { return DUAL ? 2 : 4; }  // packed blocks per wave
-// LDS DMA instructions one wave issues per unit: its row pieces, the 1 KB
-// weight pieces of its blocks and one for all their (scale, bias) words.
-// Every one runs with all lanes on: a DMA under a lane condition may be
-// duplicated into both arms of a branch by the compiler, and the wait counts
-// below count instructions.
-template <bool DUAL>
-constexpr int pf_insts() { return kPfMT + 4 + 1; }
+// LDS DMA instructions one wave issues per unit: its row pieces (one per
+// 16-row tile the pass fills), the 1 KB weight pieces of its blocks and one
+// for all their (scale, bias) words. Every one runs with all lanes on: a
+// DMA under a lane condition may be duplicated into both arms of a branch by
+// the compiler, and the wait counts below count instructions.
 
 __device__ inline void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
@@ -89,34 +90,17 @@ __device__ inline bf16x8_t dq8(uint32_t w, float s, float b) {
   return __builtin_bit_cast(bf16x8_t, d);
 }
 
-template <bool DUAL>
-__global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
+// One work item: rows [row0, row0 + rows) (rows <= 16 MT) of expert e's
+// weights, column group ng. MT (the 16-row tiles the rows fill) fixes how
+// many row pieces each wave moves per unit, so the pass's rows are moved
+// and multiplied once, without padding to kPassRows.
+template <bool DUAL, int MT>
+__device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, int row0, int rows,
+                                                       int64_t e, uint8_t* s_pf) {
   constexpr int NB = pf_nb<DUAL>(), NM = DUAL ? 2 : 1;
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
-  constexpr int PER = pf_insts<DUAL>();
-
-  int item = blockIdx.x;
-  const bool second = item >= a.n_items0;
-  if (second) item -= a.n_items0;
-  const PfSet& P = second ? a.s1 : a.s0;
-  const int pass = item / P.ng, ng = item - pass * P.ng;
-
-  // ---- the pass: rows [row0, row0 + rows) of expert e
-  int row0, rows;
-  int64_t e = 0;
-  if (P.pass_n) {
-    const int np = min(static_cast<int>(*P.pass_n), P.max_pass);
-    if (pass >= np) return;
-    const u32x2_t t = *reinterpret_cast<const u32x2_t*>(P.pass_tab + 2 * pass);
-    row0 = min(static_cast<int>(t[0]), P.rows_max);
-    rows = min(min(static_cast<int>(t[1] >> 16), kPassRows), P.rows_max - row0);
-    e = min(static_cast<int>(t[1] & 0xffffu), P.n_exp - 1);
-  } else {
-    row0 = pass * kPassRows;
-    rows = min(kPassRows, P.rows_static - row0);
-  }
-  if (rows <= 0) return;
+  constexpr int PER = MT + NB * NM + 1;  // LDS DMA instructions per wave and unit
+  static_assert(NB * NM == 4, "four 1 KB weight pieces per wave and unit");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -131,9 +115,9 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
 #pragma unroll
   for (int b = 0; b < NB; ++b)
     bsrc[b] = wexp + static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * nu * BB;
-  const uint16_t* asrc[kPfMT];
+  const uint16_t* asrc[MT];
 #pragma unroll
-  for (int pc = 0; pc < kPfMT; ++pc) {
+  for (int pc = 0; pc < MT; ++pc) {
     const int r = 4 * (pc * kPfWaves + wave) + j;  // pass row of this lane's chunk
     const int rr = min(r, rows - 1);               // rows past the pass repeat its last
     int64_t xr = row0 + rr;
@@ -146,81 +130,90 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   // 0..31 into the spare 512 bytes
   constexpr int SBL = 32 / NB;  // lanes per block
   const int sbl = lane & 31;
-  const int sb_blk = sbl / SBL, sb_off = NM * 1024 + 16 * (sbl % SBL);
+  const uint8_t* sb_src = wexp + static_cast<int64_t>(min(tile0 + sbl / SBL, P.nt - 1)) * nu * BB +
+                          NM * 1024 + 16 * (sbl % SBL);
 
   auto issue = [&](int u, int st) {
     uint8_t* sa = s_pf + st * kPfStageBytes;
 #pragma unroll
-    for (int pc = 0; pc < kPfMT; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
+    for (int pc = 0; pc < MT; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
     uint8_t* sb = sa + kPfABytes + wave * kPfWaveBBytes;
     const int64_t uo = static_cast<int64_t>(u) * BB;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int m = 0; m < NM; ++m) dma16(bsrc[b] + uo + m * 1024 + 16 * lane, sb + (b * NM + m) * 1024);
-    const uint8_t* gs = bsrc[0] + uo + sb_off;
-#pragma unroll
-    for (int b = 1; b < NB; ++b)
-      if (sb_blk == b) gs = bsrc[b] + uo + sb_off;
-    dma16(gs, sb + 4096);
+    dma16(sb_src + uo, sb + 4096);
   };
 
-  f32x4_t acc[kPfMT][NB][NM];
+  f32x4_t acc[MT][NB][NM];
 #pragma unroll
-  for (int mt = 0; mt < kPfMT; ++mt)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int m = 0; m < NM; ++m) acc[mt][b][m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  issue(0, 0);
-  if (nu > 1) issue(1, 1);
+  // the ring: units u + 1 .. u + kPfStages - 2 are in flight while unit u
+  // is multiplied; unit u + kPfStages - 1 is issued into the buffer of u - 1
+#pragma unroll
+  for (int st = 0; st < kPfStages - 1; ++st)
+    if (st < nu) issue(st, st);
   for (int u = 0; u < nu; ++u) {
-    // this wave's DMA of unit u has landed (only unit u + 1's may still be
+    // this wave's DMA of unit u has landed (only later units' may still be
     // in flight); after the barrier every wave's has, and every wave is done
     // with the buffer of unit u - 1
-    if (u + 1 < nu)
+    const int ahead = min(kPfStages - 2, nu - 1 - u);
+    if (ahead >= 2)
+      wait_vmcnt<2 * PER>();
+    else if (ahead == 1)
       wait_vmcnt<PER>();
     else
       wait_vmcnt0();
     lds_dma_barrier();
-    if (u + 2 < nu) issue(u + 2, (u + 2) % kPfStages);
+    if (u + kPfStages - 1 < nu) issue(u + kPfStages - 1, (u + kPfStages - 1) % kPfStages);
 
     const uint8_t* sa = s_pf + (u % kPfStages) * kPfStageBytes;
     const uint8_t* sb = sa + kPfABytes + wave * kPfWaveBBytes;
-    bf16x8_t B[NB][NM][4];
+    // the unit's packed words and (scale, bias) pairs; each k-slice q is
+    // dequantised right before its MFMAs, so that only one slice of weights
+    // is live in registers
+    u32x4_t W[NB][NM];
+    float sc[NB][NM][2], bi[NB][NM][2];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        const u32x4_t W = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
+        W[b][m] = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
         const u32x2_t sbw = *reinterpret_cast<const u32x2_t*>(sb + 4096 + b * (NM * 128) + m * 128 + 8 * i16);
-        const float s0 = __uint_as_float(sbw[0] << 16), s1 = __uint_as_float(sbw[0] & 0xffff0000u);
-        const float b0 = __uint_as_float(sbw[1] << 16), b1 = __uint_as_float(sbw[1] & 0xffff0000u);
-        B[b][m][0] = dq8(W[0], s0, b0);
-        B[b][m][1] = dq8(W[1], s0, b0);
-        B[b][m][2] = dq8(W[2], s1, b1);
-        B[b][m][3] = dq8(W[3], s1, b1);
+        sc[b][m][0] = __uint_as_float(sbw[0] << 16);
+        sc[b][m][1] = __uint_as_float(sbw[0] & 0xffff0000u);
+        bi[b][m][0] = __uint_as_float(sbw[1] << 16);
+        bi[b][m][1] = __uint_as_float(sbw[1] & 0xffff0000u);
       }
     }
 #pragma unroll
-    for (int mt = 0; mt < kPfMT; ++mt) {
-      if (16 * mt >= rows) break;
-      const uint8_t* ar = sa + (16 * mt + i16) * 256;
+    for (int q = 0; q < 4; ++q) {
+      bf16x8_t B[NB][NM];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bf16x8_t A = *reinterpret_cast<const bf16x8_t*>(ar + (((4 * q + j) ^ i16) << 4));
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) B[b][m] = dq8(W[b][m][q], sc[b][m][q >> 1], bi[b][m][q >> 1]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const bf16x8_t A =
+            *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int m = 0; m < NM; ++m) acc[mt][b][m] = mfma_bf16(A, B[b][m][q], acc[mt][b][m]);
+          for (int m = 0; m < NM; ++m) acc[mt][b][m] = mfma_bf16(A, B[b][m], acc[mt][b][m]);
       }
     }
   }
 
   // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile, column i16
 #pragma unroll
-  for (int mt = 0; mt < kPfMT; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int t = tile0 + b;
@@ -241,13 +234,68 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   }
 }
 
+// Block -> work item. The hardware dispatches block b to XCD b % 8, each
+// XCD taking its blocks in order. Routed passes go to XCDs round-robin and
+// an XCD runs all column groups of one pass back to back, so the pass's
+// rows are fetched into that XCD's L2 once; the shared expert's column
+// groups go round-robin and an XCD runs all passes of one group back to
+// back, so the group's weights are fetched once. Blocks past the work
+// (padding, passes the sort did not fill) exit.
+template <bool DUAL>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
+  int b = blockIdx.x;
+  const bool second = b >= a.n_items0;
+  if (second) b -= a.n_items0;
+  const PfSet& P = second ? a.s1 : a.s0;
+  const int x = b % kXcds, l = b / kXcds;
+  int pass, ng;
+  if (P.pass_n) {
+    pass = x + kXcds * (l / P.ng);
+    ng = l % P.ng;
+  } else {
+    const int np = (P.rows_static + kPassRows - 1) / kPassRows;
+    ng = x + kXcds * (l / np);
+    pass = l % np;
+    if (ng >= P.ng) return;
+  }
+
+  // ---- the pass: rows [row0, row0 + rows) of expert e
+  int row0, rows;
+  int64_t e = 0;
+  if (P.pass_n) {
+    const int npass = min(static_cast<int>(*P.pass_n), P.max_pass);
+    if (pass >= npass) return;
+    const u32x2_t t = *reinterpret_cast<const u32x2_t*>(P.pass_tab + 2 * pass);
+    row0 = min(static_cast<int>(t[0]), P.rows_max);
+    rows = min(min(static_cast<int>(t[1] >> 16), kPassRows), P.rows_max - row0);
+    e = min(static_cast<int>(t[1] & 0xffffu), P.n_exp - 1);
+  } else {
+    row0 = pass * kPassRows;
+    rows = min(kPassRows, P.rows_static - row0);
+  }
+  if (rows <= 0) return;
+  static_assert(kPfMT == 4 || kPfMT == 8, "row-tile dispatch below covers 4 or 8 tiles");
+  switch ((rows + 15) / 16) {
+    case 1: pf_item<DUAL, 1>(P, ng, row0, rows, e, s_pf); break;
+    case 2: pf_item<DUAL, 2>(P, ng, row0, rows, e, s_pf); break;
+    case 3: pf_item<DUAL, 3>(P, ng, row0, rows, e, s_pf); break;
+    case 4: pf_item<DUAL, 4>(P, ng, row0, rows, e, s_pf); break;
+    case 5:
+    case 6: pf_item<DUAL, (kPfMT >= 6 ? 6 : 4)>(P, ng, row0, rows, e, s_pf); break;
+    default: pf_item<DUAL, kPfMT>(P, ng, row0, rows, e, s_pf); break;
+  }
+}
+
 }  // namespace
 
 int pf_items(PfSet& s, bool dual) {
   const int per_group = kPfWaves * (dual ? pf_nb<true>() : pf_nb<false>());
   s.ng = (s.nt + per_group - 1) / per_group;
-  const int passes = s.pass_n ? s.max_pass : (s.rows_static + kPassRows - 1) / kPassRows;
-  return passes * s.ng;
+  if (s.pass_n)  // pass-major per XCD
+    return kXcds * s.ng * ((s.max_pass + kXcds - 1) / kXcds);
+  const int np = (s.rows_static + kPassRows - 1) / kPassRows;  // group-major per XCD
+  return kXcds * np * ((s.ng + kXcds - 1) / kXcds);
 }
 
 size_t pf_lds_bytes() { return static_cast<size_t>(kPfStages) * kPfStageBytes; }
