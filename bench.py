@@ -245,14 +245,15 @@ def main():
     tok_s = T * K / (ms_total / 1e3)
 
     # ---- per-stage timing: graphs of R layers that run only the first j
-    # kernel stages (j = 1..4); stage j's marginal time inside the layer is
+    # kernel stages (j = 1..len(stages)); stage j's marginal time inside the layer is
     # the difference of consecutive graphs' times (HIP events on the kernels'
     # stream around each replay)
     work = W.stage_work(m, T, U, wl.router_bias, packed=not args.no_pack)
     stages = [s[0] for s in work]
     reps = max(1, args.profile_steps // R)
     cum = [0.0]
-    for j in range(1, 5):
+    ns = len(stages)
+    for j in range(1, ns + 1):
         gj = capture(lambda j=j: [blocks[i].forward_partial(x, y, j) for i in range(R)])
         with torch.cuda.stream(stream):
             gj.replay()
@@ -266,10 +267,10 @@ def main():
         torch.cuda.synchronize()
         cum.append(e0.elapsed_time(e1) / (R * reps))
         del gj
-    dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(4)]
+    dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(ns)]
     stage_us = {s: round(dur[j] * 1e3, 2) for j, s in enumerate(stages)}
 
-    dom = max(range(4), key=lambda j: dur[j])
+    dom = max(range(ns), key=lambda j: dur[j])
     name, sbytes, sflops = work[dom]
     path = W.forward_path(m, T, packed=not args.no_pack)
     prefill = path != "decode"

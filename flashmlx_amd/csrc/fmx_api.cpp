@@ -128,6 +128,7 @@ constexpr size_t kCounterBytes = (kMoEMaxTokens / kRouterTok + 64) * sizeof(uint
 struct MoELayout {
   uint32_t* counters;
   uint16_t* logits;
+  uint32_t* lgw;
   uint16_t* probs;
   uint32_t* inds;
   uint16_t* scores;
@@ -136,6 +137,7 @@ struct MoELayout {
   uint8_t* slots;
   float* sgate;
   uint16_t *xp, *h, *hs, *d, *sd;
+  uint32_t* dw;
   float* sd_part;
   size_t total;
 };
@@ -149,6 +151,7 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   const int64_t n = T * k;
   L.counters = static_cast<uint32_t*>(ar.take(kCounterBytes));
   L.logits = static_cast<uint16_t*>(ar.take(T * (E + 1) * 2));
+  L.lgw = static_cast<uint32_t*>(ar.take(T * (E + 1) * 4));
   L.probs = static_cast<uint16_t*>(ar.take(T * E * 2));
   L.inds = static_cast<uint32_t*>(ar.take(n * 4));
   L.scores = static_cast<uint16_t*>(ar.take(n * 2));
@@ -172,6 +175,7 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
   L.sd = static_cast<uint16_t*>(ar.take(Is ? T * H * 2 : 0));
+  L.dw = static_cast<uint32_t*>(ar.take(T <= kDecMaxT ? n * H * 4 : 0));
   L.total = ar.used;
   return L;
 }
@@ -850,9 +854,10 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.sgu = pk + PL.sgu;
     da.sdn = pk + PL.sdn;
     da.logits = L.logits;
+    da.lgw = L.lgw;
     da.hs = L.hs;
     da.h = L.h;
-    da.d = L.d;
+    da.dw = L.dw;
     da.sd_part = L.sd_part;
     da.inds = L.inds;
     da.scores = L.scores;
@@ -862,6 +867,8 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.seg = L.seg;
     da.slots = L.slots;
     da.counter = L.counters;
+    // the last entries: the routers' arrival counters stop at 1 + T / kRouterTok
+    da.cb_counter = L.counters + kCounterBytes / 4 - kDecMaxColBlocks;
     da.y = static_cast<uint16_t*>(y);
     if (decode_plan(da)) {
       FMX_HIP(mark(0));
@@ -872,9 +879,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       FMX_HIP(mark(2));
       if (n_stages < 3) return ok();
       FMX_HIP(launch_decode_k3(da, stream));
-      FMX_HIP(mark(3));
-      if (n_stages < 4) return ok();
-      FMX_HIP(launch_decode_k4(da, stream));
+      FMX_HIP(mark(3));  // the combine runs inside K3
       FMX_HIP(mark(4));
       return ok();
     }

@@ -6,9 +6,10 @@
 //       |  shared expert gate/up + SwiGLU (routing-independent, streams
 //       meanwhile)
 //   K2  routed experts' gate/up + SwiGLU tiles
-//   K3  per 16 columns of H: the down projections of every routed expert and
-//       of the shared expert, then the top-k weighted combine and the gated
-//       shared add, written straight to y
+//   K3  per 64 columns of H: the down projections of every routed expert and
+//       of the shared expert; the last workgroup to finish a column block
+//       does its top-k weighted combine and the gated shared add, written
+//       straight to y
 //
 // Reference: server/src/model.cpp:750-807 (moe_block), :673-734 (switch_mlp:
 // gather_qmm gate/up/down, SwiGLU), :736-748 (shared_expert_mlp), :14-25
@@ -16,9 +17,11 @@
 //
 // Rows of every MFMA tile are indexed by token: a token selects an expert at
 // most once, so expert e's tile rows are the tokens that routed to it and no
-// gather or sort is needed for the products. The only cross-workgroup
-// handoff inside a kernel is K1's router (release/acquire fences in a few
-// dozen workgroups); everything else meets at kernel boundaries.
+// gather or sort is needed for the products. Workgroups of one kernel hand
+// data over in two places, K1's logits and K3's column blocks, both the same
+// way: device-scope stores, a wait for their completion, then a device-scope
+// arrival counter; the last arrival reads with device-scope loads. No
+// workgroup ever waits for another.
 #include <algorithm>
 
 #include "fmx_dev.hpp"
@@ -31,7 +34,11 @@ namespace {
 __host__ __device__ inline int xstride(int K) { return K + 8; }
 
 constexpr int kDecWaves = kDecThreads / kWave;
-constexpr int kRouterColsPerWg = 2;  // two columns per router workgroup, H halves per wave
+constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;        // quad_reduce's LDS
+constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
+constexpr int kDecK1LpBytes = kDecWaves * kDecMaxT * 8;              // router partials per wave
+
+constexpr int kDecK1LgBytes = kDecMaxT * (kDecMaxE + 1) * 2;         // every token's logits
 
 // Units [u0, u1) (u1 - u0 <= NU) of one 16-row tile (blocks of BB bytes from
 // tile_base), all loads in flight together, against activation rows in LDS
@@ -60,12 +67,11 @@ __device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, 
   }
 }
 
-// Waves 2p and 2p+1 of a workgroup compute tile pair slot p over K halves 0
-// and 1; the second half's partial sums reach the first through LDS (s_red:
-// 2 x 8 x 64 floats).
-__device__ inline void pair_reduce(f32x4_t& acc0, f32x4_t& acc1, int wave, int lane, float* s_red) {
-  float* slot = s_red + (wave >> 1) * 8 * kWave;
-  if (wave & 1) {
+// Waves 1..3 hand their partial sums over K quarters 1..3 to wave 0 through
+// LDS (s_red: 3 x 8 x 64 floats); wave 0 adds them in wave order.
+__device__ inline void quad_reduce(f32x4_t& acc0, f32x4_t& acc1, int wave, int lane, float* s_red) {
+  if (wave > 0) {
+    float* slot = s_red + (wave - 1) * 8 * kWave;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       slot[i * kWave + lane] = acc0[i];
@@ -73,83 +79,118 @@ __device__ inline void pair_reduce(f32x4_t& acc0, f32x4_t& acc1, int wave, int l
     }
   }
   __syncthreads();
-  if (!(wave & 1)) {
+  if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc0[i] += slot[i * kWave + lane];
-      acc1[i] += slot[(4 + i) * kWave + lane];
+    for (int w = 0; w < kDecWaves - 1; ++w) {
+      const float* slot = s_red + w * 8 * kWave;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc0[i] += slot[i * kWave + lane];
+        acc1[i] += slot[(4 + i) * kWave + lane];
+      }
     }
   }
 }
 
 // ---------------------------------------------------------------- K1: router
 
-// Softmax (fp64, exp_det, fixed-order normaliser) and top-k of token t by
+// Softmax (fp64, exp_det, fixed-order normaliser) and top-k of NT tokens by
 // one wave, as model.cpp:764-775 with the renormalisation of
 // moe-support-plan.md:319-322: the k largest bf16 probabilities, ties to the
-// lower expert index, slots ordered (probability desc, index asc).
-// lrow: the token's E (+1) logits in LDS.
-template <int NPER>
-__device__ void route_token(const DecodeArgs& a, int t, const uint16_t* lrow, int lane, uint32_t* s_inds) {
-  const int E = a.E;
-  double lv[NPER];
-  double m = -__builtin_huge_val();
+// lower expert index, slots ordered (probability desc, index asc). The
+// tokens' dependent fp64 chains are interleaved; tokens ts[n] >= T are
+// computed on padding and not written. s_lg: every token's E (+1) logits.
+template <int NPER, int NT>
+__device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uint16_t* s_lg, int lane,
+                             uint32_t* s_inds) {
+  const int E = a.E, ld = E + 1;
+  double lv[NT][NPER], ex[NT][NPER], m[NT], s[NT];
 #pragma unroll
-  for (int i = 0; i < NPER; ++i) {
-    const int e = lane + 64 * i;
-    lv[i] = e < E ? static_cast<double>(bf16_to_f32(lrow[e])) : -__builtin_huge_val();
-    m = fmax(m, lv[i]);
+  for (int n = 0; n < NT; ++n) {
+    const int t = min(ts[n], a.T - 1);
+    m[n] = -__builtin_huge_val();
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int e = lane + 64 * i;
+      lv[n][i] = e < E ? static_cast<double>(bf16_to_f32(s_lg[t * ld + e])) : -__builtin_huge_val();
+      m[n] = fmax(m[n], lv[n][i]);
+    }
   }
-  m = __ockl_wfred_max_f64(m);
+#pragma unroll
+  for (int n = 0; n < NT; ++n) m[n] = __ockl_wfred_max_f64(m[n]);
   // lane l sums e = l, l + 64, ... in turn; six butterfly steps then give
   // every lane the same total
-  double ex[NPER];
-  double s = 0.0;
 #pragma unroll
-  for (int i = 0; i < NPER; ++i) {
-    const int e = lane + 64 * i;
-    ex[i] = e < E ? exp_det(lv[i] - m) : 0.0;
-    s += ex[i];
-  }
+  for (int n = 0; n < NT; ++n) {
+    s[n] = 0.0;
 #pragma unroll
-  for (int w = 32; w >= 1; w >>= 1) s += __shfl_xor(s, w);
-  uint32_t key[NPER];
-#pragma unroll
-  for (int i = 0; i < NPER; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = 0u;
-    if (e < E) {
-      const uint16_t p = f64_to_bf16(ex[i] / s);
-      if (a.probs) a.probs[static_cast<int64_t>(t) * E + e] = p;
-      // probabilities are >= 0: their bf16 patterns order like their values
-      key[i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
+    for (int i = 0; i < NPER; ++i) {
+      const int e = lane + 64 * i;
+      ex[n][i] = e < E ? exp_det(lv[n][i] - m[n]) : 0.0;
+      s[n] += ex[n][i];
     }
   }
-  float sc_sum = 0.0f;
-  uint32_t my_key = 0u;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) s[n] += __shfl_xor(s[n], w);
+  uint32_t key[NT][NPER];
+#pragma unroll
+  for (int n = 0; n < NT; ++n)
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int e = lane + 64 * i;
+      key[n][i] = 0u;
+      if (e < E) {
+        const uint16_t p = f64_to_bf16(ex[n][i] / s[n]);
+        if (a.probs && ts[n] < a.T) a.probs[static_cast<int64_t>(ts[n]) * E + e] = p;
+        // probabilities are >= 0: their bf16 patterns order like their values
+        key[n][i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
+      }
+    }
+  float sc_sum[NT];
+  uint32_t my_key[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    sc_sum[n] = 0.0f;
+    my_key[n] = 0u;
+  }
   for (int j = 0; j < a.k; ++j) {
-    uint32_t best = 0u;
+    uint32_t best[NT];
 #pragma unroll
-    for (int i = 0; i < NPER; ++i) best = max(best, key[i]);
-    best = __ockl_wfred_max_u32(best);
+    for (int n = 0; n < NT; ++n) {
+      best[n] = 0u;
 #pragma unroll
-    for (int i = 0; i < NPER; ++i)
-      if (key[i] == best) key[i] = 0u;
-    sc_sum += bf16_to_f32(static_cast<uint16_t>(best >> 16));  // fp32, slot order
-    if (lane == j) my_key = best;
-  }
-  if (lane < a.k) {
-    const uint32_t e = 0xffffu - (my_key & 0xffffu);
-    uint16_t sc = static_cast<uint16_t>(my_key >> 16);
-    if (a.norm) {
-      const double den = static_cast<double>(round_bf16(sc_sum));
-      sc = f32_to_bf16(static_cast<float>(static_cast<double>(bf16_to_f32(sc)) / den));
+      for (int i = 0; i < NPER; ++i) best[n] = max(best[n], key[n][i]);
     }
-    s_inds[t * a.k + lane] = e;
-    a.inds[t * a.k + lane] = e;
-    a.scores[t * a.k + lane] = sc;
+#pragma unroll
+    for (int n = 0; n < NT; ++n) best[n] = __ockl_wfred_max_u32(best[n]);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+      for (int i = 0; i < NPER; ++i)
+        if (key[n][i] == best[n]) key[n][i] = 0u;
+      sc_sum[n] += bf16_to_f32(static_cast<uint16_t>(best[n] >> 16));  // fp32, slot order
+      if (lane == j) my_key[n] = best[n];
+    }
   }
-  if (lane == 0 && a.wsg) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int t = ts[n];
+    if (t >= a.T) continue;
+    if (lane < a.k) {
+      const uint32_t e = 0xffffu - (my_key[n] & 0xffffu);
+      uint16_t sc = static_cast<uint16_t>(my_key[n] >> 16);
+      if (a.norm) {
+        const double den = static_cast<double>(round_bf16(sc_sum[n]));
+        sc = f32_to_bf16(static_cast<float>(static_cast<double>(bf16_to_f32(sc)) / den));
+      }
+      s_inds[t * a.k + lane] = e;
+      a.inds[t * a.k + lane] = e;
+      a.scores[t * a.k + lane] = sc;
+    }
+    if (lane == 0 && a.wsg) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
+  }
 }
 
 // The last router workgroup: routing of every token, the ascending list of
@@ -160,15 +201,28 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   __shared__ uint32_t s_seg[kDecMaxE + 1];
   __shared__ uint16_t s_segof[kDecMaxE];
   __shared__ uint8_t s_used[kDecMaxE];
+  __shared__ uint8_t s_slot[kDecMaxE * kDecMaxT];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, E = a.E, k = a.k, n = T * k;
   const int ld = E + 1;
-  // every token's logits -> LDS in one round trip
-  for (int i = tid; i < T * ld; i += kDecThreads) s_lg[i] = a.logits[i];
+  // every token's logits -> LDS in one round trip (device-scope loads: the
+  // other router workgroups' device-scope stores completed before their
+  // arrivals were counted)
+  const int ncols = E + (a.wsg ? 1 : 0);
+  for (int i = tid; i < ncols * T; i += kDecThreads) {
+    const int c = i / T, t = i - c * T;
+    const uint16_t v = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    s_lg[t * ld + c] = v;
+    a.logits[t * ld + c] = v;
+  }
   for (int e = tid; e < E; e += kDecThreads) s_used[e] = 0;
   __syncthreads();
-  for (int t = wave; t < T; t += kDecWaves) route_token<NPER>(a, t, s_lg + t * ld, lane, s_inds);
+  // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
+  for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
+    const int ts[2] = {t0, t0 + kDecWaves};
+    route_tokens<NPER, 2>(a, ts, s_lg, lane, s_inds);
+  }
   __syncthreads();
   for (int i = tid; i < n; i += kDecThreads) s_used[s_inds[i]] = 1;
   __syncthreads();
@@ -187,122 +241,110 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
     }
     if (lane == 0) s_seg[0] = U;
   }
+  for (int i = tid; i < E * kDecMaxT; i += kDecThreads) s_slot[i] = 0xff;
   __syncthreads();
   const int U = static_cast<int>(s_seg[0]);
   for (int i = tid; i <= U; i += kDecThreads) a.seg[i] = s_seg[i];
-  // slot table, one byte per (expert u, token t): written as whole words
-  for (int i = tid; i < U * (kDecMaxT / 4); i += kDecThreads) {
-    const int u = i / (kDecMaxT / 4), t0 = 4 * (i - u * (kDecMaxT / 4));
-    uint32_t word = 0xffffffffu;
-    for (int q = 0; q < 4; ++q) {
-      const int t = t0 + q;
-      if (t >= T) continue;
-      for (int j = 0; j < k; ++j)
-        if (s_segof[s_inds[t * k + j]] == u) word = (word & ~(0xffu << (8 * q))) | (static_cast<uint32_t>(j) << (8 * q));
-    }
-    reinterpret_cast<uint32_t*>(a.slots)[i] = word;
-  }
+  // slot table, one byte per (expert u, token t): entry (t, j) marks its
+  // expert's row, then the rows go out as whole words
+  for (int i = tid; i < n; i += kDecThreads) s_slot[s_segof[s_inds[i]] * kDecMaxT + i / k] = static_cast<uint8_t>(i % k);
+  __syncthreads();
+  for (int i = tid; i < U * (kDecMaxT / 4); i += kDecThreads)
+    reinterpret_cast<uint32_t*>(a.slots)[i] = reinterpret_cast<const uint32_t*>(s_slot)[i];
 }
 
-// Router columns 2*wg, 2*wg + 1 (column E: the shared-expert gate row) for
-// every token: logits = x . w_c in fp64 (bf16 products are exact in fp32,
-// their sum is exact in fp64 and so independent of order), rounded once to
-// bf16 (model.cpp:762, :792-799). Waves 2c, 2c+1 take the two halves of H;
-// every lane's partial sum of every token goes to LDS and 16 threads per
-// (column, token) add them up.
+// Router column c (column E: the shared-expert gate row) for every token,
+// one per workgroup: logits = x . w_c in fp64 (bf16 products are exact in
+// fp32, their sum is exact in fp64 and so independent of order), rounded
+// once to bf16 (model.cpp:762, :792-799). Lane g of the workgroup takes
+// 16-byte chunk g of H; each wave's partial sums meet in one reduce-scatter
+// and the four waves' in LDS. The last router workgroup to finish derives
+// the routing.
 template <int NPER>
-__device__ void dec_router(const DecodeArgs& a, int wg, uint16_t* s_x, double* s_lp) {
+__device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   __shared__ int s_last;
+  double* s_lp = reinterpret_cast<double*>(smem);
+  uint16_t* s_lg = reinterpret_cast<uint16_t*>(smem + kDecK1LpBytes);
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecK1LpBytes + kDecK1LgBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, T = a.T, E = a.E, xs = xstride(H);
   const int ncols = E + (a.wsg ? 1 : 0);
-  const int c = min(wg * kRouterColsPerWg + (wave >> 1), ncols - 1);
-  const int hh = wave & 1, half_oct = H / 16;
-  const uint16_t* wrow = c < E ? a.wr + static_cast<int64_t>(c) * H : a.wsg;
+  const int nch = H / 8;
   dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  u32x4_t wv[kDecRouterChunks];
-#pragma unroll
-  for (int i = 0; i < kDecRouterChunks; ++i) {
-    const int ch = hh * half_oct + min(lane + 64 * i, half_oct - 1);
-    wv[i] = *reinterpret_cast<const u32x4_t*>(wrow + ch * 8);
-  }
+  const uint16_t* wrow = c < E ? a.wr + static_cast<int64_t>(c) * H : a.wsg;
+  const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(wrow + min(tid, nch - 1) * 8);
+  const bool biased = c < E && a.lbias;
+  const uint16_t lb = biased ? a.lbias[c] : 0;
   wait_vmcnt0();
-  __syncthreads();
-  double wd[kDecRouterChunks * 8];
+  lds_dma_barrier();
+  double wd[8];
 #pragma unroll
-  for (int i = 0; i < kDecRouterChunks; ++i) {
-    const bool ok = lane + 64 * i < half_oct;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      wd[8 * i + 2 * q] = ok ? static_cast<double>(__uint_as_float(wv[i][q] << 16)) : 0.0;
-      wd[8 * i + 2 * q + 1] = ok ? static_cast<double>(__uint_as_float(wv[i][q] & 0xffff0000u)) : 0.0;
-    }
+  for (int q = 0; q < 4; ++q) {
+    wd[2 * q] = tid < nch ? static_cast<double>(__uint_as_float(wv[q] << 16)) : 0.0;
+    wd[2 * q + 1] = tid < nch ? static_cast<double>(__uint_as_float(wv[q] & 0xffff0000u)) : 0.0;
   }
-#pragma unroll 1
-  for (int t = 0; t < T; ++t) {
-    double acc = 0.0;
+  double part[kDecMaxT];
 #pragma unroll
-    for (int i = 0; i < kDecRouterChunks; ++i) {
-      const int ch = hh * half_oct + min(lane + 64 * i, half_oct - 1);
-      const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(s_x + t * xs + ch * 8);
+  for (int t = 0; t < kDecMaxT; ++t) {
+    part[t] = 0.0;
+    if (t < T) {
+      const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(s_x + t * xs + min(tid, nch - 1) * 8);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] << 16)), wd[8 * i + 2 * q], acc);
-        acc = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] & 0xffff0000u)), wd[8 * i + 2 * q + 1], acc);
+        part[t] = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] << 16)), wd[2 * q], part[t]);
+        part[t] = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] & 0xffff0000u)), wd[2 * q + 1], part[t]);
       }
     }
-    s_lp[(t * kDecWaves + wave) * kWave + lane] = acc;
   }
+  // lane l then holds the wave's total of token l >> 2
+  const double r = reduce_scatter64<kDecMaxT>(part, lane);
+  if ((lane & 3) == 0) s_lp[wave * kDecMaxT + (lane >> 2)] = r;
   __syncthreads();
-  // (column cc, token t) <- 16 threads, each adding 8 of its 128 partials
-  for (int g = tid >> 4; g < kRouterColsPerWg * T; g += kDecThreads / 16) {
-    const int cc = g / T, t = g - cc * T, r = tid & 15;
-    const double* p = s_lp + (t * kDecWaves + 2 * cc) * kWave;
-    double v = 0.0;
+  // The logits go out as device-scope stores (written through to the
+  // device's coherence point) from wave 0; once they have completed, thread
+  // 0 counts this workgroup in. The last one reads them with device-scope
+  // loads: no cache-wide write-back or invalidation is needed on either side.
+  if (wave == 0) {
+    if (tid < T) {
+      double v = 0.0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v += p[r * 8 + q];
-#pragma unroll
-    for (int w = 8; w >= 1; w >>= 1) v += __shfl_xor(v, w);
-    const int col = wg * kRouterColsPerWg + cc;
-    if (r == 0 && col < ncols) {
+      for (int q = 0; q < kDecWaves; ++q) v += s_lp[q * kDecMaxT + tid];
       uint16_t l = f64_to_bf16(v);
-      if (col < E && a.lbias)
-        l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(a.lbias[col])));
-      a.logits[static_cast<int64_t>(t) * (E + 1) + col] = l;
+      if (biased) l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(lb)));
+      __hip_atomic_store(a.lgw + c * T + tid, static_cast<uint32_t>(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  }
-  // the last router workgroup to arrive sees every logit (release by each,
-  // acquire by the last) and finishes the routing
-  __syncthreads();
-  if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    s_last = atomicAdd(a.counter, 1u) == static_cast<uint32_t>(a.n_rt - 1);
+    wait_vmcnt0();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               static_cast<uint32_t>(ncols - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  route_finish<NPER>(a, s_x);
+  route_finish<NPER>(a, s_lg);
   if (tid == 0) *a.counter = 0u;  // every router workgroup has arrived
 }
 
-// Shared expert gate/up + SwiGLU for tile pair `pair` (model.cpp:741-747):
-// hs[t, n] = swiglu(x_t . Wg[n], x_t . Wu[n]) for every token.
-__device__ void dec_shared_gu(const DecodeArgs& a, int pair, uint16_t* s_x, float* s_red) {
+// Shared expert gate/up + SwiGLU for tile pair tp (model.cpp:741-747):
+// hs[t, n] = swiglu(x_t . Wg[n], x_t . Wu[n]) for every token; wave q
+// multiplies K quarter q.
+__device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
+  float* s_red = reinterpret_cast<float*>(smem);
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, T = a.T, Is = a.Is, xs = xstride(H);
-  const int nu = H / 128, half = (nu + 1) / 2;
-  const int tile = 2 * pair + (wave >> 1);
-  const int u0 = (wave & 1) ? half : 0, u1 = (wave & 1) ? nu : half;
+  const int nu = H / 128;
+  const int u0 = (nu * wave) / kDecWaves, u1 = (nu * (wave + 1)) / kDecWaves;
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  tile_units_lds<true, 8>(a.sgu + static_cast<int64_t>(tile) * nu * kBlockPair, u0, u1, xl, lane, acc0, acc1);
-  pair_reduce(acc0, acc1, wave, lane, s_red);
-  if (wave & 1) return;
-  const int n = tile * 16 + m;
+  tile_units_lds<true, kDecK2Units>(a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair, u0, u1, xl, lane,
+                                     acc0, acc1);
+  quad_reduce(acc0, acc1, wave, lane, s_red);
+  if (wave != 0) return;
+  const int n = tp * 16 + m;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
@@ -311,21 +353,15 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int pair, uint16_t* s_x, floa
   }
 }
 
-// LDS: [router lane partials (16 x 4 x 64 doubles) or the pair reduction]
-// then the staged activation rows.
+// Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
 template <int NPER>
 __global__ __launch_bounds__(kDecThreads) void dec_k1(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int wg = blockIdx.x;
-  if (wg < a.n_rt) {
-    double* s_lp = reinterpret_cast<double*>(smem);
-    uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecRouterLpBytes);
-    dec_router<NPER>(a, wg, s_x, s_lp);
-  } else {
-    float* s_red = reinterpret_cast<float*>(smem);
-    uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecRouterLpBytes);
-    dec_shared_gu(a, wg - a.n_rt, s_x, s_red);
-  }
+  const int w = blockIdx.x;
+  if (w < a.n_rt)
+    dec_router<NPER>(a, w, smem);
+  else
+    dec_shared_gu(a, w - a.n_rt, smem);
 }
 
 // ---------------------------------------------------------------- K2: routed gate/up
@@ -346,18 +382,22 @@ __device__ void dec_sort(const DecodeArgs& a) {
   sort_block<kDecThreads>(s_inds, n, a.k, a.E, a.sort, s_cnt, s_rank, s_tmp);
 }
 
+// Routed expert number u, gate/up tile pair tp (h columns 16 tp .. 16 tp + 15),
+// one per workgroup: wave w multiplies K quarter w (model.cpp:703-715). Small
+// equal workgroups keep the grid's last round nearly full. The last
+// workgroup runs the sort for the routing accessors.
 __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* s_red = reinterpret_cast<float*>(smem);
-  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecRouterLpBytes);
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, I = a.I, xs = xstride(H);
-  if (blockIdx.x == a.max_seg * a.gu_pairs) {
+  if (blockIdx.x == a.max_seg * a.gu_tiles) {
     dec_sort(a);
     return;
   }
-  const int u = blockIdx.x / a.gu_pairs, pair = blockIdx.x - u * a.gu_pairs;
+  const int u = blockIdx.x / a.gu_tiles, tp = blockIdx.x - u * a.gu_tiles;
   // routing tables first: a workgroup without an expert leaves before it
   // starts any LDS DMA
   const int U = static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg)));
@@ -365,19 +405,23 @@ __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
   const int e = static_cast<int>(min(a.seg[1 + u], static_cast<uint32_t>(a.E - 1)));
   const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.slots + u * kDecMaxT);
   const uint32_t slot4 = srow[lane & 3];  // slots of tokens 4*(lane&3) .. +3
-  // activation rows -> LDS (DMA), in flight with the weight loads
-  dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  const int nu = H / 128, half = (nu + 1) / 2;
-  const int tile = 2 * pair + (wave >> 1);
-  const int u0 = (wave & 1) ? half : 0, u1 = (wave & 1) ? nu : half;
+  // the activation rows of the tokens that selected e -> LDS rows t (DMA), in
+  // flight with the weight loads; the other rows stay unset, and their
+  // products land in output rows that are never stored
+  for (int t = wave; t < T; t += kDecWaves) {
+    const uint32_t slot = (__shfl(slot4, t >> 2) >> (8 * (t & 3))) & 0xffu;
+    if (slot < static_cast<uint32_t>(k)) dma_row(a.x + static_cast<int64_t>(t) * H, H, s_x + t * xs, lane);
+  }
+  const int nu = H / 128;
+  const int u0 = (nu * wave) / kDecWaves, u1 = (nu * (wave + 1)) / kDecWaves;
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  tile_units_lds<true, 8>(a.gu + static_cast<int64_t>(e) * a.gu_es + static_cast<int64_t>(tile) * nu * kBlockPair,
-                          u0, u1, xl, lane, acc0, acc1);
-  pair_reduce(acc0, acc1, wave, lane, s_red);
-  if (wave & 1) return;
-  const int n = tile * 16 + m;
+  tile_units_lds<true, kDecK2Units>(a.gu + static_cast<int64_t>(e) * a.gu_es + static_cast<int64_t>(tp) * nu * kBlockPair,
+                                     u0, u1, xl, lane, acc0, acc1);
+  quad_reduce(acc0, acc1, wave, lane, s_red);
+  if (wave != 0) return;
+  const int n = tp * 16 + m;
   // lane 16j + c holds rows 4j..4j+3: their slots are the bytes of word j
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll
@@ -393,6 +437,77 @@ __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
 
 constexpr int kDnTiles = 4;  // 16-row tiles of H per K3 workgroup (one per wave)
 constexpr int kDnMaxUnits = 16;
+
+// The top-k weighted combine of column block cb (columns 64 cb .. 64 cb + 63)
+// for every token (model.cpp:782-803): y = bf16(sum over slots, fp32 in slot
+// order, of bf16(d * score)) + bf16(sigmoid(gate) * bf16(shared down, K
+// slices added in order)). d and the shared slices were written by other
+// workgroups with device-scope stores; they are read with device-scope loads.
+__device__ void dec_combine(const DecodeArgs& a, int cb) {
+  const int T = a.T, k = a.k, H = a.H;
+  for (int g = threadIdx.x; g < T * 32; g += kDecThreads) {
+    const int t = g >> 5, c = cb * 64 + 2 * (g & 31);
+    uint32_t dv[2 * kDecMaxK];
+    uint16_t sv[kDecMaxK];
+#pragma unroll
+    for (int q = 0; q < kDecMaxK; ++q) {
+      const int qq = min(q, k - 1);
+      const uint32_t* p = a.dw + static_cast<int64_t>(t * k + qq) * H + c;
+      dv[2 * q] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      dv[2 * q + 1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sv[q] = a.scores[t * k + qq];
+    }
+    uint32_t sp[2 * kDecSdSplit];
+    if (a.Is > 0) {
+#pragma unroll
+      for (int ks = 0; ks < kDecSdSplit; ++ks) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(a.sd_part) + (static_cast<int64_t>(ks) * T + t) * H + c;
+        sp[2 * ks] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sp[2 * ks + 1] = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kDecMaxK; ++q) {
+      if (q < k) {
+        const float sc = bf16_to_f32(sv[q]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i] += round_bf16(bf16_to_f32(static_cast<uint16_t>(dv[2 * q + i])) * sc);
+      }
+    }
+    float yv[2] = {round_bf16(acc[0]), round_bf16(acc[1])};
+    if (a.Is > 0) {
+      const float gt = a.sgate[t];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        float sd = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < kDecSdSplit; ++ks) sd += __uint_as_float(sp[2 * ks + i]);
+        yv[i] += round_bf16(gt * round_bf16(sd));
+      }
+    }
+    *reinterpret_cast<uint32_t*>(a.y + static_cast<int64_t>(t) * H + c) =
+        static_cast<uint32_t>(f32_to_bf16(yv[0])) | (static_cast<uint32_t>(f32_to_bf16(yv[1])) << 16);
+  }
+}
+
+// Counts a K3 workgroup's outputs for column block cb in, once every wave's
+// device-scope stores have completed; the last of the block's contributors
+// (its U routed experts and the shared expert's K slices) combines the block
+// and resets the count.
+__device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
+  __shared__ int s_last_cb;
+  wait_vmcnt0();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t target = static_cast<uint32_t>(U + (a.Is > 0 ? kDecSdSplit : 0));
+    s_last_cb = __hip_atomic_fetch_add(a.cb_counter + cb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target - 1;
+  }
+  __syncthreads();
+  if (!s_last_cb) return;
+  dec_combine(a, cb);
+  if (threadIdx.x == 0) __hip_atomic_store(a.cb_counter + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Routed expert number u, columns 64*cb .. 64*cb + 63 of H (model.cpp:718-721):
 // d[t*k + slot, n] = h[t*k + slot] . Wd_e[n] for the tokens t that selected
@@ -426,8 +541,10 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
     const int t = 4 * j + i;
     const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
     if (t < T && slot < static_cast<uint32_t>(k))
-      a.d[static_cast<int64_t>(t * k + slot) * H + n] = f32_to_bf16(acc[i]);
+      __hip_atomic_store(a.dw + static_cast<int64_t>(t * k + slot) * H + n, static_cast<uint32_t>(f32_to_bf16(acc[i])),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  dec_arrive(a, cb, U);
 }
 
 // Shared expert down projection, columns 64*cb .. +63, K slice ks of
@@ -450,8 +567,11 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
-    if (t < T) a.sd_part[(static_cast<int64_t>(ks) * T + t) * H + n] = acc[i];
+    if (t < T)
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(a.sd_part) + (static_cast<int64_t>(ks) * T + t) * H + n,
+                         __float_as_uint(acc[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  dec_arrive(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
 }
 
 __global__ __launch_bounds__(kDecThreads) void dec_k3(DecodeArgs a) {
@@ -465,76 +585,17 @@ __global__ __launch_bounds__(kDecThreads) void dec_k3(DecodeArgs a) {
     dec_down_shared(a, (wg - n_routed) / kDecSdSplit, (wg - n_routed) % kDecSdSplit, s_a);
 }
 
-// ---------------------------------------------------------------- K4: combine
-
-// y = sum over slots (fp32, slot order) of bf16(d * score) -> bf16
-//   + bf16(sigmoid(gate) * bf16(shared down, K slices added in order)) -> bf16
-// (model.cpp:782-803); one thread per 8 columns of a token.
-__global__ __launch_bounds__(kDecThreads) void dec_k4(DecodeArgs a) {
-  const int oct = a.H / 8;
-  const int g = blockIdx.x * kDecThreads + threadIdx.x;
-  if (g >= a.T * oct) return;
-  const int t = g / oct, o = g - t * oct;
-  // every load first (one round trip), then the arithmetic in slot order
-  u32x4_t dv[kDecMaxK];
-  uint16_t sv[kDecMaxK];
-#pragma unroll
-  for (int q = 0; q < kDecMaxK; ++q) {
-    const int qq = min(q, a.k - 1);
-    dv[q] = *reinterpret_cast<const u32x4_t*>(a.d + static_cast<int64_t>(t * a.k + qq) * a.H + o * 8);
-    sv[q] = a.scores[t * a.k + qq];
-  }
-  f32x4_t sp[2 * kDecSdSplit];
-  if (a.Is > 0) {
-#pragma unroll
-    for (int ks = 0; ks < kDecSdSplit; ++ks) {
-      const float* p = a.sd_part + (static_cast<int64_t>(ks) * a.T + t) * a.H + o * 8;
-      sp[2 * ks] = *reinterpret_cast<const f32x4_t*>(p);
-      sp[2 * ks + 1] = *reinterpret_cast<const f32x4_t*>(p + 4);
-    }
-  }
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int q = 0; q < kDecMaxK; ++q) {
-    if (q < a.k) {
-      const float sc = bf16_to_f32(sv[q]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += round_bf16(__uint_as_float(dv[q][i] << 16) * sc);
-        acc[2 * i + 1] += round_bf16(__uint_as_float(dv[q][i] & 0xffff0000u) * sc);
-      }
-    }
-  }
-  float yv[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) yv[i] = round_bf16(acc[i]);
-  if (a.Is > 0) {
-    float sd[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < kDecSdSplit; ++ks) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sd[i] += sp[2 * ks][i];
-        sd[4 + i] += sp[2 * ks + 1][i];
-      }
-    }
-    const float gt = a.sgate[t];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) yv[i] += round_bf16(gt * round_bf16(sd[i]));
-  }
-  u32x4_t w;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    w[i] = static_cast<uint32_t>(f32_to_bf16(yv[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(yv[2 * i + 1])) << 16);
-  *reinterpret_cast<u32x4_t*>(a.y + static_cast<int64_t>(t) * a.H + o * 8) = w;
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------- host side
 
-static size_t k12_lds(const DecodeArgs& a) {
-  return kDecRouterLpBytes + static_cast<size_t>(a.T) * xstride(a.H) * 2;
+static size_t k1_lds(const DecodeArgs& a) {
+  return std::max(kDecQuadRedBytes, kDecK1LpBytes + kDecK1LgBytes) + static_cast<size_t>(a.T) * xstride(a.H) * 2;
+}
+
+// K2: the quarter reduction, then the staged rows
+static size_t k2_lds(const DecodeArgs& a) {
+  return kDecQuadRedBytes + static_cast<size_t>(a.T) * xstride(a.H) * 2;
 }
 
 static size_t k3_lds(const DecodeArgs& a) {
@@ -546,31 +607,31 @@ static size_t k3_lds(const DecodeArgs& a) {
 bool decode_plan(DecodeArgs& a) {
   const int nu_i = a.I / 128, nu_s = a.Is / 128;
   if (a.T < 1 || a.T > kDecMaxT || a.k < 1 || a.k > kDecMaxK || a.E < 1 || a.E > kDecMaxE ||
-      a.H % 512 || a.I % 128 || a.Is % 128 || a.H > kDecRouterChunks * kWave * 16 ||
+      a.H % 512 || a.I % 128 || a.Is % 128 || a.H / 8 > kDecThreads ||
       a.H / 128 > 16 || nu_i > kDnMaxUnits ||
       (nu_s + kDecSdSplit - 1) / kDecSdSplit > kDnMaxUnits || (a.Is > 0 && nu_s < kDecSdSplit) ||
-      a.H % (16 * kDnTiles))
+      a.H % (16 * kDnTiles) || a.H / (16 * kDnTiles) > kDecMaxColBlocks)
     return false;
-  a.n_rt = (a.E + (a.Is > 0 ? 1 : 0) + kRouterColsPerWg - 1) / kRouterColsPerWg;
-  a.n_sgu = a.Is / 32;
+  a.n_rt = a.E + (a.Is > 0 ? 1 : 0);
+  a.n_sgu = a.Is / 16;
   a.max_seg = std::min(a.E, a.T * a.k);
-  a.gu_pairs = a.I / 32;
-  return k12_lds(a) <= 160 * 1024 && k3_lds(a) <= 160 * 1024;
+  a.gu_tiles = a.I / 16;
+  return k1_lds(a) <= 160 * 1024 && k2_lds(a) <= 160 * 1024 && k3_lds(a) <= 160 * 1024;
 }
 
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.n_rt + a.n_sgu), block(kDecThreads);
   if (a.E <= 64)
-    hipLaunchKernelGGL(dec_k1<1>, grid, block, k12_lds(a), stream, a);
+    hipLaunchKernelGGL(dec_k1<1>, grid, block, k1_lds(a), stream, a);
   else if (a.E <= 128)
-    hipLaunchKernelGGL(dec_k1<2>, grid, block, k12_lds(a), stream, a);
+    hipLaunchKernelGGL(dec_k1<2>, grid, block, k1_lds(a), stream, a);
   else
-    hipLaunchKernelGGL(dec_k1<4>, grid, block, k12_lds(a), stream, a);
+    hipLaunchKernelGGL(dec_k1<4>, grid, block, k1_lds(a), stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(dec_k2, dim3(a.max_seg * a.gu_pairs + 1), dim3(kDecThreads), k12_lds(a), stream, a);
+  hipLaunchKernelGGL(dec_k2, dim3(a.max_seg * a.gu_tiles + 1), dim3(kDecThreads), k2_lds(a), stream, a);
   return hipGetLastError();
 }
 
@@ -581,10 +642,5 @@ hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode_k4(const DecodeArgs& a, hipStream_t stream) {
-  const int n = a.T * (a.H / 8);
-  hipLaunchKernelGGL(dec_k4, dim3((n + kDecThreads - 1) / kDecThreads), dim3(kDecThreads), 0, stream, a);
-  return hipGetLastError();
-}
 
 }  // namespace fmx

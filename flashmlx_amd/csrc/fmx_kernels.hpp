@@ -121,10 +121,8 @@ constexpr int kDecMaxT = 16;            // tokens
 constexpr int kDecMaxK = 16;            // top-k
 constexpr int kDecMaxE = 256;           // experts
 constexpr int kDecThreads = 256;        // K1, K2 workgroups
-constexpr int kDecSdSplit = 4;         // K slices of the shared expert's down projection
-constexpr int kDecRouterLpBytes = kDecMaxT * 4 * 64 * 8;  // K1/K2 LDS ahead of the staged rows
-                                        // (router lane partials; pair reductions)
-constexpr int kDecRouterChunks = 2;     // 16-byte chunks per lane of half a router row (H <= 2048)
+constexpr int kDecSdSplit = 4;          // K slices of the shared expert's down projection
+constexpr int kDecMaxColBlocks = 32;    // 64-column blocks of H (K3 arrival counters)
 constexpr int kPackedBlockSingle = 1152;  // bytes of one (16-row tile, 128-k unit) block
 constexpr int kPackedBlockPair = 2304;    // gate + up
 
@@ -141,9 +139,11 @@ struct DecodeArgs {
   const uint8_t* sgu;       // packed shared gate/up pair
   const uint8_t* sdn;       // packed shared down
   uint16_t* logits;         // [T, E+1] bf16 (column E: shared gate logit)
+  uint32_t* lgw;            // [E+1][T] the same logits (low halves), between K1 workgroups
   uint16_t* hs;             // [T, Is] shared SwiGLU output
   uint16_t* h;              // [T*k, I] routed SwiGLU output, entry order
-  uint16_t* d;              // [T*k, H] routed down projections, entry order
+  uint32_t* dw;             // [T*k, H] routed down projections, entry order, bf16 in the
+                            //   low halves (written and read with device-scope accesses)
   float* sd_part;           // [kDecSdSplit, T, H] shared down projection, fp32 K-slice sums
   uint32_t* inds;           // [T, k]
   uint16_t* scores;         // [T, k] bf16
@@ -153,17 +153,17 @@ struct DecodeArgs {
   uint32_t* seg;            // [1 + max_seg]: U, then the routed experts ascending
   uint8_t* slots;           // [max_seg][16]: slot of token t for routed expert u, or 0xff
   uint32_t* counter;        // router arrival counter: zero on entry, zero on exit
+  uint32_t* cb_counter;     // [H / 64] K3 arrivals per column block: zero on entry and exit
   uint16_t* y;              // [T, H] bf16
   // launch shape (decode_plan)
-  int n_rt, n_sgu;          // K1: router workgroups (one per column), shared gate/up pairs
-  int max_seg, gu_pairs;    // K2: expert slots x tile pairs
+  int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
+  int max_seg, gu_tiles;    // K2: expert slots x gate/up tile pairs
 };
 // Fills the launch shape; false when the shapes are outside the decode path.
 bool decode_plan(DecodeArgs& a);
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream);
-hipError_t launch_decode_k4(const DecodeArgs& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- prefill (T > 16)
 // The expert GEMMs of the MoE block for prefill on packed weights

@@ -99,7 +99,8 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
                                                        int64_t e, uint8_t* s_pf) {
   constexpr int NB = pf_nb<DUAL>(), NM = DUAL ? 2 : 1;
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
-  constexpr int PER = MT + NB * NM + 1;  // LDS DMA instructions per wave and unit
+  constexpr int PA = (4 * MT + kPfWaves - 1) / kPfWaves;  // 4-row pieces per wave and unit
+  constexpr int PER = PA + NB * NM + 1;                  // LDS DMA instructions per wave and unit
   static_assert(NB * NM == 4, "four 1 KB weight pieces per wave and unit");
 
   const int lane = threadIdx.x & 63;
@@ -115,9 +116,9 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 #pragma unroll
   for (int b = 0; b < NB; ++b)
     bsrc[b] = wexp + static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * nu * BB;
-  const uint16_t* asrc[MT];
+  const uint16_t* asrc[PA];
 #pragma unroll
-  for (int pc = 0; pc < MT; ++pc) {
+  for (int pc = 0; pc < PA; ++pc) {
     const int r = 4 * (pc * kPfWaves + wave) + j;  // pass row of this lane's chunk
     const int rr = min(r, rows - 1);               // rows past the pass repeat its last
     int64_t xr = row0 + rr;
@@ -136,7 +137,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   auto issue = [&](int u, int st) {
     uint8_t* sa = s_pf + st * kPfStageBytes;
 #pragma unroll
-    for (int pc = 0; pc < MT; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
+    for (int pc = 0; pc < PA; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
     uint8_t* sb = sa + kPfABytes + wave * kPfWaveBBytes;
     const int64_t uo = static_cast<int64_t>(u) * BB;
 #pragma unroll
@@ -282,7 +283,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
     case 3: pf_item<DUAL, 3>(P, ng, row0, rows, e, s_pf); break;
     case 4: pf_item<DUAL, 4>(P, ng, row0, rows, e, s_pf); break;
     case 5:
-    case 6: pf_item<DUAL, (kPfMT >= 6 ? 6 : 4)>(P, ng, row0, rows, e, s_pf); break;
+    case 6: pf_item<DUAL, (kPfMT >= 6 ? 6 : kPfMT)>(P, ng, row0, rows, e, s_pf); break;
     default: pf_item<DUAL, kPfMT>(P, ng, row0, rows, e, s_pf); break;
   }
 }

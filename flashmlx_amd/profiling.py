@@ -23,8 +23,7 @@ import sys
 STAGE_OF = [
     (r"dec_k1", "router+shared_gate_up"),
     (r"dec_k2", "gate_up"),
-    (r"dec_k3", "down"),
-    (r"dec_k4", "combine"),
+    (r"dec_k3", "down+combine"),
     (r"router_kernel|sort_kernel", "router+sort"),
     (r"pf_gemm<true", "gate_up"),
     (r"pf_gemm<false", "down"),

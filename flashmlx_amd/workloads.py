@@ -239,8 +239,7 @@ def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = Fa
             ("router+shared_gate_up", router_b + 2 * pw(Is, H) + x_b + T * (E + 1) * 2 + hs_b,
              router_f + sgu_f),
             ("gate_up", U * 2 * pw(I, H) + x_b + h_b, gu_f),
-            ("down", U * pw(H, I) + (pw(H, Is) if Is else 0) + h_b + hs_b + d_b + sd_b, dn_f + sdn_f),
-            ("combine", d_b + sd_b + y_b, 0),
+            ("down+combine", U * pw(H, I) + (pw(H, Is) if Is else 0) + h_b + hs_b + y_b, dn_f + sdn_f),
         ]
     return [
         ("router+sort", router_b + x_b + x_b, router_f),
