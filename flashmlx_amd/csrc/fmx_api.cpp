@@ -123,7 +123,10 @@ int bind_workspace(Arena& ar, void* ws, size_t ws_bytes, size_t need, hipStream_
 constexpr int64_t kMoEMaxTokens = 65536;
 // K slices of the shared expert's down projection (K = Is is long, N = H short)
 constexpr int kSharedDownSplit = kDecSdSplit;
-constexpr size_t kCounterBytes = (kMoEMaxTokens / kRouterTok + 64) * sizeof(uint32_t);
+// the routers' arrival counters (1 + T / kRouterTok at most), then the
+// decode combine's per-column-block counters
+constexpr size_t kRouterCounterWords = kMoEMaxTokens / kRouterTok + 64;
+constexpr size_t kCounterBytes = (kRouterCounterWords + kDecMaxColBlocks * kDecCbStride) * sizeof(uint32_t);
 
 struct MoELayout {
   uint32_t* counters;
@@ -867,8 +870,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.seg = L.seg;
     da.slots = L.slots;
     da.counter = L.counters;
-    // the last entries: the routers' arrival counters stop at 1 + T / kRouterTok
-    da.cb_counter = L.counters + kCounterBytes / 4 - kDecMaxColBlocks;
+    da.cb_counter = L.counters + kRouterCounterWords;
     da.y = static_cast<uint16_t*>(y);
     if (decode_plan(da)) {
       FMX_HIP(mark(0));

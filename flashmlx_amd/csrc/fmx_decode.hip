@@ -437,6 +437,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
 
 constexpr int kDnTiles = 4;  // 16-row tiles of H per K3 workgroup (one per wave)
 constexpr int kDnMaxUnits = 16;
+constexpr int kDnSmallUnits = 12;  // a ring this short leaves room for four workgroups per CU
 
 // The top-k weighted combine of column block cb (columns 64 cb .. 64 cb + 63)
 // for every token (model.cpp:782-803): y = bf16(sum over slots, fp32 in slot
@@ -501,18 +502,21 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t target = static_cast<uint32_t>(U + (a.Is > 0 ? kDecSdSplit : 0));
-    s_last_cb = __hip_atomic_fetch_add(a.cb_counter + cb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == target - 1;
+    s_last_cb = __hip_atomic_fetch_add(a.cb_counter + cb * kDecCbStride, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == target - 1;
   }
   __syncthreads();
   if (!s_last_cb) return;
   dec_combine(a, cb);
-  if (threadIdx.x == 0) __hip_atomic_store(a.cb_counter + cb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.cb_counter + cb * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Routed expert number u, columns 64*cb .. 64*cb + 63 of H (model.cpp:718-721):
 // d[t*k + slot, n] = h[t*k + slot] . Wd_e[n] for the tokens t that selected
 // expert e. Wave w computes tile 4*cb + w over the whole of I in one batch of
 // loads; the tokens' h rows are staged in LDS (rows indexed by token).
+template <int NU>
 __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -533,7 +537,7 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_a + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = acc;
-  tile_units_lds<false, kDnMaxUnits>(tb, 0, nu, xl, lane, acc, unused);
+  tile_units_lds<false, NU>(tb, 0, nu, xl, lane, acc, unused);
   const int n = tile * 16 + m;
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll
@@ -549,6 +553,7 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
 
 // Shared expert down projection, columns 64*cb .. +63, K slice ks of
 // kDecSdSplit (model.cpp:746-747): fp32 partial sums sd_part[ks][t][n].
+template <int NU>
 __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s_a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -562,7 +567,7 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_a + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = acc;
-  tile_units_lds<false, kDnMaxUnits>(tb, 0, nu, xl, lane, acc, unused);
+  tile_units_lds<false, NU>(tb, 0, nu, xl, lane, acc, unused);
   const int n = tile * 16 + m;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -574,15 +579,20 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
   dec_arrive(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
 }
 
+// Workgroups [0, n_shared): the shared expert's column blocks and K slices,
+// first, since they do not depend on the routing's size; then the routed
+// experts' column blocks.
+template <int NU>
 __global__ __launch_bounds__(kDecThreads) void dec_k3(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_a = reinterpret_cast<uint16_t*>(smem);
   const int nblk = a.H / (16 * kDnTiles);
-  const int wg = blockIdx.x, n_routed = a.max_seg * nblk;
-  if (wg < n_routed)
-    dec_down_routed(a, wg / nblk, wg - (wg / nblk) * nblk, s_a);
+  const int n_shared = a.Is > 0 ? nblk * kDecSdSplit : 0;
+  const int wg = blockIdx.x;
+  if (wg < n_shared)
+    dec_down_shared<NU>(a, wg / kDecSdSplit, wg % kDecSdSplit, s_a);
   else
-    dec_down_shared(a, (wg - n_routed) / kDecSdSplit, (wg - n_routed) % kDecSdSplit, s_a);
+    dec_down_routed<NU>(a, (wg - n_shared) / nblk, (wg - n_shared) % nblk, s_a);
 }
 
 }  // namespace
@@ -638,7 +648,12 @@ hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
 hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream) {
   const int nblk = a.H / (16 * kDnTiles);
   const int n = a.max_seg * nblk + (a.Is > 0 ? nblk * kDecSdSplit : 0);
-  hipLaunchKernelGGL(dec_k3, dim3(n), dim3(kDecThreads), k3_lds(a), stream, a);
+  const int nu_s = a.Is / 128;
+  const int units = std::max(a.I / 128, (nu_s + kDecSdSplit - 1) / kDecSdSplit);
+  if (units <= kDnSmallUnits)
+    hipLaunchKernelGGL(dec_k3<kDnSmallUnits>, dim3(n), dim3(kDecThreads), k3_lds(a), stream, a);
+  else
+    hipLaunchKernelGGL(dec_k3<kDnMaxUnits>, dim3(n), dim3(kDecThreads), k3_lds(a), stream, a);
   return hipGetLastError();
 }
 

@@ -123,6 +123,9 @@ constexpr int kDecMaxE = 256;           // experts
 constexpr int kDecThreads = 256;        // K1, K2 workgroups
 constexpr int kDecSdSplit = 4;          // K slices of the shared expert's down projection
 constexpr int kDecMaxColBlocks = 32;    // 64-column blocks of H (K3 arrival counters)
+// K3 arrival counters sit kDecCbStride words (256 bytes) apart: device-scope
+// atomics on one line are served one at a time
+constexpr int kDecCbStride = 64;
 constexpr int kPackedBlockSingle = 1152;  // bytes of one (16-row tile, 128-k unit) block
 constexpr int kPackedBlockPair = 2304;    // gate + up
 
@@ -153,7 +156,7 @@ struct DecodeArgs {
   uint32_t* seg;            // [1 + max_seg]: U, then the routed experts ascending
   uint8_t* slots;           // [max_seg][16]: slot of token t for routed expert u, or 0xff
   uint32_t* counter;        // router arrival counter: zero on entry, zero on exit
-  uint32_t* cb_counter;     // [H / 64] K3 arrivals per column block: zero on entry and exit
+  uint32_t* cb_counter;     // [H / 64, stride kDecCbStride] K3 arrivals per column block: zero on entry and exit
   uint16_t* y;              // [T, H] bf16
   // launch shape (decode_plan)
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
