@@ -16,128 +16,105 @@ namespace {
 
 constexpr int kSortWaves = kSortThreads / kWave;
 
-// One walk over wave `wave`'s contiguous range of entries [r0, r1), in tiles
-// of 64: within a tile the lanes holding an equal key are found with one
-// ballot per key bit; the lowest of them (the leader) reads the wave's
-// running count of that key, hands it to the others and adds the group's
-// size. An entry's rank among the equal keys of its wave's range is then
-// running count + rank in the tile. With SCATTER, position = base[key][wave]
-// + that rank, written to the outputs.
-template <bool SCATTER>
-__device__ void sort_walk(const uint16_t* s_key, uint16_t* s_run, const uint16_t* s_base, int r0,
-                          int r1, int k, int nbits, int wave, int lane, const SortOut& o) {
-  uint16_t* run = s_run + wave * kSortMaxE;
-  for (int t0 = r0; t0 < r1; t0 += kWave) {
-    const int i = t0 + lane;
-    const bool valid = i < r1;
-    const uint32_t key = valid ? s_key[i] : 0u;
-    uint64_t eq = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (key >> b) & 1u;
-      const uint64_t m = __ballot(bit);
-      eq &= bit ? m : ~m;
-    }
-    const int leader = valid ? __ffsll(static_cast<unsigned long long>(eq)) - 1 : lane;
-    const bool lead = valid && leader == lane;
-    uint32_t v = lead ? run[key] : 0u;
-    v = __shfl(v, leader);
-    if (lead) run[key] = static_cast<uint16_t>(v + __popcll(eq));
-    if (SCATTER && valid) {
-      const uint32_t pos = s_base[key * kSortWaves + wave] + v + __popcll(eq & lanes_below(lane));
-      if (o.order) o.order[pos] = static_cast<uint32_t>(i);
-      if (o.inv) o.inv[i] = pos;
-      if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
-      if (o.idx) o.idx[pos] = key;
-    }
-  }
-}
-
 }  // namespace
 
-// Stable counting sort of n keys (< E; larger ones count as E - 1) by one
-// workgroup, in LDS: keys are read once (batched), wave w owns the entry
-// range [w * span, (w + 1) * span), a walk counts each key per wave, the
-// (key-major, wave-minor) scan of the counts gives base[key][wave], and a
-// second walk scatters. Then offsets and the segment and pass tables.
+// Stable counting sort of n keys (< E; larger ones count as E - 1), one
+// workgroup per key value e. Every workgroup histograms all keys in LDS
+// (LDS atomics; counts do not depend on order) and scans the histogram, so
+// each knows every key's first sorted position; workgroup e then walks the
+// entries in order, 1024 at a time, and gives each entry of key e its
+// position: offset[e] + the number of earlier entries of key e (a ballot
+// per wave, the waves' counts in order, a running total), which is the
+// stable order. The outputs' scattered stores spread over E workgroups.
+// Workgroup 0 writes offsets and the segment and pass counts; workgroup e
+// its own segment and passes.
 __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys, int n, int k,
                                                             int E, SortOut o) {
   __shared__ uint16_t s_key[kSortMaxN];
-  __shared__ uint16_t s_run[kSortWaves * kSortMaxE];
-  __shared__ uint16_t s_base[kSortMaxE * kSortWaves];
-  __shared__ uint32_t s_off[kSortMaxE + 1];
+  __shared__ uint32_t s_cnt[kSortMaxE];
   __shared__ uint32_t s_tmp[kSortWaves + 1];
+  __shared__ uint32_t s_wcnt[kSortWaves];
+  __shared__ uint32_t s_mine[4];  // offset, count, segment and first pass of key e
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nbits = E <= 1 ? 1 : 32 - __builtin_clz(static_cast<uint32_t>(E - 1));
+  const int e = blockIdx.x;
   const uint32_t emax = static_cast<uint32_t>(E - 1);
 
+  for (int i = tid; i < E; i += kSortThreads) s_cnt[i] = 0u;
+  __syncthreads();
 #pragma unroll 8
-  for (int i = tid; i < n; i += kSortThreads) s_key[i] = static_cast<uint16_t>(min(keys[i], emax));
-  for (int i = tid; i < kSortWaves * E; i += kSortThreads) s_run[(i / E) * kSortMaxE + i % E] = 0;
-  __syncthreads();
-
-  const int span = ((n + kSortWaves - 1) / kSortWaves + kWave - 1) / kWave * kWave;
-  const int r0 = min(wave * span, n), r1 = min(r0 + span, n);
-  sort_walk<false>(s_key, s_run, nullptr, r0, r1, k, nbits, wave, lane, o);
-  __syncthreads();
-
-  // key-major exclusive scan of the per-wave counts
-  const int total = E * kSortWaves;
-  const int per = (total + kSortThreads - 1) / kSortThreads;
-  const int beg = min(tid * per, total), end = min(beg + per, total);
-  uint32_t local = 0;
-  for (int j = beg; j < end; ++j) local += s_run[(j % kSortWaves) * kSortMaxE + j / kSortWaves];
-  uint32_t runv = block_exclusive_scan<kSortThreads>(local, s_tmp, nullptr);
-  for (int j = beg; j < end; ++j) {
-    const int e = j / kSortWaves, w = j % kSortWaves;
-    s_base[j] = static_cast<uint16_t>(runv);
-    if (w == 0) s_off[e] = runv;
-    runv += s_run[w * kSortMaxE + e];
+  for (int i = tid; i < n; i += kSortThreads) {
+    const uint32_t key = min(keys[i], emax);
+    s_key[i] = static_cast<uint16_t>(key);
+    atomicAdd(&s_cnt[key], 1u);
   }
-  if (tid == 0) s_off[E] = static_cast<uint32_t>(n);
   __syncthreads();
-  for (int e = lane; e < E; e += kWave) s_run[wave * kSortMaxE + e] = 0;  // each wave clears its row
-  for (int e = tid; e <= E; e += kSortThreads) o.offsets[e] = s_off[e];
-  __syncthreads();
-  sort_walk<true>(s_key, s_run, s_base, r0, r1, k, nbits, wave, lane, o);
 
-  // segment table of the non-empty keys, ascending, and the pass table
-  if (o.seg_off) {
-    const int eper = (E + kSortThreads - 1) / kSortThreads;
-    const int eb = min(tid * eper, E), ee = min(eb + eper, E);
-    uint32_t cnt = 0, pcnt = 0;
-    for (int e = eb; e < ee; ++e) {
-      const uint32_t c = s_off[e + 1] - s_off[e];
-      cnt += c ? 1u : 0u;
-      pcnt += (c + kPassRows - 1) / kPassRows;
-    }
-    uint32_t U = 0, NP = 0;
-    uint32_t u = block_exclusive_scan<kSortThreads>(cnt, s_tmp, &U);
-    uint32_t p = block_exclusive_scan<kSortThreads>(pcnt, s_tmp, &NP);
-    for (int e = eb; e < ee; ++e) {
-      const uint32_t off = s_off[e], c = s_off[e + 1] - off;
-      if (c) {
-        if (o.seg_exp) o.seg_exp[u] = static_cast<uint32_t>(e);
-        o.seg_off[u] = off;
-        ++u;
-        if (o.pass_tab) {
-          for (uint32_t r = 0; r < c; r += kPassRows, ++p) {
-            o.pass_tab[2 * p] = off + r;
-            o.pass_tab[2 * p + 1] = static_cast<uint32_t>(e) | (min(c - r, static_cast<uint32_t>(kPassRows)) << 16);
-          }
-        }
-      }
-    }
+  // offsets, segment numbers and first passes of every key (E <= kSortThreads)
+  const uint32_t c = tid < E ? s_cnt[tid] : 0u;
+  uint32_t U = 0, NP = 0;
+  const uint32_t off = block_exclusive_scan<kSortThreads>(c, s_tmp, nullptr);
+  const uint32_t u = block_exclusive_scan<kSortThreads>(c ? 1u : 0u, s_tmp, &U);
+  const uint32_t p = block_exclusive_scan<kSortThreads>((c + kPassRows - 1) / kPassRows, s_tmp, &NP);
+  if (tid == e) {
+    s_mine[0] = off;
+    s_mine[1] = c;
+    s_mine[2] = u;
+    s_mine[3] = p;
+  }
+  if (e == 0) {
+    if (tid < E) o.offsets[tid] = off;
     if (tid == 0) {
-      o.seg_off[U] = static_cast<uint32_t>(n);
+      o.offsets[E] = static_cast<uint32_t>(n);
+      if (o.seg_off) o.seg_off[U] = static_cast<uint32_t>(n);
       if (o.seg_n) *o.seg_n = U;
       if (o.pass_n) *o.pass_n = NP;
     }
+  }
+  __syncthreads();
+  const uint32_t my_off = s_mine[0], my_c = s_mine[1];
+  if (my_c == 0) return;  // workgroup-uniform
+  if (tid == 0 && o.seg_off) {
+    const uint32_t su = s_mine[2];
+    if (o.seg_exp) o.seg_exp[su] = static_cast<uint32_t>(e);
+    o.seg_off[su] = my_off;
+    if (o.pass_tab) {
+      uint32_t pp = s_mine[3];
+      for (uint32_t r = 0; r < my_c; r += kPassRows, ++pp) {
+        o.pass_tab[2 * pp] = my_off + r;
+        o.pass_tab[2 * pp + 1] = static_cast<uint32_t>(e) | (min(my_c - r, static_cast<uint32_t>(kPassRows)) << 16);
+      }
+    }
+  }
+
+  // the entries of key e, in order
+  uint32_t run = my_off;
+  for (int base = 0; base < n; base += kSortThreads) {
+    const int i = base + tid;
+    const bool match = i < n && s_key[i] == static_cast<uint16_t>(e);
+    const uint64_t b = __ballot(match);
+    if (lane == 0) s_wcnt[wave] = static_cast<uint32_t>(__popcll(b));
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (int w = 0; w < kSortWaves; ++w) {
+      const uint32_t cw = s_wcnt[w];
+      before += w < wave ? cw : 0u;
+      all += cw;
+    }
+    if (match) {
+      const uint32_t pos = run + before + static_cast<uint32_t>(__popcll(b & lanes_below(lane)));
+      if (o.order) o.order[pos] = static_cast<uint32_t>(i);
+      if (o.inv) o.inv[i] = pos;
+      if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
+      if (o.idx) o.idx[pos] = static_cast<uint32_t>(e);
+    }
+    run += all;
+    __syncthreads();  // s_wcnt is rewritten by the next chunk
   }
 }
 
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
                        hipStream_t stream) {
-  hipLaunchKernelGGL(sort_kernel, dim3(1), dim3(kSortThreads), 0, stream, keys, n, k, E, o);
+  hipLaunchKernelGGL(sort_kernel, dim3(E), dim3(kSortThreads), 0, stream, keys, n, k, E, o);
   return hipGetLastError();
 }
 
