@@ -197,7 +197,7 @@ struct PfArgs {
 };
 // Fills ng / max_pass of a set; items of it.
 int pf_items(PfSet& s, bool dual);
-size_t pf_lds_bytes();
+size_t pf_lds_bytes(bool dual);
 hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream);
 
 struct PackArgs {

@@ -12,17 +12,17 @@
 // Work item = one pass x one column group. A pass is at most 64 rows that
 // share an expert (the sort's pass table cuts every expert's segment of
 // sorted rows into passes; the shared expert's passes are 64 consecutive
-// tokens). A column group is 4 waves x 4 weight tiles of 16 rows: 128
-// SwiGLU columns (2 gate/up tile pairs per wave) or 256 down columns. The
+// tokens). A column group is 4 waves x 2 weight tiles of 16 rows: 64
+// SwiGLU columns (one gate/up tile pair per wave) or 128 down columns. The
 // workgroup walks K in 128-k units through a ring of LDS stages that LDS
 // DMA fills, with no registers held for loads in flight: per unit, the
 // pass's activation rows (its 16-row tiles x 256 bytes, gathered through
-// the row map) and each wave's four packed blocks (weight words, then all
-// four blocks' scale/bias words in one piece). One barrier per unit; after
-// it the unit kPfStages - 1 ahead is issued into the buffer that every wave
-// finished with in the previous iteration. Two stages (72 KB) let two
-// workgroups share a CU, so one's dequantisation overlaps the other's
-// MFMAs and loads.
+// the row map) and each wave's two packed blocks (weight words, then both
+// blocks' scale/bias words in one 4-byte-per-lane piece). One barrier per
+// unit; after it the unit kPfStages - 1 ahead is issued into the buffer
+// that every wave finished with in the previous iteration. Two stages
+// (50 KB) let three workgroups share a CU, so one's dequantisation
+// overlaps the others' MFMAs and loads.
 //
 // Activation rows sit in LDS as 16-byte chunks XOR-swizzled by row (chunk c
 // of row r at slot c ^ (r & 15)), so the 16 lanes that read one k-slice of
@@ -47,16 +47,23 @@ constexpr int kPfThreads = 256;
 constexpr int kPfWaves = kPfThreads / kWave;
 constexpr int kPfMT = kPassRows / 16;                        // 16-row tiles per pass
 constexpr int kPfABytes = kPassRows * 256;                   // a pass's rows, one unit
-// a wave's share of one unit: the weight words of its blocks (4 KB: 2 pairs
-// or 4 singles), then their (scale, bias) words (512 bytes) and 512 bytes
-// that the idle half of the DMA wave writes
-constexpr int kPfWaveBBytes = 4096 + 1024;
-constexpr int kPfStageBytes = kPfABytes + kPfWaves * kPfWaveBBytes;
 constexpr int kPfStages = 2;
 constexpr int kXcds = 8;  // MI355X: 8 XCDs, each with its own L2
 
+// Packed blocks per wave: one gate/up pair or two single blocks (2 KB of
+// weight words per unit), so a workgroup's two stages fit three workgroups
+// in a CU's LDS.
 template <bool DUAL>
-constexpr int pf_nb() { return DUAL ? 2 : 4; }  // packed blocks per wave
+constexpr int pf_nb() { return DUAL ? 1 : 2; }
+template <bool DUAL>
+constexpr int pf_nm() { return DUAL ? 2 : 1; }
+// a wave's share of one unit: its 1 KB weight pieces, then the blocks'
+// (scale, bias) words (256 bytes, one 4-byte DMA per lane)
+template <bool DUAL>
+constexpr int pf_wave_bbytes() { return pf_nb<DUAL>() * pf_nm<DUAL>() * 1024 + 256; }
+template <bool DUAL>
+constexpr int pf_stage_bytes() { return kPfABytes + kPfWaves * pf_wave_bbytes<DUAL>(); }
+
 // LDS DMA instructions one wave issues per unit: its row pieces (one per
 // 16-row tile the pass fills), the 1 KB weight pieces of its blocks and one
 // for all their (scale, bias) words. Every one runs with all lanes on: a
@@ -65,6 +72,9 @@ constexpr int pf_nb() { return DUAL ? 2 : 4; }  // packed blocks per wave
 
 __device__ inline void dma16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ inline void dma4(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
 __device__ inline uint32_t pack_bf16x2(float a, float b) {
@@ -97,11 +107,13 @@ __device__ inline bf16x8_t dq8(uint32_t w, float s, float b) {
 template <bool DUAL, int MT>
 __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, int row0, int rows,
                                                        int64_t e, uint8_t* s_pf) {
-  constexpr int NB = pf_nb<DUAL>(), NM = DUAL ? 2 : 1;
+  constexpr int NB = pf_nb<DUAL>(), NM = pf_nm<DUAL>();
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
   constexpr int PA = (4 * MT + kPfWaves - 1) / kPfWaves;  // 4-row pieces per wave and unit
   constexpr int PER = PA + NB * NM + 1;                  // LDS DMA instructions per wave and unit
-  static_assert(NB * NM == 4, "four 1 KB weight pieces per wave and unit");
+  constexpr int WB = pf_wave_bbytes<DUAL>(), SBO = NB * NM * 1024;  // wave's stage share, its sb offset
+  constexpr int STAGE = pf_stage_bytes<DUAL>();
+  static_assert(NB * NM * 128 == 256, "the blocks' (scale, bias) words fill one 4-byte DMA");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -126,25 +138,23 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     asrc[pc] = P.x + xr * P.ldx + 8 * (i16 ^ (r & 15));
   }
 
-  // the (scale, bias) piece: lane l < 32 fetches 16 bytes of block l / SBL's
-  // 16 x 8 (single) or 2 x 16 x 8 (pair) bytes; lanes 32..63 repeat lanes
-  // 0..31 into the spare 512 bytes
-  constexpr int SBL = 32 / NB;  // lanes per block
-  const int sbl = lane & 31;
-  const uint8_t* sb_src = wexp + static_cast<int64_t>(min(tile0 + sbl / SBL, P.nt - 1)) * nu * BB +
-                          NM * 1024 + 16 * (sbl % SBL);
+  // the (scale, bias) piece: lane l fetches 4 bytes of block l / SBL's
+  // 16 x 8 (single) or 2 x 16 x 8 (pair) bytes
+  constexpr int SBL = kWave / NB;  // lanes per block
+  const uint8_t* sb_src = wexp + static_cast<int64_t>(min(tile0 + lane / SBL, P.nt - 1)) * nu * BB +
+                          NM * 1024 + 4 * (lane % SBL);
 
   auto issue = [&](int u, int st) {
-    uint8_t* sa = s_pf + st * kPfStageBytes;
+    uint8_t* sa = s_pf + st * STAGE;
 #pragma unroll
     for (int pc = 0; pc < PA; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
-    uint8_t* sb = sa + kPfABytes + wave * kPfWaveBBytes;
+    uint8_t* sb = sa + kPfABytes + wave * WB;
     const int64_t uo = static_cast<int64_t>(u) * BB;
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int m = 0; m < NM; ++m) dma16(bsrc[b] + uo + m * 1024 + 16 * lane, sb + (b * NM + m) * 1024);
-    dma16(sb_src + uo, sb + 4096);
+    dma4(sb_src + uo, sb + SBO);
   };
 
   f32x4_t acc[MT][NB][NM];
@@ -174,8 +184,8 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     lds_dma_barrier();
     if (u + kPfStages - 1 < nu) issue(u + kPfStages - 1, (u + kPfStages - 1) % kPfStages);
 
-    const uint8_t* sa = s_pf + (u % kPfStages) * kPfStageBytes;
-    const uint8_t* sb = sa + kPfABytes + wave * kPfWaveBBytes;
+    const uint8_t* sa = s_pf + (u % kPfStages) * STAGE;
+    const uint8_t* sb = sa + kPfABytes + wave * WB;
     // the unit's packed words and (scale, bias) pairs; each k-slice q is
     // dequantised right before its MFMAs, so that only one slice of weights
     // is live in registers
@@ -186,7 +196,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         W[b][m] = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
-        const u32x2_t sbw = *reinterpret_cast<const u32x2_t*>(sb + 4096 + b * (NM * 128) + m * 128 + 8 * i16);
+        const u32x2_t sbw = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
         sc[b][m][0] = __uint_as_float(sbw[0] << 16);
         sc[b][m][1] = __uint_as_float(sbw[0] & 0xffff0000u);
         bi[b][m][0] = __uint_as_float(sbw[1] << 16);
@@ -299,15 +309,17 @@ int pf_items(PfSet& s, bool dual) {
   return kXcds * np * ((s.ng + kXcds - 1) / kXcds);
 }
 
-size_t pf_lds_bytes() { return static_cast<size_t>(kPfStages) * kPfStageBytes; }
+size_t pf_lds_bytes(bool dual) {
+  return static_cast<size_t>(kPfStages) * (dual ? pf_stage_bytes<true>() : pf_stage_bytes<false>());
+}
 
 hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream) {
   const int n = a.n_items0 + a.n_items1;
   if (n == 0) return hipSuccess;
   if (dual)
-    hipLaunchKernelGGL(pf_gemm<true>, dim3(n), dim3(kPfThreads), pf_lds_bytes(), stream, a);
+    hipLaunchKernelGGL(pf_gemm<true>, dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
   else
-    hipLaunchKernelGGL(pf_gemm<false>, dim3(n), dim3(kPfThreads), pf_lds_bytes(), stream, a);
+    hipLaunchKernelGGL(pf_gemm<false>, dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
   return hipGetLastError();
 }
 
