@@ -42,6 +42,14 @@ CFLAGS = [
 ]
 
 
+# per-source additions. The decode kernels fold MFMA results into their
+# accumulators with VALU FMAs: MFMAs that write VGPRs save an accumulator
+# register move per value.
+EXTRA_FLAGS = {
+    "csrc/fmx_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and pathlib.Path(cand).exists():
@@ -49,8 +57,8 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libfmx.so)")
 
 
-def _compile(cc: str, src: pathlib.Path, obj: pathlib.Path) -> tuple[str, int, str]:
-    cmd = [cc, "-x", "hip", *CFLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(cc: str, src: pathlib.Path, obj: pathlib.Path, extra: list) -> tuple[str, int, str]:
+    cmd = [cc, "-x", "hip", *CFLAGS, *extra, "-c", str(src), "-o", str(obj)]
     p = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature; that warning is expected
     err = "\n".join(
@@ -71,7 +79,7 @@ def build(verbose: bool = False) -> pathlib.Path:
             src = HERE / rel
             obj = OBJDIR / (src.name + ".o")
             objs.append(obj)
-            jobs.append(ex.submit(_compile, cc, src, obj))
+            jobs.append(ex.submit(_compile, cc, src, obj, EXTRA_FLAGS.get(rel, [])))
         failed = []
         for j in jobs:
             src, rc, err = j.result()
