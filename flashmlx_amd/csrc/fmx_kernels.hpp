@@ -31,7 +31,8 @@ __host__ __device__ inline int max_passes(int64_t n, int64_t E) {
   return static_cast<int>((n < E ? n : E) + (n + kPassRows - 1) / kPassRows);
 }
 
-// Sort in one workgroup of 1024 threads (separate launch), LDS-resident.
+// Sort by one workgroup of 1024 threads per key value (separate launch),
+// keys LDS-resident.
 constexpr int kSortThreads = 1024;
 constexpr int kSortMaxN = 32 * 1024;       // keys held in LDS (16 bits each)
 constexpr int kSortMaxE = 1024;            // per-wave key counters in LDS
@@ -115,8 +116,8 @@ hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStrea
 
 // ---------------------------------------------------------------- decode (T <= 16)
 // The MoE block for decode batches on packed weights (fmx_decode.hip):
-// K1 router + shared gate/up, K2 routed gate/up, K3 down projections,
-// K4 combine.
+// K1 router + shared gate/up, K2 routed gate/up, K3 down projections and
+// the combine.
 constexpr int kDecMaxT = 16;            // tokens
 constexpr int kDecMaxK = 16;            // top-k
 constexpr int kDecMaxE = 256;           // experts
