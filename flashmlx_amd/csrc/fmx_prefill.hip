@@ -84,19 +84,26 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
 
 // The 8 weights of a packed word (element 2i at nibble position i, 2i + 1 at
 // i + 4) as bf16(s*q + b) in natural element order. Masking the even and the
-// odd nibble positions into bytes lets v_cvt_f32_ubyte{0..3} read each
-// weight directly (bytes 0..3 of lo: elements 0, 4, 1, 5; of hi: 2, 6, 3, 7).
+// odd nibble positions into bytes gives bytes 0..3 of lo = elements 0, 4, 1,
+// 5 and of hi = 2, 6, 3, 7. A byte 0..15 is the FP8 (E4M3) encoding of
+// q * 2^-9 (the subnormal and first normal binade are evenly spaced), and
+// v_cvt_scalef32_pk_f32_fp8 converts two such bytes to fp32 with a
+// power-of-two scale, so 2^9 gives q exactly: one instruction per two
+// weights instead of one per weight. s*q + b is then one fma in fp32,
+// rounded once to bf16.
+constexpr float kFp8Q = 512.0f;  // 2^9: FP8 byte q (0..15) -> q
+
 __device__ inline bf16x8_t dq8(uint32_t w, float s, float b) {
-  uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-  // keeps the byte extracts below from folding into per-nibble bit-field
-  // extracts (one more instruction per weight)
-  asm volatile("" : "+v"(lo), "+v"(hi));
-  auto q = [](uint32_t v, int i) { return static_cast<float>((v >> (8 * i)) & 0xffu); };
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  const f32x2_t q04 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, kFp8Q, false);  // elements 0, 4
+  const f32x2_t q15 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, kFp8Q, true);   // 1, 5
+  const f32x2_t q26 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, kFp8Q, false);  // 2, 6
+  const f32x2_t q37 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, kFp8Q, true);   // 3, 7
   u32x4_t d;
-  d[0] = pack_bf16x2(__builtin_fmaf(s, q(lo, 0), b), __builtin_fmaf(s, q(lo, 2), b));
-  d[1] = pack_bf16x2(__builtin_fmaf(s, q(hi, 0), b), __builtin_fmaf(s, q(hi, 2), b));
-  d[2] = pack_bf16x2(__builtin_fmaf(s, q(lo, 1), b), __builtin_fmaf(s, q(lo, 3), b));
-  d[3] = pack_bf16x2(__builtin_fmaf(s, q(hi, 1), b), __builtin_fmaf(s, q(hi, 3), b));
+  d[0] = pack_bf16x2(__builtin_fmaf(s, q04[0], b), __builtin_fmaf(s, q15[0], b));
+  d[1] = pack_bf16x2(__builtin_fmaf(s, q26[0], b), __builtin_fmaf(s, q37[0], b));
+  d[2] = pack_bf16x2(__builtin_fmaf(s, q04[1], b), __builtin_fmaf(s, q15[1], b));
+  d[3] = pack_bf16x2(__builtin_fmaf(s, q26[1], b), __builtin_fmaf(s, q37[1], b));
   return __builtin_bit_cast(bf16x8_t, d);
 }
 
@@ -286,15 +293,13 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
     rows = min(kPassRows, P.rows_static - row0);
   }
   if (rows <= 0) return;
-  static_assert(kPfMT == 4 || kPfMT == 8, "row-tile dispatch below covers 4 or 8 tiles");
+  // one call site per tile count: each inlined copy is compiled on its own
+  static_assert(kPfMT == 4, "row-tile dispatch below covers passes of up to 4 tiles");
   switch ((rows + 15) / 16) {
     case 1: pf_item<DUAL, 1>(P, ng, row0, rows, e, s_pf); break;
     case 2: pf_item<DUAL, 2>(P, ng, row0, rows, e, s_pf); break;
     case 3: pf_item<DUAL, 3>(P, ng, row0, rows, e, s_pf); break;
-    case 4: pf_item<DUAL, 4>(P, ng, row0, rows, e, s_pf); break;
-    case 5:
-    case 6: pf_item<DUAL, (kPfMT >= 6 ? 6 : kPfMT)>(P, ng, row0, rows, e, s_pf); break;
-    default: pf_item<DUAL, kPfMT>(P, ng, row0, rows, e, s_pf); break;
+    default: pf_item<DUAL, 4>(P, ng, row0, rows, e, s_pf); break;
   }
 }
 

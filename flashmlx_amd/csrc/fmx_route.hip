@@ -382,6 +382,7 @@ __device__ void sort_small(const uint32_t* keys, int n, int k, int E, const Sort
 
 constexpr int kLgWaves = 8;
 constexpr int kLgThreads = kLgWaves * kWave;
+constexpr int kLgBatch = 8;  // 16-byte chunks of x and w in flight per lane
 
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
@@ -400,19 +401,28 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   const uint16_t* wrow = col < E ? a.wr + static_cast<int64_t>(col) * H : a.wsg;
   const int nch = H / 8;
   f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-  for (int base = 0; base < nch; base += 4 * kLgWaves) {
-    const int ch = base + 4 * wave + kk;
-    u32x4_t xv = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
-    if (ch < nch) {  // chunks past H contribute exact zeros
-      xv = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
-      wv = *reinterpret_cast<const u32x4_t*>(wrow + ch * 8);
+  // kLgBatch chunks per lane are loaded together (one memory latency per
+  // batch, not per chunk), then multiplied in the same chunk order
+  constexpr int kLgStep = 4 * kLgWaves;
+  for (int base = 0; base < nch; base += kLgStep * kLgBatch) {
+    u32x4_t xv[kLgBatch], wv[kLgBatch];
+#pragma unroll
+    for (int b = 0; b < kLgBatch; ++b) {
+      const int ch = min(base + kLgStep * b + 4 * wave + kk, nch - 1);
+      xv[b] = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
+      wv[b] = *reinterpret_cast<const u32x4_t*>(wrow + ch * 8);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const double x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
-      const double w0 = __uint_as_float(wv[i] << 16), w1 = __uint_as_float(wv[i] & 0xffff0000u);
-      acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
-      acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
+    for (int b = 0; b < kLgBatch; ++b) {
+      if (base + kLgStep * b + 4 * wave + kk >= nch)  // chunks past H contribute exact zeros
+        xv[b] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const double x0 = __uint_as_float(xv[b][i] << 16), x1 = __uint_as_float(xv[b][i] & 0xffff0000u);
+        const double w0 = __uint_as_float(wv[b][i] << 16), w1 = __uint_as_float(wv[b][i] & 0xffff0000u);
+        acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
+      }
     }
   }
   f64x4_t acc = acc0 + acc1;
