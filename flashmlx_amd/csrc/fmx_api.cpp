@@ -126,7 +126,9 @@ constexpr int kSharedDownSplit = kDecSdSplit;
 // the routers' arrival counters (1 + T / kRouterTok at most), then the
 // decode combine's per-column-block counters
 constexpr size_t kRouterCounterWords = kMoEMaxTokens / kRouterTok + 64;
-constexpr size_t kCounterBytes = (kRouterCounterWords + kDecMaxColBlocks * kDecCbStride) * sizeof(uint32_t);
+constexpr size_t kCbCounterWords = static_cast<size_t>(kDecMaxColBlocks) * kDecCbStride;
+constexpr size_t kGuCounterWords = static_cast<size_t>(kDecMaxE) * kDecGuWords;
+constexpr size_t kCounterBytes = (kRouterCounterWords + kCbCounterWords + kGuCounterWords) * sizeof(uint32_t);
 
 struct MoELayout {
   uint32_t* counters;
@@ -871,17 +873,22 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.slots = L.slots;
     da.counter = L.counters;
     da.cb_counter = L.counters + kRouterCounterWords;
+    da.gu_counter = L.counters + kRouterCounterWords + kCbCounterWords;
     da.y = static_cast<uint16_t*>(y);
     if (decode_plan(da)) {
       FMX_HIP(mark(0));
       FMX_HIP(launch_decode_k1(da, stream));
       FMX_HIP(mark(1));
       if (n_stages < 2) return ok();
-      FMX_HIP(launch_decode_k2(da, stream));
+      if (n_stages < 3) {  // gate/up alone
+        FMX_HIP(launch_decode_k2(da, stream));
+        FMX_HIP(mark(2));
+        return ok();
+      }
+      // gate/up, down and combine in one grid
+      FMX_HIP(launch_decode_k23(da, stream));
       FMX_HIP(mark(2));
-      if (n_stages < 3) return ok();
-      FMX_HIP(launch_decode_k3(da, stream));
-      FMX_HIP(mark(3));  // the combine runs inside K3
+      FMX_HIP(mark(3));
       FMX_HIP(mark(4));
       return ok();
     }

@@ -15,13 +15,24 @@
 // gather_qmm gate/up/down, SwiGLU), :736-748 (shared_expert_mlp), :14-25
 // (compiled SwiGLU), :757-775 (router), :682-700 (sort).
 //
+// A whole forward runs K2 and K3 as one grid (K23): the gate/up tiles first,
+// then the down workgroups, which start streaming their weights while the
+// last gate/up tiles finish and wait (bounded) only for their own expert's
+// h rows. A forward that stops after the gate/up stage runs K2 alone.
+//
 // Rows of every MFMA tile are indexed by token: a token selects an expert at
 // most once, so expert e's tile rows are the tokens that routed to it and no
 // gather or sort is needed for the products. Workgroups of one kernel hand
-// data over in two places, K1's logits and K3's column blocks, both the same
-// way: device-scope stores, a wait for their completion, then a device-scope
-// arrival counter; the last arrival reads with device-scope loads. No
-// workgroup ever waits for another.
+// data over in three places, K1's logits, K23's h rows and K3's column
+// blocks, all the same way: device-scope stores, a wait for their
+// completion, then a device-scope arrival counter. For the logits and the
+// column blocks the last arrival does the consuming work; K23's down
+// workgroups instead poll their expert's done flag. A down workgroup waits
+// only on gate/up tiles with lower indices, and tiles never wait. Each XCD
+// dispatches its workgroups in index order, so when the lowest-indexed
+// waiting workgroup waits, every XCD has dispatched each tile it waits on
+// (an XCD whose slots all hold waiting workgroups has dispatched everything
+// below their indices): those tiles finish and the wait ends.
 #include <algorithm>
 
 #include "fmx_dev.hpp"
@@ -217,6 +228,9 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
     a.logits[t * ld + c] = v;
   }
   for (int e = tid; e < E; e += kDecThreads) s_used[e] = 0;
+  // K23's per-expert gate/up counters and done flags start the next grid at zero
+  for (int i = tid; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads)
+    __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
   for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
@@ -385,19 +399,21 @@ __device__ void dec_sort(const DecodeArgs& a) {
 // Routed expert number u, gate/up tile pair tp (h columns 16 tp .. 16 tp + 15),
 // one per workgroup: wave w multiplies K quarter w (model.cpp:703-715). Small
 // equal workgroups keep the grid's last round nearly full. The last
-// workgroup runs the sort for the routing accessors.
-__global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// workgroup runs the sort for the routing accessors. SIGNAL (in K23): the h
+// values go out as device-scope stores and, once they have completed, the
+// tile is counted in on its expert's gate/up counter.
+template <bool SIGNAL>
+__device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, I = a.I, xs = xstride(H);
-  if (blockIdx.x == a.max_seg * a.gu_tiles) {
+  if (b == a.max_seg * a.gu_tiles) {
     dec_sort(a);
     return;
   }
-  const int u = blockIdx.x / a.gu_tiles, tp = blockIdx.x - u * a.gu_tiles;
+  const int u = b / a.gu_tiles, tp = b - u * a.gu_tiles;
   // routing tables first: a workgroup without an expert leaves before it
   // starts any LDS DMA
   const int U = static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg)));
@@ -428,9 +444,33 @@ __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
     const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k))
-      a.h[static_cast<int64_t>(t * k + slot) * I + n] = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
+    if (t < T && slot < static_cast<uint32_t>(k)) {
+      uint16_t* dst = a.h + static_cast<int64_t>(t * k + slot) * I + n;
+      const uint16_t v = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
+      if (SIGNAL)
+        __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else
+        *dst = v;
+    }
   }
+  if (SIGNAL) {
+    wait_vmcnt0();  // wave 0's device-scope stores have completed
+    if (lane == 0) {
+      uint32_t* g = a.gu_counter + u * kDecGuWords;
+      const uint32_t prev = __hip_atomic_fetch_add(g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (prev == static_cast<uint32_t>(a.gu_tiles - 1)) {  // the expert's last tile: every h store is done
+#pragma unroll
+        for (int c = 1; c <= kDecGuFlags; ++c)
+          __hip_atomic_store(g + c * kDecCbStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// K2 alone (forwards that stop after the gate/up stage)
+__global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  dec_gu_tile<false>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- K3: down projections
@@ -516,6 +556,16 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
 // d[t*k + slot, n] = h[t*k + slot] . Wd_e[n] for the tokens t that selected
 // expert e. Wave w computes tile 4*cb + w over the whole of I in one batch of
 // loads; the tokens' h rows are staged in LDS (rows indexed by token).
+//
+// h is written by gate/up workgroups of the same grid (K23). Wave 0 reads
+// one copy of its expert's done flag, then every wave issues its weight
+// loads (they do not depend on h); loads complete in order, so the flag's
+// value is in while the weights are still in flight. Until the flag is set,
+// wave 0 polls it (s_sleep between reads, at most kDecWaitPolls reads: far
+// beyond any real wait, a guard against a hang) while the other waves wait at
+// a barrier. Then every wave fetches its h rows with device-scope DMA.
+constexpr int kDecWaitPolls = 1 << 21;
+
 template <int NU>
 __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_a) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -526,18 +576,42 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
   const int e = static_cast<int>(min(a.seg[1 + u], static_cast<uint32_t>(a.E - 1)));
   const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.slots + u * kDecMaxT);
   const uint32_t slot4 = srow[lane & 3];
-  // tokens' h rows -> LDS rows t (rows of tokens that did not select e stay
-  // unset: their products land in output rows that are never stored)
-  for (int t = wave; t < T; t += kDecWaves) {
-    const uint32_t slot = (__shfl(slot4, t >> 2) >> (8 * (t & 3))) & 0xffu;
-    if (slot < static_cast<uint32_t>(k)) dma_row(a.h + static_cast<int64_t>(t * k + slot) * I, I, s_a + t * xs, lane);
-  }
   const int nu = I / 128, tile = kDnTiles * cb + wave;
   const uint8_t* tb = a.dn + static_cast<int64_t>(e) * a.dn_es + static_cast<int64_t>(tile) * nu * kBlockSingle;
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_a + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = acc;
-  tile_units_lds<false, NU>(tb, 0, nu, xl, lane, acc, unused);
+  const uint32_t* flag = a.gu_counter + u * kDecGuWords + (1 + cb % kDecGuFlags) * kDecCbStride;
+  uint32_t done = 0;
+  if (wave == 0) done = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  PkUnit<false> L[NU];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < NU; ++d) L[d] = pk_load<false>(tb + min(d, nu - 1) * kBlockSingle, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  if (wave == 0) {
+    done = __builtin_amdgcn_readfirstlane(done);
+    for (int poll = 1; done == 0 && poll < kDecWaitPolls; ++poll) {
+      __builtin_amdgcn_s_sleep(16);
+      done = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+  }
+  lds_dma_barrier();  // wave 0 has seen the flag (no wait for the weights in flight)
+  for (int t = wave; t < T; t += kDecWaves) {
+    const uint32_t slot = (__shfl(slot4, t >> 2) >> (8 * (t & 3))) & 0xffu;
+    if (slot < static_cast<uint32_t>(k))
+      dma_row<kCpolDevice>(a.h + static_cast<int64_t>(t * k + slot) * I, I, s_a + t * xs, lane);
+  }
+  wait_vmcnt0();
+  lds_dma_barrier();
+#pragma unroll
+  for (int d = 0; d < NU; ++d) {
+    if (d < nu) {
+      bf16x8_t A[4];
+      lds_a(xl + d * 128, A);
+      pk_unit<false>(L[d], A, acc, unused);
+    }
+  }
   const int n = tile * 16 + m;
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll
@@ -579,20 +653,27 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
   dec_arrive(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
 }
 
-// Workgroups [0, n_shared): the shared expert's column blocks and K slices,
-// first, since they do not depend on the routing's size; then the routed
-// experts' column blocks.
+// K23 in dispatch order: K2's workgroups (the gate/up tiles, expert-major,
+// then the sort), the shared expert's down workgroups (they wait for
+// nothing), then the routed down workgroups, expert-major, so that the
+// experts whose tiles were dispatched first are the first waited on.
+// (Dispatching an expert's down workgroups right behind its tiles, about one
+// resident grid later, measured slower: their waits hold slots that the
+// tiles still need.)
 template <int NU>
-__global__ __launch_bounds__(kDecThreads) void dec_k3(DecodeArgs a) {
+__global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_a = reinterpret_cast<uint16_t*>(smem);
-  const int nblk = a.H / (16 * kDnTiles);
-  const int n_shared = a.Is > 0 ? nblk * kDecSdSplit : 0;
-  const int wg = blockIdx.x;
-  if (wg < n_shared)
-    dec_down_shared<NU>(a, wg / kDecSdSplit, wg % kDecSdSplit, s_a);
+  const int D = a.H / (16 * kDnTiles);
+  const int n_gu = a.max_seg * a.gu_tiles + 1;
+  const int n_shared = a.Is > 0 ? D * kDecSdSplit : 0;
+  const int b = blockIdx.x;
+  if (b < n_gu)
+    dec_gu_tile<true>(a, b, smem);
+  else if (b - n_gu < n_shared)
+    dec_down_shared<NU>(a, (b - n_gu) / kDecSdSplit, (b - n_gu) % kDecSdSplit, s_a);
   else
-    dec_down_routed<NU>(a, (wg - n_shared) / nblk, (wg - n_shared) % nblk, s_a);
+    dec_down_routed<NU>(a, (b - n_gu - n_shared) / D, (b - n_gu - n_shared) % D, s_a);
 }
 
 }  // namespace
@@ -645,15 +726,23 @@ hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream) {
+static int k3_workgroups(const DecodeArgs& a) {
   const int nblk = a.H / (16 * kDnTiles);
-  const int n = a.max_seg * nblk + (a.Is > 0 ? nblk * kDecSdSplit : 0);
+  return a.max_seg * nblk + (a.Is > 0 ? nblk * kDecSdSplit : 0);
+}
+
+static bool k3_small_ring(const DecodeArgs& a) {
   const int nu_s = a.Is / 128;
-  const int units = std::max(a.I / 128, (nu_s + kDecSdSplit - 1) / kDecSdSplit);
-  if (units <= kDnSmallUnits)
-    hipLaunchKernelGGL(dec_k3<kDnSmallUnits>, dim3(n), dim3(kDecThreads), k3_lds(a), stream, a);
+  return std::max(a.I / 128, (nu_s + kDecSdSplit - 1) / kDecSdSplit) <= kDnSmallUnits;
+}
+
+hipError_t launch_decode_k23(const DecodeArgs& a, hipStream_t stream) {
+  const int n = a.max_seg * a.gu_tiles + 1 + k3_workgroups(a);
+  const size_t lds = std::max(k2_lds(a), k3_lds(a));
+  if (k3_small_ring(a))
+    hipLaunchKernelGGL(dec_k23<kDnSmallUnits>, dim3(n), dim3(kDecThreads), lds, stream, a);
   else
-    hipLaunchKernelGGL(dec_k3<kDnMaxUnits>, dim3(n), dim3(kDecThreads), k3_lds(a), stream, a);
+    hipLaunchKernelGGL(dec_k23<kDnMaxUnits>, dim3(n), dim3(kDecThreads), lds, stream, a);
   return hipGetLastError();
 }
 

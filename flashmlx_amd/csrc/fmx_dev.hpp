@@ -184,13 +184,17 @@ __device__ inline double reduce_scatter64(double (&v)[N], int lane) {
 // global_load_lds_dwordx4 moves a wave's 64 x 16 bytes (a 1 KB piece of the
 // row) straight into LDS, with no registers and no wait at the issuing point;
 // in a last, partial piece the lanes past the row's end do not take part.
-// Called by one whole wave (dst must be wave-uniform).
+// Called by one whole wave (dst must be wave-uniform). CPOL is the loads'
+// cache policy: kCpolDevice (sc1) reads data that other workgroups of the
+// same grid wrote with device-scope stores.
+constexpr int kCpolDevice = 16;
+template <int CPOL = 0>
 __device__ inline void dma_row(const uint16_t* src, int K, uint16_t* s_dst, int lane) {
   for (int pc = 0; pc * 512 < K; ++pc) {
     if (pc * 512 + 8 * lane < K)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + pc * 512 + 8 * lane),
                                        (__attribute__((address_space(3))) void*)(s_dst + pc * 512),
-                                       16, 0, 0);
+                                       16, 0, CPOL);
   }
 }
 

@@ -117,7 +117,7 @@ hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStrea
 // ---------------------------------------------------------------- decode (T <= 16)
 // The MoE block for decode batches on packed weights (fmx_decode.hip):
 // K1 router + shared gate/up, K2 routed gate/up, K3 down projections and
-// the combine.
+// the combine; a whole forward runs K2 and K3 as one grid (K23).
 constexpr int kDecMaxT = 16;            // tokens
 constexpr int kDecMaxK = 16;            // top-k
 constexpr int kDecMaxE = 256;           // experts
@@ -127,6 +127,12 @@ constexpr int kDecMaxColBlocks = 32;    // 64-column blocks of H (K3 arrival cou
 // K3 arrival counters sit kDecCbStride words (256 bytes) apart: device-scope
 // atomics on one line are served one at a time
 constexpr int kDecCbStride = 64;
+// K23 per routed expert: the gate/up tiles' arrival counter, then
+// kDecGuFlags copies of a done flag that the last tile sets (the down
+// workgroups poll the copies, spread over separate lines, and never the line
+// the tiles count on); each on its own kDecCbStride-word line
+constexpr int kDecGuFlags = 4;
+constexpr int kDecGuWords = (1 + kDecGuFlags) * kDecCbStride;
 constexpr int kPackedBlockSingle = 1152;  // bytes of one (16-row tile, 128-k unit) block
 constexpr int kPackedBlockPair = 2304;    // gate + up
 
@@ -158,6 +164,8 @@ struct DecodeArgs {
   uint8_t* slots;           // [max_seg][16]: slot of token t for routed expert u, or 0xff
   uint32_t* counter;        // router arrival counter: zero on entry, zero on exit
   uint32_t* cb_counter;     // [H / 64, stride kDecCbStride] K3 arrivals per column block: zero on entry and exit
+  uint32_t* gu_counter;     // [max_seg][kDecGuWords] K23: gate/up tiles finished per routed expert
+                            //   and their done flags; K1 zeroes them for every forward
   uint16_t* y;              // [T, H] bf16
   // launch shape (decode_plan)
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
@@ -167,7 +175,7 @@ struct DecodeArgs {
 bool decode_plan(DecodeArgs& a);
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream);
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream);
-hipError_t launch_decode_k3(const DecodeArgs& a, hipStream_t stream);
+hipError_t launch_decode_k23(const DecodeArgs& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- prefill (T > 16)
 // The expert GEMMs of the MoE block for prefill on packed weights

@@ -22,8 +22,8 @@ import sys
 # kernel name -> MoE stage (the four kernel stages of fmx_moe_block_forward)
 STAGE_OF = [
     (r"dec_k1", "router+shared_gate_up"),
-    (r"dec_k2", "gate_up"),
-    (r"dec_k3", "down+combine"),
+    (r"dec_k23", "gate_up+down+combine"),
+    (r"dec_k2", "gate_up"),  # launched alone only by forwards that stop after gate/up
     (r"router_kernel|sort_kernel", "router+sort"),
     (r"pf_gemm<true", "gate_up"),
     (r"pf_gemm<false", "down"),

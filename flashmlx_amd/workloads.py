@@ -213,6 +213,16 @@ def decode_path(m: dict, tokens: int, packed: bool = True) -> bool:
     return forward_path(m, tokens, packed) == "decode"
 
 
+def kernel_groups(m: dict, tokens: int, packed: bool = True) -> list:
+    """The kernels of a whole forward as [(name, [stage indices of
+    stage_work])]: on the decode path gate/up, down and combine run as one
+    grid, so its time in the layer is the marginal time of those stages
+    together; elsewhere each stage is its own kernel group."""
+    if decode_path(m, tokens, packed):
+        return [("router+shared_gate_up", [0]), ("gate_up+down+combine", [1, 2])]
+    return [("router+sort", [0]), ("gate_up", [1]), ("down", [2]), ("combine", [3])]
+
+
 def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = False,
                packed: bool = True) -> list:
     """Algorithmic work of each kernel stage of one MoE-layer call, in launch

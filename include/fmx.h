@@ -223,9 +223,9 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
  * (hipEvent_t, as void*) on `stream` at its stage boundaries:
  *   stage_events[0] before the router, [1] after routing and sort,
  *   [2] after the gate/up GEMMs, [3] after the down GEMMs, [4] after the
- *   combine (for n_tokens <= 16 on packed weights the combine runs inside
- *   the down kernel and [3], [4] are recorded together). Used to time each
- *   stage's kernels; no counterpart in the reference. */
+ *   combine (for n_tokens <= 16 on packed weights gate/up, down and combine
+ *   run as one grid and [2], [3], [4] are recorded together after it). Used
+ *   to time each stage's kernels; no counterpart in the reference. */
 #define FMX_MOE_STAGE_EVENTS 5
 int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weights* w,
                                    const void* x, int64_t n_tokens, void* y, void* workspace,
@@ -234,7 +234,8 @@ int fmx_moe_block_forward_profiled(const fmx_moe_config* cfg, const fmx_moe_weig
 
 /* fmx_moe_block_forward that launches only its first n_stages kernel stages
  * (1..4: router, gate/up, down, combine; 4 = the whole forward, y complete;
- * for n_tokens <= 16 on packed weights 3 already completes y).
+ * for n_tokens <= 16 on packed weights 2 runs the gate/up kernel alone and
+ * 3 already runs the whole forward's gate/up + down + combine grid).
  * Timing graphs of 1, 2, 3 and 4 stages gives each stage's marginal time
  * inside the layer. No counterpart in the reference (a measurement aid). */
 int fmx_moe_block_forward_partial(const fmx_moe_config* cfg, const fmx_moe_weights* w,
