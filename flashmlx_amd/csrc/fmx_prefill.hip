@@ -210,6 +210,16 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
         bi[b][m][1] = __uint_as_float(sbw[1] & 0xffff0000u);
       }
     }
+    // every activation operand of the unit is read up front (one LDS round
+    // trip per unit, not one per k-slice); the first slice's dequantisation
+    // runs while they land
+    bf16x8_t A[4][MT];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       bf16x8_t B[NB][NM];
@@ -218,14 +228,11 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 #pragma unroll
         for (int m = 0; m < NM; ++m) B[b][m] = dq8(W[b][m][q], sc[b][m][q >> 1], bi[b][m][q >> 1]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const bf16x8_t A =
-            *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int m = 0; m < NM; ++m) acc[mt][b][m] = mfma_bf16(A, B[b][m], acc[mt][b][m]);
-      }
+          for (int m = 0; m < NM; ++m) acc[mt][b][m] = mfma_bf16(A[q][mt], B[b][m], acc[mt][b][m]);
     }
   }
 
