@@ -58,6 +58,9 @@ WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
              note="prefill 512 tokens, per-expert router logit bias ~ N(0,1)"),
     Workload("qwen3_decode_b1", QWEN3, 1, 4, note="decode batch 1"),
     Workload("qwen3_decode_b8", QWEN3, 8, 4, note="decode batch 8"),
+    Workload("qwen15_decode_b16", QWEN15, 16, 6, router_bias=True,
+             note="decode batch 16 (the largest decode batch), per-expert router logit bias ~ N(0,1)"),
+    Workload("qwen3_decode_b16", QWEN3, 16, 7, note="decode batch 16 (up to 128 routed experts)"),
     Workload("qwen3_prefill_1024", QWEN3, 1024, 4, note="prefill 1024 tokens"),
     Workload("tiny_t5", TINY, 5, 11, note="tiny shapes, 5 tokens"),
     Workload("tiny_t40", TINY, 40, 12, router_bias=True, note="tiny shapes, 40 tokens, skewed"),

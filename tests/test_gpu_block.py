@@ -34,6 +34,7 @@ CASES = [("tiny_t5", True), ("tiny_t5", False), ("tiny_t40", True), ("tiny_norm_
          ("qwen15_decode_b8", True), ("qwen15_decode_b8", False), ("qwen15_prefill_512", True),
          ("qwen15_prefill_512", False),
          ("qwen3_decode_b1", True), ("qwen3_decode_b8", True), ("qwen3_decode_b8", False),
+         ("qwen15_decode_b16", True), ("qwen3_decode_b16", True),
          ("qwen3_prefill_1024", True)]
 
 
