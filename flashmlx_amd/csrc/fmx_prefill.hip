@@ -260,9 +260,10 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 }
 
 // Block -> work item. The hardware dispatches block b to XCD b % 8, each
-// XCD taking its blocks in order. Routed passes go to XCDs round-robin and
-// an XCD runs all column groups of one pass back to back, so the pass's
-// rows are fetched into that XCD's L2 once; the shared expert's column
+// XCD taking its blocks in order. Each XCD takes a contiguous eighth of the
+// routed passes and runs all column groups of one pass back to back, so the
+// pass's rows are fetched into that XCD's L2 once and an expert's further
+// passes find its weights there; the shared expert's column
 // groups go round-robin and an XCD runs all passes of one group back to
 // back, so the group's weights are fetched once. Blocks past the work
 // (padding, passes the sort did not fill) exit.
@@ -276,7 +277,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   const int x = b % kXcds, l = b / kXcds;
   int pass, ng;
   if (P.pass_n) {
-    pass = x + kXcds * (l / P.ng);
+    // XCD x takes a contiguous range of the pass table, so an expert's
+    // passes (consecutive in the table) run back to back on one L2
+    const int npass = min(static_cast<int>(*P.pass_n), P.max_pass);
+    const int per = (npass + kXcds - 1) / kXcds;
+    if (l / P.ng >= per) return;
+    pass = x * per + l / P.ng;
     ng = l % P.ng;
   } else {
     const int np = (P.rows_static + kPassRows - 1) / kPassRows;

@@ -24,7 +24,7 @@ STAGE_OF = [
     (r"dec_k1", "router+shared_gate_up"),
     (r"dec_k23", "gate_up+down+combine"),
     (r"dec_k2", "gate_up"),  # launched alone only by forwards that stop after gate/up
-    (r"router_kernel|sort_kernel", "router+sort"),
+    (r"router_kernel|logits_kernel|topk_kernel|sort_kernel", "router+sort"),
     (r"pf_gemm<true", "gate_up"),
     (r"pf_gemm<false", "down"),
     (r"qgemm_kernel<true", "gate_up"),
