@@ -31,6 +31,10 @@ TINY_NORM = dict(name="tiny-norm", hidden=320, n_experts=12, top_k=3, inter=192,
 # H = 384 leaves the down projection's last column group part-filled
 SMALL = dict(name="small", hidden=384, n_experts=6, top_k=2, inter=256, shared_inter=256,
              norm_topk=False)
+# the smallest shapes that the packed-weight decode kernels take (H a multiple
+# of 512, the shared expert's down projection split four ways)
+SMALL_DEC = dict(name="small-dec", hidden=512, n_experts=8, top_k=2, inter=256, shared_inter=512,
+                 norm_topk=False)
 
 # synth stream ids, one per tensor
 S_X, S_ROUTER, S_RBIAS = 1, 2, 3
@@ -69,6 +73,7 @@ WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
              note="packable small shapes, 23 tokens (one pass per expert)"),
     Workload("small_t200", SMALL, 200, 15,
              note="packable small shapes, 200 tokens (experts over several passes)"),
+    Workload("small_dec_t4", SMALL_DEC, 4, 16, note="small shapes on the decode kernels, 4 tokens"),
 ]}
 
 

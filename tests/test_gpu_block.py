@@ -29,6 +29,7 @@ def _run(wl_key, fmx, oracle, tokens=None, pack=True):
 
 
 CASES = [("tiny_t5", True), ("tiny_t5", False), ("tiny_t40", True), ("tiny_norm_t33", True),
+         ("small_dec_t4", True), ("small_dec_t4", False),
          ("qwen15_decode_b1", True), ("qwen15_decode_b1", False), ("qwen15_decode_b4", True),
          ("small_t23", True), ("small_t200", True), ("small_t200", False),
          ("qwen15_decode_b8", True), ("qwen15_decode_b8", False), ("qwen15_prefill_512", True),
