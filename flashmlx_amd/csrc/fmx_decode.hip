@@ -47,6 +47,15 @@ __host__ __device__ inline int xstride(int K) { return K + 8; }
 constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;        // quad_reduce's LDS
 constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
+// Gate/up tile pairs per K2 workgroup (their loads in flight together, the
+// routing tables and staged rows shared): two when the grid has at least
+// kDecK2PairGrid tile pairs (about two resident grids of one-pair
+// workgroups; the grid is sized for max_seg experts, of which fewer are
+// usually routed), else one, so that a small batch still spreads over every
+// CU. Measured (Qwen1.5): two pairs -6 % per layer at B=8, -11 % at B=16;
+// +2 % at B=4, where one is kept.
+constexpr int kDecK2MaxPairs = 2;
+constexpr int kDecK2PairGrid = 2 * 4 * 256;
 constexpr int kDecK1LpBytes = kDecWaves * kDecMaxT * 8;              // router partials per wave
 
 constexpr int kDecK1LgBytes = kDecMaxT * (kDecMaxE + 1) * 2;         // every token's logits
@@ -74,6 +83,31 @@ __device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, 
       bf16x8_t A[4];
       lds_a(xl + (u0 + d) * 128, A);
       pk_unit<DUAL>(L[d], A, acc0, acc1);
+    }
+  }
+}
+
+// tile_units_lds for NP tile pairs at once: every pair's loads are issued
+// before the one wait, then the pairs are multiplied in turn.
+template <int NP, int NU>
+__device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0, int u1, const uint16_t* xl,
+                                       int lane, f32x4_t (&acc)[NP][2]) {
+  PkUnit<true> L[NP][NU];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+#pragma unroll
+    for (int d = 0; d < NU; ++d) L[p][d] = pk_load<true>(base[p] + min(u0 + d, u1 - 1) * kBlockPair, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<NP * NU * pk_load_insts<true>()>();
+  lds_dma_barrier();
+#pragma unroll
+  for (int d = 0; d < NU; ++d) {
+    if (u0 + d < u1) {
+      bf16x8_t A[4];
+      lds_a(xl + (u0 + d) * 128, A);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) pk_unit<true>(L[p][d], A, acc[p][0], acc[p][1]);
     }
   }
 }
@@ -402,18 +436,18 @@ __device__ void dec_sort(const DecodeArgs& a) {
 // workgroup runs the sort for the routing accessors. SIGNAL (in K23): the h
 // values go out as device-scope stores and, once they have completed, the
 // tile is counted in on its expert's gate/up counter.
-template <bool SIGNAL>
+template <bool SIGNAL, int NP>
 __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
-  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
+  uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + NP * kDecQuadRedBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, I = a.I, xs = xstride(H);
-  if (b == a.max_seg * a.gu_tiles) {
+  if (b == a.max_seg * a.gu_wgs) {
     dec_sort(a);
     return;
   }
-  const int u = b / a.gu_tiles, tp = b - u * a.gu_tiles;
+  const int u = b / a.gu_wgs, tp0 = (b - u * a.gu_wgs) * NP;
   // routing tables first: a workgroup without an expert leaves before it
   // starts any LDS DMA
   const int U = static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg)));
@@ -432,25 +466,36 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
   const int u0 = (nu * wave) / kDecWaves, u1 = (nu * (wave + 1)) / kDecWaves;
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
-  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  tile_units_lds<true, kDecK2Units>(a.gu + static_cast<int64_t>(e) * a.gu_es + static_cast<int64_t>(tp) * nu * kBlockPair,
-                                     u0, u1, xl, lane, acc0, acc1);
-  quad_reduce(acc0, acc1, wave, lane, s_red);
+  f32x4_t acc[NP][2];
+  const uint8_t* base[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    acc[p][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    acc[p][1] = acc[p][0];
+    base[p] = a.gu + static_cast<int64_t>(e) * a.gu_es + static_cast<int64_t>(tp0 + p) * nu * kBlockPair;
+  }
+  pairs_units_lds<NP, kDecK2Units>(base, u0, u1, xl, lane, acc);
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+    quad_reduce(acc[p][0], acc[p][1], wave, lane, s_red + p * (kDecQuadRedBytes / 4));
   if (wave != 0) return;
-  const int n = tp * 16 + m;
   // lane 16j + c holds rows 4j..4j+3: their slots are the bytes of word j
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * j + i;
-    const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k)) {
-      uint16_t* dst = a.h + static_cast<int64_t>(t * k + slot) * I + n;
-      const uint16_t v = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
-      if (SIGNAL)
-        __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      else
-        *dst = v;
+  for (int p = 0; p < NP; ++p) {
+    const int n = (tp0 + p) * 16 + m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * j + i;
+      const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
+      if (t < T && slot < static_cast<uint32_t>(k)) {
+        uint16_t* dst = a.h + static_cast<int64_t>(t * k + slot) * I + n;
+        const uint16_t v = swiglu_bf16(round_bf16(acc[p][0][i]), round_bf16(acc[p][1][i]));
+        if (SIGNAL)
+          __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *dst = v;
+      }
     }
   }
   if (SIGNAL) {
@@ -458,7 +503,7 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
     if (lane == 0) {
       uint32_t* g = a.gu_counter + u * kDecGuWords;
       const uint32_t prev = __hip_atomic_fetch_add(g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (prev == static_cast<uint32_t>(a.gu_tiles - 1)) {  // the expert's last tile: every h store is done
+      if (prev == static_cast<uint32_t>(a.gu_wgs - 1)) {  // the expert's last workgroup: every h store is done
 #pragma unroll
         for (int c = 1; c <= kDecGuFlags; ++c)
           __hip_atomic_store(g + c * kDecCbStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -468,9 +513,10 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
 }
 
 // K2 alone (forwards that stop after the gate/up stage)
+template <int NP>
 __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  dec_gu_tile<false>(a, blockIdx.x, smem);
+  dec_gu_tile<false, NP>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- K3: down projections
@@ -660,16 +706,16 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
 // (Dispatching an expert's down workgroups right behind its tiles, about one
 // resident grid later, measured slower: their waits hold slots that the
 // tiles still need.)
-template <int NU>
+template <int NU, int NP>
 __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_a = reinterpret_cast<uint16_t*>(smem);
   const int D = a.H / (16 * kDnTiles);
-  const int n_gu = a.max_seg * a.gu_tiles + 1;
+  const int n_gu = a.max_seg * a.gu_wgs + 1;
   const int n_shared = a.Is > 0 ? D * kDecSdSplit : 0;
   const int b = blockIdx.x;
   if (b < n_gu)
-    dec_gu_tile<true>(a, b, smem);
+    dec_gu_tile<true, NP>(a, b, smem);
   else if (b - n_gu < n_shared)
     dec_down_shared<NU>(a, (b - n_gu) / kDecSdSplit, (b - n_gu) % kDecSdSplit, s_a);
   else
@@ -686,7 +732,7 @@ static size_t k1_lds(const DecodeArgs& a) {
 
 // K2: the quarter reduction, then the staged rows
 static size_t k2_lds(const DecodeArgs& a) {
-  return kDecQuadRedBytes + static_cast<size_t>(a.T) * xstride(a.H) * 2;
+  return static_cast<size_t>(a.k2_pairs) * kDecQuadRedBytes + static_cast<size_t>(a.T) * xstride(a.H) * 2;
 }
 
 static size_t k3_lds(const DecodeArgs& a) {
@@ -707,6 +753,8 @@ bool decode_plan(DecodeArgs& a) {
   a.n_sgu = a.Is / 16;
   a.max_seg = std::min(a.E, a.T * a.k);
   a.gu_tiles = a.I / 16;
+  a.k2_pairs = a.max_seg * a.gu_tiles >= kDecK2PairGrid ? kDecK2MaxPairs : 1;
+  a.gu_wgs = a.gu_tiles / a.k2_pairs;  // I % 128 == 0: the pairs divide the tiles
   return k1_lds(a) <= 160 * 1024 && k2_lds(a) <= 160 * 1024 && k3_lds(a) <= 160 * 1024;
 }
 
@@ -722,7 +770,11 @@ hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(dec_k2, dim3(a.max_seg * a.gu_tiles + 1), dim3(kDecThreads), k2_lds(a), stream, a);
+  const dim3 grid(a.max_seg * a.gu_wgs + 1);
+  if (a.k2_pairs == 2)
+    hipLaunchKernelGGL(dec_k2<2>, grid, dim3(kDecThreads), k2_lds(a), stream, a);
+  else
+    hipLaunchKernelGGL(dec_k2<1>, grid, dim3(kDecThreads), k2_lds(a), stream, a);
   return hipGetLastError();
 }
 
@@ -736,13 +788,26 @@ static bool k3_small_ring(const DecodeArgs& a) {
   return std::max(a.I / 128, (nu_s + kDecSdSplit - 1) / kDecSdSplit) <= kDnSmallUnits;
 }
 
+template <int NU, int NP>
+static void launch_k23(const DecodeArgs& a, int n, size_t lds, hipStream_t stream) {
+  hipLaunchKernelGGL((dec_k23<NU, NP>), dim3(n), dim3(kDecThreads), lds, stream, a);
+}
+
 hipError_t launch_decode_k23(const DecodeArgs& a, hipStream_t stream) {
-  const int n = a.max_seg * a.gu_tiles + 1 + k3_workgroups(a);
+  const int n = a.max_seg * a.gu_wgs + 1 + k3_workgroups(a);
   const size_t lds = std::max(k2_lds(a), k3_lds(a));
-  if (k3_small_ring(a))
-    hipLaunchKernelGGL(dec_k23<kDnSmallUnits>, dim3(n), dim3(kDecThreads), lds, stream, a);
-  else
-    hipLaunchKernelGGL(dec_k23<kDnMaxUnits>, dim3(n), dim3(kDecThreads), lds, stream, a);
+  const bool small = k3_small_ring(a);
+  if (a.k2_pairs == 2) {
+    if (small)
+      launch_k23<kDnSmallUnits, 2>(a, n, lds, stream);
+    else
+      launch_k23<kDnMaxUnits, 2>(a, n, lds, stream);
+  } else {
+    if (small)
+      launch_k23<kDnSmallUnits, 1>(a, n, lds, stream);
+    else
+      launch_k23<kDnMaxUnits, 1>(a, n, lds, stream);
+  }
   return hipGetLastError();
 }
 

@@ -170,6 +170,7 @@ struct DecodeArgs {
   // launch shape (decode_plan)
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
   int max_seg, gu_tiles;    // K2: expert slots x gate/up tile pairs
+  int k2_pairs, gu_wgs;     // K2: tile pairs per workgroup, workgroups per expert slot
 };
 // Fills the launch shape; false when the shapes are outside the decode path.
 bool decode_plan(DecodeArgs& a);
