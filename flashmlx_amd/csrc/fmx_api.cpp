@@ -810,9 +810,10 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
   };
   int rc;
   if ((rc = check_moe_config(cfg))) return rc;
-  if (!w || !x || !y) return fail(FMX_ERR_ARG, "NULL argument");
+  if (!w) return fail(FMX_ERR_ARG, "NULL argument");
   if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens=%lld out of range", static_cast<long long>(T));
-  if (T == 0) return ok();
+  if (T == 0) return ok();  // nothing to run: x and y may be NULL (empty tensors)
+  if (!x || !y) return fail(FMX_ERR_ARG, "NULL argument");
   const fmx_moe_config& c = *cfg;
   const bool has_sh = c.shared_expert_intermediate_size > 0;
   if (!w->router_w || !aligned(w->router_w, 16)) return fail(FMX_ERR_ARG, "router_w NULL or misaligned");
@@ -1123,10 +1124,10 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, con
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   int rc;
   if ((rc = check_moe_config(cfg))) return rc;
+  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  if (T == 0) return ok();  // nothing to run: the buffers may be NULL (empty tensors)
   if (!x || !router_w || !inds || !scores) return fail(FMX_ERR_ARG, "NULL argument");
   if (!aligned(x, 16) || !aligned(router_w, 16)) return fail(FMX_ERR_ARG, "x/router_w not 16-byte aligned");
-  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens out of range");
-  if (T == 0) return ok();
   Arena ar;
   WsGuard guard(ar);
   const size_t need = moe_layout(*cfg, T, nullptr).total;

@@ -214,7 +214,8 @@ int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream s
 
 /* y [T, H] bf16 = moe_block(x [T, H] bf16), T = B*L tokens. The workspace
  * must hold fmx_moe_workspace_size(cfg, T) bytes and have been initialised
- * once with fmx_moe_workspace_init. */
+ * once with fmx_moe_workspace_init. T = 0 runs nothing and returns FMX_OK
+ * (x and y may then be NULL, as for empty tensors). */
 int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
                           const void* x, int64_t n_tokens, void* y, void* workspace,
                           size_t workspace_bytes, fmx_stream stream);

@@ -155,3 +155,21 @@ def test_workload_bytes_match_published_figure():
     assert W.algorithmic_bytes(W.QWEN3, 1, 8) == 21_766_144
     assert W.flops(W.QWEN15, 512) == 70_994_886_656
     assert W.flops(W.QWEN3, 1024) == 77_846_282_240
+
+
+def test_zero_token_calls_need_no_buffers(fmx):
+    """n_tokens = 0 runs nothing and returns FMX_OK even with NULL x / y /
+    outputs (empty tensors have no storage); one token with a NULL x is an
+    argument error, reported before any device call."""
+    from flashmlx_amd import MoEConfig
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    cfg = MoEConfig(2048, 60, 4, 1408, 5632, False).to_c()
+    w = _lib.FmxMoEWeights()
+    ws = (C.c_uint8 * 256)()
+    fwd = lib.fmx_moe_block_forward
+    assert fwd(C.byref(cfg), C.byref(w), None, 0, None, ws, 256, None) == _lib.FMX_OK
+    assert fwd(C.byref(cfg), C.byref(w), None, 1, None, ws, 256, None) == _lib.FMX_ERR_ARG
+    rt = lib.fmx_moe_router_topk
+    assert rt(C.byref(cfg), None, 0, None, None, None, None, None, ws, 256, None) == _lib.FMX_OK
+    assert rt(C.byref(cfg), None, 1, None, None, None, None, None, ws, 256, None) == _lib.FMX_ERR_ARG

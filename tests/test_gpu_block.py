@@ -91,3 +91,17 @@ def test_block_deterministic_and_reusable(gpu, fmx, oracle):
     for i in range(1, 8):
         np.testing.assert_array_equal(y4[8 * i: 8 * i + 8], y4[:8])
     assert_close(y4[:8], y1, "64-token call vs 8-token call")
+
+
+@pytest.mark.parametrize("wl_key", ["qwen15_decode_b8", "small_t23"])
+def test_block_zero_tokens(gpu, fmx, oracle, wl_key):
+    """A forward of zero tokens launches nothing and returns an empty y; the
+    same workspace then serves a normal call with the same bits as before."""
+    from flashmlx_amd import workloads as W
+    wl = W.WORKLOADS[wl_key]
+    hi = W.host_inputs(wl)
+    block, xd = W.device_block(wl, hi)
+    y1 = from_dev_bf16(block(xd))
+    y0 = block(xd[:0].contiguous())
+    assert tuple(y0.shape) == (0, xd.shape[1])
+    np.testing.assert_array_equal(from_dev_bf16(block(xd)), y1)

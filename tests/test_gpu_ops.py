@@ -178,3 +178,19 @@ def test_sort_bitexact(gpu, fmx, oracle, T, k, E):
     np.testing.assert_array_equal(from_dev_u32(idx), ridx)
     np.testing.assert_array_equal(from_dev_u32(offs), roff)
     np.testing.assert_array_equal(ro, np.argsort(inds.reshape(-1), kind="stable"))
+
+
+def test_empty_inputs(gpu, fmx, oracle):
+    """Zero rows in, zero rows out, no error: quantized_matmul with M = 0 and
+    gather_qmm with no index entries (MLX accepts empty arrays the same way)."""
+    rng = np.random.default_rng(21)
+    K, N, E = 256, 64, 4
+    w = _rand_bf16(rng, (N, K), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    out = fmx.quantized_matmul(to_dev(np.zeros((0, K), np.uint16)), to_dev_u32(rq), to_dev(rs), to_dev(rb))
+    assert tuple(out.shape) == (0, N)
+    we = _rand_bf16(rng, (E, N, K), 0.02)
+    eq, es, eb = oracle.quantize(we)
+    out = fmx.gather_qmm(to_dev(np.zeros((0, 1, K), np.uint16)), to_dev_u32(eq), to_dev(es), to_dev(eb),
+                         rhs_indices=to_dev_u32(np.zeros((0,), np.uint32)), sorted_indices=True)
+    assert tuple(out.shape) == (0, 1, N)
