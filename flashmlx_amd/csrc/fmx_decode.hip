@@ -47,6 +47,7 @@ __host__ __device__ inline int xstride(int K) { return K + 8; }
 constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;        // quad_reduce's LDS
 constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
+constexpr int kDecWarmLoads = 8;  // K1's cache warming: 16-byte loads per thread (32 KB per workgroup)
 // Gate/up tile pairs per K2 workgroup (their loads in flight together, the
 // routing tables and staged rows shared): two when the grid has at least
 // kDecK2PairGrid tile pairs (about two resident grids of one-pair
@@ -390,6 +391,26 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
   tile_units_lds<true, kDecK2Units>(a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair, u0, u1, xl, lane,
                                      acc0, acc1);
+  // Warm the device's last-level cache with this workgroup's share of the
+  // shared expert's down weights, which K23 reads after the routing: K1's
+  // HBM would otherwise idle while its router chain finishes. At most
+  // kDecWarmLoads 16-byte loads per thread, all in flight together; the
+  // values are dropped.
+  {
+    const int64_t total = static_cast<int64_t>(a.H / 16) * (a.Is / 128) * kBlockSingle;
+    const int64_t per = (total + a.n_sgu - 1) / a.n_sgu;
+    const int64_t b0 = static_cast<int64_t>(tp) * per, b1 = min(b0 + per, total);
+    uint32_t sink = 0;
+#pragma unroll
+    for (int i = 0; i < kDecWarmLoads; ++i) {
+      const int64_t off = b0 + (static_cast<int64_t>(i) * kDecThreads + threadIdx.x) * 16;
+      if (off + 16 <= b1) {
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.sdn + off);
+        sink ^= v[0];
+      }
+    }
+    asm volatile("" ::"v"(sink));
+  }
   quad_reduce(acc0, acc1, wave, lane, s_red);
   if (wave != 0) return;
   const int n = tp * 16 + m;
