@@ -606,7 +606,7 @@ __device__ void dec_combine(const DecodeArgs& a, int cb) {
 __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
   __shared__ int s_last_cb;
   wait_vmcnt0();
-  __syncthreads();
+  __syncthreads();  // also: every thread is done with the previous call's s_last_cb
   if (threadIdx.x == 0) {
     const uint32_t target = static_cast<uint32_t>(U + (a.Is > 0 ? kDecSdSplit : 0));
     s_last_cb = __hip_atomic_fetch_add(a.cb_counter + cb * kDecCbStride, 1u, __ATOMIC_RELAXED,
@@ -619,10 +619,13 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
     __hip_atomic_store(a.cb_counter + cb * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Routed expert number u, columns 64*cb .. 64*cb + 63 of H (model.cpp:718-721):
-// d[t*k + slot, n] = h[t*k + slot] . Wd_e[n] for the tokens t that selected
-// expert e. Wave w computes tile 4*cb + w over the whole of I in one batch of
-// loads; the tokens' h rows are staged in LDS (rows indexed by token).
+// Routed expert number u, columns 64*cb .. 64*cb + 63 of H for the TPW
+// column blocks cb = TPW*cbp .. (model.cpp:718-721): d[t*k + slot, n] =
+// h[t*k + slot] . Wd_e[n] for the tokens t that selected expert e. Wave w
+// computes tile 4*cb + w of each block over the whole of I in one batch of
+// loads (a short I, at most half the ring, leaves room for two blocks: half
+// the workgroups, each with twice the bytes behind one preamble); the
+// tokens' h rows are staged in LDS (rows indexed by token).
 //
 // h is written by gate/up workgroups of the same grid (K23). Wave 0 reads
 // one copy of its expert's done flag, then every wave issues its weight
@@ -633,8 +636,10 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
 // a barrier. Then every wave fetches its h rows with device-scope DMA.
 constexpr int kDecWaitPolls = 1 << 21;
 
-template <int NU>
-__device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_a) {
+template <int NU, int TPW>
+__device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s_a) {
+  // TPW column blocks of 64 (cb = TPW*cbp + c), one 16-row tile of each per wave
+  static_assert(TPW >= 1 && TPW * 1 <= NU, "tiles per wave");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, I = a.I, xs = xstride(I);
@@ -643,18 +648,29 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
   const int e = static_cast<int>(min(a.seg[1 + u], static_cast<uint32_t>(a.E - 1)));
   const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.slots + u * kDecMaxT);
   const uint32_t slot4 = srow[lane & 3];
-  const int nu = I / 128, tile = kDnTiles * cb + wave;
-  const uint8_t* tb = a.dn + static_cast<int64_t>(e) * a.dn_es + static_cast<int64_t>(tile) * nu * kBlockSingle;
+  const int nu = I / 128;  // TPW * nu <= NU (launch_decode_k23)
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_a + min(m, T - 1) * xs + 8 * j;
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = acc;
-  const uint32_t* flag = a.gu_counter + u * kDecGuWords + (1 + cb % kDecGuFlags) * kDecCbStride;
+  const uint8_t* tb[TPW];
+#pragma unroll
+  for (int c = 0; c < TPW; ++c) {
+    const int tile = kDnTiles * (TPW * cbp + c) + wave;
+    tb[c] = a.dn + static_cast<int64_t>(e) * a.dn_es + static_cast<int64_t>(tile) * nu * kBlockSingle;
+  }
+  f32x4_t acc[TPW], unused = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < TPW; ++c) acc[c] = unused;
+  const uint32_t* flag = a.gu_counter + u * kDecGuWords + (1 + cbp % kDecGuFlags) * kDecCbStride;
   uint32_t done = 0;
   if (wave == 0) done = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // the ring's NU slots: tile c's units at c * (NU / TPW) ..
+  constexpr int PER = NU / TPW;
   PkUnit<false> L[NU];
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < NU; ++d) L[d] = pk_load<false>(tb + min(d, nu - 1) * kBlockSingle, lane);
+  for (int c = 0; c < TPW; ++c)
+#pragma unroll
+    for (int d = 0; d < PER; ++d) L[c * PER + d] = pk_load<false>(tb[c] + min(d, nu - 1) * kBlockSingle, lane);
   __builtin_amdgcn_sched_barrier(0);
   if (wave == 0) {
     done = __builtin_amdgcn_readfirstlane(done);
@@ -672,24 +688,29 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cb, uint16_t* s_
   wait_vmcnt0();
   lds_dma_barrier();
 #pragma unroll
-  for (int d = 0; d < NU; ++d) {
+  for (int d = 0; d < PER; ++d) {
     if (d < nu) {
       bf16x8_t A[4];
       lds_a(xl + d * 128, A);
-      pk_unit<false>(L[d], A, acc, unused);
+#pragma unroll
+      for (int c = 0; c < TPW; ++c) pk_unit<false>(L[c * PER + d], A, acc[c], unused);
     }
   }
-  const int n = tile * 16 + m;
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * j + i;
-    const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k))
-      __hip_atomic_store(a.dw + static_cast<int64_t>(t * k + slot) * H + n, static_cast<uint32_t>(f32_to_bf16(acc[i])),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int c = 0; c < TPW; ++c) {
+    const int n = (kDnTiles * (TPW * cbp + c) + wave) * 16 + m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * j + i;
+      const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
+      if (t < T && slot < static_cast<uint32_t>(k))
+        __hip_atomic_store(a.dw + static_cast<int64_t>(t * k + slot) * H + n, static_cast<uint32_t>(f32_to_bf16(acc[c][i])),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
-  dec_arrive(a, cb, U);
+#pragma unroll
+  for (int c = 0; c < TPW; ++c) dec_arrive(a, TPW * cbp + c, U);
 }
 
 // Shared expert down projection, columns 64*cb .. +63, K slice ks of
@@ -727,20 +748,20 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
 // (Dispatching an expert's down workgroups right behind its tiles, about one
 // resident grid later, measured slower: their waits hold slots that the
 // tiles still need.)
-template <int NU, int NP>
+template <int NU, int NP, int TPW>
 __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_a = reinterpret_cast<uint16_t*>(smem);
-  const int D = a.H / (16 * kDnTiles);
+  const int D = a.H / (16 * kDnTiles) / TPW;  // routed down workgroups per expert
   const int n_gu = a.max_seg * a.gu_wgs + 1;
-  const int n_shared = a.Is > 0 ? D * kDecSdSplit : 0;
+  const int n_shared = a.Is > 0 ? (a.H / (16 * kDnTiles)) * kDecSdSplit : 0;
   const int b = blockIdx.x;
   if (b < n_gu)
     dec_gu_tile<true, NP>(a, b, smem);
   else if (b - n_gu < n_shared)
     dec_down_shared<NU>(a, (b - n_gu) / kDecSdSplit, (b - n_gu) % kDecSdSplit, s_a);
   else
-    dec_down_routed<NU>(a, (b - n_gu - n_shared) / D, (b - n_gu - n_shared) % D, s_a);
+    dec_down_routed<NU, TPW>(a, (b - n_gu - n_shared) / D, (b - n_gu - n_shared) % D, s_a);
 }
 
 }  // namespace
@@ -799,19 +820,40 @@ hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-static int k3_workgroups(const DecodeArgs& a) {
-  const int nblk = a.H / (16 * kDnTiles);
-  return a.max_seg * nblk + (a.Is > 0 ? nblk * kDecSdSplit : 0);
-}
-
 static bool k3_small_ring(const DecodeArgs& a) {
   const int nu_s = a.Is / 128;
   return std::max(a.I / 128, (nu_s + kDecSdSplit - 1) / kDecSdSplit) <= kDnSmallUnits;
 }
 
-template <int NU, int NP>
+// Column blocks per routed down workgroup: two when a tile's units fill at
+// most half the load ring (I <= 768 with the 12-unit ring) and the grid has
+// at least kDecK3PairGrid routed down workgroups (about two resident grids),
+// else one. Measured (Qwen3, I = 768): -3 % per layer at B=16, +14 % at B=1
+// (half of 256 workgroups leaves CUs idle), where one is kept.
+constexpr int kDecK3PairGrid = 2 * 4 * 256;
+
+static int k3_blocks_per_wg(const DecodeArgs& a) {
+  const int ring = k3_small_ring(a) ? kDnSmallUnits : kDnMaxUnits;
+  const int nblk = a.H / (16 * kDnTiles);
+  return (2 * (a.I / 128) <= ring && nblk % 2 == 0 && a.max_seg * nblk >= kDecK3PairGrid) ? 2 : 1;
+}
+
+static int k3_workgroups(const DecodeArgs& a) {
+  const int nblk = a.H / (16 * kDnTiles);
+  return a.max_seg * (nblk / k3_blocks_per_wg(a)) + (a.Is > 0 ? nblk * kDecSdSplit : 0);
+}
+
+template <int NU, int NP, int TPW>
 static void launch_k23(const DecodeArgs& a, int n, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((dec_k23<NU, NP>), dim3(n), dim3(kDecThreads), lds, stream, a);
+  hipLaunchKernelGGL((dec_k23<NU, NP, TPW>), dim3(n), dim3(kDecThreads), lds, stream, a);
+}
+
+template <int NU, int NP>
+static void launch_k23_tpw(const DecodeArgs& a, int n, size_t lds, hipStream_t stream) {
+  if (k3_blocks_per_wg(a) == 2)
+    launch_k23<NU, NP, 2>(a, n, lds, stream);
+  else
+    launch_k23<NU, NP, 1>(a, n, lds, stream);
 }
 
 hipError_t launch_decode_k23(const DecodeArgs& a, hipStream_t stream) {
@@ -820,14 +862,14 @@ hipError_t launch_decode_k23(const DecodeArgs& a, hipStream_t stream) {
   const bool small = k3_small_ring(a);
   if (a.k2_pairs == 2) {
     if (small)
-      launch_k23<kDnSmallUnits, 2>(a, n, lds, stream);
+      launch_k23_tpw<kDnSmallUnits, 2>(a, n, lds, stream);
     else
-      launch_k23<kDnMaxUnits, 2>(a, n, lds, stream);
+      launch_k23_tpw<kDnMaxUnits, 2>(a, n, lds, stream);
   } else {
     if (small)
-      launch_k23<kDnSmallUnits, 1>(a, n, lds, stream);
+      launch_k23_tpw<kDnSmallUnits, 1>(a, n, lds, stream);
     else
-      launch_k23<kDnMaxUnits, 1>(a, n, lds, stream);
+      launch_k23_tpw<kDnMaxUnits, 1>(a, n, lds, stream);
   }
   return hipGetLastError();
 }
