@@ -639,7 +639,7 @@ constexpr int kDecWaitPolls = 1 << 21;
 template <int NU, int TPW>
 __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s_a) {
   // TPW column blocks of 64 (cb = TPW*cbp + c), one 16-row tile of each per wave
-  static_assert(TPW >= 1 && TPW * 1 <= NU, "tiles per wave");
+  static_assert(TPW == 1 || TPW == 2, "one or two column blocks per workgroup");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, I = a.I, xs = xstride(I);
