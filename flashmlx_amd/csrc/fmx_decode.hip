@@ -633,7 +633,9 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
 // value is in while the weights are still in flight. Until the flag is set,
 // wave 0 polls it (s_sleep between reads, at most kDecWaitPolls reads: far
 // beyond any real wait, a guard against a hang) while the other waves wait at
-// a barrier. Then every wave fetches its h rows with device-scope DMA.
+// a barrier. Then every wave fetches its h rows with device-scope DMA. A
+// wait that ran out stores NaN products, so that the failure shows in y
+// instead of stale rows passing for results.
 constexpr int kDecWaitPolls = 1 << 21;
 
 template <int NU, int TPW>
@@ -660,6 +662,7 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
   f32x4_t acc[TPW], unused = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < TPW; ++c) acc[c] = unused;
+  __shared__ int s_timed_out;
   const uint32_t* flag = a.gu_counter + u * kDecGuWords + (1 + cbp % kDecGuFlags) * kDecCbStride;
   uint32_t done = 0;
   if (wave == 0) done = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -678,6 +681,8 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
       __builtin_amdgcn_s_sleep(16);
       done = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
+    if (lane == 0) s_timed_out = done == 0;
+    wait_lgkmcnt0();  // the LDS write lands before the barrier (the weights stay in flight)
   }
   lds_dma_barrier();  // wave 0 has seen the flag (no wait for the weights in flight)
   for (int t = wave; t < T; t += kDecWaves) {
@@ -695,6 +700,10 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
 #pragma unroll
       for (int c = 0; c < TPW; ++c) pk_unit<false>(L[c * PER + d], A, acc[c], unused);
     }
+  }
+  if (s_timed_out) {
+#pragma unroll
+    for (int c = 0; c < TPW; ++c) acc[c] = f32x4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
   }
   const uint32_t my_slots = __shfl(slot4, j);
 #pragma unroll

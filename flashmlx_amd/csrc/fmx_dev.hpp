@@ -217,6 +217,8 @@ __device__ inline void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 __device__ inline void wait_vmcnt0() { wait_vmcnt<0>(); }
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maximum: no wait)
+__device__ inline void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 
 // Workgroup barrier for LDS written by LDS DMA that every wave has already
 // waited for (wait_vmcnt): s_barrier alone, with compiler-level memory
