@@ -69,16 +69,18 @@ def test_block_parity(gpu, fmx, oracle, wl_key, pack):
             print(f"  vs oracle({name}) tokens {sub[:2].tolist()}: {errors(got[sub[:2]], yb[sub[:2]])}")
 
 
-def test_block_deterministic_and_reusable(gpu, fmx, oracle):
+@pytest.mark.parametrize("wl_key", ["qwen3_decode_b8", "qwen15_decode_b8"])
+def test_block_deterministic_and_reusable(gpu, fmx, oracle, wl_key):
     """Same input twice -> identical bits; the workspace then serves a
     smaller call, whose rows equal the larger call's prefix rows (tokens are
     independent and x of T=1 is the first row of x of T=8). A 64-token call
     (eight copies of the 8 tokens; crosses the sort threshold and leaves the
     at-most-16-token kernels) gives the same bits for every copy, within the
-    bf16 tolerance of the 8-token call (its accumulation order differs)."""
+    bf16 tolerance of the 8-token call (its accumulation order differs); an
+    8-token call after it repeats the first call's bits."""
     import torch
     from flashmlx_amd import workloads as W
-    wl = W.WORKLOADS["qwen3_decode_b8"]
+    wl = W.WORKLOADS[wl_key]
     hi = W.host_inputs(wl)
     block, xd = W.device_block(wl, hi, max_tokens=64)
     y1 = from_dev_bf16(block(xd))
@@ -91,6 +93,9 @@ def test_block_deterministic_and_reusable(gpu, fmx, oracle):
     for i in range(1, 8):
         np.testing.assert_array_equal(y4[8 * i: 8 * i + 8], y4[:8])
     assert_close(y4[:8], y1, "64-token call vs 8-token call")
+    # back on the decode kernels after the prefill path: whatever counters
+    # and flags either path uses are back at zero, so the bits repeat
+    np.testing.assert_array_equal(from_dev_bf16(block(xd)), y1)
 
 
 @pytest.mark.parametrize("wl_key", ["qwen15_decode_b8", "small_t23"])
