@@ -69,6 +69,29 @@ def test_block_parity(gpu, fmx, oracle, wl_key, pack):
             print(f"  vs oracle({name}) tokens {sub[:2].tolist()}: {errors(got[sub[:2]], yb[sub[:2]])}")
 
 
+# Qwen1.5 shape at token counts between the named workloads: odd decode
+# batches (partial 4-token slot words, the decode plan's grid thresholds) and
+# 17, the smallest forward on the prefill GEMMs
+@pytest.mark.parametrize("T", [3, 5, 7, 12, 13, 15, 17])
+def test_block_parity_token_sweep(gpu, fmx, oracle, T):
+    import torch
+    from flashmlx_amd import workloads as W
+    wl = W.Workload(f"qwen15_t{T}", W.QWEN15, T, 100 + T, router_bias=T % 2 == 1)
+    hi = W.host_inputs(wl)
+    block, xd = W.device_block(wl, hi)
+    y = block(xd)
+    torch.cuda.synchronize()
+    assert W.decode_path(wl.model, T) == (T <= 16)
+    cfg, w = oracle_args(hi, wl.model, oracle.quantize)
+    sub = np.arange(T)
+    ry, rinds, rscores = oracle.moe_block(cfg, w, hi.x, oracle.ACC_A, tokens=sub)
+    r = block.routing()
+    np.testing.assert_array_equal(from_dev_u32(r["inds"]), rinds)
+    np.testing.assert_array_equal(from_dev_bf16(r["scores"]), rscores)
+    e = assert_close(from_dev_bf16(y), ry, f"qwen15 T={T} y")
+    print(f"qwen15 T={T}: {e}")
+
+
 @pytest.mark.parametrize("wl_key", ["qwen3_decode_b8", "qwen15_decode_b8"])
 def test_block_deterministic_and_reusable(gpu, fmx, oracle, wl_key):
     """Same input twice -> identical bits; the workspace then serves a
