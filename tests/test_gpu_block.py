@@ -70,7 +70,8 @@ def test_block_parity(gpu, fmx, oracle, wl_key, pack):
 
 
 # Qwen1.5 shape at token counts between the named workloads: odd decode
-# batches (partial 4-token slot words, the decode plan's grid thresholds) and
+# batches (partial 4-token slot words; one gate/up tile pair per workgroup up
+# to 5 tokens, two from 7) and
 # 17, the smallest forward on the prefill GEMMs
 @pytest.mark.parametrize("T", [3, 5, 7, 12, 13, 15, 17])
 def test_block_parity_token_sweep(gpu, fmx, oracle, T):
