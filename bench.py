@@ -6,17 +6,22 @@ top-k weighted combine, gated shared expert) over one batch of tokens
 already resident in HBM. Steps cycle over `--layers` copies of the layer's
 weights (distinct HBM addresses, 24 by default like a 24-layer model) so that
 the weights stream from HBM rather than the 256 MB last-level cache, and run
-as a captured HIP graph. Prints ONE JSON line.
+as captured HIP graphs. Every graph is replayed before the clock starts; the
+K timed steps are repeated `--trials` times and the median trial is reported.
+Prints ONE JSON line.
 
-Default workload: Qwen1.5-MoE-A2.7B-shape MoE block, decode batch 8 (seed 2).
-Other workloads: --workload (flashmlx_amd/workloads.py).
+Headline workload: Qwen1.5-MoE-A2.7B-shape MoE block, decode batch 8 (seed
+2). The same invocation measures the other single-GPU MoE-layer configs
+(`--configs`, default all: Qwen1.5 decode batch 1 and 4, prefill 512;
+Qwen3-30B-A3B decode batch 1 and 8, prefill 1024), each with its own
+roofline, under "configs".
 
 Per-stage timing: graphs of the first j kernel stages of every layer give
 each stage's marginal time (HIP events on the stream the kernels run on);
 the dominant kernel's average duration (the stages it runs, together) gives
-the roofline figure. The same
-command under `rocprofv3 --kernel-trace --stats` gives the per-kernel
-averages that the summaries under profiles/ quote.
+the roofline figure. The same command under `rocprofv3 --kernel-trace
+--stats` gives the per-kernel averages that the summaries under profiles/
+quote.
 
 `--copy-calibration MIB` instead runs a plain device copy of MIB MiB five
 times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
@@ -27,6 +32,7 @@ import argparse
 import json
 import os
 import platform
+import statistics
 import subprocess
 import sys
 import time
@@ -35,6 +41,10 @@ METRIC = "MoE-layer tok/s; decode HBM GB/s and prefill MFMA % on 1 MI355X"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 ROOT = os.path.dirname(os.path.abspath(__file__))
+HEADLINE = "qwen15_decode_b8"
+# the other single-GPU MoE-layer configurations of the benchmark
+CONFIGS = ["qwen15_decode_b1", "qwen15_decode_b4", "qwen15_prefill_512", "qwen3_decode_b1",
+           "qwen3_decode_b8", "qwen3_prefill_1024"]
 
 
 def log(*a):
@@ -52,6 +62,16 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def host_threads() -> int:
+    """Threads this process may use: its CPU affinity, capped by the
+    OMP_NUM_THREADS share the environment gives it."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
 def load_traffic(workload: str, stage: str):
     """HBM bytes per launch of a stage's kernel from the committed rocprofv3
     --pmc summary (profiles/traffic_<workload>.json), if there is one."""
@@ -64,11 +84,14 @@ def load_traffic(workload: str, stage: str):
         return None
 
 
-def cpu_baseline(wl, seconds: float):
+def cpu_baseline(wl, y_gpu, inds_gpu, seconds: float):
     """The CPU oracle (C restatement of the reference's MLX CPU semantics,
     fp32 accumulation) timed on this host on a bounded sample of the same
-    workload."""
+    workload, at 1 thread and at the host's thread share; and, as the
+    checker, the GPU output of the timed config against the oracle's."""
     sys.path.insert(0, ROOT)
+    import numpy as np
+
     from flashmlx_amd import workloads as W
     from oracle import oracle as O
 
@@ -78,33 +101,59 @@ def cpu_baseline(wl, seconds: float):
     m = wl.model
     cfg = dict(hidden=m["hidden"], n_experts=m["n_experts"], top_k=m["top_k"], inter=m["inter"],
                shared_inter=m["shared_inter"], norm_topk=m["norm_topk"])
-    w = dict(router_w=hi.router_w, router_bias=hi.router_bias, gate=q(hi.gate), up=q(hi.up),
+    rq = q if wl.router_quant else (lambda a: a)
+    w = dict(router_w=rq(hi.router_w), router_bias=hi.router_bias, gate=q(hi.gate), up=q(hi.up),
              down=q(hi.down))
     if m["shared_inter"]:
         w.update(shared_gate=q(hi.shared_gate), shared_up=q(hi.shared_up),
-                 shared_down=q(hi.shared_down), shared_expert_gate_w=hi.shared_expert_gate_w)
+                 shared_down=q(hi.shared_down), shared_expert_gate_w=rq(hi.shared_expert_gate_w))
     T = wl.tokens
-    # bounded sample: whole calls for small batches, a token slice for prefill
     per_call = T if T <= 16 else 16
     tokens = None if per_call == T else list(range(per_call))
-    O.moe_block(cfg, w, hi.x, O.ACC_A, tokens=tokens)  # warm-up
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        O.moe_block(cfg, w, hi.x, O.ACC_A, tokens=tokens)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {
-        "value": round(n * per_call / el, 3),
-        "unit": "tok/s",
-        "cores": O.get_threads(),
-        "kind": "port",
-        "sample": (f"{n} oracle MoE-layer calls x {per_call} tokens ({'all' if tokens is None else 'first'} "
-                   f"of {T}; routing over all {T}) in {el:.1f}s, fp32 accumulate, "
-                   f"{O.get_threads()} OpenMP threads on {cpu_model()}"),
+    nproc = host_threads()
+
+    def timed(threads, secs):
+        O.set_threads(threads)
+        O.moe_block(cfg, w, hi.x, O.ACC_A, tokens=tokens)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while True:
+            O.moe_block(cfg, w, hi.x, O.ACC_A, tokens=tokens)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= secs:
+                return n, el
+
+    n1, e1 = timed(1, seconds / 2)
+    nn, en = timed(nproc, seconds / 2)
+    model = cpu_model()
+    # parity of the timed config's GPU output (all rows) against the oracle
+    O.set_threads(nproc)
+    ry, rinds, _ = O.moe_block(cfg, w, hi.x, O.ACC_A)
+    g = O.bf16_to_f32(y_gpu).astype(np.float64)
+    r = O.bf16_to_f32(ry).astype(np.float64)
+    d = np.abs(g - r)
+    parity = {
+        "vs": "CPU oracle, fp32 accumulation (mode A)",
+        "rows": int(T),
+        "max_abs": float(d.max()),
+        "mean_rel": float((d / np.maximum(np.abs(r), 1e-6)).mean()),
+        "rel_l2": float(np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)),
+        "within_rtol_2e-2_atol_1e-2": bool((d <= 1e-2 + 2e-2 * np.abs(r)).all()),
+        "routing_bitexact": bool(np.array_equal(inds_gpu, rinds)),
     }
+    sample = (f"oracle MoE-layer calls x {per_call} tokens ({'all' if tokens is None else 'first'} of {T}; "
+              f"routing over all {T}), fp32 accumulate, on {model}: {nn} calls in {en:.1f}s on {nproc} "
+              f"OpenMP threads, {n1} calls in {e1:.1f}s on 1 thread")
+    return {
+        "value": round(nn * per_call / en, 3),
+        "unit": "tok/s",
+        "cores": nproc,
+        "kind": "port",
+        "sample": sample,
+        "single_thread_value": round(n1 * per_call / e1, 3),
+        "cpu_model": model,
+        "nproc": os.cpu_count(),
+    }, parity
 
 
 def copy_calibration(mib: int) -> None:
@@ -120,70 +169,48 @@ def copy_calibration(mib: int) -> None:
     print(json.dumps({"copy_calibration_bytes": n, "launches": 5}), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2400)
-    ap.add_argument("--warmup", type=int, default=240)
-    ap.add_argument("--workload", default="qwen15_decode_b8")
-    ap.add_argument("--layers", type=int, default=24, help="weight copies cycled over")
-    ap.add_argument("--profile-steps", type=int, default=480, help="steps of the per-stage timing pass")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-pack", action="store_true",
-                    help="MLX-layout weights only (no fmx_pack_expert_weights re-layout)")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
-    args = ap.parse_args()
-
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build runs the MoE layer on one GPU only; "
-                                   "run bench.py with --gpus 1",
-                          "n_gpus": args.gpus}), flush=True)
-        sys.exit(2)
-    if args.copy_calibration:
-        copy_calibration(args.copy_calibration)
-        return
-
-    sys.path.insert(0, ROOT)
+def build_layers(wl, R: int, pack: bool):
+    """R copies of one layer's weights at distinct addresses (the MLX-layout
+    expert arrays released after packing), and x."""
     import torch
 
     from flashmlx_amd import workloads as W
     from flashmlx_amd.moe import MoEBlock, MoEWeights, QWeight
 
-    wl = W.WORKLOADS[args.workload]
-    m = wl.model
-    T = wl.tokens
-    torch.cuda.set_device(0)
+    block0, x = W.device_block(wl, W.DeviceSynth(wl), pack=pack, drop_mlx=pack)
 
-    log(f"workload {wl.key}: generating inputs")
-    hi = W.host_inputs(wl)
-    block0, x = W.device_block(wl, hi, pack=not args.no_pack)
-    del hi
-
-    def clone_q(q):
-        return QWeight(q.w.clone(), q.scales.clone(), q.biases.clone())
+    def clone(v):
+        if v is None:
+            return None
+        if isinstance(v, QWeight):
+            return QWeight(v.w.clone(), v.scales.clone(), v.biases.clone())
+        return v.clone()
 
     def clone_block(b):
         w = b.weights
-        nw = MoEWeights(router_w=w.router_w.clone(), gate=clone_q(w.gate), up=clone_q(w.up),
-                        down=clone_q(w.down))
-        if w.router_logit_bias is not None:
-            nw.router_logit_bias = w.router_logit_bias.clone()
-        if w.shared_gate is not None:
-            nw.shared_gate, nw.shared_up, nw.shared_down = (clone_q(w.shared_gate), clone_q(w.shared_up),
-                                                            clone_q(w.shared_down))
-            nw.shared_expert_gate_w = w.shared_expert_gate_w.clone()
-        if w.packed is not None:
-            nw.packed = w.packed.clone()
-        return MoEBlock(b.cfg, nw, max_tokens=T, pack=False)
+        nw = MoEWeights(**{f: clone(getattr(w, f)) for f in (
+            "router_w", "gate", "up", "down", "shared_gate", "shared_up", "shared_down",
+            "shared_expert_gate_w", "router_logit_bias", "packed")})
+        return MoEBlock(b.cfg, nw, max_tokens=wl.tokens, pack=False)
 
-    R = max(1, args.layers)
     blocks = [block0] + [clone_block(block0) for _ in range(R - 1)]
-    y = torch.empty_like(x)
     torch.cuda.synchronize()
+    return blocks, x
+
+
+def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: bool = True):
+    """Times K steps (layer forwards, cycling over R weight copies) `trials`
+    times after Wm warm-up steps; per-stage times from partial-forward
+    graphs; the dominant kernel's roofline figure."""
+    import torch
+
+    from flashmlx_amd import workloads as W
+
+    m, T = wl.model, wl.tokens
+    log(f"workload {wl.key}: {R} layer copies")
+    blocks, x = build_layers(wl, R, pack)
+    y = torch.empty_like(x)
     per_layer = sum(t.numel() * t.element_size() for t in blocks[0].weight_tensors())
-    log(f"{R} layer copies, {R * per_layer / 2**30:.2f} GiB of weights")
 
     # reference output (eager) and routing statistics
     blocks[0].forward_into(x, y)
@@ -192,6 +219,7 @@ def main():
     r = blocks[0].routing()
     offs = r["expert_offsets"].cpu().numpy().astype("int64")
     U = int((offs[1:] > offs[:-1]).sum())
+    inds = r["inds"].cpu().numpy().view("uint32").copy()
 
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
@@ -211,13 +239,18 @@ def main():
         for i in range(n):
             blocks[i % R].forward_into(x, y)
 
-    K, Wm = args.steps, args.warmup
     graphs = {R: capture(lambda: run_layers(R))}
     for rem in {K % R, Wm % R} - {0}:
         graphs[rem] = capture(lambda rem=rem: run_layers(rem))
+    # every graph that will be timed is replayed before the clock starts, and
     # every replay must reproduce the eager result
+    for g in graphs.values():
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
     for _ in range(3):
-        graphs[R].replay()
+        with torch.cuda.stream(stream):
+            graphs[R].replay()
         torch.cuda.synchronize()
         if not torch.equal(y, y_ref):
             raise RuntimeError("graph replay output differs from the eager output")
@@ -234,27 +267,29 @@ def main():
 
     run_steps(Wm)
     torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
     t0 = time.perf_counter()
-    ev0.record(stream)
-    run_steps(K)
-    ev1.record(stream)
-    torch.cuda.synchronize()
+    for _ in range(trials):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        run_steps(K)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        times.append(ev0.elapsed_time(ev1))
     wall = time.perf_counter() - t0
-    ms_total = ev0.elapsed_time(ev1)
+    ms_total = statistics.median(times)
     ms_step = ms_total / K
     tok_s = T * K / (ms_total / 1e3)
 
     # ---- per-stage timing: graphs of R layers that run only the first j
-    # kernel stages (j = 1..len(stages)); stage j's marginal time inside the layer is
-    # the difference of consecutive graphs' times (HIP events on the kernels'
-    # stream around each replay)
-    work = W.stage_work(m, T, U, wl.router_bias, packed=not args.no_pack)
+    # kernel stages; stage j's marginal time inside the layer is the
+    # difference of consecutive graphs' times
+    work = W.stage_work(m, T, U, wl.router_bias, packed=pack, router_quant=wl.router_quant)
     stages = [s[0] for s in work]
-    reps = max(1, args.profile_steps // R)
+    reps = max(1, profile_steps // R)
     cum = [0.0]
-    ns = len(stages)
-    for j in range(1, ns + 1):
+    for j in range(1, len(stages) + 1):
         gj = capture(lambda j=j: [blocks[i].forward_partial(x, y, j) for i in range(R)])
         with torch.cuda.stream(stream):
             gj.replay()
@@ -268,18 +303,18 @@ def main():
         torch.cuda.synchronize()
         cum.append(e0.elapsed_time(e1) / (R * reps))
         del gj
-    dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(ns)]
+    dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(len(stages))]
     stage_us = {s: round(dur[j] * 1e3, 2) for j, s in enumerate(stages)}
 
     # the dominant kernel of a whole forward: a kernel that runs several
     # stages as one grid takes their marginal times and work together
-    groups = W.kernel_groups(m, T, packed=not args.no_pack)
+    groups = W.kernel_groups(m, T, packed=pack)
     gdur = [sum(dur[i] for i in idx) for _, idx in groups]
     dom = max(range(len(groups)), key=lambda q: gdur[q])
     name, idx = groups[dom]
     sbytes = sum(work[i][1] for i in idx)
     sflops = sum(work[i][2] for i in idx)
-    path = W.forward_path(m, T, packed=not args.no_pack)
+    path = W.forward_path(m, T, packed=pack)
     prefill = path != "decode"
     if prefill:
         achieved = sflops / (gdur[dom] * 1e-3) / 1e12
@@ -294,7 +329,7 @@ def main():
     roof["algorithmic_per_launch"] = sflops if prefill else sbytes
     roof["avg_launch_us"] = round(gdur[dom] * 1e3, 2)
 
-    layer_bytes = W.algorithmic_bytes(m, T, U, wl.router_bias)
+    layer_bytes = W.algorithmic_bytes(m, T, U, wl.router_bias, wl.router_quant)
     layer_flops = W.flops(m, T)
     layer = {
         "unique_experts": U,
@@ -306,47 +341,130 @@ def main():
         "kernel_path": path,
         "stage_us": stage_us,
         "stage_bytes": {s: b for s, b, _ in work},
+        "weight_bytes_per_copy": per_layer,
     }
+    res = {
+        "workload": f"{m['name']} MoE block, {wl.note}",
+        "key": wl.key,
+        "tokens": T,
+        "seed": wl.seed,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "steps": K,
+        "warmup": Wm,
+        "trials": trials,
+        "ms_per_step": round(ms_step, 6),
+        "us_per_layer": round(ms_step * 1e3, 2),
+        "trial_ms": {"median": round(ms_total, 4), "min": round(min(times), 4),
+                     "max": round(max(times), 4)},
+        "roofline": roof,
+        "layer": layer,
+        "wall_s": round(wall, 3),
+    }
+    y_host = y_ref.view(torch.int16).cpu().numpy().view("uint16")
+    del blocks, graphs, x, y, y_ref
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res, y_host, inds
 
-    cpu = None
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2400)
+    ap.add_argument("--warmup", type=int, default=240)
+    ap.add_argument("--trials", type=int, default=20, help="timed repetitions of --steps (median)")
+    ap.add_argument("--workload", default=HEADLINE)
+    ap.add_argument("--configs", default="all",
+                    help="other MoE-layer configs measured in the same run: all, none or a comma list")
+    ap.add_argument("--layers", type=int, default=24, help="weight copies cycled over")
+    ap.add_argument("--profile-steps", type=int, default=480, help="steps of the per-stage timing pass")
+    ap.add_argument("--cpu-seconds", type=float, default=16.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-pack", action="store_true",
+                    help="MLX-layout weights only (no fmx_pack_expert_weights re-layout)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs the MoE layer on one GPU only (one GPU per "
+                                   "box); run bench.py with --gpus 1",
+                          "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
+
+    sys.path.insert(0, ROOT)
+    import torch
+
+    from flashmlx_amd import workloads as W
+
+    torch.cuda.set_device(0)
+    R = max(1, args.layers)
+    pack = not args.no_pack
+    wl = W.WORKLOADS[args.workload]
+    K, Wm = args.steps, args.warmup
+    head, y_head, inds_head = measure(wl, R, K, Wm, args.trials, args.profile_steps, pack)
+
+    if args.configs == "all":
+        keys = [k for k in CONFIGS if k != wl.key]
+    elif args.configs == "none":
+        keys = []
+    else:
+        keys = [k for k in args.configs.split(",") if k and k != wl.key]
+    configs = {}
+    for key in keys:
+        c = W.WORKLOADS[key]
+        # prefill steps are ~20x longer than decode steps: a tenth as many
+        steps = K if c.tokens <= 16 else max(R, K // 10)
+        warm = Wm if c.tokens <= 16 else max(R, Wm // 10)
+        configs[key], _, _ = measure(c, R, steps, warm, args.trials, args.profile_steps, pack)
+
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         try:
-            cpu = cpu_baseline(wl, args.cpu_seconds)
+            cpu, parity = cpu_baseline(wl, y_head, inds_head, args.cpu_seconds)
         except Exception as e:  # noqa: BLE001
             log(f"CPU baseline failed: {e}")
 
     out = {
         "metric": METRIC,
-        "value": round(tok_s, 1),
+        "value": head["value"],
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": Wm,
-        "ms_per_step": round(ms_step, 6),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) bf16 activations, N(0,0.02) weights quantized affine 4-bit g64",
         "config": {
-            "workload": f"{m['name']} MoE block, {wl.note}",
+            "workload": head["workload"],
             "key": wl.key,
-            "tokens": T,
-            "hidden": m["hidden"],
-            "experts": m["n_experts"],
-            "top_k": m["top_k"],
-            "moe_intermediate": m["inter"],
-            "shared_intermediate": m["shared_inter"],
+            "tokens": wl.tokens,
+            "hidden": wl.model["hidden"],
+            "experts": wl.model["n_experts"],
+            "top_k": wl.model["top_k"],
+            "moe_intermediate": wl.model["inter"],
+            "shared_intermediate": wl.model["shared_inter"],
             "seed": wl.seed,
             "layer_copies": R,
             "hip_graph": True,
+            "timing": f"median of {args.trials} trials of {K} steps, every graph replayed first",
             "parallelism": "single GPU",
         },
-        "roofline": roof,
-        "layer": layer,
-        "wall_s": round(wall, 3),
+        "roofline": head["roofline"],
+        "layer": head["layer"],
+        "trial_ms": head["trial_ms"],
+        "wall_s": head["wall_s"],
+        "parity": parity,
         "cpu_baseline": cpu,
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
 

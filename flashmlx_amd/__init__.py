@@ -14,6 +14,7 @@ from .moe import (  # noqa: F401
     quantized_matmul,
     router_topk,
     synth_normal_bf16,
+    synth_normal_bf16_device,
 )
 
 __all__ = [
@@ -30,4 +31,5 @@ __all__ = [
     "quantized_matmul",
     "router_topk",
     "synth_normal_bf16",
+    "synth_normal_bf16_device",
 ]

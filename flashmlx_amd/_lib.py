@@ -61,6 +61,11 @@ class FmxMoEWeights(C.Structure):
         ("shared_down", FmxQWeight),
         ("shared_expert_gate_w", C.c_void_p),
         ("packed", C.c_void_p),
+        ("packed_bytes", C.c_size_t),
+        ("router_scales", C.c_void_p),
+        ("router_biases", C.c_void_p),
+        ("shared_expert_gate_scales", C.c_void_p),
+        ("shared_expert_gate_biases", C.c_void_p),
     ]
 
 
@@ -140,6 +145,8 @@ _SIGS = {
     ),
     "fmx_synth_normal_bf16": (
         C.c_int, [C.c_void_p, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_double]),
+    "fmx_synth_normal_bf16_device": (
+        C.c_int, [C.c_void_p, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_double, C.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGS)

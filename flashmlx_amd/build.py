@@ -25,7 +25,7 @@ SOURCES = [
     "csrc/fmx_prefill.hip",
     "csrc/fmx_elem.hip",
     "csrc/fmx_api.cpp",
-    "csrc/fmx_synth.cpp",
+    "csrc/fmx_synth.hip",
 ]
 
 ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")

@@ -180,7 +180,9 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
   L.sd = static_cast<uint16_t*>(ar.take(Is ? T * H * 2 : 0));
-  L.dw = static_cast<uint32_t*>(ar.take(T <= kDecMaxT ? n * H * 4 : 0));
+  // the decode kernels' down products (forwards of at most kDecMaxT tokens);
+  // sized for min(T, kDecMaxT) at every T so that the layout only grows with T
+  L.dw = static_cast<uint32_t*>(ar.take(std::min<int64_t>(T, kDecMaxT) * k * H * 4));
   L.total = ar.used;
   return L;
 }
@@ -237,16 +239,36 @@ PackedLayout packed_layout(const fmx_moe_config& c) {
   return P;
 }
 
+// The router's rows and the shared-expert gate row (model.cpp:757-763,
+// :787-799), bf16 or quantized; null rows when absent.
+RouterRows router_rows(const fmx_moe_weights& w) {
+  return RouterRows{w.router_w, static_cast<const uint16_t*>(w.router_scales),
+                    static_cast<const uint16_t*>(w.router_biases)};
+}
+RouterRows sgate_rows(const fmx_moe_config& c, const fmx_moe_weights& w) {
+  if (c.shared_expert_intermediate_size <= 0) return RouterRows{nullptr, nullptr, nullptr};
+  return RouterRows{w.shared_expert_gate_w, static_cast<const uint16_t*>(w.shared_expert_gate_scales),
+                    static_cast<const uint16_t*>(w.shared_expert_gate_biases)};
+}
+
+// A router row set is usable: bf16 rows 16-byte aligned, or 4-bit words
+// 4-byte aligned with both scales and biases.
+bool rows_ok(const RouterRows& r) {
+  if (!r.w) return false;
+  if (!r.s) return aligned(r.w, 16) && !r.b;
+  return aligned(r.w, 4) && r.b && aligned(r.s, 2) && aligned(r.b, 2);
+}
+
 // Router launch shared by the block forward and fmx_moe_router_topk.
 int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64_t T,
-               const void* router_w, const void* lbias, const void* wsg, uint32_t* inds,
+               const RouterRows& wr, const void* lbias, const RouterRows& wsg, uint32_t* inds,
                uint16_t* scores, uint16_t* probs, float* sgate, uint16_t* xp, bool want_sort,
                bool* sorted_in_router, hipStream_t stream) {
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
-  a.wr = static_cast<const uint16_t*>(router_w);
+  a.wr = wr;
   a.lbias = static_cast<const uint16_t*>(lbias);
-  a.wsg = static_cast<const uint16_t*>(wsg);
+  a.wsg = wsg;
   a.T = static_cast<int>(T);
   a.H = static_cast<int>(c.hidden_size);
   a.E = static_cast<int>(c.num_experts);
@@ -264,7 +286,7 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   // most CUs; many token tiles: 4 columns per wave re-read x 4x less
   a.cols_per_wave = a.n_tt > 1 ? 4 : 1;
   const int64_t cols_per_tile = 4 * a.cols_per_wave;
-  a.n_ct = static_cast<int>((c.num_experts + (wsg ? 1 : 0) + cols_per_tile - 1) / cols_per_tile);
+  a.n_ct = static_cast<int>((c.num_experts + (wsg.w ? 1 : 0) + cols_per_tile - 1) / cols_per_tile);
   const int64_t n = T * c.num_experts_per_tok;
   a.fuse_sort = want_sort && router_sort_fits(n, c.num_experts) ? 1 : 0;
   a.sort.order = L.order;
@@ -534,7 +556,7 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   if (rows == 0 || p.N == 0) return ok();
   if (p.E == 0 || p.n_x == 0) return fail(FMX_ERR_SHAPE, "empty w or x batch with non-empty output");
   if (!sort_fits(rows, p.E))
-    return fail(FMX_ERR_UNSUPPORTED, "rows=%lld x experts=%lld exceed the one-workgroup sort",
+    return fail(FMX_ERR_UNSUPPORTED, "rows=%lld x experts=%lld exceed the sort's limits",
                 static_cast<long long>(rows), static_cast<long long>(p.E));
 
   Arena ar;
@@ -816,18 +838,30 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
   if (!x || !y) return fail(FMX_ERR_ARG, "NULL argument");
   const fmx_moe_config& c = *cfg;
   const bool has_sh = c.shared_expert_intermediate_size > 0;
-  if (!w->router_w || !aligned(w->router_w, 16)) return fail(FMX_ERR_ARG, "router_w NULL or misaligned");
-  if (!qw_ok(w->gate) || !qw_ok(w->up) || !qw_ok(w->down))
-    return fail(FMX_ERR_ARG, "expert weights NULL or misaligned");
-  if (has_sh && (!qw_ok(w->shared_gate) || !qw_ok(w->shared_up) || !qw_ok(w->shared_down) ||
-                 !w->shared_expert_gate_w || !aligned(w->shared_expert_gate_w, 16)))
-    return fail(FMX_ERR_ARG, "shared expert weights NULL or misaligned");
+  const RouterRows wr = router_rows(*w), wsg = sgate_rows(c, *w);
+  if (!rows_ok(wr)) return fail(FMX_ERR_ARG, "router_w (or its scales/biases) NULL or misaligned");
+  if (has_sh && !rows_ok(wsg))
+    return fail(FMX_ERR_ARG, "shared_expert_gate_w (or its scales/biases) NULL or misaligned");
+  // packed weights: the forward reads the experts from there only
+  const bool use_packed = w->packed != nullptr;
+  if (use_packed) {
+    if (!packable(c)) return fail(FMX_ERR_ARG, "packed weights given for a config that cannot be packed");
+    if (!aligned(w->packed, 256)) return fail(FMX_ERR_ARG, "packed not 256-byte aligned");
+    if (w->packed_bytes < packed_layout(c).total)
+      return fail(FMX_ERR_WORKSPACE, "packed_bytes %zu, the config needs %zu", w->packed_bytes,
+                  packed_layout(c).total);
+  } else {
+    if (!qw_ok(w->gate) || !qw_ok(w->up) || !qw_ok(w->down))
+      return fail(FMX_ERR_ARG, "expert weights NULL or misaligned");
+    if (has_sh && (!qw_ok(w->shared_gate) || !qw_ok(w->shared_up) || !qw_ok(w->shared_down)))
+      return fail(FMX_ERR_ARG, "shared expert weights NULL or misaligned");
+  }
   if (!aligned(x, 16) || !aligned(y, 16)) return fail(FMX_ERR_ARG, "x/y not 16-byte aligned");
   const int64_t H = c.hidden_size, E = c.num_experts, k = c.num_experts_per_tok;
   const int64_t I = c.moe_intermediate_size, Is = c.shared_expert_intermediate_size;
   const int64_t n = T * k;
   if (!sort_fits(n, E))
-    return fail(FMX_ERR_UNSUPPORTED, "T*k=%lld with E=%lld exceeds the one-workgroup sort",
+    return fail(FMX_ERR_UNSUPPORTED, "T*k=%lld with E=%lld exceeds the sort's limits",
                 static_cast<long long>(n), static_cast<long long>(E));
 
   Arena ar;
@@ -837,8 +871,8 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
   if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
   const MoELayout L = moe_layout(c, T, ar.base);
 
-  // decode batches (T <= 16) on packed weights: three kernels, combine included
-  if (w->packed && packable(c) && aligned(w->packed, 256)) {
+  // decode batches (T <= 16) on packed weights: two kernels, combine included
+  if (use_packed) {
     const PackedLayout PL = packed_layout(c);
     const uint8_t* pk = static_cast<const uint8_t*>(w->packed);
     DecodeArgs da{};
@@ -850,9 +884,9 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.Is = static_cast<int>(Is);
     da.norm = c.norm_topk_prob ? 1 : 0;
     da.x = static_cast<const uint16_t*>(x);
-    da.wr = static_cast<const uint16_t*>(w->router_w);
+    da.wr = wr;
     da.lbias = static_cast<const uint16_t*>(w->router_logit_bias);
-    da.wsg = has_sh ? static_cast<const uint16_t*>(w->shared_expert_gate_w) : nullptr;
+    da.wsg = wsg;
     da.gu = pk + PL.gu;
     da.gu_es = PL.gu_es;
     da.dn = pk + PL.dn;
@@ -898,8 +932,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     // grid, combine
     FMX_HIP(mark(0));
     bool sorted = false;
-    if ((rc = run_router(c, L, x, T, w->router_w, w->router_logit_bias,
-                         has_sh ? w->shared_expert_gate_w : nullptr, L.inds, L.scores, L.probs,
+    if ((rc = run_router(c, L, x, T, wr, w->router_logit_bias, wsg, L.inds, L.scores, L.probs,
                          has_sh ? L.sgate : nullptr, nullptr, true, &sorted, stream)))
       return rc;
     if (!sorted) {
@@ -988,8 +1021,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
   // 1. router + top-k (+ sort when it fits in the router's last workgroup)
   FMX_HIP(mark(0));
   bool sorted = false;
-  if ((rc = run_router(c, L, x, T, w->router_w, w->router_logit_bias,
-                       has_sh ? w->shared_expert_gate_w : nullptr, L.inds, L.scores, L.probs,
+  if ((rc = run_router(c, L, x, T, wr, w->router_logit_bias, wsg, L.inds, L.scores, L.probs,
                        has_sh ? L.sgate : nullptr, L.xp, true, &sorted, stream)))
     return rc;
   if (!sorted) {
@@ -1134,7 +1166,8 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, con
   if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
   if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
   const MoELayout L = moe_layout(*cfg, T, ar.base);
-  return run_router(*cfg, L, x, T, router_w, lbias, nullptr, inds, static_cast<uint16_t*>(scores),
+  return run_router(*cfg, L, x, T, RouterRows{router_w, nullptr, nullptr}, lbias,
+                    RouterRows{nullptr, nullptr, nullptr}, inds, static_cast<uint16_t*>(scores),
                     static_cast<uint16_t*>(probs), nullptr, nullptr, false, nullptr, stream);
 }
 
@@ -1155,7 +1188,7 @@ int fmx_moe_sort(const uint32_t* inds, int64_t T, int32_t k, int64_t E, uint32_t
   if (T < 0 || k < 1 || E < 1) return fail(FMX_ERR_SHAPE, "bad sizes");
   const int64_t n = T * k;
   if (n == 0) return ok();
-  if (!sort_fits(n, E)) return fail(FMX_ERR_UNSUPPORTED, "n=%lld, E=%lld exceed the one-workgroup sort",
+  if (!sort_fits(n, E)) return fail(FMX_ERR_UNSUPPORTED, "n=%lld, E=%lld exceed the sort's limits",
                                     static_cast<long long>(n), static_cast<long long>(E));
   Arena ar;
   WsGuard guard(ar);

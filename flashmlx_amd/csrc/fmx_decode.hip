@@ -235,7 +235,7 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
       a.inds[t * a.k + lane] = e;
       a.scores[t * a.k + lane] = sc;
     }
-    if (lane == 0 && a.wsg) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
+    if (lane == 0 && a.wsg.w) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
   }
 }
 
@@ -255,7 +255,7 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   // every token's logits -> LDS in one round trip (device-scope loads: the
   // other router workgroups' device-scope stores completed before their
   // arrivals were counted)
-  const int ncols = E + (a.wsg ? 1 : 0);
+  const int ncols = E + (a.wsg.w ? 1 : 0);
   for (int i = tid; i < ncols * T; i += kDecThreads) {
     const int c = i / T, t = i - c * T;
     const uint16_t v = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
@@ -303,9 +303,10 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
 }
 
 // Router column c (column E: the shared-expert gate row) for every token,
-// one per workgroup: logits = x . w_c in fp64 (bf16 products are exact in
-// fp32, their sum is exact in fp64 and so independent of order), rounded
-// once to bf16 (model.cpp:762, :792-799). Lane g of the workgroup takes
+// one per workgroup: logits = x . w_c in fp64 (the products of bf16 x with
+// bf16 or dequantised 4-bit weights are exact in fp64, and so is their sum up
+// to far below the bf16 rounding step, independent of order), rounded once
+// to bf16 (model.cpp:757-763, :787-799). Lane g of the workgroup takes
 // 16-byte chunk g of H; each wave's partial sums meet in one reduce-scatter
 // and the four waves' in LDS. The last router workgroup to finish derives
 // the routing.
@@ -318,21 +319,18 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, T = a.T, E = a.E, xs = xstride(H);
-  const int ncols = E + (a.wsg ? 1 : 0);
+  const int ncols = E + (a.wsg.w ? 1 : 0);
   const int nch = H / 8;
   dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  const uint16_t* wrow = c < E ? a.wr + static_cast<int64_t>(c) * H : a.wsg;
-  const u32x4_t wv = *reinterpret_cast<const u32x4_t*>(wrow + min(tid, nch - 1) * 8);
+  const RChunk wv = c < E ? load_rchunk(a.wr, c, H, min(tid, nch - 1))
+                          : load_rchunk(a.wsg, 0, H, min(tid, nch - 1));
   const bool biased = c < E && a.lbias;
   const uint16_t lb = biased ? a.lbias[c] : 0;
   wait_vmcnt0();
   lds_dma_barrier();
   double wd[8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    wd[2 * q] = tid < nch ? static_cast<double>(__uint_as_float(wv[q] << 16)) : 0.0;
-    wd[2 * q + 1] = tid < nch ? static_cast<double>(__uint_as_float(wv[q] & 0xffff0000u)) : 0.0;
-  }
+  for (int q = 0; q < 8; ++q) wd[q] = tid < nch ? wv.get(q) : 0.0;
   double part[kDecMaxT];
 #pragma unroll
   for (int t = 0; t < kDecMaxT; ++t) {

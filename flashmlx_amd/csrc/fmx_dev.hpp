@@ -178,6 +178,40 @@ __device__ inline double reduce_scatter64(double (&v)[N], int lane) {
   return r;
 }
 
+// ------------------------------------------------------------------ router rows
+
+// Eight consecutive weights (elements 8 ch .. 8 ch + 7) of a router row, held
+// raw until used: a 16-byte bf16 chunk, or one 4-bit word with its group's
+// scale and bias (RouterRows). get(j) is weight j as an exact double: for the
+// quantized form s*q + b of bf16 s, b and q in 0..15 (MLX's dequantised
+// value, model.cpp:758-760), whose product and sum are exact in fp64.
+struct RChunk {
+  u32x4_t v;  // the bf16 chunk, or v[0] = the 4-bit word
+  float s, b;
+  bool q;
+  __device__ inline double get(int j) const {
+    if (q) return __builtin_fma(static_cast<double>(s), static_cast<double>((v[0] >> (4 * j)) & 15u),
+                                static_cast<double>(b));
+    const uint32_t w = v[j >> 1];
+    return static_cast<double>(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16)));
+  }
+};
+
+__device__ inline RChunk load_rchunk(const RouterRows& r, int64_t row, int H, int ch) {
+  RChunk c;
+  c.q = r.s != nullptr;
+  if (c.q) {
+    c.v = u32x4_t{static_cast<const uint32_t*>(r.w)[row * (H / 8) + ch], 0u, 0u, 0u};
+    const int64_t g = row * (H / 64) + ch / 8;
+    c.s = bf16_to_f32(r.s[g]);
+    c.b = bf16_to_f32(r.b[g]);
+  } else {
+    c.v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(r.w) + row * H + ch * 8);
+    c.s = c.b = 0.0f;
+  }
+  return c;
+}
+
 // ------------------------------------------------------------------ LDS staging
 
 // One row of K bf16 (K a multiple of 8) -> LDS by LDS DMA: each

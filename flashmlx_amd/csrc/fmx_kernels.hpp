@@ -32,9 +32,11 @@ __host__ __device__ inline int max_passes(int64_t n, int64_t E) {
 }
 
 // Sort by one workgroup of 1024 threads per key value (separate launch),
-// keys LDS-resident.
+// keys LDS-resident up to kSortLdsN of them, re-read from global memory
+// (an L2-resident array) beyond.
 constexpr int kSortThreads = 1024;
-constexpr int kSortMaxN = 32 * 1024;       // keys held in LDS (16 bits each)
+constexpr int kSortLdsN = 32 * 1024;       // keys held in LDS (16 bits each)
+constexpr int64_t kSortMaxN = 1 << 22;     // keys of one sort
 constexpr int kSortMaxE = 1024;            // per-wave key counters in LDS
 bool sort_fits(int64_t n, int64_t E);
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
@@ -49,11 +51,19 @@ constexpr int kRouterThreads = 256;  // 4 waves; each wave forms 8 tokens x cols
 constexpr int kRouterSortCnt = 16 * 1024;  // LDS bytes for a fused sort's count table
 constexpr int kRouterSortMaxN = 2048;
 
+// Router rows come either as bf16 [rows, H] or as MLX affine 4-bit rows
+// (u32 [rows, H/8] with bf16 scales/biases [rows, H/64]; `s` non-null).
+struct RouterRows {
+  const void* w;
+  const uint16_t* s;
+  const uint16_t* b;
+};
+
 struct RouterArgs {
   const uint16_t* x;       // [T, H] bf16
-  const uint16_t* wr;      // [E, H] bf16
+  RouterRows wr;           // [E, H] router
   const uint16_t* lbias;   // [E] bf16 or null
-  const uint16_t* wsg;     // [H] bf16 shared-expert gate or null
+  RouterRows wsg;          // [1, H] shared-expert gate (wsg.w null: none)
   int T, H, E, k, norm;
   uint16_t* logits;        // [T, E+1] bf16 scratch (column E: shared gate logit)
   uint16_t* probs;         // [T, E] bf16 or null
@@ -139,9 +149,9 @@ constexpr int kPackedBlockPair = 2304;    // gate + up
 struct DecodeArgs {
   int T, H, E, k, I, Is, norm;
   const uint16_t* x;        // [T, H] bf16
-  const uint16_t* wr;       // [E, H] bf16 router
+  RouterRows wr;            // [E, H] router
   const uint16_t* lbias;    // [E] bf16 router logit bias or null
-  const uint16_t* wsg;      // [H] bf16 shared-expert gate row, null when Is == 0
+  RouterRows wsg;           // [1, H] shared-expert gate row (wsg.w null when Is == 0)
   const uint8_t* gu;        // packed gate/up pairs of the routed experts
   int64_t gu_es;            //   bytes per expert
   const uint8_t* dn;        // packed down projections of the routed experts

@@ -30,18 +30,18 @@
 // conflicts. The DMA writes a 1 KB piece (4 rows) per instruction and picks
 // each lane's source chunk to match.
 //
-// Weights are dequantised in registers to bf16, s*q + b evaluated in fp32
-// and rounded once, and multiplied against every 16-row tile of the pass
-// with v_mfma_f32_16x16x32_bf16 (fp32 accumulation): the dequantisation is
-// paid once per weight per pass, the MFMAs once per 16 rows.
+// Exact dequantisation (as in the decode kernels, fmx_dev.hpp): nibbles
+// become the bf16 values 128 + q, v_mfma_f32_16x16x32_bf16 forms P =
+// x.(128+q) and X = x.1 per quantisation group in fp32, and each group adds
+// s P + (b - 128 s) X to the fp32 accumulator: the weights s*q + b are never
+// rounded to bf16. (Rounding them to bf16 first, one conversion per weight
+// per pass, costs 0.5 % relative L2 error of the block output at 512 tokens
+// and puts single elements outside the bf16 parity tolerance.)
 #include "fmx_dev.hpp"
 
 namespace fmx {
 
 namespace {
-
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPfThreads = 256;
 constexpr int kPfWaves = kPfThreads / kWave;
@@ -75,36 +75,6 @@ __device__ inline void dma16(const void* g, void* lds) {
 }
 __device__ inline void dma4(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
-}
-
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-  const f32x2_t v = {a, b};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
-
-// The 8 weights of a packed word (element 2i at nibble position i, 2i + 1 at
-// i + 4) as bf16(s*q + b) in natural element order. Masking the even and the
-// odd nibble positions into bytes gives bytes 0..3 of lo = elements 0, 4, 1,
-// 5 and of hi = 2, 6, 3, 7. A byte 0..15 is the FP8 (E4M3) encoding of
-// q * 2^-9 (the subnormal and first normal binade are evenly spaced), and
-// v_cvt_scalef32_pk_f32_fp8 converts two such bytes to fp32 with a
-// power-of-two scale, so 2^9 gives q exactly: one instruction per two
-// weights instead of one per weight. s*q + b is then one fma in fp32,
-// rounded once to bf16.
-constexpr float kFp8Q = 512.0f;  // 2^9: FP8 byte q (0..15) -> q
-
-__device__ inline bf16x8_t dq8(uint32_t w, float s, float b) {
-  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
-  const f32x2_t q04 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, kFp8Q, false);  // elements 0, 4
-  const f32x2_t q15 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, kFp8Q, true);   // 1, 5
-  const f32x2_t q26 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, kFp8Q, false);  // 2, 6
-  const f32x2_t q37 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, kFp8Q, true);   // 3, 7
-  u32x4_t d;
-  d[0] = pack_bf16x2(__builtin_fmaf(s, q04[0], b), __builtin_fmaf(s, q15[0], b));
-  d[1] = pack_bf16x2(__builtin_fmaf(s, q26[0], b), __builtin_fmaf(s, q37[0], b));
-  d[2] = pack_bf16x2(__builtin_fmaf(s, q04[1], b), __builtin_fmaf(s, q15[1], b));
-  d[3] = pack_bf16x2(__builtin_fmaf(s, q26[1], b), __builtin_fmaf(s, q37[1], b));
-  return __builtin_bit_cast(bf16x8_t, d);
 }
 
 // One work item: rows [row0, row0 + rows) (rows <= 16 MT) of expert e's
@@ -193,11 +163,9 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 
     const uint8_t* sa = s_pf + (u % kPfStages) * STAGE;
     const uint8_t* sb = sa + kPfABytes + wave * WB;
-    // the unit's packed words and (scale, bias) pairs; each k-slice q is
-    // dequantised right before its MFMAs, so that only one slice of weights
-    // is live in registers
+    // the unit's packed words and (scale, bias) pairs
     u32x4_t W[NB][NM];
-    float sc[NB][NM][2], bi[NB][NM][2];
+    float sc[NB][NM][2], cb[NB][NM][2];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
 #pragma unroll
@@ -206,13 +174,12 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
         const u32x2_t sbw = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
         sc[b][m][0] = __uint_as_float(sbw[0] << 16);
         sc[b][m][1] = __uint_as_float(sbw[0] & 0xffff0000u);
-        bi[b][m][0] = __uint_as_float(sbw[1] << 16);
-        bi[b][m][1] = __uint_as_float(sbw[1] & 0xffff0000u);
+        cb[b][m][0] = __builtin_fmaf(-128.0f, sc[b][m][0], __uint_as_float(sbw[1] << 16));
+        cb[b][m][1] = __builtin_fmaf(-128.0f, sc[b][m][1], __uint_as_float(sbw[1] & 0xffff0000u));
       }
     }
     // every activation operand of the unit is read up front (one LDS round
-    // trip per unit, not one per k-slice); the first slice's dequantisation
-    // runs while they land
+    // trip per unit, not one per k-slice)
     bf16x8_t A[4][MT];
 #pragma unroll
     for (int q = 0; q < 4; ++q)
@@ -220,19 +187,31 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       for (int mt = 0; mt < MT; ++mt)
         A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
     __builtin_amdgcn_sched_barrier(0);
+    // exact dequantisation, one quantisation group (two k-slices) at a time:
+    // P = x.(128+q) and X = x.1 by MFMA, then acc += s P + (b - 128 s) X
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bf16x8_t B[NB][NM];
+    for (int g = 0; g < 2; ++g) {
+      f32x4_t X[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) X[mt] = mfma_bf16(A[2 * g + 1][mt], ones, mfma_bf16(A[2 * g][mt], ones, zero));
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int m = 0; m < NM; ++m) B[b][m] = dq8(W[b][m][q], sc[b][m][q >> 1], bi[b][m][q >> 1]);
+        for (int m = 0; m < NM; ++m) {
+          const bf16x8_t B0 = nib8(W[b][m][2 * g]), B1 = nib8(W[b][m][2 * g + 1]);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+          for (int mt = 0; mt < MT; ++mt) {
+            const f32x4_t P = mfma_bf16(A[2 * g + 1][mt], B1, mfma_bf16(A[2 * g][mt], B0, zero));
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) acc[mt][b][m] = mfma_bf16(A[q][mt], B[b][m], acc[mt][b][m]);
+            for (int i = 0; i < 4; ++i) {
+              acc[mt][b][m][i] = __builtin_fmaf(sc[b][m][g], P[i], acc[mt][b][m][i]);
+              acc[mt][b][m][i] = __builtin_fmaf(cb[b][m][g], X[mt][i], acc[mt][b][m][i]);
+            }
+          }
+        }
     }
   }
 

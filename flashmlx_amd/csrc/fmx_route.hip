@@ -27,10 +27,11 @@ constexpr int kSortWaves = kSortThreads / kWave;
 // per wave, the waves' counts in order, a running total), which is the
 // stable order. The outputs' scattered stores spread over E workgroups.
 // Workgroup 0 writes offsets and the segment and pass counts; workgroup e
-// its own segment and passes.
+// its own segment and passes. Up to kSortLdsN keys stay in LDS between the
+// two walks; more are read again from the key array (in the L2 by then).
 __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys, int n, int k,
                                                             int E, SortOut o) {
-  __shared__ uint16_t s_key[kSortMaxN];
+  __shared__ uint16_t s_key[kSortLdsN];
   __shared__ uint32_t s_cnt[kSortMaxE];
   __shared__ uint32_t s_tmp[kSortWaves + 1];
   __shared__ uint32_t s_wcnt[kSortWaves];
@@ -39,12 +40,13 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
   const int e = blockIdx.x;
   const uint32_t emax = static_cast<uint32_t>(E - 1);
 
+  const bool in_lds = n <= kSortLdsN;
   for (int i = tid; i < E; i += kSortThreads) s_cnt[i] = 0u;
   __syncthreads();
 #pragma unroll 8
   for (int i = tid; i < n; i += kSortThreads) {
     const uint32_t key = min(keys[i], emax);
-    s_key[i] = static_cast<uint16_t>(key);
+    if (in_lds) s_key[i] = static_cast<uint16_t>(key);
     atomicAdd(&s_cnt[key], 1u);
   }
   __syncthreads();
@@ -90,7 +92,8 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
   uint32_t run = my_off;
   for (int base = 0; base < n; base += kSortThreads) {
     const int i = base + tid;
-    const bool match = i < n && s_key[i] == static_cast<uint16_t>(e);
+    const bool match = i < n && (in_lds ? static_cast<uint32_t>(s_key[i]) : min(keys[i], emax)) ==
+                                    static_cast<uint32_t>(e);
     const uint64_t b = __ballot(match);
     if (lane == 0) s_wcnt[wave] = static_cast<uint32_t>(__popcll(b));
     __syncthreads();
@@ -151,19 +154,16 @@ constexpr int kRouterWaves = kRouterThreads / kWave;
 template <int TT, int CE>
 __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int lane) {
   const int H = a.H, E = a.E;
-  const int ncols = E + (a.wsg ? 1 : 0);
+  const int ncols = E + (a.wsg.w ? 1 : 0);
   const int c0 = (ct * kRouterWaves + wave) * CE;
   if (c0 >= ncols) return;  // wave-uniform
   constexpr int NV = TT * CE;
   double acc[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) acc[i] = 0.0;
-  const uint16_t* wrow[CE];
+  int col[CE];
 #pragma unroll
-  for (int c = 0; c < CE; ++c) {
-    const int col = min(c0 + c, ncols - 1);
-    wrow[c] = col < E ? a.wr + static_cast<int64_t>(col) * H : a.wsg;
-  }
+  for (int c = 0; c < CE; ++c) col[c] = min(c0 + c, ncols - 1);
   const uint16_t* xrow[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t)
@@ -171,9 +171,11 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
   const int nchunk = H / 8;
 #pragma unroll 2
   for (int ch = lane; ch < nchunk; ch += kWave) {
-    u32x4_t wv[CE], xv[TT];
+    RChunk wv[CE];
+    u32x4_t xv[TT];
 #pragma unroll
-    for (int c = 0; c < CE; ++c) wv[c] = *reinterpret_cast<const u32x4_t*>(wrow[c] + ch * 8);
+    for (int c = 0; c < CE; ++c)
+      wv[c] = col[c] < E ? load_rchunk(a.wr, col[c], H, ch) : load_rchunk(a.wsg, 0, H, ch);
 #pragma unroll
     for (int t = 0; t < TT; ++t) xv[t] = *reinterpret_cast<const u32x4_t*>(xrow[t] + ch * 8);
 #pragma unroll
@@ -181,8 +183,8 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
       double w0[CE], w1[CE];
 #pragma unroll
       for (int c = 0; c < CE; ++c) {
-        w0[c] = __uint_as_float(wv[c][i] << 16);
-        w1[c] = __uint_as_float(wv[c][i] & 0xffff0000u);
+        w0[c] = wv[c].get(2 * i);
+        w1[c] = wv[c].get(2 * i + 1);
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
@@ -285,7 +287,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
     }
     a.scores[static_cast<int64_t>(t) * a.k + lane] = out;
   }
-  if (lane == 0 && a.wsg && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
+  if (lane == 0 && a.wsg.w && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
 }
 
 static_assert(kPassRows >= kWave, "a segment of at most 64 rows is one pass");
@@ -392,25 +394,27 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, kk = lane >> 4;
   const int H = a.H, E = a.E;
-  const int ncols = E + (a.wsg ? 1 : 0);
+  const int ncols = E + (a.wsg.w ? 1 : 0);
   const int t0 = blockIdx.y * 16, c0 = blockIdx.x * 16;
   // MFMA operands: lane (i16, kk) feeds token row i16 (A) and column i16 (B)
   // at k = 8 * chunk + m for the m-th of 8 MFMAs per 16-byte chunk
   const uint16_t* xrow = a.x + static_cast<int64_t>(min(t0 + i16, a.T - 1)) * H;
   const int col = min(c0 + i16, ncols - 1);
-  const uint16_t* wrow = col < E ? a.wr + static_cast<int64_t>(col) * H : a.wsg;
+  const RouterRows& wrows = col < E ? a.wr : a.wsg;
+  const int64_t wrow = col < E ? col : 0;
   const int nch = H / 8;
   f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
   // kLgBatch chunks per lane are loaded together (one memory latency per
   // batch, not per chunk), then multiplied in the same chunk order
   constexpr int kLgStep = 4 * kLgWaves;
   for (int base = 0; base < nch; base += kLgStep * kLgBatch) {
-    u32x4_t xv[kLgBatch], wv[kLgBatch];
+    u32x4_t xv[kLgBatch];
+    RChunk wv[kLgBatch];
 #pragma unroll
     for (int b = 0; b < kLgBatch; ++b) {
       const int ch = min(base + kLgStep * b + 4 * wave + kk, nch - 1);
       xv[b] = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
-      wv[b] = *reinterpret_cast<const u32x4_t*>(wrow + ch * 8);
+      wv[b] = load_rchunk(wrows, wrow, H, ch);
     }
 #pragma unroll
     for (int b = 0; b < kLgBatch; ++b) {
@@ -419,7 +423,7 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const double x0 = __uint_as_float(xv[b][i] << 16), x1 = __uint_as_float(xv[b][i] & 0xffff0000u);
-        const double w0 = __uint_as_float(wv[b][i] << 16), w1 = __uint_as_float(wv[b][i] & 0xffff0000u);
+        const double w0 = wv[b].get(2 * i), w1 = wv[b].get(2 * i + 1);
         acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
       }
@@ -457,7 +461,7 @@ __global__ __launch_bounds__(kRouterThreads) void topk_kernel(RouterArgs a) {
 }
 
 hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream) {
-  const int ncols = a.E + (a.wsg ? 1 : 0);
+  const int ncols = a.E + (a.wsg.w ? 1 : 0);
   hipLaunchKernelGGL(logits_kernel, dim3((ncols + 15) / 16, (a.T + 15) / 16), dim3(kLgThreads), 0,
                      stream, a);
   hipError_t err = hipGetLastError();

@@ -152,6 +152,16 @@ def synth_normal_bf16(n: int, seed: int, stream: int, mean: float = 0.0,
     return out
 
 
+def synth_normal_bf16_device(shape, seed: int, stream: int, mean: float = 0.0, std: float = 1.0,
+                             device="cuda") -> torch.Tensor:
+    """synth_normal_bf16 generated on the device (same values; see fmx_synth.hip)."""
+    lib = _lib.load()
+    out = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    _lib.check(lib.fmx_synth_normal_bf16_device(out.data_ptr(), out.numel(), seed, stream, mean, std,
+                                                _stream()))
+    return out
+
+
 # --------------------------------------------------------------------- MoE block
 
 @dataclass
@@ -190,48 +200,86 @@ class QWeight:
         q.w, q.scales, q.biases = self.w.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr()
         return q
 
+    def tensors(self) -> list:
+        return [self.w, self.scales, self.biases]
+
+
+def _ptr(t) -> Optional[int]:
+    return t.data_ptr() if t is not None else None
+
 
 @dataclass
 class MoEWeights:
-    """MoEWeights (server/include/flashmlx/model.h:58-72), stacked over experts."""
-    router_w: torch.Tensor                 # bf16 [E, H]
-    gate: QWeight                          # [E, I, ..]
-    up: QWeight
-    down: QWeight                          # [E, H, ..]
+    """MoEWeights (server/include/flashmlx/model.h:58-72), stacked over experts.
+
+    The router and the shared-expert gate are a bf16 tensor or a QWeight
+    (quantized, model.cpp:758-760 and :792-796). After pack(), the MLX-layout
+    expert weights may be dropped (drop_mlx_layout): forwards read only the
+    packed copy."""
+    router_w: object                       # bf16 [E, H] or QWeight [E, H/8]
+    gate: Optional[QWeight]                # [E, I, ..]
+    up: Optional[QWeight]
+    down: Optional[QWeight]                # [E, H, ..]
     shared_gate: Optional[QWeight] = None  # [Is, ..]
     shared_up: Optional[QWeight] = None
     shared_down: Optional[QWeight] = None
-    shared_expert_gate_w: Optional[torch.Tensor] = None  # bf16 [1, H]
+    shared_expert_gate_w: object = None    # bf16 [1, H] or QWeight [1, H/8]
     router_logit_bias: Optional[torch.Tensor] = None     # bf16 [E] (no reference counterpart)
     packed: Optional[torch.Tensor] = None  # uint8 blob from pack() (no reference counterpart)
 
+    @property
+    def device(self):
+        r = self.router_w
+        return (r.w if isinstance(r, QWeight) else r).device
+
     def to_c(self) -> FmxMoEWeights:
         w = FmxMoEWeights()
-        w.router_w = self.router_w.data_ptr()
-        w.router_logit_bias = self.router_logit_bias.data_ptr() if self.router_logit_bias is not None else None
-        w.gate, w.up, w.down = self.gate.to_c(), self.up.to_c(), self.down.to_c()
-        if self.shared_gate is not None:
-            w.shared_gate = self.shared_gate.to_c()
-            w.shared_up = self.shared_up.to_c()
-            w.shared_down = self.shared_down.to_c()
-            w.shared_expert_gate_w = self.shared_expert_gate_w.data_ptr()
-        w.packed = self.packed.data_ptr() if self.packed is not None else None
+        if isinstance(self.router_w, QWeight):
+            w.router_w = self.router_w.w.data_ptr()
+            w.router_scales = self.router_w.scales.data_ptr()
+            w.router_biases = self.router_w.biases.data_ptr()
+        else:
+            w.router_w = self.router_w.data_ptr()
+        w.router_logit_bias = _ptr(self.router_logit_bias)
+        for name in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
+            q = getattr(self, name)
+            if q is not None:
+                setattr(w, name, q.to_c())
+        g = self.shared_expert_gate_w
+        if isinstance(g, QWeight):
+            w.shared_expert_gate_w = g.w.data_ptr()
+            w.shared_expert_gate_scales = g.scales.data_ptr()
+            w.shared_expert_gate_biases = g.biases.data_ptr()
+        elif g is not None:
+            w.shared_expert_gate_w = g.data_ptr()
+        if self.packed is not None:
+            w.packed = self.packed.data_ptr()
+            w.packed_bytes = self.packed.numel()
         return w
 
     def pack(self, cfg: "MoEConfig") -> None:
-        """fmx_pack_expert_weights: adds the load-time re-layout that forwards
-        of at most 16 tokens read (the MLX-layout arrays stay in use)."""
+        """fmx_pack_expert_weights: the load-time re-layout that every forward
+        then reads in place of the MLX-layout expert arrays."""
         lib = _lib.load()
         c = cfg.to_c()
         nbytes = lib.fmx_moe_packed_size(C.byref(c))
         if nbytes == 0:
             raise _lib.FmxError(_lib.FMX_ERR_UNSUPPORTED, "config cannot be packed")
         self.packed = None
-        buf = torch.empty(nbytes, dtype=torch.uint8, device=self.router_w.device)
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         w = self.to_c()
         _lib.check(lib.fmx_pack_expert_weights(C.byref(c), C.byref(w), buf.data_ptr(), nbytes,
                                                _stream()))
         self.packed = buf
+
+    def drop_mlx_layout(self) -> None:
+        """Releases the MLX-layout expert arrays once packed (the layer then
+        holds its expert weights once)."""
+        if self.packed is None:
+            raise ValueError("pack() first: the MLX-layout arrays are the only copy")
+        torch.cuda.current_stream().synchronize()  # the pack kernels have read them
+        self.gate = self.up = self.down = None
+        self.shared_gate = self.shared_up = self.shared_down = None
 
 
 class MoEBlock:
@@ -254,21 +302,26 @@ class MoEBlock:
         self.ws_bytes = self.lib.fmx_moe_workspace_size(C.byref(self._c_cfg), max_tokens)
         if self.ws_bytes == 0:
             raise _lib.FmxError(_lib.FMX_ERR_ARG, "invalid MoE config or max_tokens")
-        dev = device or weights.router_w.device
+        dev = device or weights.device
         self.workspace = torch.empty(self.ws_bytes, dtype=torch.uint8, device=dev)
         _lib.check(self.lib.fmx_moe_workspace_init(self.workspace.data_ptr(), self.ws_bytes, _stream()))
         self._last_T = 0
 
+    def refresh(self) -> None:
+        """Re-reads the weights' device pointers (after the weights changed,
+        e.g. drop_mlx_layout)."""
+        self._c_w = self.weights.to_c()
+
     def weight_tensors(self) -> list:
         """Every device tensor of the layer's weights (MLX layout and packed)."""
         w = self.weights
-        ts = [w.router_w]
-        for q in (w.gate, w.up, w.down, w.shared_gate, w.shared_up, w.shared_down):
-            if q is not None:
-                ts += [q.w, q.scales, q.biases]
-        for t in (w.shared_expert_gate_w, w.router_logit_bias, w.packed):
-            if t is not None:
-                ts.append(t)
+        ts = []
+        for q in (w.router_w, w.gate, w.up, w.down, w.shared_gate, w.shared_up, w.shared_down,
+                  w.shared_expert_gate_w, w.router_logit_bias, w.packed):
+            if isinstance(q, QWeight):
+                ts += q.tensors()
+            elif q is not None:
+                ts.append(q)
         return ts
 
     def forward_into(self, x: torch.Tensor, y: torch.Tensor) -> None:

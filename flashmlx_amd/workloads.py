@@ -52,6 +52,9 @@ class Workload:
     seed: int
     router_bias: bool = False
     note: str = ""
+    # router and shared-expert gate quantized (affine 4-bit, group 64) like
+    # every other linear, as in a checkpoint that quantizes them
+    router_quant: bool = False
 
 
 WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
@@ -74,6 +77,10 @@ WORKLOADS: Dict[str, Workload] = {w.key: w for w in [
     Workload("small_t200", SMALL, 200, 15,
              note="packable small shapes, 200 tokens (experts over several passes)"),
     Workload("small_dec_t4", SMALL_DEC, 4, 16, note="small shapes on the decode kernels, 4 tokens"),
+    Workload("qwen15_decode_b4_qrouter", QWEN15, 4, 21, router_quant=True,
+             note="decode batch 4, quantized router and shared-expert gate"),
+    Workload("small_t200_qrouter", SMALL, 200, 22, router_quant=True, router_bias=True,
+             note="packable small shapes, 200 tokens, quantized router and shared-expert gate"),
 ]}
 
 
@@ -132,11 +139,44 @@ def host_inputs(wl: Workload, tokens: Optional[int] = None) -> HostInputs:
 
 # ------------------------------------------------------------------ device side
 
-def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None, device="cuda",
-                 pack: bool = True):
-    """Uploads the inputs, quantizes the weights on the GPU (fmx_quantize),
-    packs them (fmx_pack_expert_weights) unless pack=False, and returns
-    (MoEBlock, x_device)."""
+class DeviceSynth:
+    """The tensors of HostInputs generated straight into device memory
+    (fmx_synth_normal_bf16_device: the same values), for weight sets too
+    large to build on the host."""
+
+    def __init__(self, wl: Workload, device="cuda"):
+        self.wl, self.device = wl, device
+
+    def tensor(self, name: str):
+        from .moe import synth_normal_bf16_device
+        m, s, T = self.wl.model, self.wl.seed, self.wl.tokens
+        H, E, I, Is = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"]
+        spec = dict(x=((T, H), S_X, 1.0), router_w=((E, H), S_ROUTER, W_STD),
+                    router_bias=((E,), S_RBIAS, 1.0), gate=((E, I, H), S_GATE, W_STD),
+                    up=((E, I, H), S_UP, W_STD), down=((E, H, I), S_DOWN, W_STD),
+                    shared_gate=((Is, H), S_SH_GATE, W_STD), shared_up=((Is, H), S_SH_UP, W_STD),
+                    shared_down=((H, Is), S_SH_DOWN, W_STD),
+                    shared_expert_gate_w=((1, H), S_SH_EGATE, W_STD))[name]
+        return synth_normal_bf16_device(spec[0], s, spec[1], 0.0, spec[2], self.device)
+
+    def __getattr__(self, name):
+        if name == "router_bias" and not self.wl.router_bias:
+            return None
+        if name.startswith("shared") and not self.wl.model["shared_inter"]:
+            return None
+        if name in ("x", "router_w", "router_bias", "gate", "up", "down", "shared_gate", "shared_up",
+                    "shared_down", "shared_expert_gate_w"):
+            return self.tensor(name)
+        raise AttributeError(name)
+
+
+def device_block(wl: Workload, hi, max_tokens: Optional[int] = None, device="cuda",
+                 pack: bool = True, drop_mlx: bool = False):
+    """Uploads the inputs (HostInputs, or DeviceSynth to generate them on the
+    device), quantizes the weights on the GPU (fmx_quantize), packs them
+    (fmx_pack_expert_weights) unless pack=False, and returns (MoEBlock,
+    x_device). drop_mlx: release the MLX-layout expert arrays after packing
+    (forwards read only the packed copy)."""
     import torch
 
     from .moe import MoEBlock, MoEConfig, MoEWeights, QWeight, quantize
@@ -144,6 +184,8 @@ def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None,
     m = wl.model
 
     def up(a):
+        if isinstance(a, torch.Tensor):
+            return a
         return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(device).view(torch.bfloat16)
 
     def q(a):
@@ -156,17 +198,22 @@ def device_block(wl: Workload, hi: HostInputs, max_tokens: Optional[int] = None,
                     num_experts_per_tok=m["top_k"], moe_intermediate_size=m["inter"],
                     shared_expert_intermediate_size=m["shared_inter"],
                     norm_topk_prob=m["norm_topk"])
-    w = MoEWeights(router_w=up(hi.router_w), gate=q(hi.gate), up=q(hi.up), down=q(hi.down))
+    rq = q if wl.router_quant else up
+    w = MoEWeights(router_w=rq(hi.router_w), gate=q(hi.gate), up=q(hi.up), down=q(hi.down))
     if hi.router_bias is not None:
         w.router_logit_bias = up(hi.router_bias)
     if m["shared_inter"]:
         w.shared_gate, w.shared_up, w.shared_down = q(hi.shared_gate), q(hi.shared_up), q(hi.shared_down)
-        w.shared_expert_gate_w = up(hi.shared_expert_gate_w)
-    block = MoEBlock(cfg, w, max_tokens=max_tokens or hi.x.shape[0], pack=pack)
+        w.shared_expert_gate_w = rq(hi.shared_expert_gate_w)
+    block = MoEBlock(cfg, w, max_tokens=max_tokens or wl.tokens, pack=pack)
+    if drop_mlx:
+        w.drop_mlx_layout()
+        block.refresh()
     return block, up(hi.x)
 
 
-def algorithmic_bytes(m: dict, tokens: int, unique_experts: int, router_bias: bool = False) -> int:
+def algorithmic_bytes(m: dict, tokens: int, unique_experts: int, router_bias: bool = False,
+                      router_quant: bool = False) -> int:
     """HBM bytes one MoE-layer call must move at minimum: the packed weights
     of every routed (unique) expert, the shared expert, the bf16 router and
     shared-gate rows, and the bf16 activations in and out."""
@@ -176,6 +223,9 @@ def algorithmic_bytes(m: dict, tokens: int, unique_experts: int, router_bias: bo
     shared = (2 * per_w(Is, H) + per_w(H, Is)) if Is else 0
     router = E * H * 2 + (E * 2 if router_bias else 0)
     sgate = H * 2 if Is else 0
+    if router_quant:
+        router = per_w(E, H) + (E * 2 if router_bias else 0)
+        sgate = per_w(1, H) if Is else 0
     act = 2 * tokens * H * 2
     return unique_experts * expert + shared + router + sgate + act
 
@@ -232,7 +282,7 @@ def kernel_groups(m: dict, tokens: int, packed: bool = True) -> list:
 
 
 def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = False,
-               packed: bool = True) -> list:
+               packed: bool = True, router_quant: bool = False) -> list:
     """Algorithmic work of each kernel stage of one MoE-layer call, in launch
     order: [(name, hbm_bytes, flops)]. Bytes are the weights the stage must
     read plus the activations it must read and write in HBM (the smallest
@@ -240,7 +290,10 @@ def stage_work(m: dict, tokens: int, unique_experts: int, router_bias: bool = Fa
     H, E, I, Is, k = m["hidden"], m["n_experts"], m["inter"], m["shared_inter"], m["top_k"]
     T, U = tokens, unique_experts
     pw = packed_bytes
-    router_b = E * H * 2 + (E * 2 if router_bias else 0) + (H * 2 if Is else 0)
+    if router_quant:
+        router_b = pw(E, H) + (E * 2 if router_bias else 0) + (pw(1, H) if Is else 0)
+    else:
+        router_b = E * H * 2 + (E * 2 if router_bias else 0) + (H * 2 if Is else 0)
     router_f = 2 * T * H * (E + (1 if Is else 0))
     x_b = T * H * 2
     h_b = T * k * I * 2

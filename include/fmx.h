@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FMX_ABI_VERSION 2
+#define FMX_ABI_VERSION 3
 
 typedef enum fmx_status {
   FMX_OK = 0,
@@ -101,6 +101,8 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
  * last valid row / expert on the device, so they never address memory
  * outside the arrays.
  * `sorted_indices` is a hint only: results never depend on it.
+ * Up to 2^22 output rows (prod(broadcast batch) * M) and 1024 experts;
+ * larger calls return FMX_ERR_UNSUPPORTED.
  * --------------------------------------------------------------------- */
 int fmx_gather_qmm_out_shape(const fmx_array* x, const fmx_array* w,
                              const fmx_array* lhs_indices, const fmx_array* rhs_indices,
@@ -165,9 +167,18 @@ typedef struct fmx_qweight {
   const void* biases; /* bf16 [.., N, K/64] */
 } fmx_qweight;
 
-/* MoEWeights (server/include/flashmlx/model.h:58-72), stacked layout. */
+/* MoEWeights (server/include/flashmlx/model.h:58-72), stacked layout.
+ * The router and the shared-expert gate come either unquantised (bf16 rows,
+ * model.cpp:762, :797-799) or quantized like every other linear (affine,
+ * 4 bits, group 64: model.cpp:758-760, :792-796; loaded at :389-392 and
+ * :447-455); a non-NULL *_scales pointer selects the quantized form. Their
+ * logits are formed exactly (fp64 sums of exact products, x times the
+ * dequantised s*q + b) and rounded once to bf16, in either form.
+ * When `packed` is given, the forward reads the expert weights from there
+ * only: gate/up/down and shared_gate/up/down may then be NULL (the caller may
+ * free the MLX-layout copies after fmx_pack_expert_weights). */
 typedef struct fmx_moe_weights {
-  const void* router_w;          /* bf16 [E, H] (unquantised router, model.cpp:762) */
+  const void* router_w;          /* bf16 [E, H], or u32 [E, H/8] when router_scales */
   const void* router_logit_bias; /* bf16 [E] added to the logits before softmax, or
                                     NULL. No counterpart in the reference: lets a
                                     caller skew expert loads (benchmarks).        */
@@ -177,20 +188,29 @@ typedef struct fmx_moe_weights {
   fmx_qweight shared_gate;       /* [Is, H/8] ... (ignored when Is == 0)           */
   fmx_qweight shared_up;         /* [Is, H/8] ...                                  */
   fmx_qweight shared_down;       /* [H, Is/8] ...                                  */
-  const void* shared_expert_gate_w; /* bf16 [1, H]                                 */
+  const void* shared_expert_gate_w; /* bf16 [1, H], or u32 [1, H/8] when
+                                       shared_expert_gate_scales                  */
   const void* packed;            /* NULL, or the same expert weights re-laid out by
-                                    fmx_pack_expert_weights; forwards of at most 16
-                                    tokens then read them from here. No
+                                    fmx_pack_expert_weights (read by the decode
+                                    kernels and the prefill GEMMs). No
                                     counterpart in the reference.                 */
+  size_t packed_bytes;           /* bytes of `packed`: at least
+                                    fmx_moe_packed_size(cfg), else FMX_ERR_WORKSPACE */
+  const void* router_scales;     /* bf16 [E, H/64] or NULL (bf16 router)           */
+  const void* router_biases;     /* bf16 [E, H/64]; required with router_scales   */
+  const void* shared_expert_gate_scales; /* bf16 [1, H/64] or NULL                */
+  const void* shared_expert_gate_biases; /* bf16 [1, H/64]                        */
 } fmx_moe_weights;
 
 /* Load-time re-layout of a layer's expert weights (replaces the stacking
- * step of model.cpp:368-470 as the last load-time transform; the MLX-layout
- * arrays stay valid and are still read by forwards of more than 16 tokens).
- * Packs gate+up of every routed expert as interleaved pairs, down per
- * expert, and the shared expert the same way, into `packed` (device memory
- * of fmx_moe_packed_size(cfg) bytes, 256-byte aligned). Returns 0 bytes /
- * FMX_ERR_UNSUPPORTED when H, I or Is is not a multiple of 128. */
+ * step of model.cpp:368-470 as the last load-time transform). Packs gate+up
+ * of every routed expert as interleaved pairs, down per expert, and the
+ * shared expert the same way, into `packed` (device memory of
+ * fmx_moe_packed_size(cfg) bytes, 256-byte aligned). Forwards then read only
+ * the packed copy, so the MLX-layout expert arrays can be freed once the
+ * stream has run this call: the layer holds its expert weights once (the
+ * reference keeps the per-expert arrays next to the stacked ones). Returns 0
+ * bytes / FMX_ERR_UNSUPPORTED when H, I or Is is not a multiple of 128. */
 size_t fmx_moe_packed_size(const fmx_moe_config* cfg);
 int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* src, void* packed,
                             size_t packed_bytes, fmx_stream stream);
@@ -204,7 +224,9 @@ int fmx_pack_expert_weights(const fmx_moe_config* cfg, const fmx_moe_weights* sr
 int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t n_tokens, int has_packed);
 
 /* Bytes of workspace one forward of up to max_tokens tokens needs
- * (max_tokens <= 65536). */
+ * (max_tokens <= 65536; 0 for an invalid config). Nondecreasing in
+ * max_tokens: a workspace of this size serves every forward of 0..max_tokens
+ * tokens. */
 size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens);
 
 /* Prepares a fresh workspace: clears the completion counters kept in its
@@ -266,7 +288,8 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t n_toke
 /* Sort / permutation alone (model.cpp:682-700): order = stable argsort of the
  * flattened inds, inv = argsort(order), src = order / k, idx = flat[order],
  * expert_offsets [E+1]. Any output may be NULL. Index values >= E are
- * treated as E-1. Workspace: fmx_moe_sort_workspace_size bytes (or NULL). */
+ * treated as E-1. Up to 2^22 entries (T*k) and 1024 experts. Workspace:
+ * fmx_moe_sort_workspace_size bytes (or NULL). */
 size_t fmx_moe_sort_workspace_size(int64_t n_tokens, int32_t k, int64_t num_experts);
 int fmx_moe_sort(const uint32_t* inds, int64_t n_tokens, int32_t k, int64_t num_experts,
                  uint32_t* order, uint32_t* inv, uint32_t* src, uint32_t* idx,
@@ -281,6 +304,12 @@ int fmx_moe_sort(const uint32_t* inds, int64_t n_tokens, int32_t k, int64_t num_
  * --------------------------------------------------------------------- */
 int fmx_synth_normal_bf16(uint16_t* host_out, int64_t n, uint64_t seed, uint64_t stream,
                           double mean, double std_dev);
+/* The same values written to device memory by a kernel on `stream` (for
+ * multi-GB weight sets). Its log and cos are the device library's: the bits
+ * equal the host version's except where a last-ulp fp64 difference crosses a
+ * bf16 rounding boundary (about one element in 2^44). */
+int fmx_synth_normal_bf16_device(void* out, int64_t n, uint64_t seed, uint64_t stream,
+                                 double mean, double std_dev, fmx_stream s);
 
 #ifdef __cplusplus
 }

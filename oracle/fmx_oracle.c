@@ -305,6 +305,30 @@ static uint16_t bf16_dot_exact(const uint16_t* a, const uint16_t* b, int64_t n) 
   return orc_f64_to_bf16(acc);
 }
 
+/* x . deq(w)^T of a bf16 vector and one quantized row (affine 4-bit, group
+ * 64): the dequantised weight s*q + b (bf16 s, b; q in 0..15) and its product
+ * with a bf16 x are exact in fp64, so the sum is formed as for bf16_dot_exact
+ * and rounded once (MLX: quantized_matmul of the router / shared-expert gate,
+ * model.cpp:758-760, :792-796). */
+static uint16_t q4_dot_exact(const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                             const uint16_t* b, int64_t n) {
+  double acc = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    const double q = (double)((w[i / 8] >> (4 * (i % 8))) & 15u);
+    const double sv = bf(s[i / 64]), bv = bf(b[i / 64]);
+    acc += (double)bf(x[i]) * (sv * q + bv);
+  }
+  return orc_f64_to_bf16(acc);
+}
+
+/* one router / gate row in either form: bf16 (s == NULL) or quantized */
+static uint16_t row_dot_exact(const uint16_t* x, const void* w, const uint16_t* s,
+                              const uint16_t* b, int64_t row, int64_t H) {
+  if (!s) return bf16_dot_exact(x, (const uint16_t*)w + row * H, H);
+  return q4_dot_exact(x, (const uint32_t*)w + row * (H / 8), s + row * (H / 64),
+                      b + row * (H / 64), H);
+}
+
 /* Softmax normaliser in a fixed summation order (MLX's own order is an
  * implementation detail of its CPU kernel): 64 partial sums, partial l
  * taking ex[l], ex[l+64], ... in turn, then six butterfly rounds
@@ -331,7 +355,16 @@ int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
                     const uint16_t* wr, int64_t E, const uint16_t* logit_bias,
                     int k, int norm_topk,
                     uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores) {
+  return orc_router_topk_q(x, T, H, wr, NULL, NULL, E, logit_bias, k, norm_topk, logits, probs,
+                           inds, scores);
+}
+
+int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
+                      const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
+                      const uint16_t* logit_bias, int k, int norm_topk,
+                      uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores) {
   if (k <= 0 || k > E || E > 65535) return -1;
+  if (wr_s && (!wr_b || H % 64)) return -1;
   int rc = 0;
 #pragma omp parallel
   {
@@ -346,7 +379,7 @@ int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
 #pragma omp for schedule(static)
       for (int64_t t = 0; t < T; ++t) {
         for (int64_t e = 0; e < E; ++e) {
-          uint16_t l = bf16_dot_exact(x + t * H, wr + e * H, H);
+          uint16_t l = row_dot_exact(x + t * H, wr, wr_s, wr_b, e, H);
           if (logit_bias) l = orc_f64_to_bf16((double)bf(l) + (double)bf(logit_bias[e]));
           lg[e] = l;
         }
@@ -457,8 +490,8 @@ int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
   float* acc = (float*)malloc(sizeof(float) * H);
   if (!inds || !scores || !g || !u || !a || !d || !acc) return -3;
 
-  int rc = orc_router_topk(x, T, H, w->router_w, E, w->router_bias, k, cfg->norm_topk,
-                           NULL, NULL, inds, scores);
+  int rc = orc_router_topk_q(x, T, H, w->router_w, w->router_s, w->router_b, E, w->router_bias, k,
+                             cfg->norm_topk, NULL, NULL, inds, scores);
   if (rc) return rc;
 
   const int64_t n_tok = token_subset ? n_subset : T;
@@ -484,7 +517,8 @@ int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
     for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(acc[h]);
     if (Is > 0) {
       /* shared_expert_mlp (model.cpp:736-748) and its sigmoid gate (:787-803) */
-      uint16_t gl = bf16_dot_exact(xt, w->sh_expert_gate_w, H);
+      uint16_t gl = row_dot_exact(xt, w->sh_expert_gate_w, w->sh_expert_gate_s,
+                                  w->sh_expert_gate_b, 0, H);
       float gv = orc_sigmoid_bf16(gl);
       qmv(xt, H, w->sh_gate_w, w->sh_gate_s, w->sh_gate_b, Is, mode, g);
       qmv(xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, u);

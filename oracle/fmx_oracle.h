@@ -36,8 +36,10 @@
  *                                        reduction, brute force on tiny shapes
  *   orc_qmm_t modes A/B/C                recalled MLX CPU accumulators; which
  *                                        one MLX uses is UNPINNED (reported only)
- *   orc_router_topk                      numpy fp64 logits, numpy softmax,
- *                                        full sort with (p desc, idx asc)
+ *   orc_router_topk(_q)                  numpy fp64 logits (of the bf16 rows or
+ *                                        of numpy's own dequantisation of the
+ *                                        4-bit rows), numpy softmax, full sort
+ *                                        with (p desc, idx asc)
  *   orc_moe_sort                         numpy stable argsort + invariants
  *   orc_moe_block                        dense fp64 formula on tiny shapes
  */
@@ -93,6 +95,14 @@ int orc_router_topk(const uint16_t* x, int64_t T, int64_t H,
                     const uint16_t* wr, int64_t E, const uint16_t* logit_bias,
                     int k, int norm_topk,
                     uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores);
+/* The same with the router in either form (model.cpp:757-763): wr_s == NULL:
+ * wr is bf16 [E, H]; else wr is u32 [E, H/8] (affine 4-bit, group 64) with
+ * bf16 scales/biases wr_s, wr_b [E, H/64]. Logits are exact fp64 sums
+ * rounded once to bf16 in both forms. */
+int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
+                      const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
+                      const uint16_t* logit_bias, int k, int norm_topk,
+                      uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores);
 
 /* ---- sort / permutation (model.cpp:682-700) ---------------------------- */
 /* order = stable argsort(flat inds); inv = argsort(order); src = order / k;
@@ -114,7 +124,7 @@ typedef struct {
 } orc_moe_cfg;
 
 typedef struct {
-  const uint16_t* router_w;      /* [E, H] bf16 */
+  const void* router_w;          /* [E, H] bf16, or [E, H/8] u32 when router_s */
   const uint16_t* router_bias;   /* [E] bf16 or NULL (harness extension) */
   const uint32_t* gate_w;  const uint16_t* gate_s;  const uint16_t* gate_b;   /* [E, I, ..] */
   const uint32_t* up_w;    const uint16_t* up_s;    const uint16_t* up_b;     /* [E, I, ..] */
@@ -122,7 +132,11 @@ typedef struct {
   const uint32_t* sh_gate_w; const uint16_t* sh_gate_s; const uint16_t* sh_gate_b; /* [Is, ..] */
   const uint32_t* sh_up_w;   const uint16_t* sh_up_s;   const uint16_t* sh_up_b;
   const uint32_t* sh_down_w; const uint16_t* sh_down_s; const uint16_t* sh_down_b; /* [H, ..] */
-  const uint16_t* sh_expert_gate_w; /* [1, H] bf16 */
+  const void* sh_expert_gate_w;  /* [1, H] bf16, or [1, H/8] u32 when sh_expert_gate_s */
+  const uint16_t* router_s;      /* [E, H/64] bf16 or NULL: quantized router (model.cpp:758-760) */
+  const uint16_t* router_b;
+  const uint16_t* sh_expert_gate_s; /* [1, H/64] or NULL: quantized gate (model.cpp:792-796) */
+  const uint16_t* sh_expert_gate_b;
 } orc_moe_weights;
 
 /* y [T, H] bf16. inds/scores [T,k] may be NULL. token_subset (may be NULL):

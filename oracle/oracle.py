@@ -51,7 +51,8 @@ class _W(C.Structure):
         "router_w", "router_bias",
         "gate_w", "gate_s", "gate_b", "up_w", "up_s", "up_b", "down_w", "down_s", "down_b",
         "sh_gate_w", "sh_gate_s", "sh_gate_b", "sh_up_w", "sh_up_s", "sh_up_b",
-        "sh_down_w", "sh_down_s", "sh_down_b", "sh_expert_gate_w")]
+        "sh_down_w", "sh_down_s", "sh_down_b", "sh_expert_gate_w",
+        "router_s", "router_b", "sh_expert_gate_s", "sh_expert_gate_b")]
 
 
 def load() -> C.CDLL:
@@ -78,6 +79,8 @@ def load() -> C.CDLL:
                                        C.c_int, _vp]
         lib.orc_router_topk.argtypes = [_vp, i64, i64, _vp, i64, _vp, C.c_int, C.c_int, _vp, _vp,
                                         _vp, _vp]
+        lib.orc_router_topk_q.argtypes = [_vp, i64, i64, _vp, _vp, _vp, i64, _vp, C.c_int, C.c_int,
+                                          _vp, _vp, _vp, _vp]
         lib.orc_moe_sort.argtypes = [_vp, i64, C.c_int, i64, _vp, _vp, _vp, _vp, _vp]
         lib.orc_moe_block.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp, i64,
                                       _vp, _vp, _vp]
@@ -185,18 +188,23 @@ def gather_qmm(x, wq, s, b, lhs, rhs, mode=ACC_A) -> np.ndarray:
 
 
 def router_topk(x, wr, k, norm_topk=False, logit_bias=None):
-    """-> logits [T,E], probs [T,E] (bf16 bits), inds [T,k] u32, scores [T,k] bf16."""
-    x, wr = _c(x, np.uint16), _c(wr, np.uint16)
+    """-> logits [T,E], probs [T,E] (bf16 bits), inds [T,k] u32, scores [T,k] bf16.
+    wr: bf16 [E, H], or a quantized (wq u32 [E, H/8], scales, biases) tuple."""
+    x = _c(x, np.uint16)
+    if isinstance(wr, tuple):
+        wq, ws, wb = _c(wr[0], np.uint32), _c(wr[1], np.uint16), _c(wr[2], np.uint16)
+    else:
+        wq, ws, wb = _c(wr, np.uint16), None, None
     H = x.shape[-1]
     T = x.size // H
-    E = wr.shape[0]
+    E = wq.shape[0]
     lb = None if logit_bias is None else _c(logit_bias, np.uint16)
     logits = np.empty((T, E), np.uint16)
     probs = np.empty((T, E), np.uint16)
     inds = np.empty((T, k), np.uint32)
     scores = np.empty((T, k), np.uint16)
-    rc = load().orc_router_topk(_p(x), T, H, _p(wr), E, _p(lb), k, int(norm_topk), _p(logits),
-                                _p(probs), _p(inds), _p(scores))
+    rc = load().orc_router_topk_q(_p(x), T, H, _p(wq), _p(ws), _p(wb), E, _p(lb), k,
+                                  int(norm_topk), _p(logits), _p(probs), _p(inds), _p(scores))
     assert rc == 0, rc
     return logits, probs, inds, scores
 
@@ -214,8 +222,9 @@ def moe_sort(inds, E):
 
 def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None):
     """cfg keys: hidden, n_experts, top_k, inter, shared_inter, norm_topk.
-    w keys: router_w, router_bias?, gate/up/down (wq, s, b) tuples, shared_gate/
-    shared_up/shared_down tuples?, shared_expert_gate_w?.
+    w keys: router_w (bf16, or a quantized (wq, s, b) tuple), router_bias?,
+    gate/up/down (wq, s, b) tuples, shared_gate/shared_up/shared_down tuples?,
+    shared_expert_gate_w? (bf16 or a quantized tuple).
     Returns (y [T,H] with rows only for `tokens` filled when given, inds, scores)."""
     x = _c(x, np.uint16)
     H = cfg["hidden"]
@@ -233,7 +242,12 @@ def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None):
         return a.ctypes.data
 
     ww = _W()
-    ww.router_w = ptr(w["router_w"], np.uint16)
+    r = w["router_w"]
+    if isinstance(r, tuple):  # quantized router (wq, scales, biases)
+        ww.router_w, ww.router_s, ww.router_b = (ptr(r[0], np.uint32), ptr(r[1], np.uint16),
+                                                 ptr(r[2], np.uint16))
+    else:
+        ww.router_w = ptr(r, np.uint16)
     ww.router_bias = ptr(w.get("router_bias"), np.uint16)
     for nm, key in (("gate", "gate"), ("up", "up"), ("down", "down"),
                     ("sh_gate", "shared_gate"), ("sh_up", "shared_up"), ("sh_down", "shared_down")):
@@ -243,7 +257,12 @@ def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None):
         setattr(ww, nm + "_w", ptr(t[0], np.uint32))
         setattr(ww, nm + "_s", ptr(t[1], np.uint16))
         setattr(ww, nm + "_b", ptr(t[2], np.uint16))
-    ww.sh_expert_gate_w = ptr(w.get("shared_expert_gate_w"), np.uint16)
+    g = w.get("shared_expert_gate_w")
+    if isinstance(g, tuple):  # quantized shared-expert gate
+        ww.sh_expert_gate_w, ww.sh_expert_gate_s, ww.sh_expert_gate_b = (
+            ptr(g[0], np.uint32), ptr(g[1], np.uint16), ptr(g[2], np.uint16))
+    else:
+        ww.sh_expert_gate_w = ptr(g, np.uint16)
     y = np.zeros((T, H), np.uint16)
     inds = np.empty((T, k), np.uint32)
     scores = np.empty((T, k), np.uint16)

@@ -5,7 +5,9 @@ For every MoE-layer workload (flashmlx_amd/workloads.py):
   <workload>.npz           routing: inds [T,k], scores [T,k] (bf16 bits);
                            permutation: order, inv, src, idx [T*k], offsets [E+1];
                            tokens (the sampled rows) and y_rows [len(tokens), H]
-                           (oracle accumulation mode A); tiny workloads also keep
+                           (oracle accumulation mode A); row checksums of every
+                           output row: row_sum, row_abs (sum of |y|), row_sq
+                           (sum of y^2), float64 [T]; tiny workloads also keep
                            x and every output row.
 Run: python tests/golden/make_golden.py [workload ...]
 The fixtures are data (inputs and expected outputs); no reference code is
@@ -54,17 +56,20 @@ def make(key: str) -> dict:
     cfg = dict(hidden=m["hidden"], n_experts=m["n_experts"], top_k=m["top_k"], inter=m["inter"],
                shared_inter=m["shared_inter"], norm_topk=m["norm_topk"])
     q = O.quantize
-    w = dict(router_w=hi.router_w, router_bias=hi.router_bias, gate=q(hi.gate), up=q(hi.up),
+    rq = q if wl.router_quant else (lambda a: a)
+    w = dict(router_w=rq(hi.router_w), router_bias=hi.router_bias, gate=q(hi.gate), up=q(hi.up),
              down=q(hi.down))
     if m["shared_inter"]:
         w.update(shared_gate=q(hi.shared_gate), shared_up=q(hi.shared_up),
-                 shared_down=q(hi.shared_down), shared_expert_gate_w=hi.shared_expert_gate_w)
+                 shared_down=q(hi.shared_down), shared_expert_gate_w=rq(hi.shared_expert_gate_w))
     T = hi.x.shape[0]
     tokens = sample_tokens(T)
-    y, inds, scores = O.moe_block(cfg, w, hi.x, O.ACC_A, tokens=tokens)
+    y, inds, scores = O.moe_block(cfg, w, hi.x, O.ACC_A)
     order, inv, src, idx, offsets = O.moe_sort(inds, m["n_experts"])
+    yf = O.bf16_to_f32(y).astype(np.float64)
     arrs = dict(inds=inds, scores=scores, order=order, inv=inv, src=src, idx=idx, offsets=offsets,
-                tokens=tokens.astype(np.int64), y_rows=y[tokens])
+                tokens=tokens.astype(np.int64), y_rows=y[tokens], row_sum=yf.sum(1),
+                row_abs=np.abs(yf).sum(1), row_sq=(yf * yf).sum(1))
     if m["name"].startswith("tiny"):
         arrs["x"] = hi.x
     np.savez_compressed(HERE / f"{key}.npz", **arrs)

@@ -54,13 +54,15 @@ def assert_close(got_u16, ref_u16, what="", rtol=RTOL, atol=ATOL, rel_l2=REL_L2_
     return e
 
 
-def oracle_args(hi, model, quant):
-    """(cfg, weights) for oracle.moe_block from HostInputs and a quantizer."""
+def oracle_args(hi, model, quant, router_quant=False):
+    """(cfg, weights) for oracle.moe_block from HostInputs and a quantizer;
+    router_quant: the router and shared-expert gate quantized too."""
     cfg = dict(hidden=model["hidden"], n_experts=model["n_experts"], top_k=model["top_k"],
                inter=model["inter"], shared_inter=model["shared_inter"], norm_topk=model["norm_topk"])
-    w = dict(router_w=hi.router_w, router_bias=hi.router_bias,
+    rq = quant if router_quant else (lambda a: a)
+    w = dict(router_w=rq(hi.router_w), router_bias=hi.router_bias,
              gate=quant(hi.gate), up=quant(hi.up), down=quant(hi.down))
     if model["shared_inter"]:
         w.update(shared_gate=quant(hi.shared_gate), shared_up=quant(hi.shared_up),
-                 shared_down=quant(hi.shared_down), shared_expert_gate_w=hi.shared_expert_gate_w)
+                 shared_down=quant(hi.shared_down), shared_expert_gate_w=rq(hi.shared_expert_gate_w))
     return cfg, w

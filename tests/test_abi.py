@@ -173,3 +173,79 @@ def test_zero_token_calls_need_no_buffers(fmx):
     rt = lib.fmx_moe_router_topk
     assert rt(C.byref(cfg), None, 0, None, None, None, None, None, ws, 256, None) == _lib.FMX_OK
     assert rt(C.byref(cfg), None, 1, None, None, None, None, None, ws, 256, None) == _lib.FMX_ERR_ARG
+
+
+def test_moe_workspace_size_nondecreasing(fmx):
+    """A workspace sized for max_tokens serves every smaller forward: the
+    size query never shrinks as the token count grows (the decode kernels'
+    products are held for min(T, 16) tokens at every T)."""
+    from flashmlx_amd import MoEConfig
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    for cfg in (MoEConfig(2048, 60, 4, 1408, 5632, False), MoEConfig(2048, 128, 8, 768, 0, True),
+                MoEConfig(512, 8, 2, 256, 512, False)):
+        c = cfg.to_c()
+        sizes = [lib.fmx_moe_workspace_size(C.byref(c), t)
+                 for t in list(range(0, 65)) + [100, 512, 1024, 4096, 65536]]
+        assert all(s > 0 for s in sizes)
+        assert all(b >= a for a, b in zip(sizes, sizes[1:])), sizes
+
+
+def test_packed_forward_arguments(fmx):
+    """Packed forwards do not need the MLX-layout expert arrays, but the
+    packed buffer must be 256-byte aligned and at least the config's packed
+    size; a quantized router needs its biases. Each error is reported before
+    any device call."""
+    from flashmlx_amd import MoEConfig
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    cfg = MoEConfig(2048, 60, 4, 1408, 5632, False).to_c()
+    need = lib.fmx_moe_packed_size(C.byref(cfg))
+    assert need > 0
+    buf = np.zeros(1 << 16, np.uint8)
+    p = (buf.ctypes.data + 255) // 256 * 256     # aligned host address; never dereferenced
+    ws = np.zeros(1 << 16, np.uint8)
+    wsp = (ws.ctypes.data + 255) // 256 * 256
+    w = _lib.FmxMoEWeights()
+    w.router_w = p
+    w.shared_expert_gate_w = p
+    w.packed = p
+    w.packed_bytes = need - 256
+    fwd = lib.fmx_moe_block_forward
+    R = C.byref
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_WORKSPACE
+    assert b"packed_bytes" in lib.fmx_last_error()
+    w.packed_bytes = need
+    w.packed = p + 16
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_ARG
+    w.packed = p
+    # a correctly described packed layer gets past validation without the
+    # MLX-layout arrays: the next check is the (too small) workspace
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_WORKSPACE
+    assert b"workspace" in lib.fmx_last_error()
+    # quantized router: scales without biases is an argument error
+    w.router_scales = p
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_ARG
+    w.router_biases = p
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_WORKSPACE
+    # unpacked forwards still need every expert array
+    w.packed = None
+    w.packed_bytes = 0
+    assert fwd(R(cfg), R(w), p, 1, p, wsp, 256, None) == _lib.FMX_ERR_ARG
+    assert b"expert weights" in lib.fmx_last_error()
+
+
+def test_sort_limits(fmx):
+    """The sort takes up to 2^22 entries and 1024 experts; a Qwen3 prefill
+    of 65536 tokens (524,288 entries) fits, and gather_qmm states the same
+    row limit."""
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    assert lib.fmx_moe_sort_workspace_size(65536, 8, 128) > 0
+    keys = np.zeros(16, np.uint32)   # host address; the calls below fail before using it
+    k = keys.ctypes.data
+    assert lib.fmx_moe_sort(k, 1, 8, 2048, None, None, None, None, None, None, 0, None) == \
+        _lib.FMX_ERR_UNSUPPORTED
+    assert lib.fmx_moe_sort(k, (1 << 22) // 8 + 1, 8, 128, None, None, None, None, None, None, 0,
+                            None) == _lib.FMX_ERR_UNSUPPORTED
+    assert b"limits" in lib.fmx_last_error()

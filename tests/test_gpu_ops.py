@@ -160,8 +160,10 @@ def test_router_bitexact(gpu, fmx, oracle, T, E, k, norm, H, bias):
     np.testing.assert_array_equal(from_dev_bf16(scores), rsc)
 
 
+# (10001, 4, 60) and (8192, 8, 128): 40,004 and 65,536 entries, beyond the
+# 32,768 keys the sort holds in LDS (the rest are re-read from memory)
 @pytest.mark.parametrize("T,k,E", [(1, 4, 60), (8, 8, 128), (512, 4, 60), (1024, 8, 128),
-                                   (33, 3, 5), (4096, 8, 128)])
+                                   (33, 3, 5), (4096, 8, 128), (10001, 4, 60), (8192, 8, 128)])
 def test_sort_bitexact(gpu, fmx, oracle, T, k, E):
     rng = np.random.default_rng(T * k + E)
     if T % 2:  # arbitrary keys, repeats allowed within a row
@@ -194,3 +196,41 @@ def test_empty_inputs(gpu, fmx, oracle):
     out = fmx.gather_qmm(to_dev(np.zeros((0, 1, K), np.uint16)), to_dev_u32(eq), to_dev(es), to_dev(eb),
                          rhs_indices=to_dev_u32(np.zeros((0,), np.uint32)), sorted_indices=True)
     assert tuple(out.shape) == (0, 1, N)
+
+
+def test_stack_experts(gpu, fmx, oracle):
+    """fmx_stack_experts (mx::stack of per-expert arrays, model.cpp:396-404)
+    places expert e's bytes at e * bytes, for every component of a layer."""
+    import ctypes as C
+    import torch
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    rng = np.random.default_rng(31)
+    E, N, K = 6, 40, 256
+    per = [_rand_bf16(rng, (N, K), 0.02) for _ in range(E)]
+    parts = [oracle.quantize(w) for w in per]
+    for comp, dt in ((0, np.uint32), (1, np.uint16), (2, np.uint16)):
+        devs = [to_dev_u32(p[comp]) if dt == np.uint32 else to_dev(p[comp]) for p in parts]
+        nbytes = devs[0].numel() * devs[0].element_size()
+        dst = torch.empty(E * nbytes, dtype=torch.uint8, device="cuda")
+        ptrs = (C.c_void_p * E)(*[d.data_ptr() for d in devs])
+        _lib.check(lib.fmx_stack_experts(ptrs, E, nbytes, dst.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream))
+        got = dst.cpu().numpy()
+        ref = np.stack([p[comp] for p in parts]).view(np.uint8).reshape(-1)
+        np.testing.assert_array_equal(got, ref)
+    # a NULL source is an argument error
+    ptrs = (C.c_void_p * 2)(devs[0].data_ptr(), None)
+    assert lib.fmx_stack_experts(ptrs, 2, 16, dst.data_ptr(), None) == _lib.FMX_ERR_ARG
+
+
+@pytest.mark.parametrize("n,seed,stream,mean,std", [(1 << 24, 2, 10, 0.0, 0.02), (1 << 20, 5, 1, 0.0, 1.0),
+                                                    (100_003, 3, 3, 0.5, 0.02)])
+def test_device_synth_matches_host(gpu, fmx, oracle, n, seed, stream, mean, std):
+    """fmx_synth_normal_bf16_device writes the host generator's values (the
+    bench and the decoder stack generate their multi-GB weight sets with it)."""
+    import torch
+    d = fmx.synth_normal_bf16_device((n,), seed, stream, mean, std)
+    torch.cuda.synchronize()
+    h = fmx.synth_normal_bf16(n, seed, stream, mean, std)
+    np.testing.assert_array_equal(from_dev_bf16(d), h)

@@ -320,7 +320,9 @@ def _dense_block(oracle, cfg, w, x, drop=None):
             y[t] += float(bf(scores[t, j])) * (dq["down"][e] @ (silu(g) * u))
     if cfg["shared_inter"] and drop != "shared":
         sg, su, sd = (_deq64(oracle, *w[n]) for n in ("shared_gate", "shared_up", "shared_down"))
-        gl = xf @ bf(w["shared_expert_gate_w"]).astype(np.float64).ravel()
+        g = w["shared_expert_gate_w"]
+        gw = _deq64(oracle, *g) if isinstance(g, tuple) else bf(g).astype(np.float64)
+        gl = xf @ gw.ravel()
         for t in range(x.shape[0]):
             y[t] += 1 / (1 + np.exp(-gl[t])) * (sd @ (silu(sg @ xf[t]) * (su @ xf[t])))
     return y
@@ -342,3 +344,118 @@ def test_moe_block_dense_formula(oracle, key):
     for mistake in ("swap",) + (("shared",) if cfg["shared_inter"] else ()):
         bad = _dense_block(oracle, cfg, w, hi.x, drop=mistake)
         assert np.linalg.norm(got - bad) / np.linalg.norm(bad) > 5e-2, mistake
+
+
+# ------------------------------------------------------------------ accumulation modes
+
+def _nib(wq, n, k):
+    return (int(wq[n, k // 8]) >> (4 * (k % 8))) & 15
+
+
+@pytest.mark.parametrize("mode_name", ["A", "B", "C"])
+def test_qmm_accumulation_modes_brute_force(oracle, mode_name):
+    """The three MLX CPU accumulators the oracle restates, recomputed by
+    scalar loops with explicit per-operation rounding: A sequential fp32
+    (w = s*q, + b; acc += x*w), B every operation rounded to bf16 (exact
+    rational rounding), C eight fp32 lanes over k mod 8 summed pairwise
+    ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)). Each result is rounded once to
+    bf16. A planted wrong group index (scale/bias of group k // 32) is
+    detected; the lane order itself moves only fp32-level bits, which the
+    bf16 outputs rarely show (modes A and C nearly always agree)."""
+    M, N, K = 2, 5, 128
+    x = rand_bf16((M, K))
+    wq, s, b = oracle.quantize(rand_bf16((N, K), 0.02))
+    mode = {"A": oracle.ACC_A, "B": oracle.ACC_B, "C": oracle.ACC_C}[mode_name]
+    got = oracle.qmm_t(x, wq, s, b, mode)
+    f32 = np.float32
+    xf = bf(x)
+
+    def rb_frac(v):  # bf16 of an exact rational, as a float
+        return float(bf(np.uint16(bf16_from_fraction(Fraction(v)))))
+
+    def one(m, n, wrong_group=False):
+        grp = (lambda kk: min(kk // 32, K // 64 - 1)) if wrong_group else (lambda kk: kk // 64)
+        if mode_name == "A":
+            acc = f32(0)
+            for kk in range(K):
+                g = grp(kk)
+                w = f32(f32(bf(s[n, g])) * f32(_nib(wq, n, kk))) + f32(bf(b[n, g]))
+                acc = f32(acc + f32(f32(xf[m, kk]) * f32(w)))
+            return bf16_from_fraction(Fraction(float(acc)))
+        if mode_name == "B":
+            acc = 0.0
+            for kk in range(K):
+                g = grp(kk)
+                sq = rb_frac(float(bf(s[n, g])) * _nib(wq, n, kk))
+                w = rb_frac(Fraction(sq) + Fraction(float(bf(b[n, g]))))
+                pr = rb_frac(Fraction(float(xf[m, kk])) * Fraction(w))
+                acc = rb_frac(Fraction(acc) + Fraction(pr))
+            return bf16_from_fraction(Fraction(acc))
+        lane = [f32(0)] * 8
+        for kk in range(K):
+            g = grp(kk)
+            w = f32(f32(_nib(wq, n, kk)) * f32(bf(s[n, g])))
+            w = f32(w + f32(bf(b[n, g])))
+            lane[kk % 8] = f32(lane[kk % 8] + f32(f32(xf[m, kk]) * w))
+        a = [f32(lane[i] + lane[i + 4]) for i in range(4)]
+        tot = f32(f32(a[0] + a[2]) + f32(a[1] + a[3]))
+        return bf16_from_fraction(Fraction(float(tot)))
+
+    ref = np.array([[one(m, n) for n in range(N)] for m in range(M)], np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    bad = np.array([[one(m, n, wrong_group=True) for n in range(N)] for m in range(M)], np.uint16)
+    assert (bad != ref).sum() > M * N // 2
+
+
+# ------------------------------------------------------------------ quantized router
+
+def test_router_quantized_logits_exact(oracle):
+    """A quantized router (model.cpp:758-760): each logit is the exact
+    rational x . (s*q + b) rounded once to bf16; rounding the dequantised
+    weights to bf16 first (a plausible shortcut) changes some logits."""
+    T, E, H = 3, 12, 128
+    x = rand_bf16((T, H))
+    wq, s, b = oracle.quantize(rand_bf16((E, H), 0.02))
+    logits, _, _, _ = oracle.router_topk(x, (wq, s, b), 2)
+    xf = bf(x)
+    changed = 0
+    for t in range(T):
+        for e in range(E):
+            ws = [Fraction(float(bf(s[e, kk // 64]))) * _nib(wq, e, kk) + Fraction(float(bf(b[e, kk // 64])))
+                  for kk in range(H)]
+            dot = sum(Fraction(float(xf[t, kk])) * ws[kk] for kk in range(H))
+            assert logits[t, e] == bf16_from_fraction(dot), (t, e)
+            short = sum(Fraction(float(xf[t, kk])) * Fraction(float(bf(np.uint16(bf16_from_fraction(ws[kk]))))) for kk in range(H))
+            changed += bf16_from_fraction(short) != logits[t, e]
+    assert changed > 0
+
+
+def test_router_quantized_matches_numpy(oracle):
+    """Softmax and top-k over quantized-router logits equal those over the
+    logits numpy forms from its own fp64 dequantisation."""
+    T, E, H, k = 32, 60, 256, 4
+    x = rand_bf16((T, H))
+    wq, s, b = oracle.quantize(rand_bf16((E, H), 0.02))
+    logits, probs, inds, scores = oracle.router_topk(x, (wq, s, b), k)
+    q = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(E, H).astype(np.float64)
+    deq = q * np.repeat(bf(s).astype(np.float64), 64, 1) + np.repeat(bf(b).astype(np.float64), 64, 1)
+    ref = bf16_rne_from_f64(bf(x).astype(np.float64) @ deq.T).reshape(T, E)
+    diff = np.abs(logits.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.99
+    for t in range(T):
+        order = sorted(range(E), key=lambda e: (-float(bf(probs[t, e])), e))
+        np.testing.assert_array_equal(inds[t], order[:k])
+
+
+def test_moe_block_quantized_router_dense_formula(oracle):
+    """The whole block with a quantized router and shared-expert gate
+    against the fp64 dense formula, which dequantises them with numpy."""
+    from flashmlx_amd import workloads as W
+    from helpers import oracle_args
+    wl = W.Workload("tiny_t5_q", W.TINY, 5, 11, router_quant=True)
+    hi = W.host_inputs(wl)
+    cfg, w = oracle_args(hi, wl.model, oracle.quantize, router_quant=True)
+    y, _, _ = oracle.moe_block(cfg, w, hi.x, oracle.ACC_A)
+    ref = _dense_block(oracle, cfg, w, hi.x)
+    got = bf(y).astype(np.float64)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
