@@ -123,6 +123,10 @@ _SIGS = {
         [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
          C.c_size_t, C.c_void_p, P(C.c_void_p)],
     ),
+    "fmx_moe_block_forward_noalloc": (
+        C.c_int,
+        [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p],
+    ),
     "fmx_moe_block_forward_partial": (
         C.c_int,
         [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -819,6 +820,62 @@ int fmx_moe_block_forward_partial(const fmx_moe_config* cfg, const fmx_moe_weigh
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free forward
+//
+// A fixed device array serves as the workspace of fmx_moe_block_forward_noalloc.
+// Each device the library runs on holds its own copy for the life of the
+// process. Host code never passes the array's name to a kernel or a copy: the
+// name is a host-side stand-in. The device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+namespace {
+
+static_assert(FMX_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size is a multiple of 256 bytes");
+static __device__ __align__(256) uint8_t scratch[FMX_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`; on the first call for a device,
+// also clears the completion counters at its start (on `stream`, by a fill
+// kernel, so that a caller capturing a graph records no memset node).
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  FMX_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FMX_ERR_UNSUPPORTED, "device index %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    FMX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(FMX_ERR_HIP, "hipGetSymbolAddress(scratch) gave NULL");
+    FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(p), kCounterBytes / 4, 0u, stream));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FMX_OK;
+}
+
+}  // namespace
+
+extern "C" int fmx_moe_block_forward_noalloc(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                             const void* x, int64_t T, void* y,
+                                             fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens=%lld out of range", static_cast<long long>(T));
+  if (T == 0) return ok();
+  const size_t need = moe_layout(*cfg, T, nullptr).total;
+  if (need > static_cast<size_t>(FMX_NOALLOC_SCRATCH_BYTES))
+    return fail(FMX_ERR_UNSUPPORTED,
+                "a forward of %lld tokens needs %zu bytes of workspace, more than the %d-byte "
+                "fixed scratch of the allocation-free forward",
+                static_cast<long long>(T), need, FMX_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(stream, &ws))) return rc;
+  return moe_forward(cfg, w, x, T, y, ws, FMX_NOALLOC_SCRATCH_BYTES, stream_, nullptr, 4);
+}
 
 namespace {
 

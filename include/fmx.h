@@ -242,6 +242,23 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
                           const void* x, int64_t n_tokens, void* y, void* workspace,
                           size_t workspace_bytes, fmx_stream stream);
 
+/* fmx_moe_block_forward without a workspace argument, for callers that
+ * cannot allocate (code under HIP graph capture, serving loops that forbid
+ * hipMalloc): no counterpart in the reference. It calls no allocating
+ * routine; its workspace is a fixed device array of FMX_NOALLOC_SCRATCH_BYTES
+ * bytes that the library holds on every device it runs on until the process
+ * ends. Forwards whose fmx_moe_workspace_size(cfg, n_tokens) exceeds that
+ * return FMX_ERR_UNSUPPORTED before launching anything (8 MiB: every decode
+ * batch of up to 16 tokens, and forwards of up to 93 tokens of the
+ * Qwen1.5-MoE-A2.7B shape or 138 of the Qwen3-30B-A3B shape). All calls on
+ * one device share the array:
+ * calls that overlap on one GPU (two streams, or two host threads) race and
+ * must be ordered by the caller. Each forward leaves the array's completion
+ * counters at zero for the next. */
+#define FMX_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+int fmx_moe_block_forward_noalloc(const fmx_moe_config* cfg, const fmx_moe_weights* w,
+                                  const void* x, int64_t n_tokens, void* y, fmx_stream stream);
+
 /* fmx_moe_block_forward that also records caller-created HIP events
  * (hipEvent_t, as void*) on `stream` at its stage boundaries:
  *   stage_events[0] before the router, [1] after routing and sort,
