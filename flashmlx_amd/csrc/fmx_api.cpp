@@ -143,6 +143,8 @@ struct MoELayout {
   uint8_t* slots;
   float* sgate;
   uint16_t *xp, *h, *hs, *d, *sd;
+  uint16_t *xh, *hh, *hsh;  // fp16 copies (F8 chunk order) of x, h, hs: prefill GEMM inputs
+  uint32_t* f16_flag;
   uint32_t* dw;
   float* sd_part;
   size_t total;
@@ -181,6 +183,10 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
   L.sd = static_cast<uint16_t*>(ar.take(Is ? T * H * 2 : 0));
+  L.f16_flag = static_cast<uint32_t*>(ar.take(4));
+  L.xh = static_cast<uint16_t*>(ar.take(T * H * 2));
+  L.hh = static_cast<uint16_t*>(ar.take(n * I * 2));
+  L.hsh = static_cast<uint16_t*>(ar.take(T * Is * 2));
   // the decode kernels' down products (forwards of at most kDecMaxT tokens);
   // sized for min(T, kDecMaxT) at every T so that the layout only grows with T
   L.dw = static_cast<uint32_t*>(ar.take(std::min<int64_t>(T, kDecMaxT) * k * H * 4));
@@ -264,7 +270,7 @@ bool rows_ok(const RouterRows& r) {
 int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64_t T,
                const RouterRows& wr, const void* lbias, const RouterRows& wsg, uint32_t* inds,
                uint16_t* scores, uint16_t* probs, float* sgate, uint16_t* xp, bool want_sort,
-               bool* sorted_in_router, hipStream_t stream) {
+               bool* sorted_in_router, hipStream_t stream, bool want_f16 = false) {
   RouterArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.wr = wr;
@@ -301,7 +307,11 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.base = L.sort_base;
   a.sort.pass_n = L.pass_n;
   a.sort.pass_tab = L.pass_tab;
-  if (T > kRouterManyMin) {
+  if (want_f16) {  // the prefill GEMMs' fp16 copy of x and its range flag
+    a.xh = L.xh;
+    a.f16_flag = L.f16_flag;
+  }
+  if (T > kRouterManyMin || want_f16) {
     if (sorted_in_router) *sorted_in_router = false;
     FMX_HIP(launch_router_many(a, stream));
     if (xp) FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x), T, c.hidden_size, xp, stream));
@@ -990,7 +1000,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     FMX_HIP(mark(0));
     bool sorted = false;
     if ((rc = run_router(c, L, x, T, wr, w->router_logit_bias, wsg, L.inds, L.scores, L.probs,
-                         has_sh ? L.sgate : nullptr, nullptr, true, &sorted, stream)))
+                         has_sh ? L.sgate : nullptr, nullptr, true, &sorted, stream, true)))
       return rc;
     if (!sorted) {
       SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off,
@@ -1001,15 +1011,18 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     if (n_stages < 2) return ok();
 
     const int mp = max_passes(n, E);
-    auto routed = [&](const uint8_t* wp, int64_t es, const uint16_t* xr, int64_t ldx,
-                      const uint32_t* row_map, uint16_t* out, int64_t ldo, int64_t N, int64_t K) {
+    auto routed = [&](const uint8_t* wp, int64_t es, const uint16_t* xr, const uint16_t* xrh,
+                      int64_t ldx, const uint32_t* row_map, uint16_t* out, uint16_t* outh,
+                      int64_t ldo, int64_t N, int64_t K) {
       PfSet s{};
       s.w = wp;
       s.es = es;
       s.x = xr;
+      s.xh = xrh;
       s.ldx = ldx;
       s.row_map = row_map;
       s.out = out;
+      s.outh = outh;
       s.ldo = ldo;
       s.nt = static_cast<int>(N / 16);
       s.nu = static_cast<int>(K / 128);
@@ -1021,13 +1034,15 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       s.x_rows = static_cast<int>(row_map ? T : n);
       return s;
     };
-    auto shared = [&](const uint8_t* wp, const uint16_t* xr, int64_t ldx, uint16_t* out,
-                      int64_t ldo, int64_t N, int64_t K) {
+    auto shared = [&](const uint8_t* wp, const uint16_t* xr, const uint16_t* xrh, int64_t ldx,
+                      uint16_t* out, uint16_t* outh, int64_t ldo, int64_t N, int64_t K) {
       PfSet s{};
       s.w = wp;
       s.x = xr;
+      s.xh = xrh;
       s.ldx = ldx;
       s.out = out;
+      s.outh = outh;
       s.ldo = ldo;
       s.nt = static_cast<int>(N / 16);
       s.nu = static_cast<int>(K / 128);
@@ -1038,24 +1053,30 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     const uint16_t* xb = static_cast<const uint16_t*>(x);
     {
       PfArgs pa{};
-      pa.s1 = routed(pk + PL.gu, PL.gu_es, xb, H, L.src, L.h, I, I, H);
+      pa.s1 = routed(pk + PL.gu, PL.gu_es, xb, L.xh, H, L.src, L.h, L.hh, I, I, H);
       pa.n_items1 = pf_items(pa.s1, true);
       if (has_sh) {
-        pa.s0 = shared(pk + PL.sgu, xb, H, L.hs, Is, Is, H);
+        pa.s0 = shared(pk + PL.sgu, xb, L.xh, H, L.hs, L.hsh, Is, Is, H);
         pa.n_items0 = pf_items(pa.s0, true);
       }
+      pa.f16_flag = L.f16_flag;
+      pa.flag_in = kF16FlagX;
+      pa.flag_out = kF16FlagH;
       FMX_HIP(launch_pf(pa, true, stream));
     }
     FMX_HIP(mark(2));
     if (n_stages < 3) return ok();
     {
       PfArgs pa{};
-      pa.s1 = routed(pk + PL.dn, PL.dn_es, L.h, I, nullptr, L.d, H, H, I);
+      pa.s1 = routed(pk + PL.dn, PL.dn_es, L.h, L.hh, I, nullptr, L.d, nullptr, H, H, I);
       pa.n_items1 = pf_items(pa.s1, false);
       if (has_sh) {
-        pa.s0 = shared(pk + PL.sdn, L.hs, Is, L.sd, H, H, Is);
+        pa.s0 = shared(pk + PL.sdn, L.hs, L.hsh, Is, L.sd, nullptr, H, H, Is);
         pa.n_items0 = pf_items(pa.s0, false);
       }
+      pa.f16_flag = L.f16_flag;
+      pa.flag_in = kF16FlagH;
+      pa.flag_out = 0u;
       FMX_HIP(launch_pf(pa, false, stream));
     }
     FMX_HIP(mark(3));

@@ -305,6 +305,81 @@ __device__ inline bf16x8_t nib8(uint32_t w) {
   return __builtin_bit_cast(bf16x8_t, d);
 }
 
+// ------------------------------------------------------------------ fp16 operands (prefill)
+//
+// The prefill GEMMs multiply in fp16: a weight s*q + b rounded once to fp16
+// (11 significant bits) is within 2^-11 relative of its exact value, an
+// eighth of bf16's rounding error, and a bf16 activation converts to fp16
+// exactly when its magnitude is below 65536 (values under 2^-14 keep an
+// absolute error below 2^-25 on fp16's subnormal grid). Activations at or
+// above 65536 (and inf/NaN) raise a flag that sends the GEMM to the exact
+// bf16 path instead.
+//
+// Chunk order F8: the 8 elements e0..e7 of a 16-byte activation chunk are
+// stored as e0 e4 e1 e5 e2 e6 e3 e7, the order in which dq8_f16 delivers the
+// 8 weights of a packed word, so that A and B operands pair up by position.
+
+// A byte 0..15 is the FP8 (E4M3) encoding of q * 2^-9 (the subnormal and the
+// first normal binade are evenly spaced); v_cvt_scalef32_pk_f16_fp8 with the
+// power-of-two scale 2^9 turns two such bytes into the exact fp16 values q.
+constexpr float kFp8Q = 512.0f;
+
+__host__ __device__ constexpr int f8_pos(int i) { return i < 4 ? 2 * i : 2 * i - 7; }
+
+// The 8 weights of a packed word (element 2i at nibble position i, 2i + 1 at
+// i + 4) as fp16(s*q + b) in F8 order: masking the even and the odd nibble
+// positions into bytes gives lo = elements 0, 4, 1, 5 and hi = 2, 6, 3, 7;
+// each pair is converted by one instruction and scaled by one packed fp16
+// fma (a single rounding of s*q + b).
+__device__ inline f16x8_t dq8_f16(uint32_t w, f16x2_t s, f16x2_t b) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+  const f16x2_t q04 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, kFp8Q, false);
+  const f16x2_t q15 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, kFp8Q, true);
+  const f16x2_t q26 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, kFp8Q, false);
+  const f16x2_t q37 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, kFp8Q, true);
+  const f16x2_t d0 = __builtin_elementwise_fma(q04, s, b);
+  const f16x2_t d1 = __builtin_elementwise_fma(q15, s, b);
+  const f16x2_t d2 = __builtin_elementwise_fma(q26, s, b);
+  const f16x2_t d3 = __builtin_elementwise_fma(q37, s, b);
+  return f16x8_t{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+}
+
+// (s, s) as fp16 from a bf16 (exact for |s| in [2^-17, 65504])
+__device__ inline f16x2_t f16_splat(float s) {
+  const _Float16 h = static_cast<_Float16>(s);
+  return f16x2_t{h, h};
+}
+
+__device__ inline f32x4_t mfma_f16(const f16x8_t& a, const f16x8_t& b, const f32x4_t& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// |v| >= 65536 (or inf/NaN) for a bf16 bit pattern: outside fp16's range
+__device__ inline bool bf16_f16_overflow(uint32_t h) { return (h & 0x7fffu) >= 0x4780u; }
+
+// fp16 bits of a bf16 value (round to nearest even; exact below 65536)
+__device__ inline uint32_t bf16_to_f16_bits(uint32_t h) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(h << 16)));
+}
+
+// A 16-byte chunk of 8 bf16 (natural order) as 8 fp16 in F8 order; ovf is
+// set when an element is outside fp16's range.
+__device__ inline u32x4_t bf16_chunk_to_f16_f8(u32x4_t v, bool& ovf) {
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    e[2 * i] = v[i] & 0xffffu;
+    e[2 * i + 1] = v[i] >> 16;
+  }
+  u32x4_t o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    ovf = ovf || bf16_f16_overflow(e[m]) || bf16_f16_overflow(e[m + 4]);
+    o[m] = bf16_to_f16_bits(e[m]) | (bf16_to_f16_bits(e[m + 4]) << 16);
+  }
+  return o;
+}
+
 template <bool DUAL>
 struct PkUnit {
   u32x4_t w0, w1;    // packed words (gate / up)

@@ -71,6 +71,8 @@ struct RouterArgs {
   uint16_t* scores;        // [T, k] bf16
   float* sgate;            // [T] sigmoid(shared gate logit) (bf16 value) or null
   uint16_t* xp;            // [T, H] P8 copy of x or null
+  uint16_t* xh;            // [T, H] fp16 copy of x in F8 chunk order (topk_kernel) or null
+  uint32_t* f16_flag;      // zeroed by logits_kernel; topk_kernel ORs in kF16FlagX (or null)
   uint32_t* counters;      // [n_tt + 1], zero on entry, zero on exit
   int n_tt, n_ct;          // token tiles, column tiles (4 * cols_per_wave columns each)
   int cols_per_wave;       // 1 (one token tile: decode) or 4 (prefill)
@@ -196,9 +198,11 @@ struct PfSet {
   const uint8_t* w;          // packed blocks of expert 0 (pairs for gate/up)
   int64_t es;                // bytes per expert
   const uint16_t* x;         // activation rows, bf16
-  int64_t ldx;               // elements between rows
+  const uint16_t* xh;        // the same rows in fp16, F8 chunk order
+  int64_t ldx;               // elements between rows (both copies)
   const uint32_t* row_map;   // pass row -> x row (null: identity)
   uint16_t* out;             // output rows (indexed like the pass rows), bf16
+  uint16_t* outh;            // gate/up: the same rows in fp16, F8 chunk order
   int64_t ldo;
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
@@ -214,7 +218,14 @@ struct PfSet {
 struct PfArgs {
   PfSet s0, s1;              // work items [0, n_items0) serve s0, the rest s1
   int n_items0, n_items1;
+  // f16_flag & flag_in set: an input row holds a value outside fp16's range,
+  // so the grid multiplies the bf16 rows exactly; gate/up ORs flag_out into
+  // it when one of its outputs does
+  uint32_t* f16_flag;
+  uint32_t flag_in, flag_out;
 };
+constexpr uint32_t kF16FlagX = 1u;  // x (gate/up input)
+constexpr uint32_t kF16FlagH = 2u;  // h (down input)
 // Fills ng / max_pass of a set; items of it.
 int pf_items(PfSet& s, bool dual);
 size_t pf_lds_bytes(bool dual);

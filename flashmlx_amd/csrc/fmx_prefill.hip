@@ -30,13 +30,19 @@
 // conflicts. The DMA writes a 1 KB piece (4 rows) per instruction and picks
 // each lane's source chunk to match.
 //
-// Exact dequantisation (as in the decode kernels, fmx_dev.hpp): nibbles
-// become the bf16 values 128 + q, v_mfma_f32_16x16x32_bf16 forms P =
-// x.(128+q) and X = x.1 per quantisation group in fp32, and each group adds
-// s P + (b - 128 s) X to the fp32 accumulator: the weights s*q + b are never
-// rounded to bf16. (Rounding them to bf16 first, one conversion per weight
-// per pass, costs 0.5 % relative L2 error of the block output at 512 tokens
-// and puts single elements outside the bf16 parity tolerance.)
+// Arithmetic: the weights are dequantised once per pass into fp16 (s*q + b
+// rounded once, 2^-11 relative) and multiplied with
+// v_mfma_f32_16x16x32_f16 against fp16 copies of the activation rows
+// (exact for bf16 values below 65536; the copies are written in F8 chunk
+// order, fmx_dev.hpp, by the router for x and by this gate/up grid for h).
+// When a row holds a value outside fp16's range (the forward's flag word
+// says so) the grid takes the exact bf16 path instead: nibbles become the
+// bf16 values 128 + q, the MFMA forms P = x.(128+q) and X = x.1 per
+// quantisation group in fp32, and each group adds s P + (b - 128 s) X to the
+// accumulator. (Weights rounded to bf16, as MLX's GPU kernels stage them,
+// cost 0.5 % relative L2 error of the block output at 512 tokens and put
+// single elements outside the bf16 parity tolerance; fp16 weights cost
+// 0.06 %.)
 #include "fmx_dev.hpp"
 
 namespace fmx {
@@ -81,9 +87,10 @@ __device__ inline void dma4(const void* g, void* lds) {
 // weights, column group ng. MT (the 16-row tiles the rows fill) fixes how
 // many row pieces each wave moves per unit, so the pass's rows are moved
 // and multiplied once, without padding to kPassRows.
-template <bool DUAL, int MT>
+template <bool DUAL, int MT, bool F16>
 __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, int row0, int rows,
-                                                       int64_t e, uint8_t* s_pf) {
+                                                       int64_t e, uint8_t* s_pf, uint32_t* flag,
+                                                       uint32_t flag_out) {
   constexpr int NB = pf_nb<DUAL>(), NM = pf_nm<DUAL>();
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
   constexpr int PA = (4 * MT + kPfWaves - 1) / kPfWaves;  // 4-row pieces per wave and unit
@@ -112,7 +119,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     const int rr = min(r, rows - 1);               // rows past the pass repeat its last
     int64_t xr = row0 + rr;
     if (P.row_map) xr = min(P.row_map[row0 + rr], static_cast<uint32_t>(P.x_rows - 1));
-    asrc[pc] = P.x + xr * P.ldx + 8 * (i16 ^ (r & 15));
+    asrc[pc] = (F16 ? P.xh : P.x) + xr * P.ldx + 8 * (i16 ^ (r & 15));
   }
 
   // the (scale, bias) piece: lane l fetches 4 bytes of block l / SBL's
@@ -165,57 +172,98 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     const uint8_t* sb = sa + kPfABytes + wave * WB;
     // the unit's packed words and (scale, bias) pairs
     u32x4_t W[NB][NM];
-    float sc[NB][NM][2], cb[NB][NM][2];
+    u32x2_t SB[NB][NM];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         W[b][m] = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
-        const u32x2_t sbw = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
-        sc[b][m][0] = __uint_as_float(sbw[0] << 16);
-        sc[b][m][1] = __uint_as_float(sbw[0] & 0xffff0000u);
-        cb[b][m][0] = __builtin_fmaf(-128.0f, sc[b][m][0], __uint_as_float(sbw[1] << 16));
-        cb[b][m][1] = __builtin_fmaf(-128.0f, sc[b][m][1], __uint_as_float(sbw[1] & 0xffff0000u));
+        SB[b][m] = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
       }
-    }
-    // every activation operand of the unit is read up front (one LDS round
-    // trip per unit, not one per k-slice)
-    bf16x8_t A[4][MT];
+    if constexpr (F16) {
+      // every activation operand of the unit is read up front (one LDS round
+      // trip per unit, not one per k-slice)
+      f16x8_t A[4][MT];
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
-    __builtin_amdgcn_sched_barrier(0);
-    // exact dequantisation, one quantisation group (two k-slices) at a time:
-    // P = x.(128+q) and X = x.1 by MFMA, then acc += s P + (b - 128 s) X
-    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-    const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      f32x4_t X[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) X[mt] = mfma_bf16(A[2 * g + 1][mt], ones, mfma_bf16(A[2 * g][mt], ones, zero));
+        for (int mt = 0; mt < MT; ++mt)
+          A[q][mt] = *reinterpret_cast<const f16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+      f16x2_t sc[NB][NM][2], bs[NB][NM][2];
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          const bf16x8_t B0 = nib8(W[b][m][2 * g]), B1 = nib8(W[b][m][2 * g + 1]);
+          sc[b][m][0] = f16_splat(__uint_as_float(SB[b][m][0] << 16));
+          sc[b][m][1] = f16_splat(__uint_as_float(SB[b][m][0] & 0xffff0000u));
+          bs[b][m][0] = f16_splat(__uint_as_float(SB[b][m][1] << 16));
+          bs[b][m][1] = f16_splat(__uint_as_float(SB[b][m][1] & 0xffff0000u));
+        }
+      __builtin_amdgcn_sched_barrier(0);
+      // k-slice q (32 k) of quantisation group q / 2: the weights dequantised
+      // once, multiplied against every 16-row tile of the pass
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const f32x4_t P = mfma_bf16(A[2 * g + 1][mt], B1, mfma_bf16(A[2 * g][mt], B0, zero));
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              acc[mt][b][m][i] = __builtin_fmaf(sc[b][m][g], P[i], acc[mt][b][m][i]);
-              acc[mt][b][m][i] = __builtin_fmaf(cb[b][m][g], X[mt][i], acc[mt][b][m][i]);
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            const f16x8_t B = dq8_f16(W[b][m][q], sc[b][m][q >> 1], bs[b][m][q >> 1]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][b][m] = mfma_f16(A[q][mt], B, acc[mt][b][m]);
+          }
+    } else {
+      float sc[NB][NM][2], cb[NB][NM][2];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          sc[b][m][0] = __uint_as_float(SB[b][m][0] << 16);
+          sc[b][m][1] = __uint_as_float(SB[b][m][0] & 0xffff0000u);
+          cb[b][m][0] = __builtin_fmaf(-128.0f, sc[b][m][0], __uint_as_float(SB[b][m][1] << 16));
+          cb[b][m][1] = __builtin_fmaf(-128.0f, sc[b][m][1], __uint_as_float(SB[b][m][1] & 0xffff0000u));
+        }
+      // exact dequantisation, one quantisation group (two k-slices) at a time:
+      // P = x.(128+q) and X = x.1 by MFMA, then acc += s P + (b - 128 s) X
+      // (the group's activation operands only are held, which keeps this
+      // path within the register budget of the fp16 path)
+      const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+      const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+      const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        bf16x8_t A[4][MT];
+#pragma unroll
+        for (int q = 2 * g; q < 2 * g + 2; ++q)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+        f32x4_t X[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) X[mt] = mfma_bf16(A[2 * g + 1][mt], ones, mfma_bf16(A[2 * g][mt], ones, zero));
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            const bf16x8_t B0 = nib8(W[b][m][2 * g]), B1 = nib8(W[b][m][2 * g + 1]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const f32x4_t Pg = mfma_bf16(A[2 * g + 1][mt], B1, mfma_bf16(A[2 * g][mt], B0, zero));
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                acc[mt][b][m][i] = __builtin_fmaf(sc[b][m][g], Pg[i], acc[mt][b][m][i]);
+                acc[mt][b][m][i] = __builtin_fmaf(cb[b][m][g], X[mt][i], acc[mt][b][m][i]);
+              }
             }
           }
-        }
+      }
     }
   }
 
-  // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile, column i16
+  // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile,
+  // column i16; gate/up also writes its SwiGLU rows in fp16 (F8 order) for
+  // the down grid and flags values outside fp16's range
+  bool ovf = false;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -223,19 +271,24 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       const int t = tile0 + b;
       if (t >= P.nt) continue;
       const int col = t * 16 + i16;
+      const int colh = (col & ~7) | f8_pos(col & 7);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mt + 4 * j + r;
         if (row >= rows) continue;
-        uint16_t v;
-        if (DUAL)
-          v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
-        else
-          v = f32_to_bf16(acc[mt][b][0][r]);
-        P.out[static_cast<int64_t>(row0 + row) * P.ldo + col] = v;
+        const int64_t orow = static_cast<int64_t>(row0 + row) * P.ldo;
+        if (DUAL) {
+          const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
+          P.out[orow + col] = v;
+          ovf |= bf16_f16_overflow(v);
+          P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
+        } else {
+          P.out[orow + col] = f32_to_bf16(acc[mt][b][0][r]);
+        }
       }
     }
   }
+  if (DUAL && __ballot(ovf) && lane == 0) atomicOr(flag, flag_out);
 }
 
 // Block -> work item. The hardware dispatches block b to XCD b % 8, each
@@ -285,13 +338,24 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
     rows = min(kPassRows, P.rows_static - row0);
   }
   if (rows <= 0) return;
-  // one call site per tile count: each inlined copy is compiled on its own
+  // one call site per tile count and arithmetic: each inlined copy is
+  // compiled on its own
   static_assert(kPfMT == 4, "row-tile dispatch below covers passes of up to 4 tiles");
-  switch ((rows + 15) / 16) {
-    case 1: pf_item<DUAL, 1>(P, ng, row0, rows, e, s_pf); break;
-    case 2: pf_item<DUAL, 2>(P, ng, row0, rows, e, s_pf); break;
-    case 3: pf_item<DUAL, 3>(P, ng, row0, rows, e, s_pf); break;
-    default: pf_item<DUAL, 4>(P, ng, row0, rows, e, s_pf); break;
+  const bool exact = __builtin_amdgcn_readfirstlane(*a.f16_flag & a.flag_in) != 0;
+  if (exact) {
+    switch ((rows + 15) / 16) {
+      case 1: pf_item<DUAL, 1, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+    }
+  } else {
+    switch ((rows + 15) / 16) {
+      case 1: pf_item<DUAL, 1, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+    }
   }
 }
 

@@ -390,6 +390,9 @@ typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   __shared__ double s_red[(kLgWaves - 1) * 4 * kWave];
+  // the forward's fp16-range flag starts clear (topk_kernel and the gate/up
+  // GEMMs, which run after this grid, set its bits)
+  if (a.f16_flag && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.f16_flag = 0u;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, kk = lane >> 4;
@@ -455,9 +458,21 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   }
 }
 
+// The token's row of x in fp16 (F8 chunk order) for the prefill GEMMs; a
+// value outside fp16's range sets kF16FlagX.
+__device__ void f16_row(const RouterArgs& a, int t, int lane) {
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(t) * a.H);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.xh + static_cast<int64_t>(t) * a.H);
+  bool ovf = false;
+  for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = bf16_chunk_to_f16_f8(src[ch], ovf);
+  if (__ballot(ovf) && lane == 0) atomicOr(a.f16_flag, kF16FlagX);
+}
+
 __global__ __launch_bounds__(kRouterThreads) void topk_kernel(RouterArgs a) {
   const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
-  if (t < a.T) router_token(a, t, threadIdx.x & 63);
+  if (t >= a.T) return;
+  router_token(a, t, threadIdx.x & 63);
+  if (a.xh) f16_row(a, t, threadIdx.x & 63);
 }
 
 hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream) {

@@ -180,3 +180,32 @@ def test_block_prefill_beyond_lds_sort(gpu, fmx, oracle):
     ry, _, _ = oracle.moe_block(cfg, w, hi.x, oracle.ACC_A, tokens=sub)
     e = assert_close(y[sub], ry[sub], "qwen3 t4500 sampled rows")
     print(f"qwen3 t4500: {e}")
+
+
+# Prefill rows whose values leave fp16's range: one token's x scaled by 2^12
+# (x below 65536, its SwiGLU outputs h far above) or by 2^17 (x itself above
+# 65536). The GEMMs then take the exact bf16 path for that grid; every row,
+# the scaled one included, is checked against the oracle.
+@pytest.mark.parametrize("scale_exp", [12, 17])
+def test_block_prefill_fp16_range(gpu, fmx, oracle, scale_exp):
+    import dataclasses
+
+    import torch
+    from flashmlx_amd import workloads as W
+    wl = W.WORKLOADS["small_t200"]
+    hi = W.host_inputs(wl)
+    x = hi.x.copy()
+    row = (x[7].astype(np.uint32) << 16).view(np.float32) * np.float32(2.0 ** scale_exp)
+    x[7] = (row.view(np.uint32) >> 16).astype(np.uint16)  # exact: a power-of-two scale
+    hi = dataclasses.replace(hi, x=x)
+    big = np.abs((x[7].astype(np.uint32) << 16).view(np.float32)).max()
+    assert (big >= 65536) == (scale_exp == 17)
+    block, xd = W.device_block(wl, hi)
+    y = from_dev_bf16(block(xd))
+    torch.cuda.synchronize()
+    cfg, w = oracle_args(hi, wl.model, oracle.quantize)
+    ry, rinds, _ = oracle.moe_block(cfg, w, hi.x, oracle.ACC_A)
+    np.testing.assert_array_equal(from_dev_u32(block.routing()["inds"]), rinds)
+    assert np.abs((ry[7].astype(np.uint32) << 16).view(np.float32)).max() >= 65536
+    e = assert_close(y, ry, f"small_t200 with token 7 scaled by 2^{scale_exp}")
+    print(f"fp16 range, 2^{scale_exp}: {e}")
