@@ -1,4 +1,5 @@
-"""ctypes binding of libfmx.so (the C-ABI declared in include/fmx.h).
+"""ctypes binding of libfmx.so (the C-ABI declared in include/fmx.h and
+include/fmx_model.h).
 
 This module only loads the library and declares its signatures. It raises
 ImportError when libfmx.so is missing: there is no fallback path.
@@ -66,6 +67,41 @@ class FmxMoEWeights(C.Structure):
         ("router_biases", C.c_void_p),
         ("shared_expert_gate_scales", C.c_void_p),
         ("shared_expert_gate_biases", C.c_void_p),
+    ]
+
+
+class FmxModelConfig(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_int64),
+        ("num_hidden_layers", C.c_int64),
+        ("num_attention_heads", C.c_int64),
+        ("num_key_value_heads", C.c_int64),
+        ("head_dim", C.c_int64),
+        ("vocab_size", C.c_int64),
+        ("max_position_embeddings", C.c_int64),
+        ("rms_norm_eps", C.c_float),
+        ("rope_theta", C.c_float),
+        ("moe", FmxMoEConfig),
+    ]
+
+
+class FmxLayerWeights(C.Structure):
+    _fields_ = [
+        ("input_norm_w", C.c_void_p),
+        ("post_norm_w", C.c_void_p),
+        ("qkv", C.c_void_p),
+        ("qkv_bias", C.c_void_p),
+        ("o", C.c_void_p),
+        ("moe", FmxMoEWeights),
+    ]
+
+
+class FmxModelWeights(C.Structure):
+    _fields_ = [
+        ("embed", C.c_void_p),
+        ("norm_w", C.c_void_p),
+        ("lm_head", C.c_void_p),
+        ("layers", C.POINTER(FmxLayerWeights)),
     ]
 
 
@@ -151,6 +187,29 @@ _SIGS = {
         C.c_int, [C.c_void_p, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_double]),
     "fmx_synth_normal_bf16_device": (
         C.c_int, [C.c_void_p, C.c_int64, C.c_uint64, C.c_uint64, C.c_double, C.c_double, C.c_void_p]),
+    # decoder stack (include/fmx_model.h)
+    "fmx_packed_linear_size": (C.c_size_t, [C.c_int64, C.c_int64]),
+    "fmx_pack_linear": (
+        C.c_int, [P(FmxQWeight), P(C.c_int64), C.c_int, C.c_int64, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "fmx_model_kv_cache_size": (C.c_size_t, [P(FmxModelConfig), C.c_int64, C.c_int64]),
+    "fmx_model_workspace_size": (C.c_size_t, [P(FmxModelConfig), C.c_int64]),
+    "fmx_model_workspace_init": (C.c_int, [P(FmxModelConfig), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "fmx_model_forward": (
+        C.c_int,
+        [P(FmxModelConfig), P(FmxModelWeights), C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
+         C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
+         C.c_void_p],
+    ),
+    "fmx_model_forward_traced": (
+        C.c_int,
+        [P(FmxModelConfig), P(FmxModelWeights), C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
+         C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
+         C.c_void_p, C.c_void_p],
+    ),
+    "fmx_model_workspace_hidden": (C.c_int, [P(FmxModelConfig), C.c_int64, C.c_void_p, P(C.c_void_p)]),
+    "fmx_greedy_next": (
+        C.c_int,
+        [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGS)

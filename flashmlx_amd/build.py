@@ -26,6 +26,8 @@ SOURCES = [
     "csrc/fmx_elem.hip",
     "csrc/fmx_api.cpp",
     "csrc/fmx_synth.hip",
+    "csrc/fmx_model.hip",
+    "csrc/fmx_model.cpp",
 ]
 
 ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")

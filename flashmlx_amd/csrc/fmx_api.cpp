@@ -16,8 +16,19 @@
 using namespace fmx;
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace fmx {
+// the thread's last error message, shared with the decoder-stack entry points
+int set_error(int status, const char* msg) {
+  g_last_error = msg;
+  return status;
+}
+void clear_error() { g_last_error.clear(); }
+}  // namespace fmx
+
+namespace {
 
 int fail(int status, const char* fmt, ...) {
   char buf[512];
@@ -143,7 +154,7 @@ struct MoELayout {
   uint8_t* slots;
   float* sgate;
   uint16_t *xp, *h, *hs, *d, *sd;
-  uint16_t *xh, *hh, *hsh;  // fp16 copies (F8 chunk order) of x, h, hs: prefill GEMM inputs
+  uint16_t *xh, *hh, *hsh;  // fp16 copies (P8 layout) of x, h, hs: prefill GEMM inputs
   uint32_t* f16_flag;
   uint32_t* dw;
   float* sd_part;

@@ -315,7 +315,7 @@ __device__ inline bf16x8_t nib8(uint32_t w) {
 // above 65536 (and inf/NaN) raise a flag that sends the GEMM to the exact
 // bf16 path instead.
 //
-// Chunk order F8: the 8 elements e0..e7 of a 16-byte activation chunk are
+// P8 layout (p8_slot): the 8 elements e0..e7 of a 16-byte activation chunk are
 // stored as e0 e4 e1 e5 e2 e6 e3 e7, the order in which dq8_f16 delivers the
 // 8 weights of a packed word, so that A and B operands pair up by position.
 
@@ -324,10 +324,8 @@ __device__ inline bf16x8_t nib8(uint32_t w) {
 // power-of-two scale 2^9 turns two such bytes into the exact fp16 values q.
 constexpr float kFp8Q = 512.0f;
 
-__host__ __device__ constexpr int f8_pos(int i) { return i < 4 ? 2 * i : 2 * i - 7; }
-
 // The 8 weights of a packed word (element 2i at nibble position i, 2i + 1 at
-// i + 4) as fp16(s*q + b) in F8 order: masking the even and the odd nibble
+// i + 4) as fp16(s*q + b) in P8 layout: masking the even and the odd nibble
 // positions into bytes gives lo = elements 0, 4, 1, 5 and hi = 2, 6, 3, 7;
 // each pair is converted by one instruction and scaled by one packed fp16
 // fma (a single rounding of s*q + b).
@@ -362,9 +360,9 @@ __device__ inline uint32_t bf16_to_f16_bits(uint32_t h) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(h << 16)));
 }
 
-// A 16-byte chunk of 8 bf16 (natural order) as 8 fp16 in F8 order; ovf is
+// A 16-byte chunk of 8 bf16 (natural order) as 8 fp16 in P8 layout; ovf is
 // set when an element is outside fp16's range.
-__device__ inline u32x4_t bf16_chunk_to_f16_f8(u32x4_t v, bool& ovf) {
+__device__ inline u32x4_t bf16_chunk_to_f16_p8(u32x4_t v, bool& ovf) {
   uint32_t e[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

@@ -71,7 +71,7 @@ struct RouterArgs {
   uint16_t* scores;        // [T, k] bf16
   float* sgate;            // [T] sigmoid(shared gate logit) (bf16 value) or null
   uint16_t* xp;            // [T, H] P8 copy of x or null
-  uint16_t* xh;            // [T, H] fp16 copy of x in F8 chunk order (topk_kernel) or null
+  uint16_t* xh;            // [T, H] fp16 copy of x in P8 layout (topk_kernel) or null
   uint32_t* f16_flag;      // zeroed by logits_kernel; topk_kernel ORs in kF16FlagX (or null)
   uint32_t* counters;      // [n_tt + 1], zero on entry, zero on exit
   int n_tt, n_ct;          // token tiles, column tiles (4 * cols_per_wave columns each)
@@ -198,12 +198,17 @@ struct PfSet {
   const uint8_t* w;          // packed blocks of expert 0 (pairs for gate/up)
   int64_t es;                // bytes per expert
   const uint16_t* x;         // activation rows, bf16
-  const uint16_t* xh;        // the same rows in fp16, F8 chunk order
+  const uint16_t* xh;        // the same rows in fp16, P8 layout
   int64_t ldx;               // elements between rows (both copies)
   const uint32_t* row_map;   // pass row -> x row (null: identity)
   uint16_t* out;             // output rows (indexed like the pass rows), bf16
-  uint16_t* outh;            // gate/up: the same rows in fp16, F8 chunk order
+  uint16_t* outh;            // gate/up: the same rows in fp16, P8 layout
   int64_t ldo;
+  // single-matrix sets only (both nullable): out = bf16(bf16(x.W^T) + bias[col]),
+  // then out = bf16(res[row] + out) (a residual add; res may alias out)
+  const uint16_t* bias;
+  const uint16_t* res;
+  int64_t ldr;
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)

@@ -1,0 +1,375 @@
+// fmx_model.hip -- the decoder stack around the MoE block: embedding, RMSNorm
+// (with the residual add), the attention projections for decode batches,
+// RoPE with the KV-cache write, scaled dot-product attention and greedy
+// token selection.
+//
+// Reference: server/src/model.cpp:486-497 (rms_norm, embed), :843-889
+// (attention: q/k/v linears with biases, RoPE, cache concatenation, SDPA,
+// o_proj), :891-911 (transformer_block), :1021-1033 (forward), :499-521
+// (lm_head). The projections of more than 16 rows run on the prefill GEMM
+// grid (fmx_prefill.hip); the MoE block is fmx_moe_block_forward.
+#include "fmx_dev.hpp"
+#include "fmx_model_kernels.hpp"
+
+namespace fmx {
+
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxChunks = 4;  // 16-byte chunks per thread: H <= 8192
+
+// ------------------------------------------------------------------ embedding
+
+// Row ids[t] of the bf16 table (ids outside [0, V) take the nearest row);
+// block 0 also clears the forward's fp16-range flag words.
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  const int t = blockIdx.x;
+  if (t == 0)
+    for (int i = threadIdx.x; i < a.n_flags; i += blockDim.x) a.flags[i] = 0u;
+  int64_t id = a.ids[t];
+  id = id < 0 ? 0 : (id >= a.V ? a.V - 1 : id);
+  const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.table + id * a.H);
+  u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.h + static_cast<int64_t>(t) * a.H);
+  for (int c = threadIdx.x; c < a.H / 8; c += blockDim.x) dst[c] = src[c];
+}
+
+// ------------------------------------------------------------------ RMSNorm
+
+// One workgroup per output row i (input row i * row_mul + row_add): optionally
+// x = bf16(x + delta) first (written back: the residual stream), then
+// out = bf16(bf16(x * r) * w), r = 1 / sqrt(mean(x^2) + eps), the sum of
+// squares and r in fp64 (mx::fast::rms_norm, model.cpp:486-488). outh, when
+// given, receives out in fp16 (P8 layout) for the prefill GEMMs, and a value
+// outside fp16's range sets *flag.
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(NormArgs a) {
+  __shared__ double s_red[kNormThreads / kWave];
+  const int i = blockIdx.x, tid = threadIdx.x;
+  const int64_t xr = static_cast<int64_t>(i) * a.row_mul + a.row_add;
+  const int nch = a.H / 8;
+  u32x4_t v[kNormMaxChunks];
+  double ss = 0.0;
+#pragma unroll
+  for (int q = 0; q < kNormMaxChunks; ++q) {
+    const int c = tid + q * kNormThreads;
+    if (c >= nch) break;
+    u32x4_t x = reinterpret_cast<const u32x4_t*>(a.x + xr * a.H)[c];
+    if (a.delta) {
+      const u32x4_t d = reinterpret_cast<const u32x4_t*>(a.delta + xr * a.H)[c];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t lo = f32_to_bf16(bf16_to_f32(x[m] & 0xffffu) + bf16_to_f32(d[m] & 0xffffu));
+        const uint32_t hi = f32_to_bf16(bf16_to_f32(x[m] >> 16) + bf16_to_f32(d[m] >> 16));
+        x[m] = lo | (hi << 16);
+      }
+      reinterpret_cast<u32x4_t*>(a.x_out + xr * a.H)[c] = x;
+    }
+    v[q] = x;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const double lo = bf16_to_f32(x[m] & 0xffffu), hi = bf16_to_f32(x[m] >> 16);
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((tid & 63) == 0) s_red[tid >> 6] = ss;
+  __syncthreads();
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) tot += s_red[w];
+  const double r = 1.0 / sqrt(tot / static_cast<double>(a.H) + static_cast<double>(a.eps));
+  bool ovf = false;
+#pragma unroll
+  for (int q = 0; q < kNormMaxChunks; ++q) {
+    const int c = tid + q * kNormThreads;
+    if (c >= nch) break;
+    const u32x4_t wv = reinterpret_cast<const u32x4_t*>(a.w)[c];
+    u32x4_t o;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      uint32_t e2[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const double xv = bf16_to_f32((v[q][m] >> (16 * hf)) & 0xffffu);
+        const uint16_t n = f64_to_bf16(xv * r);
+        e2[hf] = f64_to_bf16(static_cast<double>(bf16_to_f32(n)) *
+                             static_cast<double>(bf16_to_f32((wv[m] >> (16 * hf)) & 0xffffu)));
+      }
+      o[m] = e2[0] | (e2[1] << 16);
+    }
+    reinterpret_cast<u32x4_t*>(a.out + static_cast<int64_t>(i) * a.H)[c] = o;
+    if (a.outh) reinterpret_cast<u32x4_t*>(a.outh + static_cast<int64_t>(i) * a.H)[c] = bf16_chunk_to_f16_p8(o, ovf);
+  }
+  if (a.outh && __ballot(ovf) && (tid & 63) == 0) atomicOr(a.flag, 1u);
+}
+
+// ------------------------------------------------------------------ decode projections
+
+// out[t, :] for t < T <= 16 of a packed matrix (single blocks, fmx_dev.hpp):
+// one workgroup per 16-column tile, its 4 waves taking every fourth 128-k
+// unit, loads of kDnBatch units in flight per wave; exact dequantisation
+// (pk_unit: the fp32 value of x.(s*q + b)); the waves' partial sums are
+// added in wave order. Epilogue: bf16(acc), then + bias[col], then
+// res[t] + (each step rounded to bf16, as MLX's separate ops).
+constexpr int kDnBatch = 4;
+
+__global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
+  __shared__ f32x4_t s_acc[3][kWave];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int i16 = lane & 15, j = lane >> 4;
+  const int tile = blockIdx.x;
+  const uint8_t* tb = a.w + static_cast<int64_t>(tile) * a.nu * kBlockSingle;
+  const uint16_t* xrow = a.x + static_cast<int64_t>(min(i16, a.T - 1)) * a.ldx + 8 * j;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = {0.f, 0.f, 0.f, 0.f};
+  for (int u0 = wave; u0 < a.nu; u0 += 4 * kDnBatch) {
+    PkUnit<false> L[kDnBatch];
+    bf16x8_t A[kDnBatch][4];
+#pragma unroll
+    for (int d = 0; d < kDnBatch; ++d) {
+      const int u = min(u0 + 4 * d, a.nu - 1);  // units past K repeat the last and are skipped
+      L[d] = pk_load<false>(tb + static_cast<int64_t>(u) * kBlockSingle, lane);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) A[d][q] = *reinterpret_cast<const bf16x8_t*>(xrow + 128 * u + 32 * q);
+    }
+#pragma unroll
+    for (int d = 0; d < kDnBatch; ++d)
+      if (u0 + 4 * d < a.nu) pk_unit<false>(L[d], A[d], acc, unused);
+  }
+  if (wave > 0) s_acc[wave - 1][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w) acc += s_acc[w][lane];
+  const int col = tile * 16 + i16;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 4 * j + r;
+    if (t >= a.T) continue;
+    uint16_t v = f32_to_bf16(acc[r]);
+    if (a.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(a.bias[col]));
+    if (a.res) v = f32_to_bf16(bf16_to_f32(a.res[static_cast<int64_t>(t) * a.ldr + col]) + bf16_to_f32(v));
+    a.out[static_cast<int64_t>(t) * a.ldo + col] = v;
+  }
+}
+
+// ------------------------------------------------------------------ RoPE + cache
+
+__device__ inline int token_pos(const int32_t* offs, int off, int b, int l, int64_t max_seq) {
+  int64_t p = static_cast<int64_t>(offs ? offs[b] : off) + l;
+  return static_cast<int>(p < 0 ? 0 : (p >= max_seq ? max_seq - 1 : p));
+}
+
+// One workgroup per token t = b * L + l at position p = offset(b) + l:
+// q heads rotated into q_out, k heads rotated into the layer's key cache at
+// p, v heads copied into the value cache at p. Rotation of pair (i, i + hd/2)
+// by the table's (cos, sin) of p * base^(-2i/hd): each output is the exact
+// fp64 value of x1 c - x2 s (or x1 s + x2 c) rounded once to bf16
+// (mx::fast::rope, traditional = false, model.cpp:871-872).
+__global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
+  const int t = blockIdx.x;
+  const int b = t / a.L, l = t - b * a.L;
+  const int p = token_pos(a.offs, a.off, b, l, a.max_seq);
+  const int half = a.hd / 2, nq = a.nh + 2 * a.nkv;
+  const uint16_t* row = a.qkv + static_cast<int64_t>(t) * nq * a.hd;
+  const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
+  for (int it = threadIdx.x; it < (a.nh + a.nkv) * half; it += blockDim.x) {
+    const int head = it / half, i = it - head * half;
+    const uint16_t* src = row + head * a.hd;
+    const double x1 = bf16_to_f32(src[i]), x2 = bf16_to_f32(src[i + half]);
+    const double c = cs[2 * i], s = cs[2 * i + 1];
+    const uint16_t o1 = f64_to_bf16(__builtin_fma(x1, c, -(x2 * s)));
+    const uint16_t o2 = f64_to_bf16(__builtin_fma(x1, s, x2 * c));
+    uint16_t* dst;
+    if (head < a.nh) {
+      dst = a.q_out + (static_cast<int64_t>(t) * a.nh + head) * a.hd;
+    } else {
+      const int g = head - a.nh;
+      dst = a.kc + ((static_cast<int64_t>(b) * a.nkv + g) * a.max_seq + p) * a.hd;
+    }
+    dst[i] = o1;
+    dst[i + half] = o2;
+  }
+  for (int it = threadIdx.x; it < a.nkv * a.hd / 8; it += blockDim.x) {
+    const int g = it / (a.hd / 8), c = it - g * (a.hd / 8);
+    const u32x4_t v = reinterpret_cast<const u32x4_t*>(row + (a.nh + a.nkv + g) * a.hd)[c];
+    reinterpret_cast<u32x4_t*>(a.vc + ((static_cast<int64_t>(b) * a.nkv + g) * a.max_seq + p) * a.hd)[c] = v;
+  }
+}
+
+// ------------------------------------------------------------------ attention
+
+// One workgroup of kAttnThreads per (token t = b * L + l, q head h): keys
+// 0 .. p of kv head h / (nh / nkv), p = offset(b) + l (causal).
+//   s_j = scale * sum_d q_d k_jd   (fp32, d in order: exact bf16 products)
+//   e_j = exp(s_j - max s)         (fp64, the deterministic exp)
+//   out_d = sum_j e_j v_jd / sum_j e_j   (fp64, keys in order), bf16
+// (mx::fast::scaled_dot_product_attention, model.cpp:879-882). Thread d
+// forms out_d; every thread forms the same denominator in the same order.
+constexpr int kAttnThreads = 128;
+
+__global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_at[];
+  __shared__ float s_q[kAttnMaxHd];
+  __shared__ float s_max[kAttnThreads / kWave];
+  double* s_e = reinterpret_cast<double*>(s_at);
+  float* s_s = reinterpret_cast<float*>(s_at + static_cast<size_t>(a.max_seq) * 8);
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int b = t / a.L, l = t - b * a.L;
+  const int p = token_pos(a.offs, a.off, b, l, a.max_seq);
+  const int nk = p + 1;
+  const int g = h / (a.nh / a.nkv);
+  const uint16_t* qrow = a.q + (static_cast<int64_t>(t) * a.nh + h) * a.hd;
+  const int64_t cbase = (static_cast<int64_t>(b) * a.nkv + g) * a.max_seq * a.hd;
+  const uint16_t* kb = a.kc + cbase;
+  const uint16_t* vb = a.vc + cbase;
+  for (int d = tid; d < a.hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qrow[d]);
+  __syncthreads();
+
+  float m = -__builtin_huge_valf();
+  for (int jk = tid; jk < nk; jk += kAttnThreads) {
+    const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(jk) * a.hd);
+    float acc = 0.0f;
+    for (int c = 0; c < a.hd / 8; ++c) {
+      const u32x4_t kv = kr[c];
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        acc = __builtin_fmaf(s_q[8 * c + 2 * mm], bf16_to_f32(kv[mm] & 0xffffu), acc);
+        acc = __builtin_fmaf(s_q[8 * c + 2 * mm + 1], bf16_to_f32(kv[mm] >> 16), acc);
+      }
+    }
+    const float s = acc * a.scale;
+    s_s[jk] = s;
+    m = fmaxf(m, s);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((tid & 63) == 0) s_max[tid >> 6] = m;
+  __syncthreads();
+  m = s_max[0];
+#pragma unroll
+  for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, s_max[w]);
+  for (int jk = tid; jk < nk; jk += kAttnThreads)
+    s_e[jk] = exp_det(static_cast<double>(s_s[jk]) - static_cast<double>(m));
+  __syncthreads();
+
+  bool ovf = false;
+  for (int d = tid; d < a.hd; d += kAttnThreads) {
+    double num = 0.0, den = 0.0;
+    for (int jk = 0; jk < nk; ++jk) {
+      const double e = s_e[jk];
+      den += e;
+      num = __builtin_fma(e, static_cast<double>(bf16_to_f32(vb[static_cast<int64_t>(jk) * a.hd + d])), num);
+    }
+    const uint16_t o = f64_to_bf16(num / den);
+    const int64_t oc = static_cast<int64_t>(h) * a.hd + d;
+    a.out[static_cast<int64_t>(t) * a.ldo + oc] = o;
+    if (a.outh) {
+      ovf = ovf || bf16_f16_overflow(o);
+      a.outh[static_cast<int64_t>(t) * a.ldo + ((oc & ~7) | p8_slot(oc & 7))] =
+          static_cast<uint16_t>(bf16_to_f16_bits(o));
+    }
+  }
+  if (a.outh && __ballot(ovf) && (tid & 63) == 0) atomicOr(a.flag, 1u);
+}
+
+// ------------------------------------------------------------------ greedy
+
+// ids[b] = argmax of logits row b (the first of equal maxima, as mx::argmax);
+// offs[b] += inc when offs is given (the next decode position).
+__global__ __launch_bounds__(1024) void greedy_kernel(GreedyArgs a) {
+  __shared__ float s_v[1024 / kWave];
+  __shared__ int64_t s_i[1024 / kWave];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* row = a.logits + static_cast<int64_t>(b) * a.ld;
+  float best = -__builtin_huge_valf();
+  int64_t bi = a.V;
+  for (int64_t v = tid; v < a.V; v += blockDim.x) {
+    const float x = bf16_to_f32(row[v]);
+    if (x > best || (x == best && v < bi)) {  // NaN never wins
+      best = x;
+      bi = v;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ob = __shfl_xor(best, o);
+    const int64_t oi = __shfl_xor(bi, o);
+    if (ob > best || (ob == best && oi < bi)) {
+      best = ob;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = best;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w)
+    if (s_v[w] > best || (s_v[w] == best && s_i[w] < bi)) {
+      best = s_v[w];
+      bi = s_i[w];
+    }
+  if (bi >= a.V) bi = 0;  // an all-NaN row
+  a.ids[b] = static_cast<int32_t>(bi);
+  if (a.offs) a.offs[b] += a.inc;
+}
+
+__global__ __launch_bounds__(256) void copy_u32_kernel(const uint32_t* src, uint32_t* dst, int64_t n) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256)
+    dst[i] = src[i];
+}
+
+}  // namespace
+
+hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(copy_u32_kernel, dim3(static_cast<uint32_t>(blocks < 1024 ? blocks : 1024)), dim3(256),
+                     0, stream, src, dst, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t stream) {
+  if (a.T == 0) return hipSuccess;
+  hipLaunchKernelGGL(embed_kernel, dim3(a.T), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+bool rmsnorm_fits(int64_t H) { return H % 8 == 0 && H / 8 <= kNormThreads * kNormMaxChunks; }
+
+hipError_t launch_rmsnorm(const NormArgs& a, int n_rows, hipStream_t stream) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(kNormThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_dec(const DenseArgs& a, hipStream_t stream) {
+  if (a.T == 0 || a.nt == 0) return hipSuccess;
+  hipLaunchKernelGGL(dense_dec_kernel, dim3(a.nt), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_cache(const RopeArgs& a, int T, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_cache_kernel, dim3(T), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+size_t attn_lds_bytes(int64_t max_seq) { return static_cast<size_t>(max_seq) * 12; }
+
+hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream) {
+  if (T == 0) return hipSuccess;
+  hipLaunchKernelGGL(attn_kernel, dim3(T, a.nh), dim3(kAttnThreads), attn_lds_bytes(a.max_seq), stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_greedy(const GreedyArgs& a, int B, hipStream_t stream) {
+  if (B == 0) return hipSuccess;
+  hipLaunchKernelGGL(greedy_kernel, dim3(B), dim3(1024), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace fmx

@@ -33,8 +33,8 @@
 // Arithmetic: the weights are dequantised once per pass into fp16 (s*q + b
 // rounded once, 2^-11 relative) and multiplied with
 // v_mfma_f32_16x16x32_f16 against fp16 copies of the activation rows
-// (exact for bf16 values below 65536; the copies are written in F8 chunk
-// order, fmx_dev.hpp, by the router for x and by this gate/up grid for h).
+// (exact for bf16 values below 65536; the copies are written in the P8
+// layout, fmx_dev.hpp, by the router for x and by this gate/up grid for h).
 // When a row holds a value outside fp16's range (the forward's flag word
 // says so) the grid takes the exact bf16 path instead: nibbles become the
 // bf16 values 128 + q, the MFMA forms P = x.(128+q) and X = x.1 per
@@ -261,7 +261,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   }
 
   // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile,
-  // column i16; gate/up also writes its SwiGLU rows in fp16 (F8 order) for
+  // column i16; gate/up also writes its SwiGLU rows in fp16 (P8 layout) for
   // the down grid and flags values outside fp16's range
   bool ovf = false;
 #pragma unroll
@@ -271,7 +271,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       const int t = tile0 + b;
       if (t >= P.nt) continue;
       const int col = t * 16 + i16;
-      const int colh = (col & ~7) | f8_pos(col & 7);
+      const int colh = (col & ~7) | p8_slot(col & 7);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mt + 4 * j + r;
@@ -283,7 +283,11 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
           ovf |= bf16_f16_overflow(v);
           P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
         } else {
-          P.out[orow + col] = f32_to_bf16(acc[mt][b][0][r]);
+          uint16_t v = f32_to_bf16(acc[mt][b][0][r]);
+          if (P.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(P.bias[col]));
+          if (P.res)
+            v = f32_to_bf16(bf16_to_f32(P.res[static_cast<int64_t>(row0 + row) * P.ldr + col]) + bf16_to_f32(v));
+          P.out[orow + col] = v;
         }
       }
     }

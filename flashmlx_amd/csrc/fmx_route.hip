@@ -458,13 +458,13 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   }
 }
 
-// The token's row of x in fp16 (F8 chunk order) for the prefill GEMMs; a
+// The token's row of x in fp16 (P8 layout) for the prefill GEMMs; a
 // value outside fp16's range sets kF16FlagX.
 __device__ void f16_row(const RouterArgs& a, int t, int lane) {
   const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(t) * a.H);
   u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.xh + static_cast<int64_t>(t) * a.H);
   bool ovf = false;
-  for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = bf16_chunk_to_f16_f8(src[ch], ovf);
+  for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = bf16_chunk_to_f16_p8(src[ch], ovf);
   if (__ballot(ovf) && lane == 0) atomicOr(a.f16_flag, kF16FlagX);
 }
 

@@ -1,0 +1,133 @@
+/*
+ * fmx_model.h -- C-ABI of the decoder stack around the MoE block (libfmx.so).
+ *
+ * Replaces LlamaModel's forward for MoE models (every layer MoE, as
+ * Qwen1.5-MoE-A2.7B): embedding, per layer RMSNorm -> attention (q/k/v
+ * linears with biases, RoPE, KV cache, scaled dot-product attention, o_proj)
+ * -> residual -> RMSNorm -> MoE block (fmx_moe_block_forward) -> residual,
+ * then the final RMSNorm and lm_head. Conventions as in fmx.h: device
+ * pointers, asynchronous on `stream`, status codes, no allocation when a
+ * workspace is given.
+ *
+ * Linear weights are read in the packed layout of fmx_pack_linear (the same
+ * 0.5625 bytes per weight as MLX's affine 4-bit, group 64 arrays).
+ */
+#ifndef FMX_MODEL_H
+#define FMX_MODEL_H
+
+#include "fmx.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ModelConfig (server/include/flashmlx/model.h:20-54) for an all-MoE
+ * decoder: head_dim = hidden_size / num_attention_heads when 0. Limits:
+ * hidden_size and num_attention_heads * head_dim multiples of 128 (and
+ * hidden_size <= 8192), head_dim even, a multiple of 8 and <= 256,
+ * num_attention_heads a multiple of num_key_value_heads, vocab_size a
+ * multiple of 16, max_position_embeddings <= 4096. */
+typedef struct fmx_model_config {
+  int64_t hidden_size;
+  int64_t num_hidden_layers;
+  int64_t num_attention_heads;
+  int64_t num_key_value_heads;
+  int64_t head_dim;
+  int64_t vocab_size;
+  int64_t max_position_embeddings;
+  float rms_norm_eps;
+  float rope_theta;
+  fmx_moe_config moe; /* every layer's MoE block */
+} fmx_model_config;
+
+/* One layer (LlamaModel::LayerWeights, model.h:242-254, and MoEWeights).
+ * qkv: the q, k and v linears packed one after the other (fmx_pack_linear
+ * with three parts); qkv_bias: the q, k and v linear biases
+ * (model.cpp:864-866) concatenated, bf16 [(nh + 2 nkv) * hd], or NULL. */
+typedef struct fmx_layer_weights {
+  const void* input_norm_w; /* bf16 [H] */
+  const void* post_norm_w;  /* bf16 [H] */
+  const void* qkv;          /* packed [(nh + 2 nkv) * hd, H] */
+  const void* qkv_bias;
+  const void* o;            /* packed [H, nh * hd] */
+  fmx_moe_weights moe;
+} fmx_layer_weights;
+
+/* embed: the embedding table as bf16 [V, H] (the reference dequantizes a
+ * quantized table once at load, model.cpp:214-224, and gathers rows from it,
+ * :490-497); lm_head: packed [V, H] (model.cpp:499-521); layers: a host
+ * array of num_hidden_layers entries. */
+typedef struct fmx_model_weights {
+  const void* embed;
+  const void* norm_w; /* bf16 [H] */
+  const void* lm_head;
+  const fmx_layer_weights* layers;
+} fmx_model_weights;
+
+/* Load-time packing of a quantized linear (replaces the per-call
+ * quantized_matmul operands of LlamaModel::linear_fast, model.cpp:476-480):
+ * n_parts MLX-layout matrices of rows[i] x K (w u32 [rows, K/8], scales and
+ * biases bf16 [rows, K/64]) stacked into one packed matrix of sum(rows) rows.
+ * K a multiple of 128, every rows[i] a multiple of 16. */
+size_t fmx_packed_linear_size(int64_t n_rows, int64_t K);
+int fmx_pack_linear(const fmx_qweight* parts, const int64_t* rows, int n_parts, int64_t K,
+                    void* packed, size_t packed_bytes, fmx_stream stream);
+
+/* KV cache of the stack: keys and values of every layer, bf16
+ * [layers][2][cache_batch][nkv][cache_max_seq][hd]. */
+size_t fmx_model_kv_cache_size(const fmx_model_config* cfg, int64_t cache_batch,
+                               int64_t cache_max_seq);
+
+/* Workspace for forwards of up to max_tokens = batch * seq_len tokens,
+ * including the RoPE table; fmx_model_workspace_init fills the table and
+ * prepares the MoE blocks' counters (once, before the first forward). */
+size_t fmx_model_workspace_size(const fmx_model_config* cfg, int64_t max_tokens);
+int fmx_model_workspace_init(const fmx_model_config* cfg, void* workspace,
+                             size_t workspace_bytes, fmx_stream stream);
+
+/* logits = forward(input_ids) (LlamaModel::forward, model.cpp:1021-1033):
+ *   input_ids int32 [batch, seq_len] (device); sequence b's tokens sit at
+ *   cache positions offset(b) .. offset(b) + seq_len - 1, where offset(b) =
+ *   cache_offsets[b] (device int32 [batch], per-sequence offsets as in
+ *   forward_heterogeneous, model.cpp:990-1019) or cache_offset when
+ *   cache_offsets is NULL. Each layer writes the new keys/values into
+ *   kv_cache (sequence b in cache slot b < cache_batch) and attends causally
+ *   to positions 0 .. its own. Device offsets are clamped to the cache.
+ *   logits bf16 [batch, seq_len, V], or [batch, V] (the last position of
+ *   each sequence) when logits_last_only. */
+int fmx_model_forward(const fmx_model_config* cfg, const fmx_model_weights* w,
+                      const int32_t* input_ids, int64_t batch, int64_t seq_len,
+                      int64_t cache_offset, const int32_t* cache_offsets, void* kv_cache,
+                      int64_t cache_batch, int64_t cache_max_seq, int logits_last_only,
+                      void* logits, void* workspace, size_t workspace_bytes, fmx_stream stream);
+
+/* fmx_model_forward that also copies each layer's expert choice into
+ * routing (device u32 [layers][batch * seq_len][k], the MoE block's inds in
+ * token order, slots ordered as fmx_moe_block_forward orders them). A
+ * debugging view, as LlamaModel's debug_forward (model.h:125): lets a
+ * reference run take the same expert choice where a router is at a near-tie. */
+int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weights* w,
+                             const int32_t* input_ids, int64_t batch, int64_t seq_len,
+                             int64_t cache_offset, const int32_t* cache_offsets, void* kv_cache,
+                             int64_t cache_batch, int64_t cache_max_seq, int logits_last_only,
+                             void* logits, void* workspace, size_t workspace_bytes,
+                             fmx_stream stream, uint32_t* routing);
+
+/* The residual stream after the last layer of the latest forward on this
+ * workspace, bf16 [n_tokens, H] (every row when that forward returned the
+ * logits of every position; the last position of each sequence otherwise).
+ * Valid until the next call on the workspace. A debugging view, as
+ * LlamaModel's debug_forward / debug_embed (model.h:125-126). */
+int fmx_model_workspace_hidden(const fmx_model_config* cfg, int64_t n_tokens, const void* workspace,
+                               const void** hidden);
+
+/* Greedy next token: ids[b] = argmax_v logits[b * row_stride + v] (the
+ * first of equal maxima, as mx::argmax); when offsets is not NULL,
+ * offsets[b] += advance (the next decode step's cache position). */
+int fmx_greedy_next(const void* logits, int64_t batch, int64_t vocab, int64_t row_stride,
+                    int32_t* ids, int32_t* offsets, int32_t advance, fmx_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FMX_MODEL_H */

@@ -473,10 +473,10 @@ static void qmv(const uint16_t* x, int64_t K, const uint32_t* w, const uint16_t*
     out[n] = qdot_row(x, w + n * (K / 8), s + n * (K / 64), b + n * (K / 64), K, mode);
 }
 
-int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
-                  const uint16_t* x, int64_t T, int mode,
-                  const int64_t* token_subset, int64_t n_subset,
-                  uint16_t* y, uint32_t* inds_out, uint16_t* scores_out) {
+static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                          const uint16_t* x, int64_t T, int mode,
+                          const int64_t* token_subset, int64_t n_subset, const uint32_t* forced,
+                          uint16_t* y, uint32_t* inds_out, uint16_t* scores_out) {
   const int64_t H = cfg->hidden, E = cfg->n_experts, I = cfg->inter, Is = cfg->shared_inter;
   const int k = cfg->top_k;
   if (cfg->group_size != 64 || cfg->bits != 4 || H % 64 || I % 64 || (Is && Is % 64)) return -1;
@@ -490,9 +490,31 @@ int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
   float* acc = (float*)malloc(sizeof(float) * H);
   if (!inds || !scores || !g || !u || !a || !d || !acc) return -3;
 
+  uint16_t* probs = forced ? (uint16_t*)malloc(sizeof(uint16_t) * T * E) : NULL;
+  if (forced && !probs) return -3;
   int rc = orc_router_topk_q(x, T, H, w->router_w, w->router_s, w->router_b, E, w->router_bias, k,
-                             cfg->norm_topk, NULL, NULL, inds, scores);
+                             cfg->norm_topk, NULL, probs, inds, scores);
   if (rc) return rc;
+  if (forced) {
+    /* the given expert choice, with this router's probabilities as scores
+     * (renormalised as the router does) */
+    for (int64_t t = 0; t < T; ++t) {
+      for (int j = 0; j < k; ++j) {
+        uint32_t e = forced[t * k + j];
+        if (e >= (uint32_t)E) e = (uint32_t)(E - 1);
+        inds[t * k + j] = e;
+        scores[t * k + j] = probs[t * E + e];
+      }
+      if (cfg->norm_topk) {
+        float sum = 0.0f;
+        for (int j = 0; j < k; ++j) sum += bf(scores[t * k + j]);
+        const uint16_t sb = rb(sum);
+        for (int j = 0; j < k; ++j)
+          scores[t * k + j] = rb((float)((double)bf(scores[t * k + j]) / (double)bf(sb)));
+      }
+    }
+    free(probs);
+  }
 
   const int64_t n_tok = token_subset ? n_subset : T;
   const int64_t wst_gu = I * (H / 8), sst_gu = I * (H / 64);
@@ -540,4 +562,137 @@ int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
   free(d);
   free(acc);
   return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* decoder stack pieces                                                      */
+/* ------------------------------------------------------------------------ */
+
+/* mx::fast::rms_norm (model.cpp:486-488) as MLX's fallback composes it
+ * (recalled): x in fp32, x * rsqrt(mean(x^2) + eps) cast to bf16, then the
+ * bf16 product with the weight. Restated with the sum of squares and the
+ * normaliser in fp64, x * r rounded to bf16 and the product with w (two bf16
+ * values, exact in fp64) rounded once. */
+int orc_rms_norm(const uint16_t* x, int64_t T, int64_t H, const uint16_t* w, float eps,
+                 uint16_t* out) {
+  if (T < 0 || H <= 0) return -1;
+#pragma omp parallel for schedule(static)
+  for (int64_t t = 0; t < T; ++t) {
+    const uint16_t* xr = x + t * H;
+    double ss = 0.0;
+    for (int64_t i = 0; i < H; ++i) {
+      const double v = (double)bf(xr[i]);
+      ss += v * v;
+    }
+    const double r = 1.0 / sqrt(ss / (double)H + (double)eps);
+    for (int64_t i = 0; i < H; ++i) {
+      const uint16_t n = orc_f64_to_bf16((double)bf(xr[i]) * r);
+      out[t * H + i] = orc_f64_to_bf16((double)bf(n) * (double)bf(w[i]));
+    }
+  }
+  return 0;
+}
+
+/* RoPE angles of mx::fast::rope (traditional = false, scale 1,
+ * model.cpp:871-872): theta(p, i) = p * base^(-2i/hd) for i < hd/2, as
+ * (cos, sin) pairs rounded to fp32: cs[(p * hd/2 + i) * 2 + {0, 1}]. */
+void orc_rope_table(int64_t n_pos, int64_t hd, double base, float* cs) {
+  const int64_t half = hd / 2;
+  for (int64_t i = 0; i < half; ++i) {
+    const double inv = pow(base, -(2.0 * (double)i) / (double)hd);
+    for (int64_t p = 0; p < n_pos; ++p) {
+      const double th = (double)p * inv;
+      cs[(p * half + i) * 2] = (float)cos(th);
+      cs[(p * half + i) * 2 + 1] = (float)sin(th);
+    }
+  }
+}
+
+/* Non-traditional RoPE in place on x [T, n_heads, hd] at positions pos[T]:
+ * element pairs (i, i + hd/2) rotate by theta(pos, i):
+ *   x1' = x1 cos - x2 sin,  x2' = x1 sin + x2 cos,
+ * each from the exact products (bf16 x fp32 is exact in fp64), rounded once
+ * to bf16. */
+int orc_rope(uint16_t* x, int64_t T, int64_t n_heads, int64_t hd, const int64_t* pos,
+             const float* cs) {
+  if (hd % 2) return -1;
+  const int64_t half = hd / 2;
+  for (int64_t t = 0; t < T; ++t) {
+    const float* c = cs + pos[t] * half * 2;
+    for (int64_t h = 0; h < n_heads; ++h) {
+      uint16_t* v = x + (t * n_heads + h) * hd;
+      for (int64_t i = 0; i < half; ++i) {
+        const double x1 = (double)bf(v[i]), x2 = (double)bf(v[i + half]);
+        const double co = (double)c[2 * i], si = (double)c[2 * i + 1];
+        v[i] = orc_f64_to_bf16(x1 * co - x2 * si);
+        v[i + half] = orc_f64_to_bf16(x1 * si + x2 * co);
+      }
+    }
+  }
+  return 0;
+}
+
+/* mx::fast::scaled_dot_product_attention (model.cpp:879-882) for one
+ * sequence: q [L, nh, hd] (roped), the cache of that sequence kc / vc
+ * [nkv, max_seq, hd] holding keys 0 .. q_off + L - 1; query l (position
+ * q_off + l) attends to keys 0 .. q_off + l (causal; for L = 1 that is every
+ * key). q head h reads kv head h / (nh / nkv). Scores are fp32 dot products
+ * (exact bf16 products, summed over d in order) times scale; the softmax is
+ * formed in fp64 with the deterministic exp (e_j = exp(s_j - max)), the
+ * output as sum_j e_j v_j / sum_j e_j in fp64 (keys in order, fma), rounded
+ * once to bf16: out [L, nh, hd]. */
+int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
+             const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
+             uint16_t* out) {
+  if (nkv <= 0 || nh % nkv || q_off + L > max_seq) return -1;
+  const int64_t rep = nh / nkv;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int64_t l = 0; l < L; ++l) {
+    for (int64_t h = 0; h < nh; ++h) {
+      const int64_t g = h / rep, nk = q_off + l + 1;
+      const uint16_t* qv = q + (l * nh + h) * hd;
+      const uint16_t* kb = kc + g * max_seq * hd;
+      const uint16_t* vb = vc + g * max_seq * hd;
+      float* s = (float*)malloc(sizeof(float) * nk);
+      double* e = (double*)malloc(sizeof(double) * nk);
+      float m = -INFINITY;
+      for (int64_t j = 0; j < nk; ++j) {
+        float acc = 0.0f;
+        for (int64_t d = 0; d < hd; ++d) acc += bf(qv[d]) * bf(kb[j * hd + d]);
+        s[j] = acc * scale;
+        if (s[j] > m) m = s[j];
+      }
+      double den = 0.0;
+      for (int64_t j = 0; j < nk; ++j) {
+        e[j] = orc_exp((double)s[j] - (double)m);
+        den += e[j];
+      }
+      for (int64_t d = 0; d < hd; ++d) {
+        double num = 0.0;
+        for (int64_t j = 0; j < nk; ++j) num = fma(e[j], (double)bf(vb[j * hd + d]), num);
+        out[(l * nh + h) * hd + d] = orc_f64_to_bf16(num / den);
+      }
+      free(s);
+      free(e);
+    }
+  }
+  return 0;
+}
+
+int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                  const uint16_t* x, int64_t T, int mode,
+                  const int64_t* token_subset, int64_t n_subset,
+                  uint16_t* y, uint32_t* inds_out, uint16_t* scores_out) {
+  return moe_block_impl(cfg, w, x, T, mode, token_subset, n_subset, NULL, y, inds_out, scores_out);
+}
+
+/* The MoE block with the expert choice given (inds [T, k]): the scores are
+ * this router's probabilities of those experts (renormalised when
+ * norm_topk), the rest as orc_moe_block. Lets a whole decoder stack be
+ * compared with a GPU run that chose differently at a router near-tie. */
+int orc_moe_block_routed(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                         const uint16_t* x, int64_t T, int mode, const uint32_t* inds,
+                         uint16_t* y, uint16_t* scores_out) {
+  if (!inds) return -1;
+  return moe_block_impl(cfg, w, x, T, mode, NULL, 0, inds, y, NULL, scores_out);
 }

@@ -42,6 +42,14 @@
  *                                        with (p desc, idx asc)
  *   orc_moe_sort                         numpy stable argsort + invariants
  *   orc_moe_block                        dense fp64 formula on tiny shapes
+ *   orc_rms_norm                         scale invariance, constant rows, numpy fp64
+ *   orc_rope_table / orc_rope            position 0 = identity, pair norms kept,
+ *                                        composition of rotations, numpy complex
+ *                                        rotation; MLX's rounding points inside
+ *                                        rope (bf16 vs fp32 angles) are UNPINNED
+ *   orc_sdpa                             one key = v, equal keys = mean of values,
+ *                                        causal prefix, numpy fp64 softmax(QK^T)V;
+ *                                        MLX's intermediate roundings UNPINNED
  */
 #ifndef FMX_ORACLE_H
 #define FMX_ORACLE_H
@@ -146,6 +154,28 @@ int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
                   const uint16_t* x, int64_t T, int mode,
                   const int64_t* token_subset, int64_t n_subset,
                   uint16_t* y, uint32_t* inds, uint16_t* scores);
+
+/* ---- decoder stack pieces (model.cpp:486-488, :843-911) ---------------- */
+/* out [T, H] = rms_norm(x [T, H], w [H], eps) (mx::fast::rms_norm) */
+int orc_rms_norm(const uint16_t* x, int64_t T, int64_t H, const uint16_t* w, float eps,
+                 uint16_t* out);
+/* (cos, sin) of p * base^(-2i/hd), fp32, for p < n_pos, i < hd/2:
+ * cs[(p * hd/2 + i) * 2 + {0, 1}] */
+void orc_rope_table(int64_t n_pos, int64_t hd, double base, float* cs);
+/* mx::fast::rope (traditional=false, scale 1) in place on x [T, n_heads, hd] */
+int orc_rope(uint16_t* x, int64_t T, int64_t n_heads, int64_t hd, const int64_t* pos,
+             const float* cs);
+/* mx::fast::scaled_dot_product_attention of one sequence, causal from q_off:
+ * q [L, nh, hd], kc/vc [nkv, max_seq, hd] -> out [L, nh, hd] */
+int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
+             const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
+             uint16_t* out);
+
+/* orc_moe_block with the expert choice given (inds [T, k]); scores are the
+ * router's probabilities of those experts (renormalised when norm_topk). */
+int orc_moe_block_routed(const orc_moe_cfg* cfg, const orc_moe_weights* w,
+                         const uint16_t* x, int64_t T, int mode, const uint32_t* inds,
+                         uint16_t* y, uint16_t* scores_out);
 
 /* threads used by the OpenMP loops (0 = leave the runtime default) */
 void orc_set_threads(int n);

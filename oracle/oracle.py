@@ -84,6 +84,13 @@ def load() -> C.CDLL:
         lib.orc_moe_sort.argtypes = [_vp, i64, C.c_int, i64, _vp, _vp, _vp, _vp, _vp]
         lib.orc_moe_block.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp, i64,
                                       _vp, _vp, _vp]
+        lib.orc_rms_norm.argtypes = [_vp, i64, i64, _vp, C.c_float, _vp]
+        lib.orc_rope_table.argtypes = [i64, i64, C.c_double, _vp]
+        lib.orc_rope_table.restype = None
+        lib.orc_rope.argtypes = [_vp, i64, i64, i64, _vp, _vp]
+        lib.orc_sdpa.argtypes = [_vp, i64, i64, i64, _vp, _vp, i64, i64, i64, C.c_float, _vp]
+        lib.orc_moe_block_routed.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp,
+                                             _vp, _vp]
         lib.orc_set_threads.argtypes = [C.c_int]
         lib.orc_get_threads.restype = C.c_int
         _lib = lib
@@ -220,12 +227,14 @@ def moe_sort(inds, E):
     return order, inv, src, idx, offsets
 
 
-def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None):
+def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None, inds=None):
     """cfg keys: hidden, n_experts, top_k, inter, shared_inter, norm_topk.
     w keys: router_w (bf16, or a quantized (wq, s, b) tuple), router_bias?,
     gate/up/down (wq, s, b) tuples, shared_gate/shared_up/shared_down tuples?,
     shared_expert_gate_w? (bf16 or a quantized tuple).
-    Returns (y [T,H] with rows only for `tokens` filled when given, inds, scores)."""
+    Returns (y [T,H] with rows only for `tokens` filled when given, inds, scores).
+    inds [T, k] given: that expert choice (orc_moe_block_routed), scores from
+    this router's probabilities."""
     x = _c(x, np.uint16)
     H = cfg["hidden"]
     T = x.size // H
@@ -264,10 +273,147 @@ def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None):
     else:
         ww.sh_expert_gate_w = ptr(g, np.uint16)
     y = np.zeros((T, H), np.uint16)
-    inds = np.empty((T, k), np.uint32)
     scores = np.empty((T, k), np.uint16)
+    if inds is not None:
+        inds = _c(np.asarray(inds, dtype=np.uint32).reshape(T, k), np.uint32)
+        rc = load().orc_moe_block_routed(C.byref(c), C.byref(ww), _p(x), T, mode, _p(inds), _p(y),
+                                         _p(scores))
+        assert rc == 0, rc
+        return y, inds, scores
+    inds = np.empty((T, k), np.uint32)
     sub = None if tokens is None else np.ascontiguousarray(tokens, dtype=np.int64)
     rc = load().orc_moe_block(C.byref(c), C.byref(ww), _p(x), T, mode, _p(sub),
                               0 if sub is None else sub.size, _p(y), _p(inds), _p(scores))
     assert rc == 0, rc
     return y, inds, scores
+
+
+# ---------------------------------------------------------------- decoder stack
+
+def rms_norm(x, w, eps):
+    x, w = _c(x, np.uint16), _c(w, np.uint16)
+    H = x.shape[-1]
+    out = np.empty_like(x)
+    rc = load().orc_rms_norm(_p(x), x.size // H, H, _p(w), float(eps), _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def rope_table(n_pos: int, hd: int, base: float) -> np.ndarray:
+    cs = np.empty((n_pos, hd // 2, 2), np.float32)
+    load().orc_rope_table(n_pos, hd, float(base), _p(cs))
+    return cs
+
+
+def rope(x, pos, cs):
+    """x [T, n_heads, hd] bf16 (a rotated copy is returned), pos [T]."""
+    x = np.array(x, dtype=np.uint16, copy=True, order="C")
+    pos = _c(np.asarray(pos, dtype=np.int64), np.int64)
+    T, nh, hd = x.shape
+    rc = load().orc_rope(_p(x), T, nh, hd, _p(pos), _p(_c(cs, np.float32)))
+    assert rc == 0, rc
+    return x
+
+
+def sdpa(q, kc, vc, q_off: int, scale: float):
+    """q [L, nh, hd]; kc/vc [nkv, max_seq, hd] of one sequence -> [L, nh, hd]."""
+    q, kc, vc = _c(q, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16)
+    L, nh, hd = q.shape
+    nkv, max_seq = kc.shape[0], kc.shape[1]
+    out = np.empty_like(q)
+    rc = load().orc_sdpa(_p(q), L, nh, hd, _p(kc), _p(vc), nkv, max_seq, q_off, float(scale),
+                         _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def bf16_add(a, b) -> np.ndarray:
+    """MLX add of two bf16 arrays: the fp32 sum rounded to bf16."""
+    return f32_to_bf16_array(bf16_to_f32(a) + bf16_to_f32(b))
+
+
+class DecoderStack:
+    """LlamaModel::forward (server/src/model.cpp:1021-1033) over a KV cache:
+    embed (:490-497, a bf16 table as the reference pre-dequantizes it at
+    load, :214-224), per layer transformer_block (:891-911: input norm,
+    attention :843-889 with q/k/v biases and RoPE, residual, post-attention
+    norm, moe_block, residual), final norm and lm_head (:499-521).
+
+    cfg: hidden, layers, heads, kv_heads, head_dim, vocab, eps, theta,
+    max_seq, moe (moe_block's cfg dict). w: embed [V, H] bf16, norm_w,
+    lm_head (wq, s, b), layers: list of dicts with in_w, post_w, qkv
+    (wq, s, b) of the q;k;v rows, qkv_bias bf16 or None, o (wq, s, b), moe
+    (moe_block's weight dict). B sequences share one cache offset per call.
+    """
+
+    def __init__(self, cfg: dict, w: dict, batch: int):
+        self.cfg, self.w, self.B = cfg, w, batch
+        c = cfg
+        self.cs = rope_table(c["max_seq"], c["head_dim"], c["theta"])
+        shape = (c["layers"], batch, c["kv_heads"], c["max_seq"], c["head_dim"])
+        self.kc = np.zeros(shape, np.uint16)
+        self.vc = np.zeros(shape, np.uint16)
+        self.scale = float(np.float32(1.0 / np.sqrt(c["head_dim"])))
+
+    def _router_margin(self, mw, x):
+        """Per token, the relative gap between the k-th and the (k+1)-th
+        largest router probability: where it is small, inputs that differ in
+        the last bits can select another expert."""
+        m = self.cfg["moe"]
+        k, E = m["top_k"], m["n_experts"]
+        if k >= E:
+            return np.full(x.shape[0], np.inf)
+        _, probs, _, _ = router_topk(x, mw["router_w"], k, m.get("norm_topk", False), mw.get("router_bias"))
+        p = -np.sort(-bf16_to_f32(probs).astype(np.float64), axis=1)
+        return (p[:, k - 1] - p[:, k]) / np.maximum(p[:, k - 1], 1e-300)
+
+    def forward(self, ids, offset: int, last_only: bool = True, mode=ACC_A, return_hidden=False,
+                routing=None):
+        """ids [B, L] at cache positions offset.. -> logits [B, V] (last_only)
+        or [B * L, V]; with return_hidden also the residual stream after the
+        last layer [B * L, H]. self.last_margins [layers, B * L]: each
+        token's router margin (_router_margin) in each layer; last_probs /
+        last_inds: each layer's router probabilities and expert choice.
+        routing (a list of [B * L, k] per layer): use that expert choice in
+        each layer's MoE block (moe_block(inds=...))."""
+        c, w = self.cfg, self.w
+        ids = np.asarray(ids, dtype=np.int64)
+        B, L = ids.shape
+        H, nh, nkv, hd = c["hidden"], c["heads"], c["kv_heads"], c["head_dim"]
+        h = np.ascontiguousarray(w["embed"][ids.reshape(-1)])
+        pos = np.tile(np.arange(offset, offset + L, dtype=np.int64), B)
+        margins = []
+        self.last_probs, self.last_inds = [], []
+        for li, lw in enumerate(w["layers"]):
+            n = rms_norm(h, lw["in_w"], c["eps"])
+            qkv = qmm_t(n, *lw["qkv"], mode=mode)
+            if lw.get("qkv_bias") is not None:
+                qkv = bf16_add(qkv, lw["qkv_bias"][None, :])
+            q = qkv[:, :nh * hd].reshape(B * L, nh, hd)
+            k = qkv[:, nh * hd:(nh + nkv) * hd].reshape(B * L, nkv, hd)
+            v = qkv[:, (nh + nkv) * hd:].reshape(B * L, nkv, hd)
+            q, k = rope(q, pos, self.cs), rope(k, pos, self.cs)
+            att = np.empty((B * L, nh, hd), np.uint16)
+            for b in range(B):
+                rows = slice(b * L, (b + 1) * L)
+                self.kc[li, b, :, offset:offset + L] = k[rows].transpose(1, 0, 2)
+                self.vc[li, b, :, offset:offset + L] = v[rows].transpose(1, 0, 2)
+                att[rows] = sdpa(q[rows], self.kc[li, b], self.vc[li, b], offset, self.scale)
+            o = qmm_t(att.reshape(B * L, nh * hd), *lw["o"], mode=mode)
+            h = bf16_add(h, o)
+            n2 = rms_norm(h, lw["post_w"], c["eps"])
+            y, inds, _ = moe_block(c["moe"], lw["moe"], n2, mode,
+                                   inds=None if routing is None else routing[li])
+            margins.append(self._router_margin(lw["moe"], n2))
+            self.last_probs.append(router_topk(n2, lw["moe"]["router_w"], c["moe"]["top_k"],
+                                               c["moe"].get("norm_topk", False),
+                                               lw["moe"].get("router_bias"))[1])
+            self.last_inds.append(inds)
+            h = bf16_add(h, y)
+        self.last_margins = np.stack(margins)
+        hid = h
+        if last_only:
+            h = np.ascontiguousarray(h.reshape(B, L, H)[:, -1])
+        n = rms_norm(h, w["norm_w"], c["eps"])
+        logits = qmm_t(n, *w["lm_head"], mode=mode)
+        return (logits, hid) if return_hidden else logits

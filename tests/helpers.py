@@ -66,3 +66,24 @@ def oracle_args(hi, model, quant, router_quant=False):
         w.update(shared_gate=quant(hi.shared_gate), shared_up=quant(hi.shared_up),
                  shared_down=quant(hi.shared_down), shared_expert_gate_w=rq(hi.shared_expert_gate_w))
     return cfg, w
+
+
+def assert_close_rows(got_u16, ref_u16, what="", rtol=RTOL, atol=ATOL, rel_l2=REL_L2_MAX):
+    """assert_close for rows of the decoder stack's residual stream and
+    logits: a value there is a chain of bf16-rounded sums (x + attn, + moe)
+    whose addends can exceed the result, so an element's rounding error is
+    bounded by the ulps of the row's large values, not of the element. The
+    absolute tolerance of each row is max(atol, 2^-6 * max |row|) (two bf16
+    ulps of the row's largest element); rtol and the relative L2 bound as in
+    assert_close."""
+    g = bf16_to_f32(got_u16).astype(np.float64)
+    r = bf16_to_f32(ref_u16).astype(np.float64)
+    assert g.shape == r.shape, (what, g.shape, r.shape)
+    assert np.isfinite(g).all(), f"{what}: non-finite output"
+    r2 = r.reshape(-1, r.shape[-1])
+    row_atol = np.maximum(atol, 2.0 ** -6 * np.abs(r2).max(axis=1, keepdims=True))
+    bad = np.abs(g.reshape(r2.shape) - r2) > row_atol + rtol * np.abs(r2)
+    e = errors(got_u16, ref_u16)
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements outside the row tolerance; {e}"
+    assert e["rel_l2"] <= rel_l2, f"{what}: relative L2 error {e['rel_l2']:.3g} > {rel_l2}; {e}"
+    return e

@@ -1,5 +1,5 @@
 """The C-ABI library without a GPU: it loads, exports every entry point that
-include/fmx.h declares, and its host-side logic (size queries, argument
+include/*.h declares, and its host-side logic (size queries, argument
 validation, status strings, the seeded generator) behaves. No call here
 launches a kernel."""
 from __future__ import annotations
@@ -15,9 +15,11 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 
 
 def header_functions() -> list[str]:
-    text = (ROOT / "include" / "fmx.h").read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(fmx_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(fmx_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol(fmx):
@@ -249,3 +251,36 @@ def test_sort_limits(fmx):
     assert lib.fmx_moe_sort(k, (1 << 22) // 8 + 1, 8, 128, None, None, None, None, None, None, 0,
                             None) == _lib.FMX_ERR_UNSUPPORTED
     assert b"limits" in lib.fmx_last_error()
+
+
+def test_model_sizes_and_validation(fmx):
+    """Decoder-stack entry points without a GPU: size queries for the
+    Qwen1.5-MoE-A2.7B shape, packed sizes equal to MLX's 0.5625 bytes per
+    weight, out-of-scope configs refused, and a forward with missing weights
+    refused before any launch."""
+    from flashmlx_amd import _lib
+    from flashmlx_amd.model import ModelConfig
+    lib = _lib.load()
+    cfg = ModelConfig(max_position_embeddings=512)
+    c = cfg.to_c()
+    s1 = lib.fmx_model_workspace_size(C.byref(c), 1)
+    s2 = lib.fmx_model_workspace_size(C.byref(c), 1028)
+    assert 0 < s1 < s2
+    assert lib.fmx_model_kv_cache_size(C.byref(c), 4, 384) == 24 * 2 * 4 * 16 * 384 * 128 * 2
+    assert lib.fmx_packed_linear_size(6144, 2048) == 6144 * 2048 * 9 // 16
+    assert lib.fmx_packed_linear_size(6144, 2000) == 0
+    for bad in (ModelConfig(vocab_size=100), ModelConfig(num_key_value_heads=3),
+                ModelConfig(max_position_embeddings=8192), ModelConfig(head_dim=100)):
+        assert lib.fmx_model_workspace_size(C.byref(bad.to_c()), 1) == 0
+    rc = lib.fmx_model_forward(C.byref(c), None, None, 1, 1, 0, None, None, 1, 1, 1, None, None, 0, None)
+    assert rc == _lib.FMX_ERR_ARG
+    w = _lib.FmxModelWeights()
+    w.embed = w.norm_w = w.lm_head = 16
+    w.layers = (_lib.FmxLayerWeights * 1)()
+    # zero tokens: nothing runs
+    assert lib.fmx_model_forward(C.byref(c), C.byref(w), None, 0, 5, 0, None, None, 1, 1, 1, None,
+                                 None, 0, None) == _lib.FMX_OK
+    # positions past the cache are refused on the host
+    rc = lib.fmx_model_forward(C.byref(c), C.byref(w), 16, 1, 4, 380, None, 256, 1, 382, 1, 256,
+                               256, 1 << 30, None)
+    assert rc == _lib.FMX_ERR_SHAPE, lib.fmx_last_error()
