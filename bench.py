@@ -368,6 +368,154 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
     return res, y_host, inds
 
 
+# The 24-layer Qwen1.5-MoE-A2.7B-shape decoder stack (random-init 4-bit
+# weights, seed 5): a 256-token prompt, then 128 greedy tokens, at batch 1 and 4
+STACK_CONFIGS = {"c4_stack_b1": 1, "c4_stack_b4": 4}
+STACK_PROMPT, STACK_NEW, STACK_SEED = 256, 128, 5
+
+
+def stack_step_bytes(cfg, B: int, pos: int, unique_per_layer) -> int:
+    """Algorithmic HBM bytes of one decode step of the stack: every layer's
+    attention weights and its routed (unique) and shared experts' weights at
+    0.5625 B per weight, router and norms, the KV cache read up to pos and
+    written at pos, the lm_head, embedding rows and logits."""
+    H, V, hd = cfg.hidden_size, cfg.vocab_size, cfg.hd
+    nh, nkv = cfg.num_attention_heads, cfg.num_key_value_heads
+    m = cfg.moe
+    q = lambda n, k: n * k * 9 // 16  # noqa: E731
+    exp = 3 * q(m.moe_intermediate_size, H)
+    shared = 3 * q(m.shared_expert_intermediate_size, H) + H * 2 if m.shared_expert_intermediate_size else 0
+    attn = q(cfg.n_qkv, H) + cfg.n_qkv * 2 + q(H, nh * hd)
+    kv = B * 2 * nkv * hd * 2 * (pos + 2)
+    layer = [attn + U * exp + shared + m.num_experts * H * 2 + 2 * H * 2 + kv for U in unique_per_layer]
+    return int(sum(layer) + q(V, H) + B * H * 2 + B * V * 2 + H * 2)
+
+
+def measure_stack(batches, trials: int, cpu_seconds: float):
+    """Prefill of a 256-token prompt and 128 greedy tokens per sequence on
+    the 24-layer stack, each as captured HIP graphs (one graph for the
+    prefill and the first token, one for a decode step that reads the device
+    cache offsets and advances them): the median of `trials` runs."""
+    import numpy as np
+    import torch
+
+    from flashmlx_amd import model as M
+
+    cfg = M.ModelConfig(max_position_embeddings=512)
+    V = cfg.vocab_size
+    t0 = time.perf_counter()
+    w = M.synthetic_model(cfg, STACK_SEED, keep_mlx=cpu_seconds > 0)
+    log(f"stack: 24-layer weights built in {time.perf_counter() - t0:.1f}s")
+    rng = np.random.default_rng(STACK_SEED)
+    res = {}
+    for B in batches:
+        max_seq = STACK_PROMPT + STACK_NEW
+        dm = M.DecoderModel(cfg, w, B, max_seq, B * STACK_PROMPT)
+        prompt = torch.from_numpy(rng.integers(0, V, (B, STACK_PROMPT)).astype(np.int32)).cuda()
+        logits = torch.empty((B, V), dtype=torch.bfloat16, device="cuda")
+        tok = torch.empty((B, 1), dtype=torch.int32, device="cuda")
+        offs = torch.full((B,), STACK_PROMPT, dtype=torch.int32, device="cuda")
+        # eager reference generation and the routing of one decode step
+        ref = dm.generate(prompt, STACK_NEW)
+        rt = dm.routing_buffer(B)
+        dm.forward(ref[:, :1].contiguous(), STACK_PROMPT, routing=rt)
+        uniq = [int(np.unique(r.numpy()).size) for r in rt.cpu()]
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+
+        def prefill():
+            dm.forward_into(prompt, 0, logits)
+            dm.greedy(logits, tok.view(-1))
+
+        def step():
+            dm.forward_into(tok, offs, logits)
+            dm.greedy(logits, tok.view(-1), offs, 1)
+
+        with torch.cuda.stream(stream):
+            prefill()
+            step()
+        torch.cuda.synchronize()
+        gp, gs = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gp, stream=stream):
+            prefill()
+        with torch.cuda.graph(gs, stream=stream):
+            step()
+        pre, dec, last_ok = [], [], True
+        for _ in range(trials + 1):
+            offs.fill_(STACK_PROMPT)
+            torch.cuda.synchronize()
+            e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+            e0.record(stream)
+            with torch.cuda.stream(stream):
+                gp.replay()
+                e1.record(stream)
+                for _ in range(STACK_NEW - 1):
+                    gs.replay()
+                e2.record(stream)
+            torch.cuda.synchronize()
+            pre.append(e0.elapsed_time(e1))
+            dec.append(e1.elapsed_time(e2))
+            last_ok &= bool(torch.equal(tok.view(-1), ref[:, -1]))
+        pre, dec = pre[1:], dec[1:]  # the first run warms the graphs
+        pm, dmed = statistics.median(pre), statistics.median(dec)
+        step_ms = dmed / (STACK_NEW - 1)
+        pos = STACK_PROMPT + STACK_NEW // 2
+        sb = stack_step_bytes(cfg, B, pos, uniq)
+        res[f"c4_stack_b{B}"] = {
+            "workload": (f"24-layer Qwen1.5-MoE-A2.7B-shape decoder stack, batch {B}: {STACK_PROMPT}-token "
+                         f"prompt, {STACK_NEW} greedy tokens, seed {STACK_SEED}"),
+            "value": round(B * (STACK_NEW - 1) / (dmed / 1e3), 1),
+            "unit": "tok/s (decode)",
+            "e2e_tok_s": round(B * STACK_NEW / ((pm + dmed) / 1e3), 1),
+            "prefill_ms": round(pm, 3),
+            "prefill_tok_s": round(B * STACK_PROMPT / (pm / 1e3), 1),
+            "decode_ms_per_step": round(step_ms, 4),
+            "trials": trials,
+            "graph_tokens_equal_eager": last_ok,
+            "roofline": {"bound": "hbm", "achieved": round(sb / (step_ms * 1e-3) / 1e9, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(sb / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "algorithmic_per_step": sb,
+                         "note": f"unique experts per layer from the step at position {STACK_PROMPT}: "
+                                 f"mean {np.mean(uniq):.1f}"},
+        }
+        log(f"stack B={B}: prefill {pm:.2f} ms, decode {step_ms * 1e3:.1f} us/step")
+        del dm, gp, gs
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    if cpu_seconds > 0:
+        res["c4_stack_b1"]["cpu_baseline"] = stack_cpu_baseline(cfg, w, cpu_seconds)
+    return res
+
+
+def stack_cpu_baseline(cfg, w, seconds: float):
+    """The oracle's DecoderStack (24 layers, fp32 accumulation) on this host:
+    decode steps at batch 1 after an 8-token prompt, for about `seconds`."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+
+    from flashmlx_amd import model as M
+    from oracle import oracle as O
+
+    O.build()
+    hw = M.host_weights(cfg, w)
+    nproc = host_threads()
+    O.set_threads(nproc)
+    st = O.DecoderStack(M.oracle_config(cfg, 64), hw, 1)
+    ids = np.random.default_rng(STACK_SEED).integers(0, cfg.vocab_size, (1, 8))
+    lg = st.forward(ids, 0)
+    n, t0, pos = 0, time.perf_counter(), 8
+    while time.perf_counter() - t0 < seconds and pos < 64:
+        nxt = np.array([[int(np.argmax(O.bf16_to_f32(lg[0])))]])
+        lg = st.forward(nxt, pos)
+        pos += 1
+        n += 1
+    el = time.perf_counter() - t0
+    return {"value": round(n / el, 3), "unit": "tok/s (decode, batch 1)", "cores": nproc, "kind": "port",
+            "sample": f"oracle DecoderStack, 24 layers: {n} decode steps in {el:.1f}s after an 8-token "
+                      f"prompt, on {cpu_model()}, {nproc} OpenMP threads"}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,6 +532,10 @@ def main():
     ap.add_argument("--no-pack", action="store_true",
                     help="MLX-layout weights only (no fmx_pack_expert_weights re-layout)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
+    ap.add_argument("--stack", default="all",
+                    help="decoder-stack configs measured in the same run: all, none or a comma list "
+                         "(c4_stack_b1, c4_stack_b4)")
+    ap.add_argument("--stack-trials", type=int, default=5)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -421,6 +573,13 @@ def main():
         steps = K if c.tokens <= 16 else max(R, K // 10)
         warm = Wm if c.tokens <= 16 else max(R, Wm // 10)
         configs[key], _, _ = measure(c, R, steps, warm, args.trials, args.profile_steps, pack)
+
+    skeys = list(STACK_CONFIGS) if args.stack == "all" else (
+        [] if args.stack == "none" else [k for k in args.stack.split(",") if k])
+    if skeys:
+        stack = measure_stack([STACK_CONFIGS[k] for k in skeys], args.stack_trials,
+                              0.0 if args.no_cpu_baseline else args.cpu_seconds)
+        configs.update(stack)
 
     cpu, parity = None, None
     if not args.no_cpu_baseline:

@@ -354,9 +354,12 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
     ra.q_out = M.qrot;
     ra.kc = kc;
     ra.vc = vc;
-    FMX_HIP(launch_rope_cache(ra, static_cast<int>(T), stream));
+    // single-token forwards rotate and cache inside the attention kernel
+    if (Lq > 1) FMX_HIP(launch_rope_cache(ra, static_cast<int>(T), stream));
     AttnArgs aa{};
     aa.q = M.qrot;
+    aa.qkv = Lq == 1 ? M.qkv : nullptr;
+    aa.cs = M.rope;
     aa.L = ra.L;
     aa.nh = ra.nh;
     aa.nkv = ra.nkv;

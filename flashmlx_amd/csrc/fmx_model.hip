@@ -201,68 +201,196 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
 // ------------------------------------------------------------------ attention
 
 // One workgroup of kAttnThreads per (token t = b * L + l, q head h): keys
-// 0 .. p of kv head h / (nh / nkv), p = offset(b) + l (causal).
+// 0 .. p of kv head g = h / (nh / nkv), p = offset(b) + l (causal).
 //   s_j = scale * sum_d q_d k_jd   (fp32, d in order: exact bf16 products)
 //   e_j = exp(s_j - max s)         (fp64, the deterministic exp)
-//   out_d = sum_j e_j v_jd / sum_j e_j   (fp64, keys in order), bf16
-// (mx::fast::scaled_dot_product_attention, model.cpp:879-882). Thread d
-// forms out_d; every thread forms the same denominator in the same order.
-constexpr int kAttnThreads = 128;
+//   out_d = sum_j e_j v_jd / sum_j e_j, both sums in fp64 over four
+//           contiguous quarters of the keys (keys in order within a quarter,
+//           fma), the quarter sums added in order; rounded once to bf16
+// (mx::fast::scaled_dot_product_attention, model.cpp:879-882). Scores: a
+// thread per key; the weighted sum: wave w takes quarter w, its lanes pairs
+// of dimensions.
+// ROPE (single-token forwards): the workgroup also rotates its q head and
+// its kv head's new key from the q/k/v row itself (as rope_cache_kernel
+// does), uses the new key and value for position p from LDS, and the first q
+// head of each kv group writes them into the caches; no other workgroup
+// reads position p in this launch.
+constexpr int kAttnThreads = 256;
+constexpr int kAttnWaves = kAttnThreads / kWave;
+constexpr int kAttnBatch = 32;  // keys whose value words are loaded together
 
+template <bool ROPE, int PAIRS>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t s_at[];
   __shared__ float s_q[kAttnMaxHd];
-  __shared__ float s_max[kAttnThreads / kWave];
+  __shared__ uint16_t s_knew[kAttnMaxHd], s_vnew[kAttnMaxHd];
+  __shared__ float s_max[kAttnWaves];
+  __shared__ double s_num[kAttnWaves][kAttnMaxHd];
+  __shared__ double s_den[kAttnWaves];
   double* s_e = reinterpret_cast<double*>(s_at);
   float* s_s = reinterpret_cast<float*>(s_at + static_cast<size_t>(a.max_seq) * 8);
   const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int b = t / a.L, l = t - b * a.L;
   const int p = token_pos(a.offs, a.off, b, l, a.max_seq);
   const int nk = p + 1;
-  const int g = h / (a.nh / a.nkv);
-  const uint16_t* qrow = a.q + (static_cast<int64_t>(t) * a.nh + h) * a.hd;
+  const int rep = a.nh / a.nkv, g = h / rep;
   const int64_t cbase = (static_cast<int64_t>(b) * a.nkv + g) * a.max_seq * a.hd;
-  const uint16_t* kb = a.kc + cbase;
-  const uint16_t* vb = a.vc + cbase;
-  for (int d = tid; d < a.hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qrow[d]);
-  __syncthreads();
-
-  float m = -__builtin_huge_valf();
-  for (int jk = tid; jk < nk; jk += kAttnThreads) {
-    const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(jk) * a.hd);
-    float acc = 0.0f;
-    for (int c = 0; c < a.hd / 8; ++c) {
-      const u32x4_t kv = kr[c];
-#pragma unroll
-      for (int mm = 0; mm < 4; ++mm) {
-        acc = __builtin_fmaf(s_q[8 * c + 2 * mm], bf16_to_f32(kv[mm] & 0xffffu), acc);
-        acc = __builtin_fmaf(s_q[8 * c + 2 * mm + 1], bf16_to_f32(kv[mm] >> 16), acc);
+  uint16_t* kb = a.kc + cbase;
+  uint16_t* vb = a.vc + cbase;
+  if (ROPE) {
+    const int half = a.hd / 2;
+    const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
+    const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
+    for (int i = tid; i < 2 * half; i += kAttnThreads) {
+      const int hd_i = i % half;
+      const uint16_t* src = row + (i < half ? h : a.nh + g) * a.hd;
+      const double x1 = bf16_to_f32(src[hd_i]), x2 = bf16_to_f32(src[hd_i + half]);
+      const double c = cs[2 * hd_i], sn = cs[2 * hd_i + 1];
+      const uint16_t o1 = f64_to_bf16(__builtin_fma(x1, c, -(x2 * sn)));
+      const uint16_t o2 = f64_to_bf16(__builtin_fma(x1, sn, x2 * c));
+      if (i < half) {
+        s_q[hd_i] = bf16_to_f32(o1);
+        s_q[hd_i + half] = bf16_to_f32(o2);
+      } else {
+        s_knew[hd_i] = o1;
+        s_knew[hd_i + half] = o2;
       }
     }
-    const float s = acc * a.scale;
-    s_s[jk] = s;
-    m = fmaxf(m, s);
+    for (int d = tid; d < a.hd; d += kAttnThreads) s_vnew[d] = row[(a.nh + a.nkv + g) * a.hd + d];
+    __syncthreads();
+    if (h % rep == 0)
+      for (int d = tid; d < a.hd; d += kAttnThreads) {
+        kb[static_cast<int64_t>(p) * a.hd + d] = s_knew[d];
+        vb[static_cast<int64_t>(p) * a.hd + d] = s_vnew[d];
+      }
+  } else {
+    const uint16_t* qrow = a.q + (static_cast<int64_t>(t) * a.nh + h) * a.hd;
+    for (int d = tid; d < a.hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qrow[d]);
+    __syncthreads();
+  }
+
+  // this wave's quarter of the keys for the weighted sum below; its first
+  // kAttnBatch value words are loaded now, so that their latency overlaps
+  // the scores
+  const int quarter = (nk + kAttnWaves - 1) / kAttnWaves;
+  const int j0 = min(wave * quarter, nk), j1 = min(j0 + quarter, nk);
+  const int npair = a.hd / 2;
+  // keys before jg come from the cache; with ROPE the last key (p) comes
+  // from LDS, after them (it is the last key of the last non-empty quarter)
+  const int jg = ROPE ? min(j1, p) : j1;
+  // lanes past the head's pairs read pair 0 (in bounds) and discard it
+  uint32_t vv[kAttnBatch][PAIRS];
+  int prl[PAIRS];
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) prl[i] = (lane + kWave * i) < npair ? lane + kWave * i : 0;
+  auto load_values = [&](int jb) {
+#pragma unroll
+    for (int u = 0; u < kAttnBatch; ++u) {
+      const uint32_t* vr = reinterpret_cast<const uint32_t*>(vb + static_cast<int64_t>(min(jb + u, jg - 1)) * a.hd);
+#pragma unroll
+      for (int i = 0; i < PAIRS; ++i) vv[u][i] = vr[prl[i]];
+    }
+  };
+  if (j0 < jg) load_values(j0);
+
+  // scores, a thread per key
+  float m = -__builtin_huge_valf();
+  const int nkg = ROPE ? p : nk;  // keys read from the cache
+  for (int jk = tid; jk < nkg; jk += kAttnThreads) {
+    // the key row's chunks are loaded 16 at a time, then used in order
+    float acc = 0.0f;
+    const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(jk) * a.hd);
+    const int nch = a.hd / 8;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      u32x4_t kv[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) kv[c] = kr[min(c0 + c, nch - 1)];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        if (c0 + c < nch) {
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) {
+            acc = __builtin_fmaf(s_q[8 * (c0 + c) + 2 * mm], bf16_to_f32(kv[c][mm] & 0xffffu), acc);
+            acc = __builtin_fmaf(s_q[8 * (c0 + c) + 2 * mm + 1], bf16_to_f32(kv[c][mm] >> 16), acc);
+          }
+        }
+      }
+    }
+    const float sc = acc * a.scale;
+    s_s[jk] = sc;
+    m = fmaxf(m, sc);
+  }
+  if (ROPE && tid == kAttnThreads - 1) {  // the new key, from LDS
+    float acc = 0.0f;
+    for (int d = 0; d < a.hd; ++d) acc = __builtin_fmaf(s_q[d], bf16_to_f32(s_knew[d]), acc);
+    const float sc = acc * a.scale;
+    s_s[p] = sc;
+    m = fmaxf(m, sc);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if ((tid & 63) == 0) s_max[tid >> 6] = m;
+  if (lane == 0) s_max[wave] = m;
   __syncthreads();
   m = s_max[0];
 #pragma unroll
-  for (int w = 1; w < kAttnThreads / kWave; ++w) m = fmaxf(m, s_max[w]);
+  for (int w = 1; w < kAttnWaves; ++w) m = fmaxf(m, s_max[w]);
   for (int jk = tid; jk < nk; jk += kAttnThreads)
     s_e[jk] = exp_det(static_cast<double>(s_s[jk]) - static_cast<double>(m));
   __syncthreads();
 
+  // weighted sum: wave w over keys [j0, j1), lane over dimension pairs
+  // (2 pr, 2 pr + 1), pr = lane + 64 i; the value words of kAttnBatch keys
+  // are loaded together, then used in key order
+  double num[PAIRS][2], den = 0.0;
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) num[i][0] = num[i][1] = 0.0;
+  for (int jb = j0; jb < jg; jb += kAttnBatch) {
+    if (jb != j0) load_values(jb);
+#pragma unroll
+    for (int u = 0; u < kAttnBatch; ++u) {
+      if (jb + u < jg) {
+        const double e = s_e[jb + u];
+        den += e;
+#pragma unroll
+        for (int i = 0; i < PAIRS; ++i) {
+          num[i][0] = __builtin_fma(e, static_cast<double>(bf16_to_f32(vv[u][i] & 0xffffu)), num[i][0]);
+          num[i][1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(vv[u][i] >> 16)), num[i][1]);
+        }
+      }
+    }
+  }
+  if (ROPE && jg < j1) {  // the new key's value (position p), last in key order
+    const double e = s_e[p];
+    den += e;
+    const uint32_t* vr = reinterpret_cast<const uint32_t*>(s_vnew);
+#pragma unroll
+    for (int i = 0; i < PAIRS; ++i) {
+      const uint32_t w2 = vr[prl[i]];
+      num[i][0] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w2 & 0xffffu)), num[i][0]);
+      num[i][1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w2 >> 16)), num[i][1]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PAIRS; ++i) {
+    const int pr = lane + kWave * i;
+    if (pr < npair) {
+      s_num[wave][2 * pr] = num[i][0];
+      s_num[wave][2 * pr + 1] = num[i][1];
+    }
+  }
+  if (lane == 0) s_den[wave] = den;
+  __syncthreads();
+
   bool ovf = false;
   for (int d = tid; d < a.hd; d += kAttnThreads) {
-    double num = 0.0, den = 0.0;
-    for (int jk = 0; jk < nk; ++jk) {
-      const double e = s_e[jk];
-      den += e;
-      num = __builtin_fma(e, static_cast<double>(bf16_to_f32(vb[static_cast<int64_t>(jk) * a.hd + d])), num);
+    double nsum = s_num[0][d], dsum = s_den[0];
+#pragma unroll
+    for (int w = 1; w < kAttnWaves; ++w) {
+      nsum += s_num[w][d];
+      dsum += s_den[w];
     }
-    const uint16_t o = f64_to_bf16(num / den);
+    const uint16_t o = f64_to_bf16(nsum / dsum);
     const int64_t oc = static_cast<int64_t>(h) * a.hd + d;
     a.out[static_cast<int64_t>(t) * a.ldo + oc] = o;
     if (a.outh) {
@@ -271,7 +399,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
           static_cast<uint16_t>(bf16_to_f16_bits(o));
     }
   }
-  if (a.outh && __ballot(ovf) && (tid & 63) == 0) atomicOr(a.flag, 1u);
+  if (a.outh && __ballot(ovf) && lane == 0) atomicOr(a.flag, 1u);
 }
 
 // ------------------------------------------------------------------ greedy
@@ -285,11 +413,38 @@ __global__ __launch_bounds__(1024) void greedy_kernel(GreedyArgs a) {
   const uint16_t* row = a.logits + static_cast<int64_t>(b) * a.ld;
   float best = -__builtin_huge_valf();
   int64_t bi = a.V;
-  for (int64_t v = tid; v < a.V; v += blockDim.x) {
-    const float x = bf16_to_f32(row[v]);
-    if (x > best || (x == best && v < bi)) {  // NaN never wins
-      best = x;
-      bi = v;
+  // a thread takes 16-byte chunks c = tid, tid + 1024, ... (index order, so
+  // the first maximum it sees is its lowest), loads of 4 chunks in flight;
+  // rows that are not 16-byte aligned or a multiple of 8 take the scalar loop
+  const bool vec = (a.ld % 8 == 0) && (a.V % 8 == 0) && (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0);
+  if (vec) {
+    const u32x4_t* rv = reinterpret_cast<const u32x4_t*>(row);
+    const int64_t nch = a.V / 8;
+    for (int64_t c0 = tid; c0 < nch; c0 += 4 * 1024) {
+      u32x4_t ch[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ch[u] = rv[min(c0 + 1024 * u, nch - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t c = c0 + 1024 * u;
+        if (c >= nch) break;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = bf16_to_f32((ch[u][e >> 1] >> (16 * (e & 1))) & 0xffffu);
+          if (x > best) {  // strict: within a thread indices ascend; NaN never wins
+            best = x;
+            bi = 8 * c + e;
+          }
+        }
+      }
+    }
+  } else {
+    for (int64_t v = tid; v < a.V; v += blockDim.x) {
+      const float x = bf16_to_f32(row[v]);
+      if (x > best) {
+        best = x;
+        bi = v;
+      }
     }
   }
 #pragma unroll
@@ -362,7 +517,19 @@ size_t attn_lds_bytes(int64_t max_seq) { return static_cast<size_t>(max_seq) * 1
 
 hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream) {
   if (T == 0) return hipSuccess;
-  hipLaunchKernelGGL(attn_kernel, dim3(T, a.nh), dim3(kAttnThreads), attn_lds_bytes(a.max_seq), stream, a);
+  const dim3 grid(T, a.nh);
+  const size_t lds = attn_lds_bytes(a.max_seq);
+  if (a.hd <= 128) {
+    if (a.qkv)
+      hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kAttnThreads), lds, stream, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kAttnThreads), lds, stream, a);
+  } else {
+    if (a.qkv)
+      hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(kAttnThreads), lds, stream, a);
+    else
+      hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(kAttnThreads), lds, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -66,10 +66,13 @@ hipError_t launch_rope_cache(const RopeArgs& a, int T, hipStream_t stream);
 constexpr int kAttnMaxHd = 256;
 constexpr int64_t kAttnMaxSeq = 4096;  // keys per query: 48 KB of LDS scores
 struct AttnArgs {
-  const uint16_t* q;      // [T, nh * hd] rotated
+  const uint16_t* q;      // [T, nh * hd] rotated (when qkv is null)
+  const uint16_t* qkv;    // or: the q/k/v rows of a single-token-per-sequence forward
+                          //   (L == 1), rotated and cached by the attention kernel itself
+  const float* cs;        //   with this RoPE table
   int L, nh, nkv, hd;
-  const uint16_t* kc;     // [B_cache][nkv][max_seq][hd]
-  const uint16_t* vc;
+  uint16_t* kc;           // [B_cache][nkv][max_seq][hd]
+  uint16_t* vc;
   int64_t max_seq;
   const int32_t* offs;
   int off;

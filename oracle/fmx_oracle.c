@@ -639,8 +639,9 @@ int orc_rope(uint16_t* x, int64_t T, int64_t n_heads, int64_t hd, const int64_t*
  * key). q head h reads kv head h / (nh / nkv). Scores are fp32 dot products
  * (exact bf16 products, summed over d in order) times scale; the softmax is
  * formed in fp64 with the deterministic exp (e_j = exp(s_j - max)), the
- * output as sum_j e_j v_j / sum_j e_j in fp64 (keys in order, fma), rounded
- * once to bf16: out [L, nh, hd]. */
+ * output as sum_j e_j v_j / sum_j e_j in fp64, each sum over four contiguous
+ * quarters of the keys (in order within a quarter, fma), the quarter sums
+ * added in order, rounded once to bf16: out [L, nh, hd]. */
 int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
              const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
              uint16_t* out) {
@@ -662,14 +663,25 @@ int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_
         s[j] = acc * scale;
         if (s[j] > m) m = s[j];
       }
-      double den = 0.0;
-      for (int64_t j = 0; j < nk; ++j) {
-        e[j] = orc_exp((double)s[j] - (double)m);
-        den += e[j];
+      for (int64_t j = 0; j < nk; ++j) e[j] = orc_exp((double)s[j] - (double)m);
+      /* four contiguous quarters of the keys, each summed in order, the
+       * quarter sums added in order */
+      const int64_t qn = (nk + 3) / 4;
+      double den = 0.0, dq[4];
+      for (int qi = 0; qi < 4; ++qi) {
+        const int64_t j0 = qi * qn < nk ? qi * qn : nk, j1 = j0 + qn < nk ? j0 + qn : nk;
+        dq[qi] = 0.0;
+        for (int64_t j = j0; j < j1; ++j) dq[qi] += e[j];
+        den = qi ? den + dq[qi] : dq[qi];
       }
       for (int64_t d = 0; d < hd; ++d) {
         double num = 0.0;
-        for (int64_t j = 0; j < nk; ++j) num = fma(e[j], (double)bf(vb[j * hd + d]), num);
+        for (int qi = 0; qi < 4; ++qi) {
+          const int64_t j0 = qi * qn < nk ? qi * qn : nk, j1 = j0 + qn < nk ? j0 + qn : nk;
+          double part = 0.0;
+          for (int64_t j = j0; j < j1; ++j) part = fma(e[j], (double)bf(vb[j * hd + d]), part);
+          num = qi ? num + part : part;
+        }
         out[(l * nh + h) * hd + d] = orc_f64_to_bf16(num / den);
       }
       free(s);

@@ -234,3 +234,32 @@ def test_stack_qwen15_24_layers(gpu, fmx, oracle):
         print(f"24 layers B={B}: decode vs prefill {e}")
         del dm, dm2
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("V", [151936, 1001])
+def test_greedy_next(gpu, fmx, V):
+    """fmx_greedy_next: the first of equal maxima (mx::argmax), NaN never
+    chosen, an all-equal row gives 0, on the 16-byte path (V a multiple of 8)
+    and the scalar one; the offsets advance."""
+    import torch
+    from flashmlx_amd import _lib
+    rng = np.random.default_rng(V)
+    B = 5
+    x = torch.from_numpy(rng.standard_normal((B, V)).astype(np.float32)).to(torch.bfloat16)
+    x[1, 77] = 9.0
+    x[1, V - 5] = 9.0
+    x[2, :] = 1.0
+    x[3, 10] = float("nan")
+    x[3, 11] = 20.0
+    x[4, V - 1] = 30.0
+    ids = torch.empty(B, dtype=torch.int32, device="cuda")
+    offs = torch.arange(B, dtype=torch.int32, device="cuda")
+    xd = x.cuda()
+    lib = _lib.load()
+    _lib.check(lib.fmx_greedy_next(xd.data_ptr(), B, V, V, ids.data_ptr(), offs.data_ptr(), 3,
+                                   torch.cuda.current_stream().cuda_stream))
+    got = ids.cpu().numpy()
+    ref = x.float().numpy()
+    assert got[0] == int(np.argmax(ref[0]))
+    assert got[1] == 77 and got[2] == 0 and got[3] == 11 and got[4] == V - 1
+    assert offs.cpu().tolist() == [3, 4, 5, 6, 7]
