@@ -5,6 +5,10 @@
   python -m flashmlx_amd.profiling traffic --fetch <csv> --write <csv>
          --copy-fetch <csv> --copy-write <csv> --copy-bytes N --workload KEY
       -> JSON of HBM bytes per launch of each MoE stage's kernel
+  python -m flashmlx_amd.profiling eager KEY [--forwards N]
+      -> N eager (not graph-captured) forwards of a workload's MoE block on
+         packed weights, the program that counter passes (rocprofv3 --pmc)
+         run under
 
 FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are scaled by what the same
 counter reads for a plain device copy of known size (the factor that makes
@@ -94,6 +98,20 @@ def traffic(fetch: str, write: str, copy_fetch: str, copy_write: str, copy_bytes
             "write_scale": round(fw, 4), "stages": stages, "kernels": kernels, "commands": cmds}
 
 
+def eager(key: str, n: int) -> None:
+    import torch
+
+    from . import workloads as W
+
+    wl = W.WORKLOADS[key]
+    block, x = W.device_block(wl, W.DeviceSynth(wl), pack=True, drop_mlx=True)
+    y = torch.empty_like(x)
+    for _ in range(n):
+        block.forward_into(x, y)
+    torch.cuda.synchronize()
+    print(f"{n} eager forwards of {key}", flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="what", required=True)
@@ -106,8 +124,13 @@ def main(argv=None):
     c.add_argument("--copy-bytes", type=int, required=True)
     c.add_argument("--workload", required=True)
     c.add_argument("--cmd", action="append", default=[], help="name=command of a pass")
+    e = sub.add_parser("eager")
+    e.add_argument("key")
+    e.add_argument("--forwards", type=int, default=6)
     a = ap.parse_args(argv)
-    if a.what == "trace":
+    if a.what == "eager":
+        eager(a.key, a.forwards)
+    elif a.what == "trace":
         sys.stdout.write(kernel_stats_md(a.stats, a.cmd))
     else:
         cmds = dict(s.split("=", 1) for s in a.cmd)
