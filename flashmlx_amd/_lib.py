@@ -207,6 +207,12 @@ _SIGS = {
          C.c_void_p, C.c_void_p],
     ),
     "fmx_model_workspace_hidden": (C.c_int, [P(FmxModelConfig), C.c_int64, C.c_void_p, P(C.c_void_p)]),
+    "fmx_model_config_from_json": (C.c_int, [C.c_char_p, P(FmxModelConfig), P(C.c_int32)]),
+    "fmx_checkpoint_tensor": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, P(C.c_int64), P(C.c_int32)]),
+    "fmx_model_load": (C.c_int, [C.c_char_p, P(FmxModelConfig), P(C.c_void_p), C.c_void_p]),
+    "fmx_loaded_model_weights": (P(FmxModelWeights), [C.c_void_p]),
+    "fmx_loaded_model_device_bytes": (C.c_size_t, [C.c_void_p]),
+    "fmx_loaded_model_free": (None, [C.c_void_p]),
     "fmx_greedy_next": (
         C.c_int,
         [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),

@@ -28,6 +28,7 @@ SOURCES = [
     "csrc/fmx_synth.hip",
     "csrc/fmx_model.hip",
     "csrc/fmx_model.cpp",
+    "csrc/fmx_loader.cpp",
 ]
 
 ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")

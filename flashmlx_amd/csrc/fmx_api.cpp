@@ -335,6 +335,23 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
 
 }  // namespace
 
+namespace fmx {
+// Byte offsets of a layer's packed parts (fmx_pack_expert_weights' layout),
+// for the checkpoint loader, which packs expert by expert.
+bool moe_packed_parts(const fmx_moe_config& c, size_t* gu, size_t* dn, size_t* sgu, size_t* sdn,
+                      int64_t* gu_es, int64_t* dn_es) {
+  if (check_moe_config(&c) || !packable(c)) return false;
+  const PackedLayout P = packed_layout(c);
+  *gu = P.gu;
+  *dn = P.dn;
+  *sgu = P.sgu;
+  *sdn = P.sdn;
+  *gu_es = P.gu_es;
+  *dn_es = P.dn_es;
+  return true;
+}
+}  // namespace fmx
+
 extern "C" {
 
 int fmx_abi_version(void) { return FMX_ABI_VERSION; }

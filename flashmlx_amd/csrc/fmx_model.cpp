@@ -51,6 +51,7 @@ int ok() {
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 constexpr int64_t kDenseDecMaxRows = 16;  // decode projections: at most 16 rows
+constexpr int64_t kMaxPositions = 32768;  // RoPE table rows (the cache itself: kAttnMaxSeq)
 
 struct Dims {
   int64_t H, L, nh, nkv, hd, V, P, nqkv;
@@ -82,9 +83,9 @@ int check_config(const fmx_model_config* c) {
   if ((d.nh * d.hd) % 128 || d.nqkv % 16)
     return fail(FMX_ERR_UNSUPPORTED, "heads * head_dim=%lld (a multiple of 128)", (long long)(d.nh * d.hd));
   if (d.V < 16 || d.V % 16) return fail(FMX_ERR_UNSUPPORTED, "vocab_size=%lld (a multiple of 16)", (long long)d.V);
-  if (d.P < 1 || d.P > kAttnMaxSeq)
+  if (d.P < 1 || d.P > kMaxPositions)
     return fail(FMX_ERR_UNSUPPORTED, "max_position_embeddings=%lld (1..%lld)", (long long)d.P,
-                (long long)kAttnMaxSeq);
+                (long long)kMaxPositions);
   if (c->moe.hidden_size != d.H) return fail(FMX_ERR_SHAPE, "moe.hidden_size != hidden_size");
   if (fmx_moe_workspace_size(&c->moe, 1) == 0) return fail(FMX_ERR_ARG, "invalid moe config");
   if (fmx_moe_packed_size(&c->moe) == 0)
@@ -230,7 +231,7 @@ int fmx_pack_linear(const fmx_qweight* parts, const int64_t* rows, int n_parts, 
 }
 
 size_t fmx_model_kv_cache_size(const fmx_model_config* cfg, int64_t cache_batch, int64_t cache_max_seq) {
-  if (check_config(cfg) || cache_batch < 1 || cache_max_seq < 1) return 0;
+  if (check_config(cfg) || cache_batch < 1 || cache_max_seq < 1 || cache_max_seq > kAttnMaxSeq) return 0;
   const Dims d = dims(*cfg);
   return static_cast<size_t>(d.L * 2 * cache_batch * d.nkv * cache_max_seq * d.hd * 2);
 }
@@ -293,8 +294,9 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
   if (!input_ids || !kv_cache || !logits || !workspace) return fail(FMX_ERR_ARG, "NULL buffer");
   if (B > cache_batch) return fail(FMX_ERR_SHAPE, "batch %lld > cache_batch %lld", (long long)B, (long long)cache_batch);
   const Dims d = dims(*cfg);
-  if (cache_max_seq < 1 || cache_max_seq > d.P)
-    return fail(FMX_ERR_SHAPE, "cache_max_seq=%lld (1..max_position_embeddings)", (long long)cache_max_seq);
+  if (cache_max_seq < 1 || cache_max_seq > d.P || cache_max_seq > kAttnMaxSeq)
+    return fail(FMX_ERR_SHAPE, "cache_max_seq=%lld (1..min(max_position_embeddings, %lld))",
+                (long long)cache_max_seq, (long long)kAttnMaxSeq);
   if (!cache_offsets && (cache_offset < 0 || cache_offset + Lq > cache_max_seq))
     return fail(FMX_ERR_SHAPE, "positions %lld..%lld outside the cache (%lld)", (long long)cache_offset,
                 (long long)(cache_offset + Lq - 1), (long long)cache_max_seq);

@@ -101,13 +101,13 @@ class DecoderModel:
     a KV cache of `max_batch` sequences x `max_seq` positions and a workspace
     for forwards of up to `max_tokens` tokens."""
 
-    def __init__(self, cfg: ModelConfig, w: ModelWeights, max_batch: int, max_seq: int,
-                 max_tokens: int):
+    def __init__(self, cfg: ModelConfig, w, max_batch: int, max_seq: int, max_tokens: int):
+        """w: ModelWeights, or a LoadedModel (fmx_model_load)."""
         self.lib = _lib.load()
         self.cfg, self.w = cfg, w
         self._c_cfg = cfg.to_c()
         self.max_batch, self.max_seq = max_batch, max_seq
-        dev = w.embed.device
+        dev = torch.device("cuda", torch.cuda.current_device())
         kv = self.lib.fmx_model_kv_cache_size(C.byref(self._c_cfg), max_batch, max_seq)
         ws = self.lib.fmx_model_workspace_size(C.byref(self._c_cfg), max_tokens)
         if kv == 0 or ws == 0:
@@ -117,6 +117,9 @@ class DecoderModel:
         self.ws_bytes = ws
         _lib.check(self.lib.fmx_model_workspace_init(C.byref(self._c_cfg), self.workspace.data_ptr(),
                                                      ws, _stream()))
+        if isinstance(w, LoadedModel):
+            self._c_w = w.c_weights()
+            return
         self._layers = (_lib.FmxLayerWeights * len(w.layers))()
         for i, lw in enumerate(w.layers):
             L = self._layers[i]
@@ -259,12 +262,12 @@ def synthetic_model(cfg: ModelConfig, seed: int, device="cuda", keep_mlx: bool =
         layers.append(lw)
     et = QWeight(*quantize(g((V, H), S_EMBED)))
     embed = dequantize(et.w, et.scales, et.biases)
-    del et
     lm = q((V, H), S_LM_HEAD)
     w = ModelWeights(embed=embed, norm_w=g((H,), S_NORM, 0.1, 1.0), lm_head=pack_linear([lm], H),
                      layers=layers)
     if keep_mlx:
-        w.mlx = dict(lm_head=lm)
+        w.mlx = dict(lm_head=lm, embed=et)
+    del et
     torch.cuda.synchronize()
     return w
 
@@ -303,3 +306,161 @@ def oracle_config(cfg: ModelConfig, max_seq: int) -> dict:
                 moe=dict(hidden=m.hidden_size, n_experts=m.num_experts, top_k=m.num_experts_per_tok,
                          inter=m.moe_intermediate_size, shared_inter=m.shared_expert_intermediate_size,
                          norm_topk=m.norm_topk_prob))
+
+
+# ------------------------------------------------------------------ checkpoints
+
+class LoadedModel:
+    """Weights read from an MLX checkpoint directory by fmx_model_load (the
+    library owns their device memory until close())."""
+
+    def __init__(self, handle: int, cfg: ModelConfig):
+        self.handle, self.cfg = handle, cfg
+        self.lib = _lib.load()
+
+    def c_weights(self):
+        return self.lib.fmx_loaded_model_weights(self.handle).contents
+
+    @property
+    def device_bytes(self) -> int:
+        return self.lib.fmx_loaded_model_device_bytes(self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.fmx_loaded_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 (interpreter shutdown)
+            pass
+
+
+def config_from_json(path: str) -> tuple:
+    """fmx_model_config_from_json -> (ModelConfig, tie_word_embeddings)."""
+    lib = _lib.load()
+    c = _lib.FmxModelConfig()
+    tie = C.c_int32()
+    _lib.check(lib.fmx_model_config_from_json(str(path).encode(), C.byref(c), C.byref(tie)))
+    m = c.moe
+    cfg = ModelConfig(hidden_size=c.hidden_size, num_hidden_layers=c.num_hidden_layers,
+                      num_attention_heads=c.num_attention_heads, num_key_value_heads=c.num_key_value_heads,
+                      head_dim=c.head_dim, vocab_size=c.vocab_size,
+                      max_position_embeddings=c.max_position_embeddings, rms_norm_eps=c.rms_norm_eps,
+                      rope_theta=c.rope_theta,
+                      moe=MoEConfig(hidden_size=m.hidden_size, num_experts=m.num_experts,
+                                    num_experts_per_tok=m.num_experts_per_tok,
+                                    moe_intermediate_size=m.moe_intermediate_size,
+                                    shared_expert_intermediate_size=m.shared_expert_intermediate_size,
+                                    norm_topk_prob=bool(m.norm_topk_prob), quant_bits=m.quant_bits,
+                                    quant_group_size=m.quant_group_size))
+    return cfg, bool(tie.value)
+
+
+def load_checkpoint(path: str, cfg: Optional[ModelConfig] = None) -> LoadedModel:
+    """fmx_model_load of an MLX checkpoint directory (config.json read when
+    cfg is not given)."""
+    import os
+    lib = _lib.load()
+    if cfg is None:
+        cfg, _ = config_from_json(os.path.join(path, "config.json"))
+    h = C.c_void_p()
+    _lib.check(lib.fmx_model_load(str(path).encode(), C.byref(cfg.to_c()), C.byref(h), _stream()))
+    return LoadedModel(h.value, cfg)
+
+
+def write_safetensors(path: str, tensors: dict, metadata: Optional[dict] = None) -> None:
+    """A safetensors file from {name: numpy array (uint16 for bf16, uint32,
+    ...)}; uint16 arrays are written as BF16 (the MLX checkpoints' dtype)."""
+    import json
+
+    import numpy as np
+    dt = {np.dtype(np.uint16): "BF16", np.dtype(np.uint32): "U32", np.dtype(np.float32): "F32",
+          np.dtype(np.int32): "I32"}
+    header, blobs, off = {}, [], 0
+    for name in sorted(tensors):
+        a = np.ascontiguousarray(tensors[name])
+        b = a.tobytes()
+        header[name] = {"dtype": dt[a.dtype], "shape": list(a.shape), "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    if metadata:
+        header["__metadata__"] = metadata
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little"))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def save_checkpoint(cfg: ModelConfig, w: ModelWeights, path: str, shards: int = 2) -> None:
+    """An MLX-format checkpoint of a synthetic model (keep_mlx=True): the
+    per-expert arrays under the reference's key names
+    (docs/superpowers/specs/2026-04-01-moe-support-design.md:138-151), with
+    the "model." prefix, split over `shards` files, and its config.json."""
+    import json
+    import os
+
+    import numpy as np
+
+    def h(t):
+        t = t.contiguous()
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).cpu().numpy().view(np.uint16)
+        return t.cpu().numpy().view(np.uint32)
+
+    def q(prefix, qw, out, idx=None):
+        for part, t in (("weight", qw.w), ("scales", qw.scales), ("biases", qw.biases)):
+            out[f"{prefix}.{part}"] = h(t if idx is None else t[idx])
+
+    nh, nkv, hd = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.hd
+    out = {}
+    for li, lw in enumerate(w.layers):
+        p = f"model.layers.{li}"
+        out[f"{p}.input_layernorm.weight"] = h(lw.input_norm_w)
+        out[f"{p}.post_attention_layernorm.weight"] = h(lw.post_norm_w)
+        qkv = lw.mlx["qkv"]
+        r = [0, nh * hd, (nh + nkv) * hd, (nh + 2 * nkv) * hd]
+        for i, name in enumerate(("q_proj", "k_proj", "v_proj")):
+            q(f"{p}.self_attn.{name}", QWeight(qkv.w[r[i]:r[i + 1]], qkv.scales[r[i]:r[i + 1]],
+                                               qkv.biases[r[i]:r[i + 1]]), out)
+            if lw.qkv_bias is not None:
+                out[f"{p}.self_attn.{name}.bias"] = h(lw.qkv_bias[r[i]:r[i + 1]])
+        q(f"{p}.self_attn.o_proj", lw.mlx["o"], out)
+        m = lw.moe
+        if isinstance(m.router_w, QWeight):
+            q(f"{p}.mlp.gate", m.router_w, out)
+        else:
+            out[f"{p}.mlp.gate.weight"] = h(m.router_w)
+        for e in range(cfg.moe.num_experts):
+            for name, qw in (("gate_proj", m.gate), ("up_proj", m.up), ("down_proj", m.down)):
+                q(f"{p}.mlp.experts.{e}.{name}", qw, out, e)
+        if m.shared_gate is not None:
+            for name, qw in (("gate_proj", m.shared_gate), ("up_proj", m.shared_up), ("down_proj", m.shared_down)):
+                q(f"{p}.mlp.shared_expert.{name}", qw, out)
+            if isinstance(m.shared_expert_gate_w, QWeight):
+                q(f"{p}.mlp.shared_expert_gate", m.shared_expert_gate_w, out)
+            else:
+                out[f"{p}.mlp.shared_expert_gate.weight"] = h(m.shared_expert_gate_w)
+    q("model.embed_tokens", w.mlx["embed"], out)
+    out["model.norm.weight"] = h(w.norm_w)
+    q("lm_head", w.mlx["lm_head"], out)
+    os.makedirs(path, exist_ok=True)
+    names = sorted(out)
+    for s in range(shards):
+        part = {n: out[n] for n in names[s::shards]}
+        write_safetensors(os.path.join(path, f"model-{s + 1:05d}-of-{shards:05d}.safetensors"), part,
+                          {"format": "mlx"})
+    mc = cfg.moe
+    conf = dict(model_type="qwen2_moe", hidden_size=cfg.hidden_size, num_hidden_layers=cfg.num_hidden_layers,
+                num_attention_heads=nh, num_key_value_heads=nkv, head_dim=hd, vocab_size=cfg.vocab_size,
+                max_position_embeddings=cfg.max_position_embeddings, rms_norm_eps=cfg.rms_norm_eps,
+                rope_theta=cfg.rope_theta, tie_word_embeddings=False, num_experts=mc.num_experts,
+                num_experts_per_tok=mc.num_experts_per_tok, moe_intermediate_size=mc.moe_intermediate_size,
+                shared_expert_intermediate_size=mc.shared_expert_intermediate_size,
+                norm_topk_prob=mc.norm_topk_prob, quantization=dict(group_size=64, bits=4))
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(conf, f, indent=1)

@@ -24,9 +24,10 @@ extern "C" {
 /* ModelConfig (server/include/flashmlx/model.h:20-54) for an all-MoE
  * decoder: head_dim = hidden_size / num_attention_heads when 0. Limits:
  * hidden_size and num_attention_heads * head_dim multiples of 128 (and
- * hidden_size <= 8192), head_dim even, a multiple of 8 and <= 256,
+ * hidden_size <= 8192), head_dim a multiple of 8 and <= 256,
  * num_attention_heads a multiple of num_key_value_heads, vocab_size a
- * multiple of 16, max_position_embeddings <= 4096. */
+ * multiple of 16, max_position_embeddings <= 32768 (the RoPE table); a KV
+ * cache holds at most 4096 positions per sequence. */
 typedef struct fmx_model_config {
   int64_t hidden_size;
   int64_t num_hidden_layers;
@@ -120,6 +121,42 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
  * LlamaModel's debug_forward / debug_embed (model.h:125-126). */
 int fmx_model_workspace_hidden(const fmx_model_config* cfg, int64_t n_tokens, const void* workspace,
                                const void** hidden);
+
+/* ------------------------------------------------------------------------
+ * Quantized-checkpoint loader (LlamaModel::load_config / load_weights /
+ * build_weight_cache / build_moe_weight_cache, model.cpp:100-470)
+ * --------------------------------------------------------------------- */
+
+/* config.json of an MLX checkpoint -> fmx_model_config, with the keys and
+ * defaults of load_config (model.cpp:111-140): quantization.bits /
+ * group_size into cfg->moe.quant_bits / quant_group_size. The host-side
+ * parse only; tie_word_embeddings (may be NULL) receives that key. */
+int fmx_model_config_from_json(const char* config_json_path, fmx_model_config* cfg,
+                               int32_t* tie_word_embeddings);
+
+/* Metadata of one tensor of a checkpoint directory (every *.safetensors
+ * file, in name order; a "model." key prefix dropped, model.cpp:160-170):
+ * dtype ("BF16", "U32", ...; 8 bytes), shape (up to 8 dims), ndim. Host-side. */
+int fmx_checkpoint_tensor(const char* dir, const char* name, char* dtype, int64_t* shape,
+                          int32_t* ndim);
+
+/* Loads an all-MoE checkpoint (MLX affine 4-bit, group 64; keys
+ * layers.N.{input_layernorm, post_attention_layernorm}.weight,
+ * layers.N.self_attn.{q,k,v,o}_proj.{weight,scales,biases} (+ q/k/v .bias),
+ * layers.N.mlp.gate.*, layers.N.mlp.experts.E.{gate,up,down}_proj.*,
+ * layers.N.mlp.shared_expert.* and .shared_expert_gate.*, embed_tokens.*,
+ * norm.weight, lm_head.* (or the embedding's when tied)) into device memory
+ * the returned object owns: each tensor is read once and packed in place
+ * (experts one by one), so the expert weights exist once, in the packed
+ * layout; the embedding is dequantized to bf16 as the reference does at
+ * load. Synchronous on `stream`. Missing tensors, wrong dtypes or shapes
+ * return an error naming the tensor. */
+typedef struct fmx_loaded_model fmx_loaded_model;
+int fmx_model_load(const char* dir, const fmx_model_config* cfg, fmx_loaded_model** out,
+                   fmx_stream stream);
+const fmx_model_weights* fmx_loaded_model_weights(const fmx_loaded_model* model);
+size_t fmx_loaded_model_device_bytes(const fmx_loaded_model* model);
+void fmx_loaded_model_free(fmx_loaded_model* model);
 
 /* Greedy next token: ids[b] = argmax_v logits[b * row_stride + v] (the
  * first of equal maxima, as mx::argmax); when offsets is not NULL,

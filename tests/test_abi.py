@@ -270,7 +270,7 @@ def test_model_sizes_and_validation(fmx):
     assert lib.fmx_packed_linear_size(6144, 2048) == 6144 * 2048 * 9 // 16
     assert lib.fmx_packed_linear_size(6144, 2000) == 0
     for bad in (ModelConfig(vocab_size=100), ModelConfig(num_key_value_heads=3),
-                ModelConfig(max_position_embeddings=8192), ModelConfig(head_dim=100)):
+                ModelConfig(max_position_embeddings=65536), ModelConfig(head_dim=100)):
         assert lib.fmx_model_workspace_size(C.byref(bad.to_c()), 1) == 0
     rc = lib.fmx_model_forward(C.byref(c), None, None, 1, 1, 0, None, None, 1, 1, 1, None, None, 0, None)
     assert rc == _lib.FMX_ERR_ARG
