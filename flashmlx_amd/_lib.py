@@ -206,6 +206,12 @@ _SIGS = {
          C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p, C.c_size_t,
          C.c_void_p, C.c_void_p],
     ),
+    "fmx_model_forward_batched": (
+        C.c_int,
+        [P(FmxModelConfig), P(FmxModelWeights), C.c_void_p, C.c_int64, C.c_int64, C.c_int64,
+         C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_int64, C.c_int, C.c_void_p, C.c_void_p,
+         C.c_size_t, C.c_void_p, C.c_void_p],
+    ),
     "fmx_model_workspace_hidden": (C.c_int, [P(FmxModelConfig), C.c_int64, C.c_void_p, P(C.c_void_p)]),
     "fmx_model_config_from_json": (C.c_int, [C.c_char_p, P(FmxModelConfig), P(C.c_int32)]),
     "fmx_checkpoint_tensor": (C.c_int, [C.c_char_p, C.c_char_p, C.c_char_p, P(C.c_int64), P(C.c_int32)]),
@@ -216,6 +222,19 @@ _SIGS = {
     "fmx_greedy_next": (
         C.c_int,
         [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+    "fmx_scheduler_create": (
+        C.c_int,
+        [P(FmxModelConfig), P(FmxModelWeights), C.c_int64, C.c_int64, C.c_int64, C.c_void_p,
+         P(C.c_void_p)]),
+    "fmx_scheduler_submit": (
+        C.c_int, [C.c_void_p, P(C.c_int32), C.c_int64, C.c_int64, C.c_float, P(C.c_int64)]),
+    "fmx_scheduler_step": (
+        C.c_int, [C.c_void_p, P(C.c_int64), P(C.c_int32), C.c_int64, P(C.c_int64)]),
+    "fmx_scheduler_has_work": (C.c_int, [C.c_void_p]),
+    "fmx_scheduler_active_count": (C.c_int64, [C.c_void_p]),
+    "fmx_scheduler_drain_completed": (
+        C.c_int, [C.c_void_p, P(C.c_int64), C.c_int64, P(C.c_int64)]),
+    "fmx_scheduler_free": (None, [C.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGS)

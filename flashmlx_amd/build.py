@@ -29,6 +29,7 @@ SOURCES = [
     "csrc/fmx_model.hip",
     "csrc/fmx_model.cpp",
     "csrc/fmx_loader.cpp",
+    "csrc/fmx_sched.cpp",
 ]
 
 ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")

@@ -283,6 +283,17 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
                              const int32_t* cache_offsets, void* kv_cache, int64_t cache_batch,
                              int64_t cache_max_seq, int last_only, void* logits, void* workspace,
                              size_t workspace_bytes, fmx_stream stream_, uint32_t* routing) {
+  return fmx_model_forward_batched(cfg, w, input_ids, B, Lq, cache_offset, cache_offsets, nullptr, kv_cache,
+                                   cache_batch, cache_max_seq, last_only, logits, workspace, workspace_bytes,
+                                   stream_, routing);
+}
+
+int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weights* w,
+                              const int32_t* input_ids, int64_t B, int64_t Lq, int64_t cache_offset,
+                              const int32_t* cache_offsets, const int32_t* cache_slots, void* kv_cache,
+                              int64_t cache_batch, int64_t cache_max_seq, int last_only, void* logits,
+                              void* workspace, size_t workspace_bytes, fmx_stream stream_,
+                              uint32_t* routing) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   FMX_RC(check_config(cfg));
   if (!w || !w->embed || !w->norm_w || !w->lm_head || !w->layers)
@@ -292,7 +303,8 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
   if (T == 0) return ok();
   if (T > 65536) return fail(FMX_ERR_UNSUPPORTED, "%lld tokens (at most 65536)", (long long)T);
   if (!input_ids || !kv_cache || !logits || !workspace) return fail(FMX_ERR_ARG, "NULL buffer");
-  if (B > cache_batch) return fail(FMX_ERR_SHAPE, "batch %lld > cache_batch %lld", (long long)B, (long long)cache_batch);
+  if (!cache_slots && B > cache_batch)
+    return fail(FMX_ERR_SHAPE, "batch %lld > cache_batch %lld", (long long)B, (long long)cache_batch);
   const Dims d = dims(*cfg);
   if (cache_max_seq < 1 || cache_max_seq > d.P || cache_max_seq > kAttnMaxSeq)
     return fail(FMX_ERR_SHAPE, "cache_max_seq=%lld (1..min(max_position_embeddings, %lld))",
@@ -353,6 +365,8 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
     ra.offs = cache_offsets;
     ra.off = static_cast<int>(cache_offset);
     ra.max_seq = cache_max_seq;
+    ra.slots = cache_slots;
+    ra.n_slots = static_cast<int>(cache_batch);
     ra.q_out = M.qrot;
     ra.kc = kc;
     ra.vc = vc;
@@ -371,6 +385,8 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
     aa.max_seq = cache_max_seq;
     aa.offs = cache_offsets;
     aa.off = ra.off;
+    aa.slots = cache_slots;
+    aa.n_slots = ra.n_slots;
     aa.scale = scale;
     aa.out = M.attn;
     aa.ldo = d.nh * d.hd;

@@ -161,6 +161,13 @@ __device__ inline int token_pos(const int32_t* offs, int off, int b, int l, int6
   return static_cast<int>(p < 0 ? 0 : (p >= max_seq ? max_seq - 1 : p));
 }
 
+// cache slot of sequence b: slots[b] (clamped to the cache) or b
+__device__ inline int64_t cache_slot(const int32_t* slots, int n_slots, int b) {
+  if (!slots) return b;
+  const int s = slots[b];
+  return s < 0 ? 0 : (s >= n_slots ? n_slots - 1 : s);
+}
+
 // One workgroup per token t = b * L + l at position p = offset(b) + l:
 // q heads rotated into q_out, k heads rotated into the layer's key cache at
 // p, v heads copied into the value cache at p. Rotation of pair (i, i + hd/2)
@@ -171,6 +178,7 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
   const int t = blockIdx.x;
   const int b = t / a.L, l = t - b * a.L;
   const int p = token_pos(a.offs, a.off, b, l, a.max_seq);
+  const int64_t slot = cache_slot(a.slots, a.n_slots, b);
   const int half = a.hd / 2, nq = a.nh + 2 * a.nkv;
   const uint16_t* row = a.qkv + static_cast<int64_t>(t) * nq * a.hd;
   const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
@@ -186,7 +194,7 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
       dst = a.q_out + (static_cast<int64_t>(t) * a.nh + head) * a.hd;
     } else {
       const int g = head - a.nh;
-      dst = a.kc + ((static_cast<int64_t>(b) * a.nkv + g) * a.max_seq + p) * a.hd;
+      dst = a.kc + ((slot * a.nkv + g) * a.max_seq + p) * a.hd;
     }
     dst[i] = o1;
     dst[i + half] = o2;
@@ -194,7 +202,7 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
   for (int it = threadIdx.x; it < a.nkv * a.hd / 8; it += blockDim.x) {
     const int g = it / (a.hd / 8), c = it - g * (a.hd / 8);
     const u32x4_t v = reinterpret_cast<const u32x4_t*>(row + (a.nh + a.nkv + g) * a.hd)[c];
-    reinterpret_cast<u32x4_t*>(a.vc + ((static_cast<int64_t>(b) * a.nkv + g) * a.max_seq + p) * a.hd)[c] = v;
+    reinterpret_cast<u32x4_t*>(a.vc + ((slot * a.nkv + g) * a.max_seq + p) * a.hd)[c] = v;
   }
 }
 
@@ -235,7 +243,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
   const int p = token_pos(a.offs, a.off, b, l, a.max_seq);
   const int nk = p + 1;
   const int rep = a.nh / a.nkv, g = h / rep;
-  const int64_t cbase = (static_cast<int64_t>(b) * a.nkv + g) * a.max_seq * a.hd;
+  const int64_t cbase = (cache_slot(a.slots, a.n_slots, b) * a.nkv + g) * a.max_seq * a.hd;
   uint16_t* kb = a.kc + cbase;
   uint16_t* vb = a.vc + cbase;
   if (ROPE) {

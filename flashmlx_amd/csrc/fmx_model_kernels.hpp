@@ -49,7 +49,8 @@ struct DenseArgs {
 hipError_t launch_dense_dec(const DenseArgs& a, hipStream_t stream);
 
 // Positions: token t = b * L + l sits at offs[b] + l (device offsets) or
-// off + l, clamped to [0, max_seq).
+// off + l, clamped to [0, max_seq); its keys and values live in cache slot
+// slots[b] (or b).
 struct RopeArgs {
   const uint16_t* qkv;    // [T, (nh + 2 nkv) * hd]: q heads, k heads, v heads
   int L, nh, nkv, hd;
@@ -57,6 +58,8 @@ struct RopeArgs {
   const int32_t* offs;
   int off;
   int64_t max_seq;
+  const int32_t* slots;   // cache slot of each sequence (null: slot b), clamped to n_slots
+  int n_slots;
   uint16_t* q_out;        // [T, nh * hd] rotated q
   uint16_t* kc;           // this layer's caches [B_cache][nkv][max_seq][hd]
   uint16_t* vc;
@@ -76,6 +79,8 @@ struct AttnArgs {
   int64_t max_seq;
   const int32_t* offs;
   int off;
+  const int32_t* slots;   // as RopeArgs
+  int n_slots;
   float scale;
   uint16_t* out;          // [T, nh * hd] bf16 (row stride ldo)
   int64_t ldo;

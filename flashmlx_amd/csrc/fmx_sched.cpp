@@ -1,0 +1,312 @@
+// fmx_sched.cpp -- the server loop's batched decode (include/fmx_model.h):
+// requests admitted into the slots of a KV pool, prefilled one at a time,
+// and decoded together, one greedy token per live request per step.
+//
+// Reference: server/src/scheduler.cpp:19-101 (BatchScheduler submit / step /
+// has_work / drain_completed / active_count), :103-232 (prefill_request:
+// slot, batch-1 prefill at offset 0, first token from the last position),
+// :527-680 (decode_batched: every live request's next token, one batched
+// forward, argmax, per-request append and done check), kv_pool.cpp (slots of
+// max_context positions). The pool here is the decoder stack's KV cache
+// itself: a live request keeps its slot, and a decode step passes every
+// request's slot and cache offset to fmx_model_forward_batched, so no cache
+// is copied into a left-padded batch cache or flushed back
+// (batch_kv_cache.cpp:10-91, scheduler.cpp:556-576, :658-678).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <deque>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "../../include/fmx_model.h"
+
+namespace fmx {
+int set_error(int status, const char* msg);
+void clear_error();
+}  // namespace fmx
+
+using namespace fmx;
+
+namespace {
+
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  return set_error(status, buf);
+}
+
+#define FMX_HIP(expr)                                                              \
+  do {                                                                             \
+    hipError_t e_ = (expr);                                                        \
+    if (e_ != hipSuccess)                                                          \
+      return fail(FMX_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));            \
+  } while (0)
+
+#define FMX_RC(expr)     \
+  do {                   \
+    int rc_ = (expr);    \
+    if (rc_) return rc_; \
+  } while (0)
+
+struct Request {
+  std::vector<int32_t> prompt;
+  int64_t max_tokens = 0;
+  int slot = -1;          // KV pool slot while active
+  int64_t offset = 0;     // cache positions filled
+  int64_t generated = 0;
+  int32_t next = 0;       // the latest token, the next step's input
+};
+
+}  // namespace
+
+struct fmx_scheduler {
+  fmx_model_config cfg{};
+  const fmx_model_weights* w = nullptr;
+  hipStream_t stream = nullptr;
+  int64_t n_slots = 0, max_context = 0, max_prompt = 0, V = 0;
+  void *kv = nullptr, *ws = nullptr, *logits = nullptr;
+  size_t ws_bytes = 0;
+  int32_t *d_ids = nullptr, *d_offs = nullptr, *d_slots = nullptr, *d_next = nullptr;
+  int32_t* h_buf = nullptr;  // pinned: ids, offsets, slots going up; next tokens coming back
+  // pending queue: written by submit (any thread), read by step
+  std::mutex pending_mu;
+  std::deque<std::pair<int64_t, Request>> pending;
+  int64_t next_id = 0;
+  // active requests by id (ids grow with submission, so this is also the
+  // batch order of a decode step); touched by step only
+  std::map<int64_t, Request> active;
+  std::vector<int> free_slots;
+  std::mutex completed_mu;
+  std::vector<int64_t> completed;
+  ~fmx_scheduler() {
+    for (void* p : {kv, ws, logits, static_cast<void*>(d_ids), static_cast<void*>(d_offs),
+                    static_cast<void*>(d_slots), static_cast<void*>(d_next)})
+      if (p) (void)hipFree(p);
+    if (h_buf) (void)hipHostFree(h_buf);
+  }
+};
+
+namespace {
+
+// prefill_request (scheduler.cpp:103-211): batch-1 prefill of the prompt into
+// slot r.slot at offset 0, first token = argmax of the last position
+int prefill(fmx_scheduler& s, Request& r) {
+  const int64_t n = static_cast<int64_t>(r.prompt.size());
+  int32_t* h = s.h_buf;
+  for (int64_t i = 0; i < n; ++i) h[i] = r.prompt[static_cast<size_t>(i)];
+  h[n] = r.slot;
+  FMX_HIP(hipMemcpyAsync(s.d_ids, h, static_cast<size_t>(n * 4), hipMemcpyHostToDevice, s.stream));
+  FMX_HIP(hipMemcpyAsync(s.d_slots, h + n, 4, hipMemcpyHostToDevice, s.stream));
+  FMX_RC(fmx_model_forward_batched(&s.cfg, s.w, s.d_ids, 1, n, 0, nullptr, s.d_slots, s.kv, s.n_slots,
+                                   s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
+  FMX_RC(fmx_greedy_next(s.logits, 1, s.V, s.V, s.d_next, nullptr, 0, s.stream));
+  FMX_HIP(hipMemcpyAsync(h, s.d_next, 4, hipMemcpyDeviceToHost, s.stream));
+  FMX_HIP(hipStreamSynchronize(s.stream));
+  r.offset = n;
+  r.next = h[0];
+  r.generated = 1;
+  return FMX_OK;
+}
+
+// decode_batched (scheduler.cpp:527-627): one token for every request of live
+int decode(fmx_scheduler& s, const std::vector<Request*>& live) {
+  const int64_t B = static_cast<int64_t>(live.size());
+  int32_t* h = s.h_buf;
+  for (int64_t b = 0; b < B; ++b) {
+    h[b] = live[static_cast<size_t>(b)]->next;
+    h[B + b] = static_cast<int32_t>(live[static_cast<size_t>(b)]->offset);
+    h[2 * B + b] = live[static_cast<size_t>(b)]->slot;
+  }
+  FMX_HIP(hipMemcpyAsync(s.d_ids, h, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
+  FMX_HIP(hipMemcpyAsync(s.d_offs, h + B, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
+  FMX_HIP(hipMemcpyAsync(s.d_slots, h + 2 * B, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
+  FMX_RC(fmx_model_forward_batched(&s.cfg, s.w, s.d_ids, B, 1, 0, s.d_offs, s.d_slots, s.kv, s.n_slots,
+                                   s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
+  FMX_RC(fmx_greedy_next(s.logits, B, s.V, s.V, s.d_next, nullptr, 0, s.stream));
+  int32_t* back = h + 3 * B;
+  FMX_HIP(hipMemcpyAsync(back, s.d_next, static_cast<size_t>(B * 4), hipMemcpyDeviceToHost, s.stream));
+  FMX_HIP(hipStreamSynchronize(s.stream));
+  for (int64_t b = 0; b < B; ++b) {
+    Request& r = *live[static_cast<size_t>(b)];
+    r.next = back[b];
+    r.generated += 1;
+    r.offset += 1;
+  }
+  return FMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmx_scheduler_create(const fmx_model_config* cfg, const fmx_model_weights* w, int64_t n_slots,
+                         int64_t max_context, int64_t max_prompt, fmx_stream stream, fmx_scheduler** out) {
+  if (!cfg || !w || !out) return fail(FMX_ERR_ARG, "NULL argument");
+  *out = nullptr;
+  if (n_slots < 1 || n_slots > FMX_SCHED_MAX_SLOTS || max_prompt < 1 || max_context < max_prompt + 1)
+    return fail(FMX_ERR_SHAPE, "n_slots %lld (1..%d), max_context %lld, max_prompt %lld", (long long)n_slots,
+                FMX_SCHED_MAX_SLOTS, (long long)max_context, (long long)max_prompt);
+  const size_t kv = fmx_model_kv_cache_size(cfg, n_slots, max_context);
+  const int64_t max_tokens = max_prompt > n_slots ? max_prompt : n_slots;
+  const size_t wsb = fmx_model_workspace_size(cfg, max_tokens);
+  if (!kv || !wsb)
+    return fail(FMX_ERR_UNSUPPORTED, "config, max_context %lld or max_prompt %lld outside the decoder stack's limits",
+                (long long)max_context, (long long)max_prompt);
+  auto s = new fmx_scheduler();
+  s->cfg = *cfg;
+  s->w = w;
+  s->stream = static_cast<hipStream_t>(stream);
+  s->n_slots = n_slots;
+  s->max_context = max_context;
+  s->max_prompt = max_prompt;
+  s->V = cfg->vocab_size;
+  s->ws_bytes = wsb;
+  auto body = [&]() -> int {
+    FMX_HIP(hipMalloc(&s->kv, kv));
+    FMX_HIP(hipMalloc(&s->ws, wsb));
+    FMX_HIP(hipMalloc(&s->logits, static_cast<size_t>(n_slots * s->V * 2)));
+    FMX_HIP(hipMalloc(reinterpret_cast<void**>(&s->d_ids), static_cast<size_t>(max_tokens * 4)));
+    FMX_HIP(hipMalloc(reinterpret_cast<void**>(&s->d_offs), static_cast<size_t>(n_slots * 4)));
+    FMX_HIP(hipMalloc(reinterpret_cast<void**>(&s->d_slots), static_cast<size_t>(n_slots * 4)));
+    FMX_HIP(hipMalloc(reinterpret_cast<void**>(&s->d_next), static_cast<size_t>(n_slots * 4)));
+    FMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_buf),
+                          static_cast<size_t>((max_tokens + 4 * n_slots + 4) * 4), hipHostMallocDefault));
+    FMX_RC(fmx_model_workspace_init(cfg, s->ws, wsb, stream));
+    FMX_HIP(hipStreamSynchronize(s->stream));
+    for (int64_t i = n_slots - 1; i >= 0; --i) s->free_slots.push_back(static_cast<int>(i));
+    return FMX_OK;
+  };
+  const int rc = body();
+  if (rc) {
+    delete s;
+    return rc;
+  }
+  *out = s;
+  clear_error();
+  return FMX_OK;
+}
+
+int fmx_scheduler_submit(fmx_scheduler* s, const int32_t* prompt, int64_t n, int64_t max_tokens,
+                         float temperature, int64_t* request_id) {
+  if (!s || !prompt || !request_id) return fail(FMX_ERR_ARG, "NULL argument");
+  if (temperature != 0.0f)
+    return fail(FMX_ERR_UNSUPPORTED, "temperature %g: only greedy decoding (temperature 0)", (double)temperature);
+  if (n < 1 || n > s->max_prompt)
+    return fail(FMX_ERR_SHAPE, "prompt of %lld tokens (1..%lld)", (long long)n, (long long)s->max_prompt);
+  if (max_tokens < 1 || n + max_tokens > s->max_context)
+    return fail(FMX_ERR_SHAPE, "%lld prompt + %lld new tokens exceed the %lld positions of a slot", (long long)n,
+                (long long)max_tokens, (long long)s->max_context);
+  for (int64_t i = 0; i < n; ++i)
+    if (prompt[i] < 0 || prompt[i] >= s->V)
+      return fail(FMX_ERR_ARG, "prompt token %d outside the vocabulary of %lld", prompt[i], (long long)s->V);
+  Request r;
+  r.prompt.assign(prompt, prompt + n);
+  r.max_tokens = max_tokens;
+  {
+    std::lock_guard<std::mutex> lock(s->pending_mu);
+    const int64_t id = s->next_id++;
+    s->pending.emplace_back(id, std::move(r));
+    *request_id = id;
+  }
+  clear_error();
+  return FMX_OK;
+}
+
+int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, int64_t capacity,
+                       int64_t* n_new) {
+  if (!s || !n_new || !request_ids || !tokens) return fail(FMX_ERR_ARG, "NULL argument");
+  if (capacity < 2 * s->n_slots)
+    return fail(FMX_ERR_SHAPE, "capacity %lld < 2 * n_slots (%lld)", (long long)capacity, (long long)s->n_slots);
+  int64_t n = 0;
+  auto emit = [&](int64_t id, int32_t tok) {
+    request_ids[n] = id;
+    tokens[n] = tok;
+    ++n;
+  };
+  std::vector<int64_t> done;
+  // 1. admit pending requests while slots are free (scheduler.cpp:28-42)
+  {
+    std::lock_guard<std::mutex> lock(s->pending_mu);
+    while (!s->pending.empty() && !s->free_slots.empty()) {
+      const int64_t id = s->pending.front().first;
+      Request r = std::move(s->pending.front().second);
+      s->pending.pop_front();
+      r.slot = s->free_slots.back();
+      s->free_slots.pop_back();
+      const int rc = prefill(*s, r);
+      if (rc) {
+        s->free_slots.push_back(r.slot);
+        *n_new = n;
+        return rc;
+      }
+      emit(id, r.next);
+      // a request for one token is done after its prefill
+      if (r.generated >= r.max_tokens) done.push_back(id);
+      s->active.emplace(id, std::move(r));
+    }
+  }
+  // 2. one decode step of every request still decoding (scheduler.cpp:44-69)
+  std::vector<Request*> live;
+  std::vector<int64_t> live_ids;
+  for (auto& kv : s->active)
+    if (kv.second.generated < kv.second.max_tokens) {
+      live.push_back(&kv.second);
+      live_ids.push_back(kv.first);
+    }
+  if (!live.empty()) {
+    const int rc = decode(*s, live);
+    if (rc) {
+      *n_new = n;
+      return rc;
+    }
+    for (size_t b = 0; b < live.size(); ++b) {
+      emit(live_ids[b], live[b]->next);
+      if (live[b]->generated >= live[b]->max_tokens) done.push_back(live_ids[b]);
+    }
+  }
+  // 3. free the slots of completed requests (scheduler.cpp:71-82)
+  if (!done.empty()) {
+    std::lock_guard<std::mutex> lock(s->completed_mu);
+    for (int64_t id : done) {
+      auto it = s->active.find(id);
+      s->free_slots.push_back(it->second.slot);
+      s->active.erase(it);
+      s->completed.push_back(id);
+    }
+  }
+  *n_new = n;
+  clear_error();
+  return FMX_OK;
+}
+
+int fmx_scheduler_has_work(fmx_scheduler* s) {
+  if (!s) return 0;
+  std::lock_guard<std::mutex> lock(s->pending_mu);
+  return !s->pending.empty() || !s->active.empty();
+}
+
+int64_t fmx_scheduler_active_count(const fmx_scheduler* s) {
+  return s ? static_cast<int64_t>(s->active.size()) : 0;
+}
+
+int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_t capacity, int64_t* n) {
+  if (!s || !n || (capacity > 0 && !request_ids)) return fail(FMX_ERR_ARG, "NULL argument");
+  std::lock_guard<std::mutex> lock(s->completed_mu);
+  const int64_t m = static_cast<int64_t>(s->completed.size());
+  const int64_t take = m < capacity ? m : capacity;
+  for (int64_t i = 0; i < take; ++i) request_ids[i] = s->completed[static_cast<size_t>(i)];
+  s->completed.erase(s->completed.begin(), s->completed.begin() + take);
+  *n = take;
+  clear_error();
+  return FMX_OK;
+}
+
+void fmx_scheduler_free(fmx_scheduler* s) { delete s; }
+
+}  // extern "C"

@@ -96,6 +96,28 @@ class ModelWeights:
     mlx: dict = field(default_factory=dict)  # MLX-layout lm_head kept on request
 
 
+def c_weights(w):
+    """(fmx_model_weights, the per-layer array it points to) for ModelWeights
+    or a LoadedModel; keep both alive while the library may read them."""
+    if isinstance(w, LoadedModel):
+        return w.c_weights(), None
+    layers = (_lib.FmxLayerWeights * len(w.layers))()
+    for i, lw in enumerate(w.layers):
+        L = layers[i]
+        L.input_norm_w = lw.input_norm_w.data_ptr()
+        L.post_norm_w = lw.post_norm_w.data_ptr()
+        L.qkv = lw.qkv.data_ptr()
+        L.qkv_bias = lw.qkv_bias.data_ptr() if lw.qkv_bias is not None else None
+        L.o = lw.o.data_ptr()
+        L.moe = lw.moe.to_c()
+    c_w = _lib.FmxModelWeights()
+    c_w.embed = w.embed.data_ptr()
+    c_w.norm_w = w.norm_w.data_ptr()
+    c_w.lm_head = w.lm_head.data_ptr()
+    c_w.layers = layers
+    return c_w, layers
+
+
 class DecoderModel:
     """LlamaModel::forward (server/src/model.cpp:1021-1033) on libfmx, with
     a KV cache of `max_batch` sequences x `max_seq` positions and a workspace
@@ -117,23 +139,7 @@ class DecoderModel:
         self.ws_bytes = ws
         _lib.check(self.lib.fmx_model_workspace_init(C.byref(self._c_cfg), self.workspace.data_ptr(),
                                                      ws, _stream()))
-        if isinstance(w, LoadedModel):
-            self._c_w = w.c_weights()
-            return
-        self._layers = (_lib.FmxLayerWeights * len(w.layers))()
-        for i, lw in enumerate(w.layers):
-            L = self._layers[i]
-            L.input_norm_w = lw.input_norm_w.data_ptr()
-            L.post_norm_w = lw.post_norm_w.data_ptr()
-            L.qkv = lw.qkv.data_ptr()
-            L.qkv_bias = lw.qkv_bias.data_ptr() if lw.qkv_bias is not None else None
-            L.o = lw.o.data_ptr()
-            L.moe = lw.moe.to_c()
-        self._c_w = _lib.FmxModelWeights()
-        self._c_w.embed = w.embed.data_ptr()
-        self._c_w.norm_w = w.norm_w.data_ptr()
-        self._c_w.lm_head = w.lm_head.data_ptr()
-        self._c_w.layers = self._layers
+        self._c_w, self._layers = c_weights(w)
 
     def kv_views(self):
         """(keys, values) as bf16 [layers, max_batch, nkv, max_seq, hd]."""
@@ -203,6 +209,71 @@ class DecoderModel:
             if i + 1 < n_new:
                 self.forward_into(ids, L + i, logits)
         return out
+
+
+class BatchScheduler:
+    """BatchScheduler (server/include/flashmlx/scheduler.h:37-99) on the
+    native loop of fmx_sched.cpp: submit / step / has_work / drain_completed
+    / active_count over a KV pool of n_slots slots of max_context positions.
+    Greedy decoding only (temperature 0)."""
+
+    def __init__(self, cfg: ModelConfig, w, n_slots: int, max_context: int, max_prompt: int):
+        self.lib = _lib.load()
+        self.cfg, self.w = cfg, w
+        self._c_cfg = cfg.to_c()
+        self._c_w, self._layers = c_weights(w)
+        self.n_slots = n_slots
+        h = C.c_void_p()
+        _lib.check(self.lib.fmx_scheduler_create(C.byref(self._c_cfg), C.byref(self._c_w), n_slots,
+                                                 max_context, max_prompt, _stream(), C.byref(h)))
+        self._h = h
+        self._ids = (C.c_int64 * (2 * n_slots))()
+        self._toks = (C.c_int32 * (2 * n_slots))()
+
+    def close(self):
+        if self._h:
+            self.lib.fmx_scheduler_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def submit(self, prompt, max_tokens: int, temperature: float = 0.0) -> int:
+        """Queues a request (prompt: a sequence of token ids); returns its id."""
+        p = (C.c_int32 * len(prompt))(*[int(t) for t in prompt])
+        rid = C.c_int64()
+        _lib.check(self.lib.fmx_scheduler_submit(self._h, p, len(prompt), max_tokens,
+                                                 float(temperature), C.byref(rid)))
+        return rid.value
+
+    def step(self) -> dict:
+        """One iteration; {request id: [tokens generated in this step]}."""
+        n = C.c_int64()
+        _lib.check(self.lib.fmx_scheduler_step(self._h, self._ids, self._toks, 2 * self.n_slots,
+                                               C.byref(n)))
+        out: dict = {}
+        for i in range(n.value):
+            out.setdefault(self._ids[i], []).append(self._toks[i])
+        return out
+
+    def has_work(self) -> bool:
+        return bool(self.lib.fmx_scheduler_has_work(self._h))
+
+    def active_count(self) -> int:
+        return int(self.lib.fmx_scheduler_active_count(self._h))
+
+    def drain_completed(self) -> list:
+        buf = (C.c_int64 * 256)()
+        n = C.c_int64()
+        out = []
+        while True:
+            _lib.check(self.lib.fmx_scheduler_drain_completed(self._h, buf, 256, C.byref(n)))
+            out.extend(buf[i] for i in range(n.value))
+            if n.value < 256:
+                return out
 
 
 # ------------------------------------------------------------------ synthetic weights

@@ -114,6 +114,21 @@ int fmx_model_forward_traced(const fmx_model_config* cfg, const fmx_model_weight
                              void* logits, void* workspace, size_t workspace_bytes,
                              fmx_stream stream, uint32_t* routing);
 
+/* fmx_model_forward_traced whose sequence b keeps its keys and values in
+ * cache slot cache_slots[b] (device int32 [batch], each < cache_batch and
+ * distinct; clamped to the cache) instead of slot b: the batched decode of
+ * the scheduler (forward_batched_inplace, model.h:116-123, over the slots of
+ * a KV pool) runs any subset of live sequences without copying caches into
+ * a batch cache and back (scheduler.cpp:556-576, :658-678). NULL slots:
+ * slot b; NULL routing: no record. */
+int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weights* w,
+                              const int32_t* input_ids, int64_t batch, int64_t seq_len,
+                              int64_t cache_offset, const int32_t* cache_offsets,
+                              const int32_t* cache_slots, void* kv_cache, int64_t cache_batch,
+                              int64_t cache_max_seq, int logits_last_only, void* logits,
+                              void* workspace, size_t workspace_bytes, fmx_stream stream,
+                              uint32_t* routing);
+
 /* The residual stream after the last layer of the latest forward on this
  * workspace, bf16 [n_tokens, H] (every row when that forward returned the
  * logits of every position; the last position of each sequence otherwise).
@@ -157,6 +172,55 @@ int fmx_model_load(const char* dir, const fmx_model_config* cfg, fmx_loaded_mode
 const fmx_model_weights* fmx_loaded_model_weights(const fmx_loaded_model* model);
 size_t fmx_loaded_model_device_bytes(const fmx_loaded_model* model);
 void fmx_loaded_model_free(fmx_loaded_model* model);
+
+/* ------------------------------------------------------------------------
+ * Batched decode of a server loop (BatchScheduler, scheduler.h:37-99,
+ * scheduler.cpp:19-101, :103-232, :527-680)
+ * --------------------------------------------------------------------- */
+
+/* A KV pool of n_slots slots of max_context positions (KVCachePool,
+ * kv_pool.cpp) with a request queue. Each step admits queued requests while
+ * slots are free (a batch-1 prefill into the slot; the first token is the
+ * argmax of the prompt's last position), then decodes every active request
+ * one greedy token in one fmx_model_forward_batched over the requests' own
+ * slots and offsets (no batch cache is built or flushed), then frees the
+ * slots of requests that reached max_tokens. With at most 16 requests
+ * decoding, every kernel computes a request's row on its own, so its tokens
+ * equal those of the request decoded alone (fmx_model_forward + argmax).
+ * All device memory is allocated at create; `weights` must outlive the
+ * scheduler. Steps and create synchronise `stream`. */
+#define FMX_SCHED_MAX_SLOTS 256
+typedef struct fmx_scheduler fmx_scheduler;
+int fmx_scheduler_create(const fmx_model_config* cfg, const fmx_model_weights* weights,
+                         int64_t n_slots, int64_t max_context, int64_t max_prompt,
+                         fmx_stream stream, fmx_scheduler** out);
+
+/* BatchScheduler::submit (scheduler.cpp:19-23): queues a request, safe to
+ * call from another thread than the one that steps. prompt: host int32 [n],
+ * 1 <= n <= max_prompt, each token < vocab; n + max_tokens <= max_context.
+ * temperature other than 0 (sampling, sampling.cpp) returns
+ * FMX_ERR_UNSUPPORTED. The request's id goes to *request_id. */
+int fmx_scheduler_submit(fmx_scheduler* s, const int32_t* prompt, int64_t n, int64_t max_tokens,
+                         float temperature, int64_t* request_id);
+
+/* BatchScheduler::step (scheduler.cpp:25-85): admit, decode, clean up. The
+ * tokens generated in this step go to (request_ids[i], tokens[i]) for
+ * i < *n_new (a request admitted in this step gets its first token and its
+ * second); capacity >= 2 * n_slots. A request finishes with exactly
+ * max_tokens tokens (the reference decodes one more past its first token
+ * when max_tokens is 1). */
+int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, int64_t capacity,
+                       int64_t* n_new);
+
+/* BatchScheduler::has_work / active_count / drain_completed
+ * (scheduler.cpp:87-101): queued or active requests (1/0); active requests;
+ * ids of requests finished since the last drain (up to capacity, oldest
+ * first). */
+int fmx_scheduler_has_work(fmx_scheduler* s);
+int64_t fmx_scheduler_active_count(const fmx_scheduler* s);
+int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_t capacity,
+                                  int64_t* n);
+void fmx_scheduler_free(fmx_scheduler* s);
 
 /* Greedy next token: ids[b] = argmax_v logits[b * row_stride + v] (the
  * first of equal maxima, as mx::argmax); when offsets is not NULL,

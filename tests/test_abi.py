@@ -284,3 +284,33 @@ def test_model_sizes_and_validation(fmx):
     rc = lib.fmx_model_forward(C.byref(c), C.byref(w), 16, 1, 4, 380, None, 256, 1, 382, 1, 256,
                                256, 1 << 30, None)
     assert rc == _lib.FMX_ERR_SHAPE, lib.fmx_last_error()
+
+
+def test_scheduler_validation(fmx):
+    """Scheduler entry points without a GPU: pool shapes outside the limits
+    and NULL handles are refused before any allocation."""
+    from flashmlx_amd import _lib
+    from flashmlx_amd.model import ModelConfig
+    lib = _lib.load()
+    c = ModelConfig(max_position_embeddings=512).to_c()
+    w = _lib.FmxModelWeights()
+    h = C.c_void_p()
+    for n_slots, max_ctx, max_prompt in ((0, 64, 8), (257, 64, 8), (4, 8, 8), (4, 64, 0)):
+        rc = lib.fmx_scheduler_create(C.byref(c), C.byref(w), n_slots, max_ctx, max_prompt, None, C.byref(h))
+        assert rc == _lib.FMX_ERR_SHAPE, (n_slots, max_ctx, max_prompt)
+        assert not h.value
+    # a context beyond the attention kernel's cache limit
+    rc = lib.fmx_scheduler_create(C.byref(c), C.byref(w), 4, 8192, 8, None, C.byref(h))
+    assert rc == _lib.FMX_ERR_UNSUPPORTED
+    assert lib.fmx_scheduler_create(None, C.byref(w), 4, 64, 8, None, C.byref(h)) == _lib.FMX_ERR_ARG
+    assert lib.fmx_scheduler_has_work(None) == 0
+    assert lib.fmx_scheduler_active_count(None) == 0
+    n = C.c_int64()
+    assert lib.fmx_scheduler_drain_completed(None, None, 0, C.byref(n)) == _lib.FMX_ERR_ARG
+    p = (C.c_int32 * 1)(0)
+    rid = C.c_int64()
+    assert lib.fmx_scheduler_submit(None, p, 1, 1, 0.0, C.byref(rid)) == _lib.FMX_ERR_ARG
+    ids = (C.c_int64 * 2)()
+    toks = (C.c_int32 * 2)()
+    assert lib.fmx_scheduler_step(None, ids, toks, 2, C.byref(n)) == _lib.FMX_ERR_ARG
+    lib.fmx_scheduler_free(None)
