@@ -370,7 +370,7 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
 
 # The 24-layer Qwen1.5-MoE-A2.7B-shape decoder stack (random-init 4-bit
 # weights, seed 5): a 256-token prompt, then 128 greedy tokens, at batch 1 and 4
-STACK_CONFIGS = {"c4_stack_b1": 1, "c4_stack_b4": 4}
+STACK_CONFIGS = {"c4_stack_b1": 1, "c4_stack_b4": 4, "c4_stack_b8": 8}
 STACK_PROMPT, STACK_NEW, STACK_SEED = 256, 128, 5
 
 
@@ -480,12 +480,50 @@ def measure_stack(batches, trials: int, cpu_seconds: float):
                                  f"mean {np.mean(uniq):.1f}"},
         }
         log(f"stack B={B}: prefill {pm:.2f} ms, decode {step_ms * 1e3:.1f} us/step")
+        res[f"c4_stack_b{B}"]["scheduler"] = measure_scheduler(cfg, w, prompt, ref, max_seq)
         del dm, gp, gs
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
     if cpu_seconds > 0:
         res["c4_stack_b1"]["cpu_baseline"] = stack_cpu_baseline(cfg, w, cpu_seconds)
     return res
+
+
+def measure_scheduler(cfg, w, prompt, ref, max_seq: int) -> dict:
+    """The same B requests through the native server loop (BatchScheduler:
+    batch-1 prefills into pool slots, then batched decode steps with a host
+    round trip per step): wall-clock tok/s of the whole run, the decode
+    steps' mean wall time once every request is admitted, and whether each
+    request's tokens equal the batched generation's."""
+    from flashmlx_amd import model as M
+
+    B = prompt.shape[0]
+    rows = prompt.cpu().numpy().tolist()
+    sched = M.BatchScheduler(cfg, w, B, max_seq, STACK_PROMPT)
+    out = {}
+    runs = []
+    for _ in range(2):  # the first run captures the decode graph
+        ids = [sched.submit(r, STACK_NEW) for r in rows]
+        toks = {i: [] for i in ids}
+        t0 = time.perf_counter()
+        steps = []
+        while sched.has_work():
+            ts = time.perf_counter()
+            for rid, t in sched.step().items():
+                toks[rid].extend(t)
+            steps.append(time.perf_counter() - ts)
+        wall = time.perf_counter() - t0
+        sched.drain_completed()
+        runs.append((wall, steps[1:], toks, ids))
+    wall, dsteps, toks, ids = runs[-1]
+    want = ref.cpu().numpy()
+    out["tok_s"] = round(B * STACK_NEW / wall, 1)
+    out["wall_ms"] = round(wall * 1e3, 2)
+    out["decode_ms_per_step_wall"] = round(1e3 * sum(dsteps) / max(len(dsteps), 1), 4)
+    out["tokens_equal_batched_generate"] = all(toks[i] == want[b].tolist() for b, i in enumerate(ids))
+    sched.close()
+    log(f"scheduler B={B}: {out['tok_s']} tok/s, decode step {out['decode_ms_per_step_wall']} ms wall")
+    return out
 
 
 def stack_cpu_baseline(cfg, w, seconds: float):
@@ -534,7 +572,7 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB")
     ap.add_argument("--stack", default="all",
                     help="decoder-stack configs measured in the same run: all, none or a comma list "
-                         "(c4_stack_b1, c4_stack_b4)")
+                         "(c4_stack_b1, c4_stack_b4, c4_stack_b8)")
     ap.add_argument("--stack-trials", type=int, default=5)
     args = ap.parse_args()
 

@@ -84,11 +84,19 @@ struct fmx_scheduler {
   std::vector<int> free_slots;
   std::mutex completed_mu;
   std::vector<int64_t> completed;
+  // decode step of batch B (forward + argmax) as a HIP graph, captured on
+  // the second step of that batch size; its inputs are the device ids,
+  // offsets and slots, refilled before every launch
+  std::vector<hipGraphExec_t> graphs;
+  std::vector<int> uses;
   ~fmx_scheduler() {
+    for (hipGraphExec_t g : graphs)
+      if (g) (void)hipGraphExecDestroy(g);
     for (void* p : {kv, ws, logits, static_cast<void*>(d_ids), static_cast<void*>(d_offs),
                     static_cast<void*>(d_slots), static_cast<void*>(d_next)})
       if (p) (void)hipFree(p);
     if (h_buf) (void)hipHostFree(h_buf);
+    if (stream) (void)hipStreamDestroy(stream);
   }
 };
 
@@ -126,9 +134,33 @@ int decode(fmx_scheduler& s, const std::vector<Request*>& live) {
   FMX_HIP(hipMemcpyAsync(s.d_ids, h, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
   FMX_HIP(hipMemcpyAsync(s.d_offs, h + B, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
   FMX_HIP(hipMemcpyAsync(s.d_slots, h + 2 * B, static_cast<size_t>(B * 4), hipMemcpyHostToDevice, s.stream));
-  FMX_RC(fmx_model_forward_batched(&s.cfg, s.w, s.d_ids, B, 1, 0, s.d_offs, s.d_slots, s.kv, s.n_slots,
-                                   s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
-  FMX_RC(fmx_greedy_next(s.logits, B, s.V, s.V, s.d_next, nullptr, 0, s.stream));
+  auto launch = [&]() -> int {
+    FMX_RC(fmx_model_forward_batched(&s.cfg, s.w, s.d_ids, B, 1, 0, s.d_offs, s.d_slots, s.kv, s.n_slots,
+                                     s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
+    return fmx_greedy_next(s.logits, B, s.V, s.V, s.d_next, nullptr, 0, s.stream);
+  };
+  hipGraphExec_t& exec = s.graphs[static_cast<size_t>(B)];
+  if (!exec && ++s.uses[static_cast<size_t>(B)] >= 2) {
+    FMX_HIP(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+    const int rc = launch();
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s.stream, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    if (e != hipSuccess) return fail(FMX_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    const hipError_t ei = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (ei != hipSuccess) {
+      exec = nullptr;
+      return fail(FMX_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(ei));
+    }
+  }
+  if (exec)
+    FMX_HIP(hipGraphLaunch(exec, s.stream));
+  else
+    FMX_RC(launch());
   int32_t* back = h + 3 * B;
   FMX_HIP(hipMemcpyAsync(back, s.d_next, static_cast<size_t>(B * 4), hipMemcpyDeviceToHost, s.stream));
   FMX_HIP(hipStreamSynchronize(s.stream));
@@ -161,13 +193,18 @@ int fmx_scheduler_create(const fmx_model_config* cfg, const fmx_model_weights* w
   auto s = new fmx_scheduler();
   s->cfg = *cfg;
   s->w = w;
-  s->stream = static_cast<hipStream_t>(stream);
+  s->graphs.assign(static_cast<size_t>(n_slots + 1), nullptr);
+  s->uses.assign(static_cast<size_t>(n_slots + 1), 0);
   s->n_slots = n_slots;
   s->max_context = max_context;
   s->max_prompt = max_prompt;
   s->V = cfg->vocab_size;
   s->ws_bytes = wsb;
   auto body = [&]() -> int {
+    // the weights are ready once the caller's stream is; the scheduler
+    // works on a stream of its own (a capturable one)
+    FMX_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    FMX_HIP(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking));
     FMX_HIP(hipMalloc(&s->kv, kv));
     FMX_HIP(hipMalloc(&s->ws, wsb));
     FMX_HIP(hipMalloc(&s->logits, static_cast<size_t>(n_slots * s->V * 2)));
@@ -177,7 +214,7 @@ int fmx_scheduler_create(const fmx_model_config* cfg, const fmx_model_weights* w
     FMX_HIP(hipMalloc(reinterpret_cast<void**>(&s->d_next), static_cast<size_t>(n_slots * 4)));
     FMX_HIP(hipHostMalloc(reinterpret_cast<void**>(&s->h_buf),
                           static_cast<size_t>((max_tokens + 4 * n_slots + 4) * 4), hipHostMallocDefault));
-    FMX_RC(fmx_model_workspace_init(cfg, s->ws, wsb, stream));
+    FMX_RC(fmx_model_workspace_init(cfg, s->ws, wsb, s->stream));
     FMX_HIP(hipStreamSynchronize(s->stream));
     for (int64_t i = n_slots - 1; i >= 0; --i) s->free_slots.push_back(static_cast<int>(i));
     return FMX_OK;

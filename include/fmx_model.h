@@ -188,7 +188,10 @@ void fmx_loaded_model_free(fmx_loaded_model* model);
  * decoding, every kernel computes a request's row on its own, so its tokens
  * equal those of the request decoded alone (fmx_model_forward + argmax).
  * All device memory is allocated at create; `weights` must outlive the
- * scheduler. Steps and create synchronise `stream`. */
+ * scheduler. create waits for `stream` (the one the weights were made on);
+ * the scheduler then works on a stream of its own, and each step returns
+ * with its work finished. The decode step of each batch size runs as a HIP
+ * graph from the second time that size occurs. */
 #define FMX_SCHED_MAX_SLOTS 256
 typedef struct fmx_scheduler fmx_scheduler;
 int fmx_scheduler_create(const fmx_model_config* cfg, const fmx_model_weights* weights,
