@@ -565,6 +565,233 @@ static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Nemotron-H MoE block                                                      */
+/* ------------------------------------------------------------------------ */
+
+float orc_sigmoid_f32(uint16_t logit) {
+  return (float)(1.0 / (1.0 + orc_exp(-(double)bf(logit))));
+}
+
+/* nemotron_h.cpp:1022-1049 for one token: lg [E] bf16 logits in; inds, scores out */
+static void nh_select(const orc_nh_cfg* c, const uint16_t* lg, const float* cbias, float* orig,
+                      float* sel, unsigned char* taken, uint32_t* inds, float* scores) {
+  const int64_t E = c->n_experts;
+  const int k = c->top_k;
+  for (int64_t e = 0; e < E; ++e) {
+    orig[e] = orc_sigmoid_f32(lg[e]);
+    sel[e] = cbias ? orig[e] + cbias[e] : orig[e];
+  }
+  if (c->n_group > 1) {
+    /* group score: the two largest sel of the group, added (:1031) */
+    const int64_t G = E / c->n_group;
+    float gs[1024];
+    for (int g = 0; g < c->n_group; ++g) {
+      float m1 = -INFINITY, m2 = -INFINITY;
+      for (int64_t e = g * G; e < (g + 1) * G; ++e) {
+        if (sel[e] > m1) {
+          m2 = m1;
+          m1 = sel[e];
+        } else if (sel[e] > m2) {
+          m2 = sel[e];
+        }
+      }
+      gs[g] = m1 + m2;
+    }
+    /* the topk_group best groups stay (group score desc, index asc); the
+     * others' experts get selection score 0 (:1032-1039) */
+    unsigned char keep[1024];
+    memset(keep, 0, sizeof keep);
+    for (int r = 0; r < c->topk_group; ++r) {
+      int best = -1;
+      for (int g = 0; g < c->n_group; ++g)
+        if (!keep[g] && (best < 0 || gs[g] > gs[best])) best = g;
+      keep[best] = 1;
+    }
+    for (int g = 0; g < c->n_group; ++g)
+      if (!keep[g])
+        for (int64_t e = g * G; e < (g + 1) * G; ++e) sel[e] = 0.0f;
+  }
+  /* top-k of sel (:1042-1043), ties to the lower index */
+  memset(taken, 0, (size_t)E);
+  for (int j = 0; j < k; ++j) {
+    int64_t best = -1;
+    for (int64_t e = 0; e < E; ++e)
+      if (!taken[e] && (best < 0 || sel[e] > sel[best])) best = e;
+    taken[best] = 1;
+    inds[j] = (uint32_t)best;
+  }
+  /* scores from the unbiased sigmoid (:1044-1049) */
+  float den = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    scores[j] = orig[inds[j]];
+    den += scores[j];
+  }
+  if (c->norm_topk && k > 1) {
+    den += 1e-20f;
+    for (int j = 0; j < k; ++j) scores[j] = scores[j] / den;
+  }
+  for (int j = 0; j < k; ++j) scores[j] = scores[j] * c->scaling;
+}
+
+static int nh_cfg_ok(const orc_nh_cfg* c) {
+  if (c->group_size != 64 || c->bits != 4 || c->hidden % 64 || c->inter % 64 ||
+      (c->shared_inter && c->shared_inter % 64))
+    return 0;
+  if (c->top_k < 1 || c->top_k > c->n_experts || c->n_experts > 1024) return 0;
+  if (c->n_group < 1 || c->n_group > 1024 || c->n_experts % c->n_group) return 0;
+  if (c->n_group > 1 && (c->n_experts / c->n_group < 2 || c->topk_group < 1 || c->topk_group > c->n_group))
+    return 0;
+  return 1;
+}
+
+int orc_nh_route(const orc_nh_cfg* c, const uint16_t* x, int64_t T, const uint16_t* gate_w,
+                 const float* cbias, uint16_t* logits, uint32_t* inds, float* scores) {
+  if (!nh_cfg_ok(c)) return -1;
+  const int64_t E = c->n_experts, H = c->hidden;
+  int rc = 0;
+#pragma omp parallel
+  {
+    uint16_t* lg = (uint16_t*)malloc(sizeof(uint16_t) * E);
+    float* orig = (float*)malloc(sizeof(float) * E);
+    float* sel = (float*)malloc(sizeof(float) * E);
+    unsigned char* taken = (unsigned char*)malloc(E);
+    if (!lg || !orig || !sel || !taken) {
+#pragma omp atomic write
+      rc = -3;
+    } else {
+#pragma omp for schedule(static)
+      for (int64_t t = 0; t < T; ++t) {
+        for (int64_t e = 0; e < E; ++e) lg[e] = bf16_dot_exact(x + t * H, gate_w + e * H, H);
+        nh_select(c, lg, cbias, orig, sel, taken, inds + t * c->top_k, scores + t * c->top_k);
+        if (logits) memcpy(logits + t * E, lg, sizeof(uint16_t) * E);
+      }
+    }
+    free(lg);
+    free(orig);
+    free(sel);
+    free(taken);
+  }
+  return rc;
+}
+
+/* out[n] = a[K] (fp32) . deq(W[n]) for n < N, fp32 (gather_qmm / quantized_matmul
+ * of an fp32 input: the dequantised weights and the accumulation in fp32) */
+static void qmv_f32(const float* a, int64_t K, const uint32_t* w, const uint16_t* s,
+                    const uint16_t* b, int64_t N, int mode, float* out) {
+  const int64_t G = K / 64;
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    const uint32_t* wr = w + n * (K / 8);
+    const uint16_t* sr = s + n * G;
+    const uint16_t* br = b + n * G;
+    if (mode == ORC_ACC_F64) {
+      double acc = 0.0;
+      for (int64_t i = 0; i < K; ++i) {
+        const double q = (double)((wr[i / 8] >> (4 * (i % 8))) & 15u);
+        acc += (double)a[i] * ((double)bf(sr[i / 64]) * q + (double)bf(br[i / 64]));
+      }
+      out[n] = (float)acc;
+    } else {
+      float acc = 0.0f;
+      for (int64_t i = 0; i < K; ++i) {
+        const float q = (float)((wr[i / 8] >> (4 * (i % 8))) & 15u);
+        const float wv = bf(sr[i / 64]) * q + bf(br[i / 64]);
+        acc += a[i] * wv;
+      }
+      out[n] = acc;
+    }
+  }
+}
+
+/* relu2 (nemotron_h.cpp:54-63) of a bf16 row: fp32, exact */
+static void relu2_row(const uint16_t* h, int64_t n, float* a) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = bf(h[i]) > 0.0f ? bf(h[i]) : 0.0f;
+    a[i] = v * v;
+  }
+}
+
+int orc_nh_moe_block(const orc_nh_cfg* c, const orc_nh_weights* w, const uint16_t* x, int64_t T,
+                     int mode, const uint32_t* forced, uint16_t* y, uint32_t* inds_out,
+                     float* scores_out) {
+  if (!nh_cfg_ok(c) || (mode != ORC_ACC_F64 && mode != ORC_ACC_A)) return -1;
+  const int64_t H = c->hidden, E = c->n_experts, I = c->inter, Is = c->shared_inter;
+  const int k = c->top_k;
+  uint32_t* inds = (uint32_t*)malloc(sizeof(uint32_t) * T * k);
+  float* scores = (float*)malloc(sizeof(float) * T * k);
+  uint16_t* lg = (uint16_t*)malloc(sizeof(uint16_t) * T * E);
+  const int64_t Imax = I > Is ? I : Is;
+  uint16_t* hb = (uint16_t*)malloc(sizeof(uint16_t) * Imax);
+  float* a = (float*)malloc(sizeof(float) * Imax);
+  float* d = (float*)malloc(sizeof(float) * H);
+  float* acc = (float*)malloc(sizeof(float) * H);
+  float* orig = (float*)malloc(sizeof(float) * E);
+  float* sel = (float*)malloc(sizeof(float) * E);
+  unsigned char* taken = (unsigned char*)malloc(E);
+  if (!inds || !scores || !lg || !hb || !a || !d || !acc || !orig || !sel || !taken) return -3;
+  int rc = orc_nh_route(c, x, T, w->gate_w, w->cbias, lg, inds, scores);
+  if (rc) return rc;
+  if (forced) {
+    /* the given choice, scored as the router scores its own (:1044-1049) */
+    orc_nh_cfg one = *c;
+    for (int64_t t = 0; t < T; ++t) {
+      float den = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        uint32_t e = forced[t * k + j];
+        if (e >= (uint32_t)E) e = (uint32_t)(E - 1);
+        inds[t * k + j] = e;
+        scores[t * k + j] = orc_sigmoid_f32(lg[t * E + e]);
+        den += scores[t * k + j];
+      }
+      if (one.norm_topk && k > 1) {
+        den += 1e-20f;
+        for (int j = 0; j < k; ++j) scores[t * k + j] = scores[t * k + j] / den;
+      }
+      for (int j = 0; j < k; ++j) scores[t * k + j] = scores[t * k + j] * one.scaling;
+    }
+  }
+  const int64_t wst1 = I * (H / 8), sst1 = I * (H / 64);
+  const int64_t wst2 = H * (I / 8), sst2 = H * (I / 64);
+  for (int64_t t = 0; t < T; ++t) {
+    const uint16_t* xt = x + t * H;
+    for (int64_t h = 0; h < H; ++h) acc[h] = 0.0f;
+    /* switch_mlp: fc1 -> relu2 -> fc2 (:1086-1094), the weighted sum (:1098-1099) */
+    for (int j = 0; j < k; ++j) {
+      const int64_t e = inds[t * k + j];
+      qmv(xt, H, w->fc1_w + e * wst1, w->fc1_s + e * sst1, w->fc1_b + e * sst1, I, mode, hb);
+      relu2_row(hb, I, a);
+      qmv_f32(a, I, w->fc2_w + e * wst2, w->fc2_s + e * sst2, w->fc2_b + e * sst2, H, mode, d);
+      const float sc = scores[t * k + j];
+      for (int64_t h = 0; h < H; ++h) {
+        const float p = d[h] * sc;
+        acc[h] = acc[h] + p;
+      }
+    }
+    for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(acc[h]);
+    if (Is > 0) {
+      /* shared expert (:1102-1108): up -> relu2 -> down, added in fp32 */
+      qmv(xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, hb);
+      relu2_row(hb, Is, a);
+      qmv_f32(a, Is, w->sh_down_w, w->sh_down_s, w->sh_down_b, H, mode, d);
+      for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(bf(y[t * H + h]) + d[h]);
+    }
+  }
+  if (inds_out) memcpy(inds_out, inds, sizeof(uint32_t) * T * k);
+  if (scores_out) memcpy(scores_out, scores, sizeof(float) * T * k);
+  free(inds);
+  free(scores);
+  free(lg);
+  free(hb);
+  free(a);
+  free(d);
+  free(acc);
+  free(orig);
+  free(sel);
+  free(taken);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* decoder stack pieces                                                      */
 /* ------------------------------------------------------------------------ */
 

@@ -47,6 +47,16 @@
  *                                        composition of rotations, numpy complex
  *                                        rotation; MLX's rounding points inside
  *                                        rope (bf16 vs fp32 angles) are UNPINNED
+ *   orc_nh_route                         top-k of the logits (sigmoid is monotone)
+ *                                        against numpy; numpy sigmoid within 1 fp32
+ *                                        ulp; group-limited and bias cases by
+ *                                        constructed inputs with known answers;
+ *                                        renormalised scores sum to the scaling
+ *   orc_nh_moe_block                     dense numpy fp64 formula on tiny shapes;
+ *                                        scaling 2 doubles y exactly; fc1 rows all
+ *                                        negative leave y = shared expert alone.
+ *                                        MLX's fp32 sigmoid (its own exp) and
+ *                                        argpartition's tie order are UNPINNED
  *   orc_sdpa                             one key = v, equal keys = mean of values,
  *                                        causal prefix, numpy fp64 softmax(QK^T)V;
  *                                        MLX's intermediate roundings UNPINNED
@@ -176,6 +186,59 @@ int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_
 int orc_moe_block_routed(const orc_moe_cfg* cfg, const orc_moe_weights* w,
                          const uint16_t* x, int64_t T, int mode, const uint32_t* inds,
                          uint16_t* y, uint16_t* scores_out);
+
+/* ---- Nemotron-H MoE block (nemotron_h.cpp:1010-1111) ------------------- */
+/* fp32(sigmoid(l)) of a bf16 logit: 1 / (1 + orc_exp(-l)) in fp64, rounded
+ * once to fp32 (mx::sigmoid of the fp32 cast logits, nemotron_h.cpp:1024). */
+float orc_sigmoid_f32(uint16_t logit);
+
+typedef struct {
+  int64_t hidden;        /* H */
+  int64_t n_experts;     /* E (n_routed_experts) */
+  int     top_k;         /* k */
+  int     norm_topk;     /* s / (sum(s) + 1e-20) when k > 1 */
+  int64_t inter;         /* I (moe_intermediate_size) */
+  int64_t shared_inter;  /* Is (moe_shared_expert_intermediate_size), 0 = none */
+  int     n_group;       /* expert groups (1: no group limit) */
+  int     topk_group;    /* groups kept */
+  float   scaling;       /* routed_scaling_factor */
+  int     group_size;    /* 64 */
+  int     bits;          /* 4 */
+} orc_nh_cfg;
+
+typedef struct {
+  const uint16_t* gate_w;  /* [E, H] bf16 router (mixer.gate.weight) */
+  const float* cbias;      /* [E] fp32 e_score_correction_bias or NULL */
+  const uint32_t* fc1_w;   const uint16_t* fc1_s;   const uint16_t* fc1_b;   /* [E, I, ..] */
+  const uint32_t* fc2_w;   const uint16_t* fc2_s;   const uint16_t* fc2_b;   /* [E, H, ..] */
+  const uint32_t* sh_up_w; const uint16_t* sh_up_s; const uint16_t* sh_up_b; /* [Is, ..] */
+  const uint32_t* sh_down_w; const uint16_t* sh_down_s; const uint16_t* sh_down_b; /* [H, ..] */
+} orc_nh_weights;
+
+/* The router (nemotron_h.cpp:1017-1050): logits = bf16(x . gate_w^T) (exact
+ * sum, one rounding); orig = orc_sigmoid_f32(logit); sel = orig + cbias
+ * (fp32); with n_group > 1 the groups (E / n_group consecutive experts) are
+ * scored by the sum of their two largest sel and every expert outside the
+ * topk_group best groups (ties: lower group index kept) gets sel = 0; the
+ * k largest sel are selected (ties: lower expert index; slots ordered sel
+ * desc, index asc); scores = orig of the selected, / (sum in slot order +
+ * 1e-20) when norm_topk and k > 1, then * scaling, all fp32. logits [T, E]
+ * may be NULL. */
+int orc_nh_route(const orc_nh_cfg* cfg, const uint16_t* x, int64_t T, const uint16_t* gate_w,
+                 const float* cbias, uint16_t* logits, uint32_t* inds, float* scores);
+
+/* The block (nemotron_h.cpp:1052-1111): for each selected expert, h =
+ * bf16(x . fc1^T) (a quantized product, `mode` as orc_qmm_t: ORC_ACC_F64
+ * or ORC_ACC_A), a = relu(h)^2 in fp32 (compiled relu2, nemotron_h.cpp:54-63:
+ * maximum with a fp32 0 promotes to fp32), d = a . fc2^T with fp32 input and
+ * output; routed = bf16(sum over slots, fp32 in slot order, of d * score);
+ * the shared expert the same way without routing, and y = bf16(routed +
+ * shared) (fp32 add). inds: the expert choice to use instead of the
+ * router's (NULL: the router's); scores are then recomputed for it.
+ * inds_out / scores_out [T, k] may be NULL. */
+int orc_nh_moe_block(const orc_nh_cfg* cfg, const orc_nh_weights* w, const uint16_t* x, int64_t T,
+                     int mode, const uint32_t* inds, uint16_t* y, uint32_t* inds_out,
+                     float* scores_out);
 
 /* threads used by the OpenMP loops (0 = leave the runtime default) */
 void orc_set_threads(int n);

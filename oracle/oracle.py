@@ -55,6 +55,28 @@ class _W(C.Structure):
         "router_s", "router_b", "sh_expert_gate_s", "sh_expert_gate_b")]
 
 
+class _NhCfg(C.Structure):
+    _fields_ = [
+        ("hidden", C.c_int64),
+        ("n_experts", C.c_int64),
+        ("top_k", C.c_int),
+        ("norm_topk", C.c_int),
+        ("inter", C.c_int64),
+        ("shared_inter", C.c_int64),
+        ("n_group", C.c_int),
+        ("topk_group", C.c_int),
+        ("scaling", C.c_float),
+        ("group_size", C.c_int),
+        ("bits", C.c_int),
+    ]
+
+
+class _NhW(C.Structure):
+    _fields_ = [(n, _vp) for n in (
+        "gate_w", "cbias", "fc1_w", "fc1_s", "fc1_b", "fc2_w", "fc2_s", "fc2_b",
+        "sh_up_w", "sh_up_s", "sh_up_b", "sh_down_w", "sh_down_s", "sh_down_b")]
+
+
 def load() -> C.CDLL:
     global _lib
     if _lib is None:
@@ -91,6 +113,11 @@ def load() -> C.CDLL:
         lib.orc_sdpa.argtypes = [_vp, i64, i64, i64, _vp, _vp, i64, i64, i64, C.c_float, _vp]
         lib.orc_moe_block_routed.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp,
                                              _vp, _vp]
+        lib.orc_sigmoid_f32.restype = C.c_float
+        lib.orc_sigmoid_f32.argtypes = [C.c_uint16]
+        lib.orc_nh_route.argtypes = [C.POINTER(_NhCfg), _vp, i64, _vp, _vp, _vp, _vp, _vp]
+        lib.orc_nh_moe_block.argtypes = [C.POINTER(_NhCfg), C.POINTER(_NhW), _vp, i64, C.c_int, _vp,
+                                         _vp, _vp, _vp]
         lib.orc_set_threads.argtypes = [C.c_int]
         lib.orc_get_threads.restype = C.c_int
         _lib = lib
@@ -417,3 +444,71 @@ class DecoderStack:
         n = rms_norm(h, w["norm_w"], c["eps"])
         logits = qmm_t(n, *w["lm_head"], mode=mode)
         return (logits, hid) if return_hidden else logits
+
+
+# ---------------------------------------------------------------- Nemotron-H MoE block
+
+def _nh_cfg(cfg: dict) -> _NhCfg:
+    return _NhCfg(cfg["hidden"], cfg["n_experts"], cfg["top_k"], int(cfg.get("norm_topk", True)),
+                  cfg["inter"], cfg.get("shared_inter", 0), cfg.get("n_group", 1),
+                  cfg.get("topk_group", 1), float(cfg.get("scaling", 1.0)), 64, 4)
+
+
+def sigmoid_f32(logit_bf16: int) -> float:
+    return load().orc_sigmoid_f32(int(logit_bf16))
+
+
+def nh_route(cfg: dict, x, gate_w, cbias=None):
+    """Nemotron-H router (nemotron_h.cpp:1017-1050) -> logits [T, E] bf16 bits,
+    inds [T, k] u32, scores [T, k] fp32. cbias: fp32 [E] or None."""
+    x, gw = _c(x, np.uint16), _c(gate_w, np.uint16)
+    H, E, k = cfg["hidden"], cfg["n_experts"], cfg["top_k"]
+    T = x.size // H
+    cb = None if cbias is None else _c(np.asarray(cbias, dtype=np.float32), np.float32)
+    logits = np.empty((T, E), np.uint16)
+    inds = np.empty((T, k), np.uint32)
+    scores = np.empty((T, k), np.float32)
+    c = _nh_cfg(cfg)
+    rc = load().orc_nh_route(C.byref(c), _p(x), T, _p(gw), _p(cb), _p(logits), _p(inds), _p(scores))
+    assert rc == 0, rc
+    return logits, inds, scores
+
+
+def nh_moe_block(cfg: dict, w: dict, x, mode=ACC_F64, inds=None):
+    """Nemotron-H MoE block (nemotron_h.cpp:1010-1111). cfg keys: hidden,
+    n_experts, top_k, norm_topk, inter, shared_inter, n_group, topk_group,
+    scaling. w keys: gate_w (bf16 [E, H]), cbias (fp32 [E] or None), fc1, fc2,
+    shared_up, shared_down ((wq, s, b) tuples; the shared ones optional).
+    inds [T, k]: that expert choice. Returns (y [T, H] bf16, inds, scores fp32)."""
+    x = _c(x, np.uint16)
+    H, k = cfg["hidden"], cfg["top_k"]
+    T = x.size // H
+    keep = []
+
+    def ptr(a, dt):
+        if a is None:
+            return None
+        a = _c(a, dt)
+        keep.append(a)
+        return a.ctypes.data
+
+    ww = _NhW()
+    ww.gate_w = ptr(w["gate_w"], np.uint16)
+    cb = w.get("cbias")
+    ww.cbias = ptr(None if cb is None else np.asarray(cb, dtype=np.float32), np.float32)
+    for nm, key in (("fc1", "fc1"), ("fc2", "fc2"), ("sh_up", "shared_up"), ("sh_down", "shared_down")):
+        t = w.get(key)
+        if t is None:
+            continue
+        setattr(ww, nm + "_w", ptr(t[0], np.uint32))
+        setattr(ww, nm + "_s", ptr(t[1], np.uint16))
+        setattr(ww, nm + "_b", ptr(t[2], np.uint16))
+    c = _nh_cfg(cfg)
+    y = np.zeros((T, H), np.uint16)
+    inds_out = np.empty((T, k), np.uint32)
+    scores = np.empty((T, k), np.float32)
+    forced = None if inds is None else _c(np.asarray(inds, dtype=np.uint32).reshape(T, k), np.uint32)
+    rc = load().orc_nh_moe_block(C.byref(c), C.byref(ww), _p(x), T, mode, _p(forced), _p(y),
+                                 _p(inds_out), _p(scores))
+    assert rc == 0, rc
+    return y, inds_out, scores
