@@ -105,6 +105,35 @@ class FmxModelWeights(C.Structure):
     ]
 
 
+class FmxNhMoEConfig(C.Structure):
+    _fields_ = [
+        ("hidden_size", C.c_int64),
+        ("n_routed_experts", C.c_int64),
+        ("num_experts_per_tok", C.c_int32),
+        ("norm_topk_prob", C.c_int32),
+        ("moe_intermediate_size", C.c_int64),
+        ("moe_shared_expert_intermediate_size", C.c_int64),
+        ("n_group", C.c_int32),
+        ("topk_group", C.c_int32),
+        ("routed_scaling_factor", C.c_float),
+        ("quant_bits", C.c_int32),
+        ("quant_group_size", C.c_int32),
+    ]
+
+
+class FmxNhMoEWeights(C.Structure):
+    _fields_ = [
+        ("gate_w", C.c_void_p),
+        ("correction_bias", C.c_void_p),
+        ("fc1", FmxQWeight),
+        ("fc2", FmxQWeight),
+        ("shared_up", FmxQWeight),
+        ("shared_down", FmxQWeight),
+        ("packed", C.c_void_p),
+        ("packed_bytes", C.c_size_t),
+    ]
+
+
 class FmxError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
@@ -235,6 +264,15 @@ _SIGS = {
     "fmx_scheduler_drain_completed": (
         C.c_int, [C.c_void_p, P(C.c_int64), C.c_int64, P(C.c_int64)]),
     "fmx_scheduler_free": (None, [C.c_void_p]),
+    "fmx_nh_moe_packed_size": (C.c_size_t, [P(FmxNhMoEConfig)]),
+    "fmx_nh_pack_expert_weights": (
+        C.c_int, [P(FmxNhMoEConfig), P(FmxNhMoEWeights), C.c_void_p, C.c_size_t, C.c_void_p]),
+    "fmx_nh_moe_workspace_size": (C.c_size_t, [P(FmxNhMoEConfig), C.c_int64]),
+    "fmx_nh_moe_block_forward": (
+        C.c_int, [P(FmxNhMoEConfig), P(FmxNhMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                  C.c_size_t, C.c_void_p]),
+    "fmx_nh_moe_workspace_routing": (
+        C.c_int, [P(FmxNhMoEConfig), C.c_int64, C.c_void_p, P(C.c_void_p), P(C.c_void_p), P(C.c_void_p)]),
 }
 
 EXPORTED = tuple(_SIGS)

@@ -30,6 +30,7 @@ SOURCES = [
     "csrc/fmx_model.cpp",
     "csrc/fmx_loader.cpp",
     "csrc/fmx_sched.cpp",
+    "csrc/fmx_nh.cpp",
 ]
 
 ARCH = os.environ.get("FMX_OFFLOAD_ARCH", "gfx950")

@@ -84,6 +84,46 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Nemotron-H (nemotron_h.cpp:1096-1108): y = astype(sum(h * scores, -2),
+// bf16) with h and the scores fp32 (the product and the k-sum in fp32, slot
+// order, each operation rounded on its own: __fmul_rn / __fadd_rn keep the
+// compiler from contracting them), then + shared (fp32 add), rounded to bf16.
+__global__ __launch_bounds__(kElemThreads) void nh_combine_kernel(NhCombineArgs a) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
+  const int quads = a.H / 4;
+  if (gid >= static_cast<int64_t>(a.T) * quads) return;
+  const int t = static_cast<int>(gid / quads), o = static_cast<int>(gid % quads);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < a.k; ++j) {
+    const int64_t ent = static_cast<int64_t>(t) * a.k + j;
+    const uint32_t row = min(a.inv[ent], static_cast<uint32_t>(a.T * a.k - 1));
+    const float s = a.scores[ent];
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.d + static_cast<int64_t>(row) * a.H + o * 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], s));
+  }
+  float out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) out[i] = round_bf16(acc[i]);
+  if (a.sd) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.sd + static_cast<int64_t>(t) * a.H + o * 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __fadd_rn(out[i], v[i]);
+  }
+  u32x2_t w;
+  w[0] = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
+  w[1] = static_cast<uint32_t>(f32_to_bf16(out[2])) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
+  *reinterpret_cast<u32x2_t*>(a.y + static_cast<int64_t>(t) * a.H + o * 4) = w;
+}
+
+hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream) {
+  const int64_t n = static_cast<int64_t>(a.T) * (a.H / 4);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(nh_combine_kernel, dim3(grid_for(n, kElemThreads)), dim3(kElemThreads), 0,
+                     stream, a);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ layouts
 __global__ __launch_bounds__(kElemThreads) void permute_p8_kernel(const uint16_t* x, int64_t n_oct,
                                                                   uint16_t* xp) {

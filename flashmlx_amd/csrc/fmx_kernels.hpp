@@ -78,6 +78,13 @@ struct RouterArgs {
   int cols_per_wave;       // 1 (one token tile: decode) or 4 (prefill)
   int fuse_sort;           // last workgroup sorts inds (needs router_sort_fits)
   SortOut sort;
+  // topk_kernel's selection: 0 = softmax (probs, scores bf16); 1 = the
+  // Nemotron-H router: sigmoid, correction bias, group limit, fp32 scores
+  int mode;
+  int n_group, topk_group; // groups of E / n_group experts; groups kept
+  float scaling;           // routed_scaling_factor
+  const float* cbias;      // [E] correction bias or null
+  float* scores32;         // [T, k] fp32 scores (mode 1)
 };
 bool router_sort_fits(int64_t n, int64_t E);
 hipError_t launch_router(const RouterArgs& a, hipStream_t stream);
@@ -209,6 +216,12 @@ struct PfSet {
   const uint16_t* bias;
   const uint16_t* res;
   int64_t ldr;
+  // single-matrix sets: act = 1 writes relu(bf16(x.W^T))^2 (fp32, exact)
+  // rounded to bf16 into out and to fp16 (P8 layout) into outh, and ORs
+  // flag_out into the flag when a value is outside fp16's range; out32
+  // (non-null) takes the fp32 products unrounded instead of out
+  int act;
+  float* out32;
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)
@@ -240,7 +253,8 @@ struct PackArgs {
   const uint32_t* w0; const uint16_t* s0; const uint16_t* b0;  // MLX layout [n_exp][N][..]
   const uint32_t* w1; const uint16_t* s1; const uint16_t* b1;  // second matrix of a pair or null
   int64_t n_exp;
-  int N, nt, nu;
+  int N, nt, nu;            // N: source rows per expert; nt * 16 >= N packed rows
+  int k_src;                // source K (0: nu * 128); groups past it pack as zeros
   uint8_t* dst;
   int64_t dst_estride;      // bytes per expert in dst
 };
@@ -259,6 +273,18 @@ struct CombineArgs {
   int T, k, H;
 };
 hipError_t launch_combine(const CombineArgs& a, hipStream_t stream);
+
+// The Nemotron-H combine: y = bf16(bf16(sum over slots, fp32 in slot order,
+// of d * score) + sd) (the add in fp32; sd null: no shared expert).
+struct NhCombineArgs {
+  const float* d;          // [T*k, H] fp32, sorted rows
+  const uint32_t* inv;     // [T*k] entry -> sorted row
+  const float* scores;     // [T, k] fp32
+  const float* sd;         // [T, H] fp32 shared-expert output or null
+  uint16_t* y;             // [T, H] bf16
+  int T, k, H;
+};
+hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 
 hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
                              hipStream_t stream);

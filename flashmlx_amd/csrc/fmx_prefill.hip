@@ -261,8 +261,9 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   }
 
   // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile,
-  // column i16; gate/up also writes its SwiGLU rows in fp16 (P8 layout) for
-  // the down grid and flags values outside fp16's range
+  // column i16; gate/up (and a relu^2 up projection) also writes its rows
+  // in fp16 (P8 layout) for the down grid and flags values outside fp16's
+  // range
   bool ovf = false;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -282,6 +283,16 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
           P.out[orow + col] = v;
           ovf |= bf16_f16_overflow(v);
           P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
+        } else if (P.out32) {
+          P.out32[orow + col] = acc[mt][b][0][r];
+        } else if (P.act) {
+          // relu^2 of the bf16 product (Nemotron-H, nemotron_h.cpp:54-63):
+          // exact in fp32; bf16 and fp16 copies for the down grid
+          const float hv = fmaxf(round_bf16(acc[mt][b][0][r]), 0.0f);
+          const float av = hv * hv;
+          P.out[orow + col] = f32_to_bf16(av);
+          ovf |= av >= 65504.0f;
+          P.outh[orow + colh] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(av));
         } else {
           uint16_t v = f32_to_bf16(acc[mt][b][0][r]);
           if (P.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(P.bias[col]));
@@ -292,7 +303,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       }
     }
   }
-  if (DUAL && __ballot(ovf) && lane == 0) atomicOr(flag, flag_out);
+  if ((DUAL || P.act) && __ballot(ovf) && lane == 0) atomicOr(flag, flag_out);
 }
 
 // Block -> work item. The hardware dispatches block b to XCD b % 8, each

@@ -314,3 +314,27 @@ def test_scheduler_validation(fmx):
     toks = (C.c_int32 * 2)()
     assert lib.fmx_scheduler_step(None, ids, toks, 2, C.byref(n)) == _lib.FMX_ERR_ARG
     lib.fmx_scheduler_free(None)
+
+
+def test_nemotron_sizes_and_validation(fmx):
+    """Nemotron-H block entry points without a GPU: packed sizes with I and
+    Is padded to whole 128-k units, configs outside the limits refused."""
+    from flashmlx_amd import _lib
+    from flashmlx_amd.nemotron import NhMoEConfig
+    lib = _lib.load()
+    cfg = NhMoEConfig()
+    c = cfg.to_c()
+    H, E, Ip, Isp = 2688, 128, 1920, 3712
+    blocks = E * (Ip // 16) * (H // 128) + E * (H // 16) * (Ip // 128) + (Isp // 16) * (H // 128) \
+        + (H // 16) * (Isp // 128)
+    got = lib.fmx_nh_moe_packed_size(C.byref(c))
+    assert blocks * 1152 <= got <= blocks * 1152 + 4 * 256
+    assert 0 < lib.fmx_nh_moe_workspace_size(C.byref(c), 1) < lib.fmx_nh_moe_workspace_size(C.byref(c), 512)
+    for bad in (NhMoEConfig(hidden_size=2700), NhMoEConfig(moe_intermediate_size=1850),
+                NhMoEConfig(n_group=3), NhMoEConfig(n_group=4, topk_group=5),
+                NhMoEConfig(num_experts_per_tok=17), NhMoEConfig(n_routed_experts=2048),
+                NhMoEConfig(quant_bits=8), NhMoEConfig(n_group=128, topk_group=1)):
+        assert lib.fmx_nh_moe_packed_size(C.byref(bad.to_c())) == 0
+    w = _lib.FmxNhMoEWeights()
+    assert lib.fmx_nh_moe_block_forward(C.byref(c), C.byref(w), None, 0, None, None, 0, None) == _lib.FMX_OK
+    assert lib.fmx_nh_moe_block_forward(C.byref(c), None, None, 1, None, None, 0, None) == _lib.FMX_ERR_ARG
