@@ -368,6 +368,180 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
     return res, y_host, inds
 
 
+# The Nemotron-H MoE block (30B-A3B layer shape: H 2688, 128 experts top-6,
+# I 1856, shared 3712, routed_scaling_factor 2.5; random-init 4-bit weights,
+# seed 16) at decode batch 1 and 8 and a 512-token prefill.
+NH_CONFIGS = {"nh30b_decode_b1": 1, "nh30b_decode_b8": 8, "nh30b_prefill_512": 512}
+NH_SEED = 16
+
+
+def nh_bytes_flops(cfg, T: int, U: int):
+    """Algorithmic HBM bytes and flops of one Nemotron-H layer forward of T
+    tokens with U distinct experts selected: per kernel grid (fc1 + shared
+    up; fc2 + shared down) the 4-bit weights (0.5625 bytes per weight, the
+    unpadded I and Is) and the products; the whole layer adds the router,
+    the correction bias and x / y."""
+    H, E, k = cfg.hidden_size, cfg.n_routed_experts, cfg.num_experts_per_tok
+    I, Is = cfg.moe_intermediate_size, cfg.moe_shared_expert_intermediate_size
+    wq = 0.5625
+    grid_bytes = int(U * I * H * wq + Is * H * wq)
+    grid_flops = 2 * T * k * I * H + 2 * T * Is * H
+    layer_bytes = 2 * grid_bytes + E * H * 2 + E * 4 + 2 * T * H * 2
+    return grid_bytes, grid_flops, layer_bytes, 2 * grid_flops + 2 * T * E * H
+
+
+def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_seconds: float):
+    """Times K Nemotron-H layer forwards cycling over R copies of the packed
+    weights (captured graphs), then each stage's kernels from stage events
+    around eager forwards; the roofline of the dominant expert grid."""
+    import numpy as np
+    import torch
+
+    from flashmlx_amd import nemotron as N
+    from flashmlx_amd.moe import synth_normal_bf16_device
+
+    cfg = N.NhMoEConfig()
+    t0 = time.perf_counter()
+    w0 = N.synthetic_nh_weights(cfg, NH_SEED)
+    w0.pack(cfg)
+    host = N.host_weights(w0) if cpu_seconds > 0 else None
+    w0.drop_mlx_layout()
+    blocks = [N.NhMoEBlock(cfg, w0, T)]
+    for _ in range(R - 1):
+        wi = N.NhMoEWeights(w0.gate_w, w0.correction_bias, None, None, packed=w0.packed.clone())
+        blocks.append(N.NhMoEBlock(cfg, wi, T))
+    x = synth_normal_bf16_device((T, cfg.hidden_size), NH_SEED, 7)
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    log(f"{key}: {R} layer copies built in {time.perf_counter() - t0:.1f}s")
+    blocks[0].forward_into(x, y)
+    torch.cuda.synchronize()
+    y_ref = y.clone()
+    r = blocks[0].routing()
+    inds = r["inds"].cpu().numpy().view("uint32").copy()
+    U = int(np.unique(inds).size)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for b in blocks:
+            b.forward_into(x, y)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for b in blocks:
+            b.forward_into(x, y)
+    for _ in range(3):
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(y, y_ref):
+            raise RuntimeError("graph replay output differs from the eager output")
+    reps = max(1, K // R)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, Wm // R)):
+            g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(trials):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        with torch.cuda.stream(stream):
+            for _ in range(reps):
+                g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    ms_total = statistics.median(times)
+    ms_step = ms_total / (reps * R)
+
+    # per-stage kernel times: events around each stage of eager forwards
+    n_prof = max(R, 4 * R if T <= 16 else R)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n_prof)]
+    with torch.cuda.stream(stream):
+        for i in range(n_prof):
+            blocks[i % R].forward_profiled(x, y, evs[i])
+    torch.cuda.synchronize()
+    names = ["router_sort", "fc1_grid", "fc2_grid", "combine"]
+    stage_ms = {nm: statistics.median([e[j].elapsed_time(e[j + 1]) for e in evs]) for j, nm in enumerate(names)}
+    grid_bytes, grid_flops, layer_bytes, layer_flops = nh_bytes_flops(cfg, T, U)
+    dom = max(("fc1_grid", "fc2_grid"), key=lambda nm: stage_ms[nm])
+    dur_s = stage_ms[dom] * 1e-3
+    if T <= 16:
+        ach = grid_bytes / dur_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic(key, dom),
+                "algorithmic_per_launch": grid_bytes}
+    else:
+        ach = grid_flops / dur_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": load_traffic(key, dom),
+                "algorithmic_per_launch": grid_flops}
+    roof["stage"] = dom
+    roof["avg_launch_us"] = round(stage_ms[dom] * 1e3, 2)
+    res = {
+        "workload": (f"Nemotron-H MoE block (30B-A3B layer shape: H 2688, 128 experts top-6 sigmoid-routed "
+                     f"with correction bias, I 1856, shared 3712, relu^2), {T} tokens, seed {NH_SEED}"),
+        "key": key,
+        "tokens": T,
+        "value": round(T / (ms_step * 1e-3), 1),
+        "unit": "tok/s",
+        "us_per_layer": round(ms_step * 1e3, 2),
+        "steps": reps * R,
+        "trials": trials,
+        "roofline": roof,
+        "layer": {"unique_experts": U, "algorithmic_bytes": layer_bytes,
+                  "hbm_gbps": round(layer_bytes / (ms_step * 1e-3) / 1e9, 1),
+                  "tflops": round(layer_flops / (ms_step * 1e-3) / 1e12, 2),
+                  "stage_us": {nm: round(v * 1e3, 2) for nm, v in stage_ms.items()}},
+    }
+    log(f"{key}: {res['us_per_layer']} us/layer, {dom} {roof['achieved']} {roof['unit']}")
+    if cpu_seconds > 0:
+        res["cpu_baseline"] = nh_cpu_baseline(cfg, host, x, y_ref, inds, T, cpu_seconds)
+    del blocks, g
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def nh_cpu_baseline(cfg, host, x, y_gpu, inds_gpu, T: int, seconds: float):
+    """The oracle's Nemotron-H block on this host on a bounded sample (the
+    first token of the workload per call, fp32 accumulation), plus the GPU
+    output's parity against it on up to 8 tokens."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    O.build()
+    oc = cfg.oracle_cfg()
+    xh = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    nproc = host_threads()
+    O.set_threads(nproc)
+    O.nh_moe_block(oc, host, xh[:1], O.ACC_A)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.nh_moe_block(oc, host, xh[:1], O.ACC_A)
+        n += 1
+    el = time.perf_counter() - t0
+    m = min(T, 8)
+    ry, rinds, _ = O.nh_moe_block(oc, host, xh[:m], O.ACC_F64)
+    g = O.bf16_to_f32(y_gpu.view(torch.int16).cpu().numpy().view(np.uint16)[:m]).astype(np.float64)
+    rr = O.bf16_to_f32(ry).astype(np.float64)
+    return {
+        "value": round(n / el, 3),
+        "unit": "tok/s",
+        "cores": nproc,
+        "kind": "port",
+        "sample": (f"oracle Nemotron-H block on 1 token per call ({n} calls in {el:.1f}s, {nproc} OpenMP "
+                   f"threads, fp32 accumulation) on {cpu_model()}"),
+        "parity_rows": m,
+        "parity_rel_l2": float(np.linalg.norm(g - rr) / max(np.linalg.norm(rr), 1e-30)),
+        "routing_bitexact": bool(np.array_equal(inds_gpu[:m], rinds)),
+    }
+
+
 # The 24-layer Qwen1.5-MoE-A2.7B-shape decoder stack (random-init 4-bit
 # weights, seed 5): a 256-token prompt, then 128 greedy tokens, at batch 1 and 4
 STACK_CONFIGS = {"c4_stack_b1": 1, "c4_stack_b4": 4, "c4_stack_b8": 8}
@@ -574,6 +748,9 @@ def main():
                     help="decoder-stack configs measured in the same run: all, none or a comma list "
                          "(c4_stack_b1, c4_stack_b4, c4_stack_b8)")
     ap.add_argument("--stack-trials", type=int, default=5)
+    ap.add_argument("--nh", default="all",
+                    help="Nemotron-H block configs measured in the same run: all, none or a comma list "
+                         "(nh30b_decode_b1, nh30b_decode_b8, nh30b_prefill_512)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -618,6 +795,14 @@ def main():
         stack = measure_stack([STACK_CONFIGS[k] for k in skeys], args.stack_trials,
                               0.0 if args.no_cpu_baseline else args.cpu_seconds)
         configs.update(stack)
+
+    nkeys = list(NH_CONFIGS) if args.nh == "all" else (
+        [] if args.nh == "none" else [k for k in args.nh.split(",") if k])
+    for key in nkeys:
+        T = NH_CONFIGS[key]
+        steps = 480 if T <= 16 else 48
+        configs[key] = measure_nh(key, T, 8, steps, max(8, steps // 10), 5,
+                                  0.0 if args.no_cpu_baseline else min(args.cpu_seconds, 6.0))
 
     cpu, parity = None, None
     if not args.no_cpu_baseline:

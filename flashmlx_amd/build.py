@@ -30,6 +30,7 @@ SOURCES = [
     "csrc/fmx_model.cpp",
     "csrc/fmx_loader.cpp",
     "csrc/fmx_sched.cpp",
+    "csrc/fmx_nh_decode.hip",
     "csrc/fmx_nh.cpp",
 ]
 
@@ -52,6 +53,7 @@ CFLAGS = [
 # register move per value.
 EXTRA_FLAGS = {
     "csrc/fmx_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "csrc/fmx_nh_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -41,11 +41,6 @@ namespace fmx {
 
 namespace {
 
-// LDS row stride (elements) of staged activation rows of length K
-__host__ __device__ inline int xstride(int K) { return K + 8; }
-
-constexpr int kDecWaves = kDecThreads / kWave;
-constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;        // quad_reduce's LDS
 constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
 constexpr int kDecWarmLoads = 8;  // K1's cache warming: 16-byte loads per thread (32 KB per workgroup)
 // Gate/up tile pairs per K2 workgroup (their loads in flight together, the
@@ -60,33 +55,6 @@ constexpr int kDecK2PairGrid = 2 * 4 * 256;
 constexpr int kDecK1LpBytes = kDecWaves * kDecMaxT * 8;              // router partials per wave
 
 constexpr int kDecK1LgBytes = kDecMaxT * (kDecMaxE + 1) * 2;         // every token's logits
-
-// Units [u0, u1) (u1 - u0 <= NU) of one 16-row tile (blocks of BB bytes from
-// tile_base), all loads in flight together, against activation rows in LDS
-// (xl: the lane's row plus 8*j). The rows' LDS DMA is the caller's last
-// memory operation before this call: right after the weight loads, vmcnt
-// (their count) proves the DMA complete while they stay in flight, and
-// the units are multiplied as their loads land.
-template <bool DUAL, int NU>
-__device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, const uint16_t* xl,
-                                      int lane, f32x4_t& acc0, f32x4_t& acc1) {
-  constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
-  PkUnit<DUAL> L[NU];
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int d = 0; d < NU; ++d) L[d] = pk_load<DUAL>(tile_base + min(u0 + d, u1 - 1) * BB, lane);
-  __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<NU * pk_load_insts<DUAL>()>();
-  lds_dma_barrier();
-#pragma unroll
-  for (int d = 0; d < NU; ++d) {
-    if (u0 + d < u1) {
-      bf16x8_t A[4];
-      lds_a(xl + (u0 + d) * 128, A);
-      pk_unit<DUAL>(L[d], A, acc0, acc1);
-    }
-  }
-}
 
 // tile_units_lds for NP tile pairs at once: every pair's loads are issued
 // before the one wait, then the pairs are multiplied in turn.
@@ -109,31 +77,6 @@ __device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0,
       lds_a(xl + (u0 + d) * 128, A);
 #pragma unroll
       for (int p = 0; p < NP; ++p) pk_unit<true>(L[p][d], A, acc[p][0], acc[p][1]);
-    }
-  }
-}
-
-// Waves 1..3 hand their partial sums over K quarters 1..3 to wave 0 through
-// LDS (s_red: 3 x 8 x 64 floats); wave 0 adds them in wave order.
-__device__ inline void quad_reduce(f32x4_t& acc0, f32x4_t& acc1, int wave, int lane, float* s_red) {
-  if (wave > 0) {
-    float* slot = s_red + (wave - 1) * 8 * kWave;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      slot[i * kWave + lane] = acc0[i];
-      slot[(4 + i) * kWave + lane] = acc1[i];
-    }
-  }
-  __syncthreads();
-  if (wave == 0) {
-#pragma unroll
-    for (int w = 0; w < kDecWaves - 1; ++w) {
-      const float* slot = s_red + w * 8 * kWave;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc0[i] += slot[i * kWave + lane];
-        acc1[i] += slot[(4 + i) * kWave + lane];
-      }
     }
   }
 }

@@ -447,4 +447,199 @@ __device__ inline void lds_a(const uint16_t* xu, bf16x8_t (&A)[4]) {
   for (int a = 0; a < 4; ++a) A[a] = *reinterpret_cast<const bf16x8_t*>(xu + 32 * a);
 }
 
+// ------------------------------------------------------------------ decode tiles
+//
+// Workgroups of kDecThreads threads (4 waves) that multiply one 16-row tile
+// over K split in four quarters, all of a quarter's loads in flight at once.
+
+// LDS row stride (elements) of staged activation rows of length K
+__host__ __device__ inline int xstride(int K) { return K + 8; }
+
+constexpr int kDecWaves = kDecThreads / kWave;
+constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;  // quad_reduce's LDS
+
+// Units [u0, u1) (u1 - u0 <= NU) of one 16-row tile (blocks of BB bytes from
+// tile_base), all loads in flight together, against activation rows in LDS
+// (xl: the lane's row plus 8*j). The rows' LDS DMA is the caller's last
+// memory operation before this call: right after the weight loads, vmcnt
+// (their count) proves the DMA complete while they stay in flight, and
+// the units are multiplied as their loads land.
+template <bool DUAL, int NU>
+__device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, const uint16_t* xl,
+                                      int lane, f32x4_t& acc0, f32x4_t& acc1) {
+  constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
+  PkUnit<DUAL> L[NU];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < NU; ++d) L[d] = pk_load<DUAL>(tile_base + min(u0 + d, u1 - 1) * BB, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<NU * pk_load_insts<DUAL>()>();
+  lds_dma_barrier();
+#pragma unroll
+  for (int d = 0; d < NU; ++d) {
+    if (u0 + d < u1) {
+      bf16x8_t A[4];
+      lds_a(xl + (u0 + d) * 128, A);
+      pk_unit<DUAL>(L[d], A, acc0, acc1);
+    }
+  }
+}
+
+// Waves 1..3 hand their partial sums over K quarters 1..3 to wave 0 through
+// LDS (s_red: 3 x 8 x 64 floats); wave 0 adds them in wave order.
+__device__ inline void quad_reduce(f32x4_t& acc0, f32x4_t& acc1, int wave, int lane, float* s_red) {
+  if (wave > 0) {
+    float* slot = s_red + (wave - 1) * 8 * kWave;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      slot[i * kWave + lane] = acc0[i];
+      slot[(4 + i) * kWave + lane] = acc1[i];
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < kDecWaves - 1; ++w) {
+      const float* slot = s_red + w * 8 * kWave;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc0[i] += slot[i * kWave + lane];
+        acc1[i] += slot[(4 + i) * kWave + lane];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ Nemotron-H selection
+// (nemotron_h.cpp:1017-1050)
+
+// fp32 ordering key: larger floats give larger keys (zeros of either sign
+// give the key of +0)
+__device__ inline uint32_t f32_key(float f) {
+  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), w);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), w);
+    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One token by one wave: orig = fp32(sigmoid(logit)) (fp64 with exp_det,
+// rounded once); sel = orig + correction bias (fp32); with groups, each
+// group's score is the sum of its two largest sel, the topk_group best
+// groups stay (ties: lower group) and the others' sel become 0; the k
+// largest sel are selected (ties: lower expert; slot order sel desc, index
+// asc); scores = orig of the selected, / (slot-order sum + 1e-20) when
+// renormalising, * scaling, every operation in fp32. lrow: the token's E
+// bf16 logits (global or LDS); lane j < k writes slot j to inds_out,
+// scores_out and (non-null) inds_lds. E <= 64 * NPER, n_group <= 64.
+template <int NPER>
+__device__ void nh_select_wave(const uint16_t* lrow, int E, int k, int norm, int n_group, int topk_group,
+                               float scaling, const float* cbias, int lane, uint32_t* inds_out,
+                               float* scores_out, uint32_t* inds_lds) {
+  constexpr int kMaxExpertsPerLane = NPER;
+  const int nblk = (E + kWave - 1) / kWave;  // wave-uniform
+  float orig[kMaxExpertsPerLane], sel[kMaxExpertsPerLane];
+#pragma unroll
+  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+    const int e = lane + 64 * i;
+    orig[i] = 0.0f;
+    sel[i] = -__builtin_huge_valf();
+    if (i < nblk && e < E) {
+      const double l = static_cast<double>(bf16_to_f32(lrow[e]));
+      orig[i] = static_cast<float>(1.0 / (1.0 + exp_det(-l)));
+      sel[i] = cbias ? orig[i] + cbias[e] : orig[i];
+    }
+  }
+  if (n_group > 1) {
+    const int G = E / n_group;
+    // lane g ends with group g's score (n_group <= 64)
+    float my_gs = -__builtin_huge_valf();
+    for (int g = 0; g < n_group; ++g) {
+      float m1 = -__builtin_huge_valf(), m2 = -__builtin_huge_valf();
+#pragma unroll
+      for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+        const int e = lane + 64 * i;
+        if (i < nblk && e < E && e / G == g) {
+          if (sel[i] > m1) {
+            m2 = m1;
+            m1 = sel[i];
+          } else if (sel[i] > m2) {
+            m2 = sel[i];
+          }
+        }
+      }
+      // merge the lanes' two largest
+#pragma unroll
+      for (int w = 32; w >= 1; w >>= 1) {
+        const float o1 = __shfl_xor(m1, w), o2 = __shfl_xor(m2, w);
+        const float hi = fmaxf(m1, o1), lo = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+        m1 = hi;
+        m2 = lo;
+      }
+      if (lane == g) my_gs = m1 + m2;
+    }
+    bool keep = false;
+    uint64_t gkey = lane < n_group
+                        ? (static_cast<uint64_t>(f32_key(my_gs)) << 32) | (0xffffffffu - static_cast<uint32_t>(lane))
+                        : 0ull;
+    for (int r = 0; r < topk_group; ++r) {
+      const uint64_t best = wave_max_u64(gkey);
+      if (gkey == best && lane < n_group) {
+        keep = true;
+        gkey = 0ull;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      const int e = lane + 64 * i;
+      const int g = min(e, E - 1) / G;
+      const bool kept = __shfl(static_cast<int>(keep), g) != 0;
+      if (i < nblk && e < E && !kept) sel[i] = 0.0f;
+    }
+  }
+  uint64_t key[kMaxExpertsPerLane];
+#pragma unroll
+  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = (i < nblk && e < E)
+                 ? (static_cast<uint64_t>(f32_key(sel[i])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
+                 : 0ull;
+  }
+  float my_sc = 0.0f, den = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = 0ull;
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i)
+      if (i < nblk) best = key[i] > best ? key[i] : best;
+    best = wave_max_u64(best);
+    const uint32_t e = 0xffffffffu - static_cast<uint32_t>(best);
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
+      if (i < nblk && key[i] == best) key[i] = 0ull;
+      if (i == static_cast<int>(e >> 6)) o = orig[i];
+    }
+    o = __shfl(o, static_cast<int>(e & 63u));  // the winner's lane holds its orig
+    den = __fadd_rn(den, o);
+    if (lane == j) {
+      my_sc = o;
+      inds_out[j] = e;
+      if (inds_lds) inds_lds[j] = e;
+    }
+  }
+  if (lane < k) {
+    float sc = my_sc;
+    if (norm && k > 1) sc = sc / __fadd_rn(den, 1e-20f);
+    scores_out[lane] = __fmul_rn(sc, scaling);
+  }
+}
+
 }  // namespace fmx

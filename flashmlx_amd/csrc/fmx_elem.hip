@@ -90,6 +90,9 @@ hipError_t launch_combine(const CombineArgs& a, hipStream_t stream) {
 // compiler from contracting them), then + shared (fp32 add), rounded to bf16.
 __global__ __launch_bounds__(kElemThreads) void nh_combine_kernel(NhCombineArgs a) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
+  // the GEMMs that read the fp16-range flag have finished: clear it for the
+  // next forward's router
+  if (gid == 0 && a.clear) *a.clear = 0u;
   const int quads = a.H / 4;
   if (gid >= static_cast<int64_t>(a.T) * quads) return;
   const int t = static_cast<int>(gid / quads), o = static_cast<int>(gid % quads);

@@ -274,6 +274,41 @@ struct CombineArgs {
 };
 hipError_t launch_combine(const CombineArgs& a, hipStream_t stream);
 
+// The Nemotron-H block for decode batches (T <= 16) on packed weights
+// (fmx_nh_decode.hip): D1 router columns (+ the shared up tiles), D2 the
+// routed fc1 tiles, D3 fc2 and the shared down, D4 the combine.
+constexpr int kNhDecMaxE = 512;       // experts (the router tables in LDS)
+constexpr int kNhDecSdSplit = 4;      // K slices of the shared down projection
+struct NhDecArgs {
+  int T, H, E, k, norm, n_group, topk_group;
+  float scaling;
+  int Ip, Isp;                 // I and Is padded to whole 128-k units
+  const uint16_t* x;           // [T, H] bf16
+  const uint16_t* gate_w;      // [E, H] bf16 router
+  const float* cbias;          // [E] or null
+  const uint8_t* fc1;          // packed [E][Ip/16 tiles][H/128 units]
+  int64_t fc1_es;
+  const uint8_t* fc2;          // packed [E][H/16 tiles][Ip/128 units]
+  int64_t fc2_es;
+  const uint8_t* sup;          // packed [Isp/16][H/128]
+  const uint8_t* sdn;          // packed [H/16][Isp/128]
+  uint16_t* logits;            // [T, E + 1] bf16 (the routing accessor's view)
+  uint32_t* lgw;               // [E][T] the logits between D1 workgroups (low halves)
+  uint32_t* inds;              // [T, k]
+  float* scores;               // [T, k] fp32
+  uint32_t* seg;               // [1 + max_seg]: U, then the selected experts ascending
+  uint8_t* slots;              // [max_seg][16]: token t's slot for expert u, or 0xff
+  uint16_t *h_hi, *h_lo;       // [T*k, Ip] relu^2 of fc1 as hi + lo bf16 (exact sum)
+  uint16_t *hs_hi, *hs_lo;     // [T, Isp] the shared expert's
+  float* d;                    // [T*k, H] fc2 products, entry order
+  float* sd_part;              // [kNhDecSdSplit][T][H] shared down, K-slice sums
+  uint16_t* y;                 // [T, H]
+  uint32_t* counter;           // D1 arrival counter: zero on entry and exit
+  int max_seg, n_sup;          // launch shape: expert slots, shared up tiles
+};
+bool nh_decode_plan(NhDecArgs& a);
+hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks);
+
 // The Nemotron-H combine: y = bf16(bf16(sum over slots, fp32 in slot order,
 // of d * score) + sd) (the add in fp32; sd null: no shared expert).
 struct NhCombineArgs {
@@ -283,6 +318,7 @@ struct NhCombineArgs {
   const float* sd;         // [T, H] fp32 shared-expert output or null
   uint16_t* y;             // [T, H] bf16
   int T, k, H;
+  uint32_t* clear;         // a word set to zero (the forward's fp16-range flag) or null
 };
 hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 

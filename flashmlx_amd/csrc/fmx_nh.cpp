@@ -106,7 +106,13 @@ NhPacked nh_packed(const fmx_nh_moe_config& c) {
   return P;
 }
 
+// router arrival counters (the fused router of forwards of at most
+// kRouterManyMin tokens: one per token tile and one more): zero on entry
+// and exit
+constexpr int64_t kNhCounterWords = 64;
+
 struct NhLayout {
+  uint32_t* counters;  // [kNhCounterWords]
   uint16_t* logits;    // [T, E + 1]
   uint32_t* inds;      // [n]
   float* scores;       // [n]
@@ -116,8 +122,14 @@ struct NhLayout {
   uint16_t* xh;        // [T, H] fp16 (P8)
   uint16_t *h, *hh;    // [n, Ip] relu^2 of fc1: bf16, fp16 (P8)
   uint16_t *hs, *hsh;  // [T, Isp] the shared expert's
-  float* d;            // [n, H] fc2 products, sorted rows
+  float* d;            // [n, H] fc2 products, sorted rows (decode: entry order)
   float* sd;           // [T, H] shared down
+  // the decode kernels' (forwards of at most kDecMaxT tokens), sized for
+  // min(T, kDecMaxT) at every T so that the layout only grows with T
+  uint32_t* lgw;       // [E][Td] logits between the router workgroups
+  uint32_t* seg;       // [1 + E]
+  uint8_t* slots;      // [E][16]
+  float* sd_part;      // [kNhDecSdSplit][Td][H]
   size_t total;
 };
 
@@ -131,6 +143,8 @@ NhLayout nh_layout(const fmx_nh_moe_config& c, int64_t T, char* base) {
   const NhPacked P = nh_packed(c);
   const int64_t E = c.n_routed_experts, k = c.num_experts_per_tok, H = c.hidden_size, n = T * k;
   NhLayout L{};
+  L.counters = static_cast<uint32_t*>(take(kNhCounterWords * 4));
+  L.f16_flag = static_cast<uint32_t*>(take(4));
   L.logits = static_cast<uint16_t*>(take(T * (E + 1) * 2));
   L.inds = static_cast<uint32_t*>(take(n * 4));
   L.scores = static_cast<float*>(take(n * 4));
@@ -145,7 +159,6 @@ NhLayout nh_layout(const fmx_nh_moe_config& c, int64_t T, char* base) {
   L.sort_base = static_cast<uint32_t*>(take(E * ((n + 63) / 64) * 4));
   L.pass_n = static_cast<uint32_t*>(take(4));
   L.pass_tab = static_cast<uint32_t*>(take(static_cast<int64_t>(max_passes(n, E)) * 8));
-  L.f16_flag = static_cast<uint32_t*>(take(4));
   L.xh = static_cast<uint16_t*>(take(T * H * 2));
   L.h = static_cast<uint16_t*>(take(n * P.Ip * 2));
   L.hh = static_cast<uint16_t*>(take(n * P.Ip * 2));
@@ -153,6 +166,11 @@ NhLayout nh_layout(const fmx_nh_moe_config& c, int64_t T, char* base) {
   L.hsh = static_cast<uint16_t*>(take(T * P.Isp * 2));
   L.d = static_cast<float*>(take(n * H * 4));
   L.sd = static_cast<float*>(take(P.Isp ? T * H * 4 : 0));
+  const int64_t Td = std::min<int64_t>(T, kDecMaxT);
+  L.lgw = static_cast<uint32_t*>(take(E * Td * 4));
+  L.seg = static_cast<uint32_t*>(take((E + 1) * 4));
+  L.slots = static_cast<uint8_t*>(take(E * kDecMaxT));
+  L.sd_part = static_cast<float*>(take(P.Isp ? kNhDecSdSplit * Td * H * 4 : 0));
   L.total = used;
   return L;
 }
@@ -211,6 +229,17 @@ int fmx_nh_pack_expert_weights(const fmx_nh_moe_config* cfg, const fmx_nh_moe_we
   return ok();
 }
 
+int fmx_nh_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream) {
+  if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
+  if (!aligned(workspace, 256)) return fail(FMX_ERR_ARG, "workspace not 256-byte aligned");
+  // the counters and the flag word that follows them (their own 256-byte slot)
+  if (workspace_bytes < (kNhCounterWords * 4 + 256))
+    return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes is too small", workspace_bytes);
+  FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(workspace), kNhCounterWords + 64, 0u,
+                          static_cast<hipStream_t>(stream)));
+  return ok();
+}
+
 size_t fmx_nh_moe_workspace_size(const fmx_nh_moe_config* cfg, int64_t max_tokens) {
   if (check_config(cfg) || max_tokens < 0 || max_tokens > kNhMaxTokens) return 0;
   return nh_layout(*cfg, std::max<int64_t>(max_tokens, 1), nullptr).total;
@@ -230,7 +259,16 @@ int fmx_nh_moe_workspace_routing(const fmx_nh_moe_config* cfg, int64_t T, const 
 
 int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w, const void* x,
                              int64_t T, void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  return fmx_nh_moe_block_forward_profiled(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr);
+}
+
+int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
+                                      const void* x, int64_t T, void* y, void* workspace,
+                                      size_t workspace_bytes, fmx_stream stream_, void* const* stage_events) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
+  auto mark = [&](int i) -> hipError_t {
+    return stage_events ? hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream) : hipSuccess;
+  };
   int rc;
   if ((rc = check_config(cfg))) return rc;
   if (!w) return fail(FMX_ERR_ARG, "NULL weights");
@@ -262,11 +300,56 @@ int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weig
     FMX_HIP(hipMallocAsync(&p, need, stream));
     base = static_cast<char*>(p);
     owned = true;
+    const hipError_t e = launch_fill_u32(static_cast<uint32_t*>(p), kNhCounterWords + 64, 0u, stream);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(p, stream);
+      return fail(FMX_ERR_HIP, "clearing the workspace: %s", hipGetErrorString(e));
+    }
   }
   auto body = [&]() -> int {
     const NhLayout L = nh_layout(c, T, base);
     const uint8_t* pk = static_cast<const uint8_t*>(w->packed);
     const uint16_t* xb = static_cast<const uint16_t*>(x);
+
+    // decode batches: the four decode kernels
+    NhDecArgs da{};
+    da.T = static_cast<int>(T);
+    da.H = static_cast<int>(H);
+    da.E = static_cast<int>(E);
+    da.k = static_cast<int>(k);
+    da.norm = c.norm_topk_prob ? 1 : 0;
+    da.n_group = c.n_group;
+    da.topk_group = c.topk_group;
+    da.scaling = c.routed_scaling_factor;
+    da.Ip = static_cast<int>(P.Ip);
+    da.Isp = static_cast<int>(P.Isp);
+    if (nh_decode_plan(da)) {
+      da.x = xb;
+      da.gate_w = static_cast<const uint16_t*>(w->gate_w);
+      da.cbias = w->correction_bias;
+      da.fc1 = pk + P.fc1;
+      da.fc1_es = P.fc1_es;
+      da.fc2 = pk + P.fc2;
+      da.fc2_es = P.fc2_es;
+      da.sup = pk + P.sup;
+      da.sdn = pk + P.sdn;
+      da.logits = L.logits;
+      da.lgw = L.lgw;
+      da.inds = L.inds;
+      da.scores = L.scores;
+      da.seg = L.seg;
+      da.slots = L.slots;
+      da.h_hi = L.h;
+      da.h_lo = L.hh;
+      da.hs_hi = L.hs;
+      da.hs_lo = L.hsh;
+      da.d = L.d;
+      da.sd_part = L.sd_part;
+      da.y = static_cast<uint16_t*>(y);
+      da.counter = L.counters;
+      FMX_HIP(launch_nh_decode(da, stream, stage_events));
+      return FMX_OK;
+    }
 
     // router: logits, selection, fp32 scores, the fp16 copy of x
     RouterArgs ra{};
@@ -287,10 +370,24 @@ int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weig
     ra.scaling = c.routed_scaling_factor;
     ra.cbias = w->correction_bias;
     ra.scores32 = L.scores;
-    FMX_HIP(launch_router_many(ra, stream));
+    ra.counters = L.counters;
     SortOut so{L.order, L.inv, L.src, L.idx, L.offsets, L.seg_n, L.seg_exp, L.seg_off,
                L.sort_base, L.pass_n, L.pass_tab};
-    FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
+    ra.sort = so;
+    FMX_HIP(mark(0));
+    if (T <= kRouterManyMin && router_sort_fits(n, E)) {
+      // one launch: logits in column workgroups, the last of each token
+      // tile selects, the last tile sorts
+      ra.n_tt = static_cast<int>((T + kRouterTok - 1) / kRouterTok);
+      ra.cols_per_wave = ra.n_tt > 1 ? 4 : 1;
+      ra.n_ct = static_cast<int>((E + 4 * ra.cols_per_wave - 1) / (4 * ra.cols_per_wave));
+      ra.fuse_sort = 1;
+      FMX_HIP(launch_router(ra, stream));
+    } else {
+      FMX_HIP(launch_router_many(ra, stream));
+      FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
+    }
+    FMX_HIP(mark(1));
 
     const int mp = max_passes(n, E);
     auto routed = [&](const uint8_t* wp, int64_t es, const uint16_t* xr, const uint16_t* xrh, int64_t ldx,
@@ -345,6 +442,7 @@ int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weig
       pa.flag_in = kF16FlagX;
       pa.flag_out = kF16FlagH;
       FMX_HIP(launch_pf(pa, false, stream));
+      FMX_HIP(mark(2));
     }
     {  // fc2 and the shared down projection, fp32 products
       PfArgs pa{};
@@ -362,6 +460,7 @@ int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weig
       pa.flag_in = kF16FlagH;
       pa.flag_out = 0u;
       FMX_HIP(launch_pf(pa, false, stream));
+      FMX_HIP(mark(3));
     }
     NhCombineArgs cb{};
     cb.d = L.d;
@@ -372,7 +471,9 @@ int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weig
     cb.T = static_cast<int>(T);
     cb.k = static_cast<int>(k);
     cb.H = static_cast<int>(H);
+    cb.clear = L.f16_flag;
     FMX_HIP(launch_nh_combine(cb, stream));
+    FMX_HIP(mark(4));
     return FMX_OK;
   };
   rc = body();

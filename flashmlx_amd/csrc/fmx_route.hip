@@ -290,130 +290,13 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
   if (lane == 0 && a.wsg.w && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
 }
 
-// ---- the Nemotron-H router (nemotron_h.cpp:1017-1050)
-
-// fp32 ordering key: larger floats give larger keys (zeros of either sign
-// give the key of +0)
-__device__ inline uint32_t f32_key(float f) {
-  const uint32_t u = f == 0.0f ? 0u : __float_as_uint(f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int w = 32; w >= 1; w >>= 1) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), w);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), w);
-    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
-}
-
-// One token by one wave: orig = fp32(sigmoid(logit)) (fp64 with exp_det,
-// rounded once); sel = orig + correction bias (fp32); with groups, each
-// group's score is the sum of its two largest sel, the topk_group best
-// groups stay (ties: lower group) and the others' sel become 0; the k
-// largest sel are selected (ties: lower expert; slot order sel desc, index
-// asc); scores = orig of the selected, / (slot-order sum + 1e-20) when
-// renormalising, * scaling, every operation in fp32.
+// The Nemotron-H selection of token t (nh_select_wave) from the logits row
+// in global memory, into inds and scores32.
 __device__ void router_token_nh(const RouterArgs& a, int t, int lane) {
-  const int E = a.E;
-  const int nblk = (E + kWave - 1) / kWave;  // wave-uniform
-  const uint16_t* lrow = a.logits + static_cast<int64_t>(t) * (E + 1);
-  float orig[kMaxExpertsPerLane], sel[kMaxExpertsPerLane];
-#pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-    const int e = lane + 64 * i;
-    orig[i] = 0.0f;
-    sel[i] = -__builtin_huge_valf();
-    if (i < nblk && e < E) {
-      const double l = static_cast<double>(bf16_to_f32(lrow[e]));
-      orig[i] = static_cast<float>(1.0 / (1.0 + exp_det(-l)));
-      sel[i] = a.cbias ? orig[i] + a.cbias[e] : orig[i];
-    }
-  }
-  if (a.n_group > 1) {
-    const int G = E / a.n_group;
-    // lane g ends with group g's score (n_group <= 64)
-    float my_gs = -__builtin_huge_valf();
-    for (int g = 0; g < a.n_group; ++g) {
-      float m1 = -__builtin_huge_valf(), m2 = -__builtin_huge_valf();
-#pragma unroll
-      for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-        const int e = lane + 64 * i;
-        if (i < nblk && e < E && e / G == g) {
-          if (sel[i] > m1) {
-            m2 = m1;
-            m1 = sel[i];
-          } else if (sel[i] > m2) {
-            m2 = sel[i];
-          }
-        }
-      }
-      // merge the lanes' two largest
-#pragma unroll
-      for (int w = 32; w >= 1; w >>= 1) {
-        const float o1 = __shfl_xor(m1, w), o2 = __shfl_xor(m2, w);
-        const float hi = fmaxf(m1, o1), lo = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
-        m1 = hi;
-        m2 = lo;
-      }
-      if (lane == g) my_gs = m1 + m2;
-    }
-    bool keep = false;
-    uint64_t gkey = lane < a.n_group
-                        ? (static_cast<uint64_t>(f32_key(my_gs)) << 32) | (0xffffffffu - static_cast<uint32_t>(lane))
-                        : 0ull;
-    for (int r = 0; r < a.topk_group; ++r) {
-      const uint64_t best = wave_max_u64(gkey);
-      if (gkey == best && lane < a.n_group) {
-        keep = true;
-        gkey = 0ull;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-      const int e = lane + 64 * i;
-      const int g = min(e, E - 1) / G;
-      const bool kept = __shfl(static_cast<int>(keep), g) != 0;
-      if (i < nblk && e < E && !kept) sel[i] = 0.0f;
-    }
-  }
-  uint64_t key[kMaxExpertsPerLane];
-#pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = (i < nblk && e < E)
-                 ? (static_cast<uint64_t>(f32_key(sel[i])) << 32) | (0xffffffffu - static_cast<uint32_t>(e))
-                 : 0ull;
-  }
-  float my_sc = 0.0f, den = 0.0f;
-  for (int j = 0; j < a.k; ++j) {
-    uint64_t best = 0ull;
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i)
-      if (i < nblk) best = key[i] > best ? key[i] : best;
-    best = wave_max_u64(best);
-    const uint32_t e = 0xffffffffu - static_cast<uint32_t>(best);
-    float o = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-      if (i < nblk && key[i] == best) key[i] = 0ull;
-      if (i == static_cast<int>(e >> 6)) o = orig[i];
-    }
-    o = __shfl(o, static_cast<int>(e & 63u));  // the winner's lane holds its orig
-    den = __fadd_rn(den, o);
-    if (lane == j) {
-      my_sc = o;
-      a.inds[static_cast<int64_t>(t) * a.k + j] = e;
-    }
-  }
-  if (lane < a.k) {
-    float sc = my_sc;
-    if (a.norm && a.k > 1) sc = sc / __fadd_rn(den, 1e-20f);
-    a.scores32[static_cast<int64_t>(t) * a.k + lane] = __fmul_rn(sc, a.scaling);
-  }
+  nh_select_wave<kMaxExpertsPerLane>(a.logits + static_cast<int64_t>(t) * (a.E + 1), a.E, a.k, a.norm,
+                                     a.n_group, a.topk_group, a.scaling, a.cbias, lane,
+                                     a.inds + static_cast<int64_t>(t) * a.k,
+                                     a.scores32 + static_cast<int64_t>(t) * a.k, nullptr);
 }
 
 static_assert(kPassRows >= kWave, "a segment of at most 64 rows is one pass");
@@ -651,12 +534,26 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
       *reinterpret_cast<u32x4_t*>(a.xp + static_cast<int64_t>(tok) * H + oc * 8) = p;
     }
   }
+  // fp16 copy (P8 layout) of the tile's x rows for the prefill GEMMs, once
+  // per token tile; a value outside fp16's range sets kF16FlagX (the flag
+  // is zero on entry: the caller's forward clears it after its GEMMs)
+  if (ct == 0 && a.xh) {
+    for (int tl = wave; tl < kRouterTok; tl += kRouterWaves) {
+      const int tok = tt * kRouterTok + tl;
+      if (tok < a.T) f16_row(a, tok, lane);
+    }
+  }
   if (!arrive_last(&a.counters[tt], static_cast<uint32_t>(a.n_ct), &s_flag)) return;
 
   // ---- phase 2 (last column tile of this token tile): softmax and top-k
+  // (mode 1: the Nemotron-H selection)
   for (int tl = wave; tl < kRouterTok; tl += kRouterWaves) {
     const int t = tt * kRouterTok + tl;
-    if (t < a.T) router_token(a, t, lane);
+    if (t >= a.T) continue;
+    if (a.mode == 1)
+      router_token_nh(a, t, lane);
+    else
+      router_token(a, t, lane);
   }
   if (tid == 0) a.counters[tt] = 0u;  // every column tile of this token tile has arrived
 

@@ -346,6 +346,9 @@ class MoEBlock:
         boundaries (before the first kernel and after each of the four
         kernel stages)."""
         T = x.numel() // self.cfg.hidden_size
+        for ev in events:  # torch creates an event's HIP handle at its first record
+            if not ev.cuda_event:
+                ev.record()
         arr = (C.c_void_p * 5)(*[ev.cuda_event for ev in events])
         _lib.check(self.lib.fmx_moe_block_forward_profiled(
             C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),

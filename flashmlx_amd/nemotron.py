@@ -120,6 +120,7 @@ class NhMoEBlock:
         if ws == 0:
             _lib.check(_lib.FMX_ERR_ARG)
         self.workspace = torch.empty(ws, dtype=torch.uint8, device=weights.gate_w.device)
+        _lib.check(self.lib.fmx_nh_moe_workspace_init(self.workspace.data_ptr(), ws, _stream()))
         self.max_tokens = max_tokens
         self._last_T = 0
 
@@ -130,6 +131,19 @@ class NhMoEBlock:
         _lib.check(self.lib.fmx_nh_moe_block_forward(
             C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),
             self.workspace.data_ptr(), self.workspace.numel(), _stream()))
+        self._last_T = T
+
+    def forward_profiled(self, x: torch.Tensor, y: torch.Tensor, events) -> None:
+        """forward_into recording 5 torch.cuda.Events at the stage
+        boundaries (router+sort, fc1, fc2, combine)."""
+        T = x.numel() // self.cfg.hidden_size
+        for e in events:  # torch creates an event's HIP handle at its first record
+            if not e.cuda_event:
+                e.record()
+        arr = (C.c_void_p * 5)(*[e.cuda_event for e in events])
+        _lib.check(self.lib.fmx_nh_moe_block_forward_profiled(
+            C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(), _stream(), arr))
         self._last_T = T
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:

@@ -78,16 +78,29 @@ int fmx_nh_pack_expert_weights(const fmx_nh_moe_config* cfg, const fmx_nh_moe_we
                                void* packed, size_t packed_bytes, fmx_stream stream);
 
 /* Bytes of workspace one forward of up to max_tokens tokens needs (0 for an
- * invalid config); nondecreasing in max_tokens. The workspace needs no
- * initialisation. */
+ * invalid config); nondecreasing in max_tokens. fmx_nh_moe_workspace_init
+ * prepares a fresh workspace once (it clears the router's arrival counters
+ * and a flag word in its first bytes, which every forward leaves cleared). */
 size_t fmx_nh_moe_workspace_size(const fmx_nh_moe_config* cfg, int64_t max_tokens);
+int fmx_nh_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream);
 
 /* y [T, H] bf16 = moe_block(x [T, H] bf16) (NemotronHModel::moe_block),
  * T = B*L tokens, on the packed weights; T = 0 runs nothing. workspace NULL:
- * the call allocates its own (stream-ordered). */
+ * the call allocates (and initialises) its own, stream-ordered. */
 int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
                              const void* x, int64_t n_tokens, void* y, void* workspace,
                              size_t workspace_bytes, fmx_stream stream);
+
+/* fmx_nh_moe_block_forward that records caller-created HIP events (as
+ * void*) on `stream` at its stage boundaries: [0] before the router, [1]
+ * after routing and the sort, [2] after the fc1 (+ shared up) grid, [3]
+ * after the fc2 (+ shared down) grid, [4] after the combine. A measurement
+ * aid with no counterpart in the reference. */
+#define FMX_NH_STAGE_EVENTS 5
+int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
+                                      const void* x, int64_t n_tokens, void* y, void* workspace,
+                                      size_t workspace_bytes, fmx_stream stream,
+                                      void* const* stage_events);
 
 /* Device views of the routing the latest forward of n_tokens tokens left in
  * the workspace: inds [T, k] u32, scores [T, k] fp32, logits [T, E + 1] bf16

@@ -61,7 +61,20 @@ def test_nh_tiny_groups_bias_padding(gpu, fmx, oracle, T):
     _check(oracle, cfg, w, _x((T, 256), 100 + T), f"tiny T={T}")
 
 
-@pytest.mark.parametrize("T", [1, 8, 96])
+@pytest.mark.parametrize("T", [1, 3, 16, 17])
+def test_nh_decode_kernels_groups_bias_padding(gpu, fmx, oracle, T):
+    """The decode kernels (T <= 16; 17 takes the prefill path): 32 experts in
+    4 groups (2 kept), top-4, a correction bias, I = 192 and Is = 640 (packed
+    as 256 and 640), H = 512."""
+    from flashmlx_amd import nemotron as N
+    cfg = N.NhMoEConfig(hidden_size=512, n_routed_experts=32, num_experts_per_tok=4,
+                        moe_intermediate_size=192, moe_shared_expert_intermediate_size=640,
+                        n_group=4, topk_group=2, routed_scaling_factor=1.5)
+    w = N.synthetic_nh_weights(cfg, 17, w_std=0.05)
+    _check(oracle, cfg, w, _x((T, 512), 500 + T), f"decode kernels T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 8, 16, 96])
 def test_nh_30b_shape(gpu, fmx, oracle, T):
     """The Nemotron-H 30B-A3B MoE layer shape, no groups, no shared expert
     gate: decode batches and a short prefill."""
