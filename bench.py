@@ -377,17 +377,21 @@ NH_SEED = 16
 
 def nh_bytes_flops(cfg, T: int, U: int):
     """Algorithmic HBM bytes and flops of one Nemotron-H layer forward of T
-    tokens with U distinct experts selected: per kernel grid (fc1 + shared
-    up; fc2 + shared down) the 4-bit weights (0.5625 bytes per weight, the
-    unpadded I and Is) and the products; the whole layer adds the router,
-    the correction bias and x / y."""
+    tokens with U distinct experts selected: per expert grid {"fc1_grid",
+    "fc2_grid"} the 4-bit weights it streams (0.5625 bytes per weight, the
+    unpadded I and Is) and its products; the whole layer adds the router,
+    the correction bias and x / y. The decode kernels (T <= 16) stream the
+    shared up projection beside the router (D1), the prefill GEMMs in the
+    fc1 grid; both run the shared down in the fc2 grid."""
     H, E, k = cfg.hidden_size, cfg.n_routed_experts, cfg.num_experts_per_tok
     I, Is = cfg.moe_intermediate_size, cfg.moe_shared_expert_intermediate_size
     wq = 0.5625
-    grid_bytes = int(U * I * H * wq + Is * H * wq)
-    grid_flops = 2 * T * k * I * H + 2 * T * Is * H
-    layer_bytes = 2 * grid_bytes + E * H * 2 + E * 4 + 2 * T * H * 2
-    return grid_bytes, grid_flops, layer_bytes, 2 * grid_flops + 2 * T * E * H
+    routed, shared = U * I * H * wq, Is * H * wq
+    grid_bytes = {"fc1_grid": int(routed + (0 if T <= 16 else shared)), "fc2_grid": int(routed + shared)}
+    grid_flops = {g: 2 * T * k * I * H + 2 * T * Is * H for g in grid_bytes}
+    layer_bytes = int(2 * (routed + shared) + E * H * 2 + E * 4 + 2 * T * H * 2)
+    layer_flops = 2 * (2 * T * k * I * H + 2 * T * Is * H) + 2 * T * E * H
+    return grid_bytes, grid_flops, layer_bytes, layer_flops
 
 
 def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_seconds: float):
@@ -468,20 +472,21 @@ def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_secon
     dom = max(("fc1_grid", "fc2_grid"), key=lambda nm: stage_ms[nm])
     dur_s = stage_ms[dom] * 1e-3
     if T <= 16:
-        ach = grid_bytes / dur_s / 1e9
+        ach = grid_bytes[dom] / dur_s / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": load_traffic(key, dom),
-                "algorithmic_per_launch": grid_bytes}
+                "algorithmic_per_launch": grid_bytes[dom]}
     else:
-        ach = grid_flops / dur_s / 1e12
+        ach = grid_flops[dom] / dur_s / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": load_traffic(key, dom),
-                "algorithmic_per_launch": grid_flops}
+                "algorithmic_per_launch": grid_flops[dom]}
     roof["stage"] = dom
     roof["avg_launch_us"] = round(stage_ms[dom] * 1e3, 2)
     res = {
         "workload": (f"Nemotron-H MoE block (30B-A3B layer shape: H 2688, 128 experts top-6 sigmoid-routed "
                      f"with correction bias, I 1856, shared 3712, relu^2), {T} tokens, seed {NH_SEED}"),
+        "kernel_path": "decode kernels D1-D4" if T <= 16 else "router + sort + prefill GEMMs + combine",
         "key": key,
         "tokens": T,
         "value": round(T / (ms_step * 1e-3), 1),
