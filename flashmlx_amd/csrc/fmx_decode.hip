@@ -197,27 +197,24 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   const int ld = E + 1;
   // every token's logits -> LDS in one round trip (device-scope loads: the
   // other router workgroups' device-scope stores completed before their
-  // arrivals were counted)
+  // arrivals were counted). The barriers below order LDS only: the global
+  // stores of this workgroup (routing, tables, counters) stay in flight and
+  // drain at the kernel's end.
   const int ncols = E + (a.wsg.w ? 1 : 0);
   for (int i = tid; i < ncols * T; i += kDecThreads) {
     const int c = i / T, t = i - c * T;
-    const uint16_t v = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    s_lg[t * ld + c] = v;
-    a.logits[t * ld + c] = v;
+    s_lg[t * ld + c] = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   }
   for (int e = tid; e < E; e += kDecThreads) s_used[e] = 0;
-  // K23's per-expert gate/up counters and done flags start the next grid at zero
-  for (int i = tid; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads)
-    __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
+  lds_barrier();
   // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
   for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
     const int ts[2] = {t0, t0 + kDecWaves};
     route_tokens<NPER, 2>(a, ts, s_lg, lane, s_inds);
   }
-  __syncthreads();
+  lds_barrier();
   for (int i = tid; i < n; i += kDecThreads) s_used[s_inds[i]] = 1;
-  __syncthreads();
+  lds_barrier();
   if (wave == 0) {
     uint32_t U = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
@@ -234,15 +231,19 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
     if (lane == 0) s_seg[0] = U;
   }
   for (int i = tid; i < E * kDecMaxT; i += kDecThreads) s_slot[i] = 0xff;
-  __syncthreads();
+  lds_barrier();
   const int U = static_cast<int>(s_seg[0]);
   for (int i = tid; i <= U; i += kDecThreads) a.seg[i] = s_seg[i];
   // slot table, one byte per (expert u, token t): entry (t, j) marks its
   // expert's row, then the rows go out as whole words
   for (int i = tid; i < n; i += kDecThreads) s_slot[s_segof[s_inds[i]] * kDecMaxT + i / k] = static_cast<uint8_t>(i % k);
-  __syncthreads();
+  lds_barrier();
   for (int i = tid; i < U * (kDecMaxT / 4); i += kDecThreads)
     reinterpret_cast<uint32_t*>(a.slots)[i] = reinterpret_cast<const uint32_t*>(s_slot)[i];
+  // K23's per-expert gate/up counters and done flags start the next grid at
+  // zero (stores issued last: they drain with the kernel, off the chain)
+  for (int i = tid; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads)
+    __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Router column c (column E: the shared-expert gate row) for every token,
@@ -252,8 +253,9 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
 // to bf16 (model.cpp:757-763, :787-799). Lane g of the workgroup takes
 // 16-byte chunk g of H; each wave's partial sums meet in one reduce-scatter
 // and the four waves' in LDS. The last router workgroup to finish derives
-// the routing.
-template <int NPER>
+// the routing. NT: T rounded up to a power of two (the reduce-scatter's
+// width).
+template <int NPER, int NT>
 __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   __shared__ int s_last;
   double* s_lp = reinterpret_cast<double*>(smem);
@@ -274,9 +276,9 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   double wd[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) wd[q] = tid < nch ? wv.get(q) : 0.0;
-  double part[kDecMaxT];
+  double part[NT];
 #pragma unroll
-  for (int t = 0; t < kDecMaxT; ++t) {
+  for (int t = 0; t < NT; ++t) {
     part[t] = 0.0;
     if (t < T) {
       const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(s_x + t * xs + min(tid, nch - 1) * 8);
@@ -287,9 +289,10 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
       }
     }
   }
-  // lane l then holds the wave's total of token l >> 2
-  const double r = reduce_scatter64<kDecMaxT>(part, lane);
-  if ((lane & 3) == 0) s_lp[wave * kDecMaxT + (lane >> 2)] = r;
+  // lane l then holds the wave's total of token l / (64 / NT)
+  constexpr int kLanesPerToken = kWave / NT;
+  const double r = reduce_scatter64<NT>(part, lane);
+  if ((lane & (kLanesPerToken - 1)) == 0) s_lp[wave * kDecMaxT + lane / kLanesPerToken] = r;
   __syncthreads();
   // The logits go out as device-scope stores (written through to the
   // device's coherence point) from wave 0; once they have completed, thread
@@ -303,6 +306,7 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
       uint16_t l = f64_to_bf16(v);
       if (biased) l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(lb)));
       __hip_atomic_store(a.lgw + c * T + tid, static_cast<uint32_t>(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      a.logits[tid * (E + 1) + c] = l;  // the routing accessor's copy
     }
     wait_vmcnt0();
     if (tid == 0)
@@ -364,12 +368,12 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
 }
 
 // Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
-template <int NPER>
+template <int NPER, int NT>
 __global__ __launch_bounds__(kDecThreads) void dec_k1(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int w = blockIdx.x;
   if (w < a.n_rt)
-    dec_router<NPER>(a, w, smem);
+    dec_router<NPER, NT>(a, w, smem);
   else
     dec_shared_gu(a, w - a.n_rt, smem);
 }
@@ -750,14 +754,28 @@ bool decode_plan(DecodeArgs& a) {
   return k1_lds(a) <= 160 * 1024 && k2_lds(a) <= 160 * 1024 && k3_lds(a) <= 160 * 1024;
 }
 
-hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {
+template <int NPER>
+static void launch_k1_nt(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.n_rt + a.n_sgu), block(kDecThreads);
-  if (a.E <= 64)
-    hipLaunchKernelGGL(dec_k1<1>, grid, block, k1_lds(a), stream, a);
-  else if (a.E <= 128)
-    hipLaunchKernelGGL(dec_k1<2>, grid, block, k1_lds(a), stream, a);
+  if (a.T <= 1)
+    hipLaunchKernelGGL((dec_k1<NPER, 1>), grid, block, k1_lds(a), stream, a);
+  else if (a.T <= 2)
+    hipLaunchKernelGGL((dec_k1<NPER, 2>), grid, block, k1_lds(a), stream, a);
+  else if (a.T <= 4)
+    hipLaunchKernelGGL((dec_k1<NPER, 4>), grid, block, k1_lds(a), stream, a);
+  else if (a.T <= 8)
+    hipLaunchKernelGGL((dec_k1<NPER, 8>), grid, block, k1_lds(a), stream, a);
   else
-    hipLaunchKernelGGL(dec_k1<4>, grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 16>), grid, block, k1_lds(a), stream, a);
+}
+
+hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {
+  if (a.E <= 64)
+    launch_k1_nt<1>(a, stream);
+  else if (a.E <= 128)
+    launch_k1_nt<2>(a, stream);
+  else
+    launch_k1_nt<4>(a, stream);
   return hipGetLastError();
 }
 

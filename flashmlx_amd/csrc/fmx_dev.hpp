@@ -264,6 +264,16 @@ __device__ inline void lds_dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Workgroup barrier for data in LDS only: waits for this wave's LDS
+// operations (lgkmcnt), not for its global stores in flight, which the
+// fence of __syncthreads would drain as well.
+__device__ inline void lds_barrier() {
+  asm volatile("" ::: "memory");
+  wait_lgkmcnt0();
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // ------------------------------------------------------------------ packed 4-bit tiles
 //
 // Packed layout (fmx_pack_expert_weights). A matrix [N, K] is cut into tiles
