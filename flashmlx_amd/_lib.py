@@ -264,6 +264,8 @@ _SIGS = {
     "fmx_scheduler_drain_completed": (
         C.c_int, [C.c_void_p, P(C.c_int64), C.c_int64, P(C.c_int64)]),
     "fmx_scheduler_free": (None, [C.c_void_p]),
+    "fmx_scheduler_set_prefix_cache": (C.c_int, [C.c_void_p, C.c_int64]),
+    "fmx_scheduler_prefix_hits": (C.c_int64, [C.c_void_p]),
     "fmx_nh_moe_packed_size": (C.c_size_t, [P(FmxNhMoEConfig)]),
     "fmx_nh_pack_expert_weights": (
         C.c_int, [P(FmxNhMoEConfig), P(FmxNhMoEWeights), C.c_void_p, C.c_size_t, C.c_void_p]),

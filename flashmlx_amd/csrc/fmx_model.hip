@@ -485,7 +485,32 @@ __global__ __launch_bounds__(256) void copy_u32_kernel(const uint32_t* src, uint
     dst[i] = src[i];
 }
 
+// one 16-byte chunk of one (layer, k/v, head, position) row per thread
+__global__ __launch_bounds__(256) void kv_copy_kernel(KvCopyArgs a) {
+  const int64_t per_row = a.hd / 8;
+  const int64_t n = a.layers * 2 * a.nkv * a.n_pos * per_row;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t c8 = i % per_row, r = i / per_row;
+    const int64_t p = r % a.n_pos, lh = r / a.n_pos;  // lh = (layer * 2 + kv) * nkv + head
+    const int64_t h = lh % a.nkv, lk = lh / a.nkv;
+    const int64_t co = (((lk * a.cache_batch + a.slot) * a.nkv + h) * a.max_seq + p) * a.hd + c8 * 8;
+    const int64_t eo = ((lk * a.nkv + h) * a.cap + p) * a.hd + c8 * 8;
+    u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.to_cache ? a.cache + co : a.entry + eo);
+    const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.to_cache ? a.entry + eo : a.cache + co);
+    *dst = *src;
+  }
+}
+
 }  // namespace
+
+hipError_t launch_kv_copy(const KvCopyArgs& a, hipStream_t stream) {
+  const int64_t n = a.layers * 2 * a.nkv * a.n_pos * (a.hd / 8);
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(kv_copy_kernel, dim3(static_cast<uint32_t>(blocks < 4096 ? blocks : 4096)), dim3(256), 0,
+                     stream, a);
+  return hipGetLastError();
+}
 
 hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;

@@ -101,4 +101,16 @@ hipError_t launch_greedy(const GreedyArgs& a, int B, hipStream_t stream);
 
 hipError_t launch_copy_u32(const uint32_t* src, uint32_t* dst, int64_t n, hipStream_t stream);
 
+// Positions [0, n_pos) of one KV-cache slot ([layers][2][cache_batch][nkv]
+// [max_seq][hd] bf16) to or from a compact copy [layers][2][nkv][cap][hd]
+// (cap >= n_pos): the scheduler's prefix cache.
+struct KvCopyArgs {
+  uint16_t* cache;
+  uint16_t* entry;
+  int64_t layers, cache_batch, nkv, max_seq, hd, cap, n_pos;
+  int64_t slot;
+  int to_cache;          // 1: entry -> cache slot; 0: cache slot -> entry
+};
+hipError_t launch_kv_copy(const KvCopyArgs& a, hipStream_t stream);
+
 }  // namespace fmx

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "../../include/fmx_model.h"
+#include "fmx_model_kernels.hpp"
 
 namespace fmx {
 int set_error(int status, const char* msg);
@@ -53,6 +54,13 @@ int fail(int status, const char* fmt, ...) {
     int rc_ = (expr);    \
     if (rc_) return rc_; \
   } while (0)
+
+// A cached prompt: its tokens and the keys/values of its positions 0 .. n-2
+// in a compact buffer [layers][2][nkv][max_prompt][hd].
+struct PrefixEntry {
+  std::vector<int32_t> tokens;
+  void* kv = nullptr;
+};
 
 struct Request {
   std::vector<int32_t> prompt;
@@ -89,7 +97,19 @@ struct fmx_scheduler {
   // offsets and slots, refilled before every launch
   std::vector<hipGraphExec_t> graphs;
   std::vector<int> uses;
+  // prefix cache (oldest first) and its free entry buffers
+  int64_t pc_max = 0, pc_hits = 0;
+  std::deque<PrefixEntry> pc;
+  std::vector<void*> pc_free;
+  void free_prefix_cache() {
+    for (auto& e : pc) pc_free.push_back(e.kv);
+    pc.clear();
+    for (void* p : pc_free) (void)hipFree(p);
+    pc_free.clear();
+    pc_max = 0;
+  }
   ~fmx_scheduler() {
+    free_prefix_cache();
     for (hipGraphExec_t g : graphs)
       if (g) (void)hipGraphExecDestroy(g);
     for (void* p : {kv, ws, logits, static_cast<void*>(d_ids), static_cast<void*>(d_offs),
@@ -102,10 +122,56 @@ struct fmx_scheduler {
 
 namespace {
 
+KvCopyArgs kv_copy_args(const fmx_scheduler& s, void* entry, int slot, int64_t n_pos, int to_cache) {
+  const fmx_model_config& c = s.cfg;
+  KvCopyArgs k{};
+  k.cache = static_cast<uint16_t*>(s.kv);
+  k.entry = static_cast<uint16_t*>(entry);
+  k.layers = c.num_hidden_layers;
+  k.cache_batch = s.n_slots;
+  k.nkv = c.num_key_value_heads;
+  k.max_seq = s.max_context;
+  k.hd = c.head_dim ? c.head_dim : c.hidden_size / c.num_attention_heads;
+  k.cap = s.max_prompt;
+  k.n_pos = n_pos;
+  k.slot = slot;
+  k.to_cache = to_cache;
+  return k;
+}
+
+// prefill_request with a prefix-cache hit (scheduler.cpp:121-168): the cached
+// keys/values of positions 0 .. n-2 into the slot, then the last prompt
+// token alone at offset n-1 (a decode step) gives the first token
+int prefill_cached(fmx_scheduler& s, Request& r, const PrefixEntry& e) {
+  const int64_t n = static_cast<int64_t>(r.prompt.size());
+  int32_t* h = s.h_buf;
+  h[0] = r.prompt.back();
+  h[1] = r.slot;
+  FMX_HIP(launch_kv_copy(kv_copy_args(s, e.kv, r.slot, n - 1, 1), s.stream));
+  FMX_HIP(hipMemcpyAsync(s.d_ids, h, 4, hipMemcpyHostToDevice, s.stream));
+  FMX_HIP(hipMemcpyAsync(s.d_slots, h + 1, 4, hipMemcpyHostToDevice, s.stream));
+  FMX_RC(fmx_model_forward_batched(&s.cfg, s.w, s.d_ids, 1, 1, n - 1, nullptr, s.d_slots, s.kv, s.n_slots,
+                                   s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
+  FMX_RC(fmx_greedy_next(s.logits, 1, s.V, s.V, s.d_next, nullptr, 0, s.stream));
+  FMX_HIP(hipMemcpyAsync(h, s.d_next, 4, hipMemcpyDeviceToHost, s.stream));
+  FMX_HIP(hipStreamSynchronize(s.stream));
+  r.offset = n;
+  r.next = h[0];
+  r.generated = 1;
+  s.pc_hits += 1;
+  return FMX_OK;
+}
+
 // prefill_request (scheduler.cpp:103-211): batch-1 prefill of the prompt into
-// slot r.slot at offset 0, first token = argmax of the last position
+// slot r.slot at offset 0, first token = argmax of the last position; with
+// the prefix cache on, a prompt seen before takes prefill_cached, and a new
+// one is cached afterwards (:213-231), the oldest entry making room
 int prefill(fmx_scheduler& s, Request& r) {
   const int64_t n = static_cast<int64_t>(r.prompt.size());
+  const bool cacheable = s.pc_max > 0 && n > 1;
+  if (cacheable)
+    for (const PrefixEntry& e : s.pc)
+      if (e.tokens == r.prompt) return prefill_cached(s, r, e);
   int32_t* h = s.h_buf;
   for (int64_t i = 0; i < n; ++i) h[i] = r.prompt[static_cast<size_t>(i)];
   h[n] = r.slot;
@@ -115,6 +181,19 @@ int prefill(fmx_scheduler& s, Request& r) {
                                    s.max_context, 1, s.logits, s.ws, s.ws_bytes, s.stream, nullptr));
   FMX_RC(fmx_greedy_next(s.logits, 1, s.V, s.V, s.d_next, nullptr, 0, s.stream));
   FMX_HIP(hipMemcpyAsync(h, s.d_next, 4, hipMemcpyDeviceToHost, s.stream));
+  if (cacheable) {
+    PrefixEntry e;
+    if (static_cast<int64_t>(s.pc.size()) >= s.pc_max) {
+      e.kv = s.pc.front().kv;
+      s.pc.pop_front();
+    } else {
+      e.kv = s.pc_free.back();
+      s.pc_free.pop_back();
+    }
+    e.tokens = r.prompt;
+    FMX_HIP(launch_kv_copy(kv_copy_args(s, e.kv, r.slot, n - 1, 0), s.stream));
+    s.pc.push_back(std::move(e));
+  }
   FMX_HIP(hipStreamSynchronize(s.stream));
   r.offset = n;
   r.next = h[0];
@@ -343,6 +422,30 @@ int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_
   clear_error();
   return FMX_OK;
 }
+
+int fmx_scheduler_set_prefix_cache(fmx_scheduler* s, int64_t max_entries) {
+  if (!s) return fail(FMX_ERR_ARG, "NULL scheduler");
+  if (max_entries < 0 || max_entries > FMX_SCHED_MAX_PREFIX_ENTRIES)
+    return fail(FMX_ERR_SHAPE, "max_entries %lld (0..%d)", (long long)max_entries, FMX_SCHED_MAX_PREFIX_ENTRIES);
+  s->free_prefix_cache();
+  const fmx_model_config& c = s->cfg;
+  const int64_t hd = c.head_dim ? c.head_dim : c.hidden_size / c.num_attention_heads;
+  const size_t bytes = static_cast<size_t>(c.num_hidden_layers * 2 * c.num_key_value_heads * s->max_prompt * hd * 2);
+  for (int64_t i = 0; i < max_entries; ++i) {
+    void* p = nullptr;
+    const hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+      s->free_prefix_cache();
+      return fail(FMX_ERR_HIP, "prefix cache entry %lld of %zu bytes: %s", (long long)i, bytes, hipGetErrorString(e));
+    }
+    s->pc_free.push_back(p);
+  }
+  s->pc_max = max_entries;
+  clear_error();
+  return FMX_OK;
+}
+
+int64_t fmx_scheduler_prefix_hits(const fmx_scheduler* s) { return s ? s->pc_hits : 0; }
 
 void fmx_scheduler_free(fmx_scheduler* s) { delete s; }
 

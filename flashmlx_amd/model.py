@@ -217,7 +217,10 @@ class BatchScheduler:
     / active_count over a KV pool of n_slots slots of max_context positions.
     Greedy decoding only (temperature 0)."""
 
-    def __init__(self, cfg: ModelConfig, w, n_slots: int, max_context: int, max_prompt: int):
+    def __init__(self, cfg: ModelConfig, w, n_slots: int, max_context: int, max_prompt: int,
+                 prefix_cache: int = 0):
+        """prefix_cache: entries of the prompt prefix cache (the reference
+        keeps 32; 0 = off)."""
         self.lib = _lib.load()
         self.cfg, self.w = cfg, w
         self._c_cfg = cfg.to_c()
@@ -227,6 +230,8 @@ class BatchScheduler:
         _lib.check(self.lib.fmx_scheduler_create(C.byref(self._c_cfg), C.byref(self._c_w), n_slots,
                                                  max_context, max_prompt, _stream(), C.byref(h)))
         self._h = h
+        if prefix_cache:
+            _lib.check(self.lib.fmx_scheduler_set_prefix_cache(h, prefix_cache))
         self._ids = (C.c_int64 * (2 * n_slots))()
         self._toks = (C.c_int32 * (2 * n_slots))()
 
@@ -261,6 +266,9 @@ class BatchScheduler:
 
     def has_work(self) -> bool:
         return bool(self.lib.fmx_scheduler_has_work(self._h))
+
+    def prefix_hits(self) -> int:
+        return int(self.lib.fmx_scheduler_prefix_hits(self._h))
 
     def active_count(self) -> int:
         return int(self.lib.fmx_scheduler_active_count(self._h))

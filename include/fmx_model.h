@@ -223,6 +223,21 @@ int fmx_scheduler_has_work(fmx_scheduler* s);
 int64_t fmx_scheduler_active_count(const fmx_scheduler* s);
 int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_t capacity,
                                   int64_t* n);
+
+/* The prefix cache of prefill_request (scheduler.cpp:121-168, :213-231; 32
+ * entries at scheduler.h:78): the keys and values of up to max_entries
+ * prompts of more than one token are kept (positions 0 .. n-2, device
+ * memory allocated by this call: layers * 2 * nkv * max_prompt * hd bf16
+ * per entry). A request whose prompt equals a cached one copies them into
+ * its slot and forwards only its last prompt token (a decode step) for its
+ * first token, as the reference does; its tokens may then differ from an
+ * uncached prefill where the last position's logits are at a near-tie.
+ * Entries match on the whole token sequence (the reference compares a
+ * hash); the oldest is evicted first (the reference evicts an arbitrary
+ * one). 0 (the default) turns the cache off and frees it. */
+#define FMX_SCHED_MAX_PREFIX_ENTRIES 1024
+int fmx_scheduler_set_prefix_cache(fmx_scheduler* s, int64_t max_entries);
+int64_t fmx_scheduler_prefix_hits(const fmx_scheduler* s);
 void fmx_scheduler_free(fmx_scheduler* s);
 
 /* Greedy next token: ids[b] = argmax_v logits[b * row_stride + v] (the

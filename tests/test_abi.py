@@ -313,6 +313,8 @@ def test_scheduler_validation(fmx):
     ids = (C.c_int64 * 2)()
     toks = (C.c_int32 * 2)()
     assert lib.fmx_scheduler_step(None, ids, toks, 2, C.byref(n)) == _lib.FMX_ERR_ARG
+    assert lib.fmx_scheduler_set_prefix_cache(None, 4) == _lib.FMX_ERR_ARG
+    assert lib.fmx_scheduler_prefix_hits(None) == 0
     lib.fmx_scheduler_free(None)
 
 

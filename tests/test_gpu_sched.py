@@ -116,3 +116,57 @@ def test_scheduler_refusals(gpu, fmx):
         assert e.value.status == status
     assert not sched.has_work()
     sched.close()
+
+
+def _alone_split(cfg, w, prompt, n_new, max_ctx):
+    """The prefix-cache path of a request run by hand: prefill of all but the
+    last prompt token, the last one as a decode step, then greedy decoding."""
+    import torch
+    from flashmlx_amd import model as M
+    dm = M.DecoderModel(cfg, w, 1, max_ctx, max(len(prompt), 1))
+    p = torch.tensor([prompt], dtype=torch.int32, device="cuda")
+    n = len(prompt)
+    dm.forward(p[:, :-1].contiguous(), 0)
+    logits = dm.forward(p[:, -1:].contiguous(), n - 1)
+    ids = torch.empty((1, 1), dtype=torch.int32, device="cuda")
+    out = []
+    for i in range(n_new):
+        dm.greedy(logits, ids.view(-1))
+        out.append(int(ids.item()))
+        if i + 1 < n_new:
+            dm.forward_into(ids, n + i, logits)
+    torch.cuda.synchronize()
+    return out
+
+
+def test_scheduler_prefix_cache(gpu, fmx):
+    """With the prefix cache on, a repeated prompt is served from the cache
+    (one hit; its tokens equal prefill of n-1 tokens + the last token as a
+    decode step, the reference's cached path), new prompts are prefilled
+    (tokens equal the request alone), and with one entry a third prompt
+    evicts the first, whose repeat is then prefilled again."""
+    import torch
+    from flashmlx_amd import model as M
+    cfg = _tiny_cfg()
+    w = M.synthetic_model(cfg, 53)
+    rng = np.random.default_rng(9)
+    p1 = rng.integers(0, cfg.vocab_size, size=9).tolist()
+    p2 = rng.integers(0, cfg.vocab_size, size=6).tolist()
+    max_ctx = 32
+    sched = M.BatchScheduler(cfg, w, 2, max_ctx, 12, prefix_cache=2)
+    toks, index, _, _ = _run(sched, [(p1, 5), (p2, 4)], [(p1, 7)], 2)
+    torch.cuda.synchronize()
+    assert sched.prefix_hits() == 1
+    by_i = {i: toks[rid] for rid, i in index.items()}
+    assert by_i[0] == _alone(cfg, w, p1, 5, max_ctx)
+    assert by_i[1] == _alone(cfg, w, p2, 4, max_ctx)
+    assert by_i[2] == _alone_split(cfg, w, p1, 7, max_ctx)
+    sched.close()
+    # one entry: p1, then p2 (evicts p1), then p1 again is a miss
+    sched = M.BatchScheduler(cfg, w, 1, max_ctx, 12, prefix_cache=1)
+    toks, index, _, _ = _run(sched, [(p1, 3), (p2, 3), (p1, 4)], [], 0)
+    torch.cuda.synchronize()
+    assert sched.prefix_hits() == 0
+    by_i = {i: toks[rid] for rid, i in index.items()}
+    assert by_i[2] == _alone(cfg, w, p1, 4, max_ctx)
+    sched.close()
