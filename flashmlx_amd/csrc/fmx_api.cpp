@@ -153,7 +153,7 @@ struct MoELayout {
   uint32_t *pass_n, *pass_tab;
   uint8_t* slots;
   float* sgate;
-  uint16_t *xp, *h, *hs, *d, *sd;
+  uint16_t *xp, *h, *hs, *d;
   uint16_t *xh, *hh, *hsh;  // fp16 copies (P8 layout) of x, h, hs: prefill GEMM inputs
   uint32_t* f16_flag;
   uint32_t* dw;
@@ -193,7 +193,6 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.hs = static_cast<uint16_t*>(ar.take(T * Is * 2));
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
-  L.sd = static_cast<uint16_t*>(ar.take(Is ? T * H * 2 : 0));
   L.f16_flag = static_cast<uint32_t*>(ar.take(4));
   L.xh = static_cast<uint16_t*>(ar.take(T * H * 2));
   L.hh = static_cast<uint16_t*>(ar.take(n * I * 2));
@@ -1079,6 +1078,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       return s;
     };
     const uint16_t* xb = static_cast<const uint16_t*>(x);
+    int sd_split = 0;
     {
       PfArgs pa{};
       pa.s1 = routed(pk + PL.gu, PL.gu_es, xb, L.xh, H, L.src, L.h, L.hh, I, I, H);
@@ -1099,8 +1099,21 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       pa.s1 = routed(pk + PL.dn, PL.dn_es, L.h, L.hh, I, nullptr, L.d, nullptr, H, H, I);
       pa.n_items1 = pf_items(pa.s1, false);
       if (has_sh) {
-        pa.s0 = shared(pk + PL.sdn, L.hs, L.hsh, Is, L.sd, nullptr, H, H, Is);
+        // up to 256 tokens (four 64-token passes) the shared down
+        // projection's K (Is) is cut into slices about as long as the routed
+        // experts' (I), fp32 partial sums added by the combine: its few long
+        // items otherwise outlast the routed ones (Qwen1.5 shape: 17 tokens
+        // 77 -> 63 us per layer, 256 tokens 121 -> 113 us; at 512 tokens the
+        // slices' extra items cost 4 %)
+        pa.s0 = shared(pk + PL.sdn, L.hs, L.hsh, Is, nullptr, nullptr, H, H, Is);
+        pa.s0.out32 = L.sd_part;
+        pa.s0.ksplit = T > 4 * kPassRows
+                           ? 1
+                           : static_cast<int>(std::min<int64_t>(std::max<int64_t>((Is + I - 1) / I, 1),
+                                                                std::min<int64_t>(kSharedDownSplit, Is / 128)));
+        pa.s0.part_stride = T * H;
         pa.n_items0 = pf_items(pa.s0, false);
+        sd_split = pa.s0.ksplit;
       }
       pa.f16_flag = L.f16_flag;
       pa.flag_in = kF16FlagH;
@@ -1113,7 +1126,8 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     cb.d = L.d;
     cb.inv = L.inv;
     cb.scores = L.scores;
-    cb.sd = has_sh ? L.sd : nullptr;
+    cb.sd_part = has_sh ? L.sd_part : nullptr;
+    cb.sd_ksplit = sd_split;
     cb.sgate = has_sh ? L.sgate : nullptr;
     cb.y = static_cast<uint16_t*>(y);
     cb.T = static_cast<int>(T);

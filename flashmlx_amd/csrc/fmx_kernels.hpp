@@ -222,6 +222,11 @@ struct PfSet {
   // (non-null) takes the fp32 products unrounded instead of out
   int act;
   float* out32;
+  // static sets with out32 only: ksplit > 1 cuts K into that many slices of
+  // whole units, one work item each; slice ks writes its fp32 sums to
+  // out32 + ks * part_stride
+  int ksplit;
+  int64_t part_stride;
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)

@@ -89,8 +89,8 @@ __device__ inline void dma4(const void* g, void* lds) {
 // and multiplied once, without padding to kPassRows.
 template <bool DUAL, int MT, bool F16>
 __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, int row0, int rows,
-                                                       int64_t e, uint8_t* s_pf, uint32_t* flag,
-                                                       uint32_t flag_out) {
+                                                       int64_t e, int ks, uint8_t* s_pf,
+                                                       uint32_t* flag, uint32_t flag_out) {
   constexpr int NB = pf_nb<DUAL>(), NM = pf_nm<DUAL>();
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
   constexpr int PA = (4 * MT + kPfWaves - 1) / kPfWaves;  // 4-row pieces per wave and unit
@@ -102,7 +102,10 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, j = lane >> 4;
-  const int nu = P.nu;
+  // K slice ks of the set's ksplit: units [kb, kb + nu) of the P.nu
+  const int kn = max(P.ksplit, 1);
+  const int kb = (P.nu * ks) / kn;
+  const int nu = (P.nu * (ks + 1)) / kn - kb;
 
   // ---- sources: this wave's packed blocks (tiles past the matrix re-read
   // its last tile and are not stored) and its row pieces' lanes
@@ -111,7 +114,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   const uint8_t* bsrc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
-    bsrc[b] = wexp + static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * nu * BB;
+    bsrc[b] = wexp + (static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * P.nu + kb) * BB;
   const uint16_t* asrc[PA];
 #pragma unroll
   for (int pc = 0; pc < PA; ++pc) {
@@ -119,13 +122,13 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     const int rr = min(r, rows - 1);               // rows past the pass repeat its last
     int64_t xr = row0 + rr;
     if (P.row_map) xr = min(P.row_map[row0 + rr], static_cast<uint32_t>(P.x_rows - 1));
-    asrc[pc] = (F16 ? P.xh : P.x) + xr * P.ldx + 8 * (i16 ^ (r & 15));
+    asrc[pc] = (F16 ? P.xh : P.x) + xr * P.ldx + 128 * kb + 8 * (i16 ^ (r & 15));
   }
 
   // the (scale, bias) piece: lane l fetches 4 bytes of block l / SBL's
   // 16 x 8 (single) or 2 x 16 x 8 (pair) bytes
   constexpr int SBL = kWave / NB;  // lanes per block
-  const uint8_t* sb_src = wexp + static_cast<int64_t>(min(tile0 + lane / SBL, P.nt - 1)) * nu * BB +
+  const uint8_t* sb_src = wexp + (static_cast<int64_t>(min(tile0 + lane / SBL, P.nt - 1)) * P.nu + kb) * BB +
                           NM * 1024 + 4 * (lane % SBL);
 
   auto issue = [&](int u, int st) {
@@ -265,6 +268,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   // in fp16 (P8 layout) for the down grid and flags values outside fp16's
   // range
   bool ovf = false;
+  float* const out32 = P.out32 ? P.out32 + ks * P.part_stride : nullptr;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -283,8 +287,8 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
           P.out[orow + col] = v;
           ovf |= bf16_f16_overflow(v);
           P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
-        } else if (P.out32) {
-          P.out32[orow + col] = acc[mt][b][0][r];
+        } else if (out32) {
+          out32[orow + col] = acc[mt][b][0][r];
         } else if (P.act) {
           // relu^2 of the bf16 product (Nemotron-H, nemotron_h.cpp:54-63):
           // exact in fp32; bf16 and fp16 copies for the down grid
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   if (second) b -= a.n_items0;
   const PfSet& P = second ? a.s1 : a.s0;
   const int x = b % kXcds, l = b / kXcds;
-  int pass, ng;
+  int pass, ng, ks = 0;
   if (P.pass_n) {
     // XCD x takes a contiguous range of the pass table, so an expert's
     // passes (consecutive in the table) run back to back on one L2
@@ -332,9 +336,12 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
     pass = x * per + l / P.ng;
     ng = l % P.ng;
   } else {
+    // XCD x runs every pass and K slice of one column group back to back
     const int np = (P.rows_static + kPassRows - 1) / kPassRows;
-    ng = x + kXcds * (l / np);
-    pass = l % np;
+    const int per = np * max(P.ksplit, 1);
+    ng = x + kXcds * (l / per);
+    pass = (l % per) % np;
+    ks = (l % per) / np;
     if (ng >= P.ng) return;
   }
 
@@ -359,17 +366,17 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   const bool exact = __builtin_amdgcn_readfirstlane(*a.f16_flag & a.flag_in) != 0;
   if (exact) {
     switch ((rows + 15) / 16) {
-      case 1: pf_item<DUAL, 1, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      case 2: pf_item<DUAL, 2, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      case 3: pf_item<DUAL, 3, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      default: pf_item<DUAL, 4, false>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 1: pf_item<DUAL, 1, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
     }
   } else {
     switch ((rows + 15) / 16) {
-      case 1: pf_item<DUAL, 1, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      case 2: pf_item<DUAL, 2, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      case 3: pf_item<DUAL, 3, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
-      default: pf_item<DUAL, 4, true>(P, ng, row0, rows, e, s_pf, a.f16_flag, a.flag_out); break;
+      case 1: pf_item<DUAL, 1, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
     }
   }
 }
@@ -382,7 +389,7 @@ int pf_items(PfSet& s, bool dual) {
   if (s.pass_n)  // pass-major per XCD
     return kXcds * s.ng * ((s.max_pass + kXcds - 1) / kXcds);
   const int np = (s.rows_static + kPassRows - 1) / kPassRows;  // group-major per XCD
-  return kXcds * np * ((s.ng + kXcds - 1) / kXcds);
+  return kXcds * np * max(s.ksplit, 1) * ((s.ng + kXcds - 1) / kXcds);
 }
 
 size_t pf_lds_bytes(bool dual) {
@@ -392,6 +399,9 @@ size_t pf_lds_bytes(bool dual) {
 hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream) {
   const int n = a.n_items0 + a.n_items1;
   if (n == 0) return hipSuccess;
+  // K slices only for static single-matrix sets with fp32 outputs
+  for (const PfSet* s : {&a.s0, &a.s1})
+    if (s->ksplit > 1 && (dual || s->pass_n || !s->out32 || s->ksplit > s->nu)) return hipErrorInvalidValue;
   if (dual)
     hipLaunchKernelGGL(pf_gemm<true>, dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
   else
