@@ -3,6 +3,7 @@
 // for all-MoE models, with the MoE block on fmx_moe_block_forward.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -370,11 +371,13 @@ int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weigh
     ra.q_out = M.qrot;
     ra.kc = kc;
     ra.vc = vc;
-    // single-token forwards rotate and cache inside the attention kernel
-    if (Lq > 1) FMX_HIP(launch_rope_cache(ra, static_cast<int>(T), stream));
+    // single-token forwards (head size up to kAttnSplitMaxHd, 64 / (hd / 8)
+    // whole keys per load) rotate and cache inside the attention kernel
+    const bool fused = Lq == 1 && d.hd <= kAttnSplitMaxHd && kWave % (d.hd / 8) == 0;
+    if (!fused) FMX_HIP(launch_rope_cache(ra, static_cast<int>(T), stream));
     AttnArgs aa{};
     aa.q = M.qrot;
-    aa.qkv = Lq == 1 ? M.qkv : nullptr;
+    aa.qkv = fused ? M.qkv : nullptr;
     aa.cs = M.rope;
     aa.L = ra.L;
     aa.nh = ra.nh;

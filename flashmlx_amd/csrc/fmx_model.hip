@@ -8,6 +8,8 @@
 // o_proj), :891-911 (transformer_block), :1021-1033 (forward), :499-521
 // (lm_head). The projections of more than 16 rows run on the prefill GEMM
 // grid (fmx_prefill.hip); the MoE block is fmx_moe_block_forward.
+#include <algorithm>
+
 #include "fmx_dev.hpp"
 #include "fmx_model_kernels.hpp"
 
@@ -217,21 +219,16 @@ __global__ __launch_bounds__(256) void rope_cache_kernel(RopeArgs a) {
 //           fma), the quarter sums added in order; rounded once to bf16
 // (mx::fast::scaled_dot_product_attention, model.cpp:879-882). Scores: a
 // thread per key; the weighted sum: wave w takes quarter w, its lanes pairs
-// of dimensions.
-// ROPE (single-token forwards): the workgroup also rotates its q head and
-// its kv head's new key from the q/k/v row itself (as rope_cache_kernel
-// does), uses the new key and value for position p from LDS, and the first q
-// head of each kv group writes them into the caches; no other workgroup
-// reads position p in this launch.
+// of dimensions. Forwards of several tokens per sequence, after
+// rope_cache_kernel (single-token forwards: attn_split_kernel).
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kAttnBatch = 32;  // keys whose value words are loaded together
 
-template <bool ROPE, int PAIRS>
+template <int PAIRS>
 __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t s_at[];
   __shared__ float s_q[kAttnMaxHd];
-  __shared__ uint16_t s_knew[kAttnMaxHd], s_vnew[kAttnMaxHd];
   __shared__ float s_max[kAttnWaves];
   __shared__ double s_num[kAttnWaves][kAttnMaxHd];
   __shared__ double s_den[kAttnWaves];
@@ -246,37 +243,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
   const int64_t cbase = (cache_slot(a.slots, a.n_slots, b) * a.nkv + g) * a.max_seq * a.hd;
   uint16_t* kb = a.kc + cbase;
   uint16_t* vb = a.vc + cbase;
-  if (ROPE) {
-    const int half = a.hd / 2;
-    const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
-    const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
-    for (int i = tid; i < 2 * half; i += kAttnThreads) {
-      const int hd_i = i % half;
-      const uint16_t* src = row + (i < half ? h : a.nh + g) * a.hd;
-      const double x1 = bf16_to_f32(src[hd_i]), x2 = bf16_to_f32(src[hd_i + half]);
-      const double c = cs[2 * hd_i], sn = cs[2 * hd_i + 1];
-      const uint16_t o1 = f64_to_bf16(__builtin_fma(x1, c, -(x2 * sn)));
-      const uint16_t o2 = f64_to_bf16(__builtin_fma(x1, sn, x2 * c));
-      if (i < half) {
-        s_q[hd_i] = bf16_to_f32(o1);
-        s_q[hd_i + half] = bf16_to_f32(o2);
-      } else {
-        s_knew[hd_i] = o1;
-        s_knew[hd_i + half] = o2;
-      }
-    }
-    for (int d = tid; d < a.hd; d += kAttnThreads) s_vnew[d] = row[(a.nh + a.nkv + g) * a.hd + d];
-    __syncthreads();
-    if (h % rep == 0)
-      for (int d = tid; d < a.hd; d += kAttnThreads) {
-        kb[static_cast<int64_t>(p) * a.hd + d] = s_knew[d];
-        vb[static_cast<int64_t>(p) * a.hd + d] = s_vnew[d];
-      }
-  } else {
-    const uint16_t* qrow = a.q + (static_cast<int64_t>(t) * a.nh + h) * a.hd;
-    for (int d = tid; d < a.hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qrow[d]);
-    __syncthreads();
-  }
+  const uint16_t* qrow = a.q + (static_cast<int64_t>(t) * a.nh + h) * a.hd;
+  for (int d = tid; d < a.hd; d += kAttnThreads) s_q[d] = bf16_to_f32(qrow[d]);
+  __syncthreads();
 
   // this wave's quarter of the keys for the weighted sum below; its first
   // kAttnBatch value words are loaded now, so that their latency overlaps
@@ -284,9 +253,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
   const int quarter = (nk + kAttnWaves - 1) / kAttnWaves;
   const int j0 = min(wave * quarter, nk), j1 = min(j0 + quarter, nk);
   const int npair = a.hd / 2;
-  // keys before jg come from the cache; with ROPE the last key (p) comes
-  // from LDS, after them (it is the last key of the last non-empty quarter)
-  const int jg = ROPE ? min(j1, p) : j1;
+  const int jg = j1;
   // lanes past the head's pairs read pair 0 (in bounds) and discard it
   uint32_t vv[kAttnBatch][PAIRS];
   int prl[PAIRS];
@@ -304,8 +271,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
 
   // scores, a thread per key
   float m = -__builtin_huge_valf();
-  const int nkg = ROPE ? p : nk;  // keys read from the cache
-  for (int jk = tid; jk < nkg; jk += kAttnThreads) {
+  for (int jk = tid; jk < nk; jk += kAttnThreads) {
     // the key row's chunks are loaded 16 at a time, then used in order
     float acc = 0.0f;
     const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(jk) * a.hd);
@@ -327,13 +293,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
     }
     const float sc = acc * a.scale;
     s_s[jk] = sc;
-    m = fmaxf(m, sc);
-  }
-  if (ROPE && tid == kAttnThreads - 1) {  // the new key, from LDS
-    float acc = 0.0f;
-    for (int d = 0; d < a.hd; ++d) acc = __builtin_fmaf(s_q[d], bf16_to_f32(s_knew[d]), acc);
-    const float sc = acc * a.scale;
-    s_s[p] = sc;
     m = fmaxf(m, sc);
   }
 #pragma unroll
@@ -368,17 +327,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
       }
     }
   }
-  if (ROPE && jg < j1) {  // the new key's value (position p), last in key order
-    const double e = s_e[p];
-    den += e;
-    const uint32_t* vr = reinterpret_cast<const uint32_t*>(s_vnew);
-#pragma unroll
-    for (int i = 0; i < PAIRS; ++i) {
-      const uint32_t w2 = vr[prl[i]];
-      num[i][0] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w2 & 0xffffu)), num[i][0]);
-      num[i][1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w2 >> 16)), num[i][1]);
-    }
-  }
 #pragma unroll
   for (int i = 0; i < PAIRS; ++i) {
     const int pr = lane + kWave * i;
@@ -403,6 +351,277 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
     a.out[static_cast<int64_t>(t) * a.ldo + oc] = o;
     if (a.outh) {
       ovf = ovf || bf16_f16_overflow(o);
+      a.outh[static_cast<int64_t>(t) * a.ldo + ((oc & ~7) | p8_slot(oc & 7))] =
+          static_cast<uint16_t>(bf16_to_f16_bits(o));
+    }
+  }
+  if (a.outh && __ballot(ovf) && lane == 0) atomicOr(a.flag, 1u);
+}
+
+// ------------------------------------------------------------------ split attention
+
+// Single-token forwards (L == 1, head size at most kAttnSplitMaxHd): one
+// workgroup per (token t, q head h), the keys 0 .. p in S = min(
+// kAttnSplitMax, ceil((p + 1) / kAttnSplitKeys)) contiguous ranges
+// [nk s / S, nk (s + 1) / S), wave s taking range s. At batch 1 the
+// kernel's time is one workgroup's chain of memory round trips, so a wave
+// issues everything its first 64 keys need at once, in the order it uses
+// them (the rotation's inputs, 64 key rows, then 16-byte value chunks of 32
+// keys: 29 loads, within the 63 a wave can have outstanding; the next 32
+// keys' values follow the scores), all as whole rows. In range s:
+//   s_j = scale * (((P_0 + P_1) + ...) + P_{hd/8-1}), P_c = sum_{d in chunk
+//         c} q_d k_jd (8 dimensions in order; exact bf16 products in fp32):
+//         lane (key, c) forms P_c, an LDS transpose hands a key's P_c to one
+//         lane, which adds them in order
+//   m_s = max of the range's scores
+//   e_j = exp(s_j - m_s) (fp64, the deterministic exp)
+//   over the key classes c = (j - j0) mod 4, each in key order:
+//   den_s = ((D_0 + D_1) + D_2) + D_3, D_c = sum_j e_j
+//   num_s,d = ((N_0 + N_1) + N_2) + N_3, N_c = sum_j e_j v_jd (fma)
+//   (lane (c, i) accumulates class c for dimensions 8i .. 8i + 7)
+// and the ranges combine through LDS, in order:
+//   M = max m_s, f_s = exp(m_s - M), den = sum_s f_s den_s,
+//   num_d = sum_s f_s num_s,d (fma; the first term a product),
+//   out_d = bf16(num_d / den)
+// (one range: f_0 = 1, the range's own sums). q and the new key are
+// rotated from the q/k/v row as rope_cache_kernel does; the new key and
+// value (position p, the last key of the last range) are used from LDS, and
+// the first q head of each kv group writes them into the caches (no
+// workgroup reads position p from the cache in this launch).
+constexpr int kAttnValKeys = 8;  // keys per class and value batch (32 keys a batch)
+constexpr int kAttnPcStride = 17;  // LDS floats per key of a round's chunk sums (16 + 1: no bank conflicts)
+
+__device__ inline int attn_splits(int nk) {
+  return min(kAttnSplitMax, (nk + kAttnSplitKeys - 1) / kAttnSplitKeys);
+}
+
+__global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_at[];
+  __shared__ float s_q[kAttnSplitMaxHd];
+  __shared__ uint16_t s_knew[kAttnSplitMaxHd], s_vnew[kAttnSplitMaxHd];
+  __shared__ double s_part[kAttnSplitMax][kAttnSplitMaxHd + 2];  // per range: m, den, num
+  __shared__ double s_f[kAttnSplitMax];
+  const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int p = token_pos(a.offs, a.off, t, 0, a.max_seq);
+  const int nk = p + 1, S = attn_splits(nk);
+  const int rep = a.nh / a.nkv, g = h / rep;
+  const int64_t cbase = (cache_slot(a.slots, a.n_slots, t) * a.nkv + g) * a.max_seq * a.hd;
+  uint16_t* kb = a.kc + cbase;
+  uint16_t* vb = a.vc + cbase;
+  const int half = a.hd / 2, nch = a.hd / 8;
+  // this wave's range; keys before jg come from the cache (p, the last key
+  // of the last range, from LDS)
+  const bool active = wave < S;
+  const int j0 = active ? static_cast<int>(static_cast<int64_t>(nk) * wave / S) : 0;
+  const int j1 = active ? static_cast<int>(static_cast<int64_t>(nk) * (wave + 1) / S) : 0;
+  const bool last = wave == S - 1;
+  const int jg = last ? j1 - 1 : j1;
+  const int jclamp = max(jg - 1, 0);  // loads past the range re-read its last cached key
+
+  // 1. the rotation's inputs: thread i < hd takes pair i mod hd/2 of q
+  // (i < hd/2) or of the new key; thread d < hd the new value's element d
+  const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
+  const bool rot = tid < a.hd;
+  const int hd_i = tid % half;
+  uint16_t rx1 = 0, rx2 = 0, rv = 0;
+  float rc = 0.0f, rsn = 0.0f;
+  if (rot) {
+    const uint16_t* src = row + (tid < half ? h : a.nh + g) * a.hd;
+    const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
+    rx1 = src[hd_i];
+    rx2 = src[hd_i + half];
+    rc = cs[2 * hd_i];
+    rsn = cs[2 * hd_i + 1];
+    rv = row[(a.nh + a.nkv + g) * a.hd + tid];
+  }
+  // 2. the first key round (64 keys: instruction c brings keys c * kpi +
+  // lane / nch, chunk lane mod nch) and value batch (lane (c, i): keys j0 +
+  // c + 4u, chunk i)
+  const int kc = lane >> 4, dc = lane & 15;
+  const bool vlane = dc < nch;
+  const int kpi = kWave / nch;                   // keys per load instruction
+  const int kk = lane / nch, kch = lane % nch;  // this lane's key in it, its chunk
+  u32x4_t kv[16], vv[kAttnValKeys], vw[kAttnValKeys];
+  auto load_keys = [&](int jb) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      if (c < nch)
+        kv[c] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(min(jb + c * kpi + kk, jclamp)) * a.hd +
+                                                  8 * kch);
+  };
+  auto load_values = [&](u32x4_t* V, int jb) {
+#pragma unroll
+    for (int u = 0; u < kAttnValKeys; ++u)
+      V[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(min(jb + kc + 4 * u, jclamp)) * a.hd +
+                                               8 * min(dc, nch - 1));
+  };
+  if (active && j0 < jg) {
+    load_keys(j0);
+    load_values(vv, j0);
+  }
+
+  // 3. rotation (one rounding of the fp64 value), the new value
+  if (rot) {
+    const double x1 = bf16_to_f32(rx1), x2 = bf16_to_f32(rx2);
+    const double c = rc, sn = rsn;
+    const uint16_t o1 = f64_to_bf16(__builtin_fma(x1, c, -(x2 * sn)));
+    const uint16_t o2 = f64_to_bf16(__builtin_fma(x1, sn, x2 * c));
+    if (tid < half) {
+      s_q[hd_i] = bf16_to_f32(o1);
+      s_q[hd_i + half] = bf16_to_f32(o2);
+    } else {
+      s_knew[hd_i] = o1;
+      s_knew[hd_i + half] = o2;
+    }
+    s_vnew[tid] = rv;
+  }
+  __syncthreads();
+  if (h % rep == 0 && tid < a.hd) {
+    kb[static_cast<int64_t>(p) * a.hd + tid] = s_knew[tid];
+    vb[static_cast<int64_t>(p) * a.hd + tid] = s_vnew[tid];
+  }
+
+  // 4. scores (LDS per wave: the range's fp64 weights, its fp32 scores,
+  // and the chunk sums of one 64-key round)
+  const int kmax = max(kAttnSplitKeys, static_cast<int>((a.max_seq + kAttnSplitMax - 1) / kAttnSplitMax));
+  double* s_e = reinterpret_cast<double*>(s_at) + static_cast<size_t>(wave) * kmax;
+  float* s_s = reinterpret_cast<float*>(s_at + static_cast<size_t>(kAttnSplitMax) * kmax * 8) +
+               static_cast<size_t>(wave) * kmax;
+  float* s_pc = reinterpret_cast<float*>(s_at + static_cast<size_t>(kAttnSplitMax) * kmax * 12) +
+                static_cast<size_t>(wave) * kWave * kAttnPcStride;
+  float m = -__builtin_huge_valf();
+  if (active) {
+    // this lane's chunk of q, 8 dimensions
+    float qc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qc[e] = s_q[8 * kch + e];
+    for (int jb = j0; jb < jg; jb += kWave) {
+      if (jb != j0) load_keys(jb);
+#pragma unroll
+      for (int c = 0; c < 16; ++c) {
+        if (c < nch) {
+          float pc = 0.0f;
+#pragma unroll
+          for (int mm = 0; mm < 4; ++mm) {
+            pc = __builtin_fmaf(qc[2 * mm], bf16_to_f32(kv[c][mm] & 0xffffu), pc);
+            pc = __builtin_fmaf(qc[2 * mm + 1], bf16_to_f32(kv[c][mm] >> 16), pc);
+          }
+          s_pc[(c * kpi + kk) * kAttnPcStride + kch] = pc;
+        }
+      }
+      // the wave's LDS operations complete in order: each lane now sums its
+      // key's chunks as the other lanes wrote them
+      __builtin_amdgcn_wave_barrier();
+      if (jb + lane < jg) {
+        float acc = s_pc[lane * kAttnPcStride];
+        for (int c = 1; c < nch; ++c) acc += s_pc[lane * kAttnPcStride + c];
+        const float sc = acc * a.scale;
+        s_s[jb + lane - j0] = sc;
+        m = fmaxf(m, sc);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (last && lane == (p - j0) % kWave) {  // the new key, from LDS (the lane that takes key p below)
+      float acc = 0.0f;
+      for (int c = 0; c < nch; ++c) {
+        float pc = 0.0f;
+        for (int e = 0; e < 8; ++e) pc = __builtin_fmaf(s_q[8 * c + e], bf16_to_f32(s_knew[8 * c + e]), pc);
+        acc = c ? acc + pc : pc;
+      }
+      const float sc = acc * a.scale;
+      s_s[p - j0] = sc;
+      m = fmaxf(m, sc);
+    }
+    // the next value batch, in flight during the softmax
+    if (j0 + 4 * kAttnValKeys < jg) load_values(vw, j0 + 4 * kAttnValKeys);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    // each lane reads back only the scores it wrote
+    for (int jk = j0 + lane; jk < j1; jk += kWave)
+      s_e[jk - j0] = exp_det(static_cast<double>(s_s[jk - j0]) - static_cast<double>(m));
+  }
+  __syncthreads();
+
+  // 5. the range's sums
+  if (active) {
+    double nv[8], dv = 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) nv[i] = 0.0;
+    auto accum = [&](const u32x4_t* V, int jb) {
+#pragma unroll
+      for (int u = 0; u < kAttnValKeys; ++u) {
+        const int j = jb + kc + 4 * u;
+        if (j < jg) {
+          const double e = s_e[j - j0];
+          dv += e;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            nv[2 * q] = __builtin_fma(e, static_cast<double>(bf16_to_f32(V[u][q] & 0xffffu)), nv[2 * q]);
+            nv[2 * q + 1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(V[u][q] >> 16)), nv[2 * q + 1]);
+          }
+        }
+        // one key's fp64 conversions at a time (converting a batch ahead
+        // would need more registers than the kernel has)
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    for (int jb = j0; jb < jg; jb += 4 * kAttnValKeys) {
+      if (jb == j0) {
+        accum(vv, jb);
+      } else if (jb == j0 + 4 * kAttnValKeys) {
+        accum(vw, jb);
+      } else {
+        load_values(vv, jb);
+        accum(vv, jb);
+      }
+    }
+    if (last && kc == (p - j0) % 4) {  // the new key's value, last of its class
+      const double e = s_e[p - j0];
+      dv += e;
+      const u32x4_t w4 = reinterpret_cast<const u32x4_t*>(s_vnew)[min(dc, nch - 1)];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        nv[2 * q] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w4[q] & 0xffffu)), nv[2 * q]);
+        nv[2 * q + 1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(w4[q] >> 16)), nv[2 * q + 1]);
+      }
+    }
+    // the classes in order: ((X_0 + X_1) + X_2) + X_3 in the lanes of class 0
+    const double d1 = __shfl(dv, lane + 16), d2 = __shfl(dv, lane + 32), d3 = __shfl(dv, lane + 48);
+    const double den = ((dv + d1) + d2) + d3;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const double n1 = __shfl(nv[i], lane + 16), n2 = __shfl(nv[i], lane + 32), n3 = __shfl(nv[i], lane + 48);
+      if (kc == 0 && vlane) s_part[wave][2 + 8 * dc + i] = ((nv[i] + n1) + n2) + n3;
+    }
+    if (lane == 0) {
+      s_part[wave][0] = static_cast<double>(m);
+      s_part[wave][1] = den;
+    }
+  }
+  __syncthreads();
+
+  // 6. the combine, ranges in order: thread d takes dimension d
+  if (tid < S) {
+    double M = s_part[0][0];
+    for (int r = 1; r < S; ++r) M = fmax(M, s_part[r][0]);
+    s_f[tid] = exp_det(s_part[tid][0] - M);
+  }
+  __syncthreads();
+  bool ovf = false;
+  if (tid < a.hd) {
+    const int d = tid;
+    double dn = 0.0, nm = 0.0;
+    for (int r = 0; r < S; ++r) {
+      const double f = s_f[r];
+      dn = r ? __builtin_fma(s_part[r][1], f, dn) : s_part[r][1] * f;
+      nm = r ? __builtin_fma(s_part[r][2 + d], f, nm) : s_part[r][2 + d] * f;
+    }
+    const uint16_t o = f64_to_bf16(nm / dn);
+    const int64_t oc = static_cast<int64_t>(h) * a.hd + d;
+    a.out[static_cast<int64_t>(t) * a.ldo + oc] = o;
+    if (a.outh) {
+      ovf = bf16_f16_overflow(o);
       a.outh[static_cast<int64_t>(t) * a.ldo + ((oc & ~7) | p8_slot(oc & 7))] =
           static_cast<uint16_t>(bf16_to_f16_bits(o));
     }
@@ -550,19 +769,20 @@ size_t attn_lds_bytes(int64_t max_seq) { return static_cast<size_t>(max_seq) * 1
 
 hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream) {
   if (T == 0) return hipSuccess;
+  if (a.qkv) {
+    if (a.L != 1 || a.hd > kAttnSplitMaxHd || a.hd % 8 || kWave % (a.hd / 8)) return hipErrorInvalidValue;
+    // LDS: per wave, a range's fp64 weights and fp32 scores, one round's chunk sums
+    const int64_t keys = std::max<int64_t>(kAttnSplitKeys, (a.max_seq + kAttnSplitMax - 1) / kAttnSplitMax);
+    hipLaunchKernelGGL(attn_split_kernel, dim3(T, a.nh), dim3(kWave * kAttnSplitMax),
+                       static_cast<size_t>(kAttnSplitMax * (keys * 12 + kWave * kAttnPcStride * 4)), stream, a);
+    return hipGetLastError();
+  }
   const dim3 grid(T, a.nh);
   const size_t lds = attn_lds_bytes(a.max_seq);
-  if (a.hd <= 128) {
-    if (a.qkv)
-      hipLaunchKernelGGL((attn_kernel<true, 1>), grid, dim3(kAttnThreads), lds, stream, a);
-    else
-      hipLaunchKernelGGL((attn_kernel<false, 1>), grid, dim3(kAttnThreads), lds, stream, a);
-  } else {
-    if (a.qkv)
-      hipLaunchKernelGGL((attn_kernel<true, 2>), grid, dim3(kAttnThreads), lds, stream, a);
-    else
-      hipLaunchKernelGGL((attn_kernel<false, 2>), grid, dim3(kAttnThreads), lds, stream, a);
-  }
+  if (a.hd <= 128)
+    hipLaunchKernelGGL((attn_kernel<1>), grid, dim3(kAttnThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL((attn_kernel<2>), grid, dim3(kAttnThreads), lds, stream, a);
   return hipGetLastError();
 }
 

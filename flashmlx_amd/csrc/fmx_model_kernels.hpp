@@ -87,6 +87,12 @@ struct AttnArgs {
   uint16_t* outh;         // null, or the same in fp16 (P8 layout); values outside fp16 set *flag
   uint32_t* flag;
 };
+// single-token forwards (qkv set; head size at most kAttnSplitMaxHd): a
+// query's keys in min(kAttnSplitMax, ceil(keys / kAttnSplitKeys))
+// contiguous ranges, one wave each
+constexpr int kAttnSplitMax = 8;
+constexpr int kAttnSplitKeys = 64;
+constexpr int kAttnSplitMaxHd = 128;
 size_t attn_lds_bytes(int64_t max_seq);
 hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream);
 

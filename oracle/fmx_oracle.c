@@ -918,6 +918,84 @@ int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_
   return 0;
 }
 
+/* The single-token attention of libfmx's split kernel (attn_split_kernel):
+ * query l's keys 0 .. nk - 1 (nk = q_off + l + 1) in S = min(8, ceil(nk /
+ * 64)) contiguous ranges [nk s / S, nk (s + 1) / S); in range s, m_s = the
+ * largest fp32 score, e_j = exp(s_j - m_s) in fp64 with the deterministic
+ * exp, and over the key classes c = (j - j0) mod 4 (each in key order)
+ * den_s = ((D_0 + D_1) + D_2) + D_3, D_c = sum e_j, and num_s likewise
+ * from N_c = sum e_j v_j (fma); then M = max_s m_s, f_s = exp(m_s - M), den = sum_s f_s den_s and num =
+ * sum_s f_s num_s (ranges in order, fma; the first term a product), out =
+ * bf16(num / den). Scores: s_j = scale * (((P_0 + P_1) + ...) + P_{hd/8-1})
+ * with P_c the fp32 sum over dimensions 8c .. 8c + 7 in order (exact bf16
+ * products). */
+int orc_sdpa_split(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
+                   const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
+                   uint16_t* out) {
+  if (nkv <= 0 || nh % nkv || q_off + L > max_seq) return -1;
+  const int64_t rep = nh / nkv;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int64_t l = 0; l < L; ++l) {
+    for (int64_t h = 0; h < nh; ++h) {
+      const int64_t g = h / rep, nk = q_off + l + 1;
+      const uint16_t* qv = q + (l * nh + h) * hd;
+      const uint16_t* kb = kc + g * max_seq * hd;
+      const uint16_t* vb = vc + g * max_seq * hd;
+      int64_t S = (nk + 63) / 64;
+      if (S > 8) S = 8;
+      float* s = (float*)malloc(sizeof(float) * nk);
+      double* ms = (double*)malloc(sizeof(double) * S);
+      double* dens = (double*)malloc(sizeof(double) * S);
+      double* nums = (double*)malloc(sizeof(double) * S * hd);
+      for (int64_t j = 0; j < nk; ++j) {
+        float acc = 0.0f;
+        for (int64_t c = 0; c < hd / 8; ++c) {
+          float pc = 0.0f;
+          for (int64_t d = 8 * c; d < 8 * c + 8; ++d) pc += bf(qv[d]) * bf(kb[j * hd + d]);
+          acc = c ? acc + pc : pc;
+        }
+        s[j] = acc * scale;
+      }
+      double M = -INFINITY;
+      for (int64_t r = 0; r < S; ++r) {
+        const int64_t j0 = nk * r / S, j1 = nk * (r + 1) / S;
+        float m = -INFINITY;
+        for (int64_t j = j0; j < j1; ++j)
+          if (s[j] > m) m = s[j];
+        ms[r] = (double)m;
+        if (ms[r] > M) M = ms[r];
+        double dc[4] = {0.0, 0.0, 0.0, 0.0};
+        for (int64_t j = j0; j < j1; ++j) dc[(j - j0) % 4] += orc_exp((double)s[j] - ms[r]);
+        dens[r] = ((dc[0] + dc[1]) + dc[2]) + dc[3];
+        for (int64_t d = 0; d < hd; ++d) {
+          double nc[4] = {0.0, 0.0, 0.0, 0.0};
+          for (int64_t j = j0; j < j1; ++j)
+            nc[(j - j0) % 4] = fma(orc_exp((double)s[j] - ms[r]), (double)bf(vb[j * hd + d]), nc[(j - j0) % 4]);
+          nums[r * hd + d] = ((nc[0] + nc[1]) + nc[2]) + nc[3];
+        }
+      }
+      double den = 0.0;
+      for (int64_t r = 0; r < S; ++r) {
+        const double f = orc_exp(ms[r] - M);
+        den = r ? fma(dens[r], f, den) : dens[r] * f;
+      }
+      for (int64_t d = 0; d < hd; ++d) {
+        double num = 0.0;
+        for (int64_t r = 0; r < S; ++r) {
+          const double f = orc_exp(ms[r] - M);
+          num = r ? fma(nums[r * hd + d], f, num) : nums[r * hd + d] * f;
+        }
+        out[(l * nh + h) * hd + d] = orc_f64_to_bf16(num / den);
+      }
+      free(s);
+      free(ms);
+      free(dens);
+      free(nums);
+    }
+  }
+  return 0;
+}
+
 int orc_moe_block(const orc_moe_cfg* cfg, const orc_moe_weights* w,
                   const uint16_t* x, int64_t T, int mode,
                   const int64_t* token_subset, int64_t n_subset,

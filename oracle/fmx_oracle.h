@@ -60,6 +60,9 @@
  *   orc_sdpa                             one key = v, equal keys = mean of values,
  *                                        causal prefix, numpy fp64 softmax(QK^T)V;
  *                                        MLX's intermediate roundings UNPINNED
+ *   orc_sdpa_split                       the same checks; within one bf16 ulp of
+ *                                        orc_sdpa at range boundaries and with
+ *                                        one range's scores far above the rest
  */
 #ifndef FMX_ORACLE_H
 #define FMX_ORACLE_H
@@ -180,6 +183,12 @@ int orc_rope(uint16_t* x, int64_t T, int64_t n_heads, int64_t hd, const int64_t*
 int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
              const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
              uint16_t* out);
+/* the same attention with the keys in up to 8 ranges of at least 64 (the
+ * single-token split kernel's order): per-range softmax sums rescaled by
+ * exp(m_s - M) and added in range order */
+int orc_sdpa_split(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_t* kc,
+                   const uint16_t* vc, int64_t nkv, int64_t max_seq, int64_t q_off, float scale,
+                   uint16_t* out);
 
 /* orc_moe_block with the expert choice given (inds [T, k]); scores are the
  * router's probabilities of those experts (renormalised when norm_topk). */

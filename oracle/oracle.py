@@ -111,6 +111,7 @@ def load() -> C.CDLL:
         lib.orc_rope_table.restype = None
         lib.orc_rope.argtypes = [_vp, i64, i64, i64, _vp, _vp]
         lib.orc_sdpa.argtypes = [_vp, i64, i64, i64, _vp, _vp, i64, i64, i64, C.c_float, _vp]
+        lib.orc_sdpa_split.argtypes = [_vp, i64, i64, i64, _vp, _vp, i64, i64, i64, C.c_float, _vp]
         lib.orc_moe_block_routed.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp,
                                              _vp, _vp]
         lib.orc_sigmoid_f32.restype = C.c_float
@@ -354,6 +355,20 @@ def sdpa(q, kc, vc, q_off: int, scale: float):
     return out
 
 
+def sdpa_split(q, kc, vc, q_off: int, scale: float):
+    """sdpa in the key ranges of the single-token split kernel
+    (fmx_oracle.c: orc_sdpa_split)."""
+    q, kc, vc = _c(q, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16)
+    L, nh, hd = q.shape
+    nkv, max_seq = kc.shape[0], kc.shape[1]
+    out = np.empty_like(q)
+    rc = load().orc_sdpa_split(_p(q), L, nh, hd, _p(kc), _p(vc), nkv, max_seq, q_off,
+                               float(scale), _p(out))
+    assert rc == 0, rc
+    return out
+
+
+
 def bf16_add(a, b) -> np.ndarray:
     """MLX add of two bf16 arrays: the fp32 sum rounded to bf16."""
     return f32_to_bf16_array(bf16_to_f32(a) + bf16_to_f32(b))
@@ -421,11 +436,13 @@ class DecoderStack:
             v = qkv[:, (nh + nkv) * hd:].reshape(B * L, nkv, hd)
             q, k = rope(q, pos, self.cs), rope(k, pos, self.cs)
             att = np.empty((B * L, nh, hd), np.uint16)
+            # single-token forwards: the split kernel's order (head sizes it takes)
+            attn = sdpa_split if L == 1 and hd <= 128 and 64 % (hd // 8) == 0 else sdpa
             for b in range(B):
                 rows = slice(b * L, (b + 1) * L)
                 self.kc[li, b, :, offset:offset + L] = k[rows].transpose(1, 0, 2)
                 self.vc[li, b, :, offset:offset + L] = v[rows].transpose(1, 0, 2)
-                att[rows] = sdpa(q[rows], self.kc[li, b], self.vc[li, b], offset, self.scale)
+                att[rows] = attn(q[rows], self.kc[li, b], self.vc[li, b], offset, self.scale)
             o = qmm_t(att.reshape(B * L, nh * hd), *lw["o"], mode=mode)
             h = bf16_add(h, o)
             n2 = rms_norm(h, lw["post_w"], c["eps"])

@@ -189,6 +189,67 @@ def test_sdpa_matches_numpy(oracle, L, q_off, nh, nkv):
         assert np.abs(got - nomask).max() > 1e-2
 
 
+def _numpy_attn(q, kc, vc, nk, scale, nkv):
+    """fp64 softmax(q k^T * scale) v over keys 0 .. nk - 1 of one query."""
+    qf, kf, vf = (bf(a).astype(np.float64) for a in (q, kc, vc))
+    nh = q.shape[1]
+    ref = np.empty((nh, q.shape[2]))
+    for h in range(nh):
+        g = h // (nh // nkv)
+        s = kf[g, :nk] @ qf[0, h] * scale
+        p = np.exp(s - s.max())
+        ref[h] = (p / p.sum()) @ vf[g, :nk]
+    return ref
+
+
+def test_sdpa_split_one_key_and_equal_keys(oracle):
+    """The split order keeps the closed forms: one key gives its value, equal
+    keys the fp64 mean of the values (here over 3 ranges: 150 keys)."""
+    kc, vc = _cache(oracle, 2, 8, 64, 1)
+    q = to_bf16(oracle, RNG.standard_normal((1, 4, 64)))
+    out = oracle.sdpa_split(q, kc, vc, 0, 0.125)
+    for h in range(4):
+        np.testing.assert_array_equal(out[0, h], vc[h // 2, 0])
+    n = 150
+    kc, vc = _cache(oracle, 1, 160, 32, n)
+    kc[:, :n] = kc[:, :1]
+    q = to_bf16(oracle, RNG.standard_normal((1, 1, 32)))
+    out = oracle.sdpa_split(q, kc, vc, n - 1, 0.2)
+    ref = bf(vc[0, :n]).astype(np.float64).mean(0)
+    got = bf(out[0, 0]).astype(np.float64)
+    assert (np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6).all()
+
+
+@pytest.mark.parametrize("nk", [1, 63, 64, 65, 129, 512, 513, 2500])
+def test_sdpa_split_matches_numpy(oracle, nk):
+    """At range-count boundaries (1 range up to 64 keys, 8 from 449) and
+    with one key's score far above the rest in the first range (every other
+    range's sums then carry f_s << 1): within one bf16 ulp of numpy's fp64
+    softmax and of the four-quarter order. A planted mistake (the ranges'
+    sums added without the exp(m_s - M) factors) is far off."""
+    nh, nkv, hd = 4, 2, 64
+    kc, vc = _cache(oracle, nkv, nk + 1, hd, nk)
+    q = to_bf16(oracle, RNG.standard_normal((1, nh, hd)))
+    kc[:, 0] = to_bf16(oracle, bf(q[0, 0]).astype(np.float64) * 3.0)  # a dominant early key
+    scale = float(np.float32(1 / np.sqrt(hd)))
+    out = oracle.sdpa_split(q, kc, vc, nk - 1, scale)
+    ref = _numpy_attn(q, kc, vc, nk, scale, nkv)
+    got = bf(out[0]).astype(np.float64)
+    assert (np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6).all()
+    quart = bf(oracle.sdpa(q, kc, vc, nk - 1, scale)[0]).astype(np.float64)
+    assert (np.abs(got - quart) <= np.abs(quart) * 2.0 ** -8 + 1e-6).all()
+    if nk > 64:  # the planted mistake: unscaled range sums
+        qf, kf, vf = (bf(a).astype(np.float64) for a in (q, kc, vc))
+        S = min(8, (nk + 63) // 64)
+        s = kf[0, :nk] @ qf[0, 0] * scale
+        num = den = 0.0
+        for r in range(S):
+            j0, j1 = nk * r // S, nk * (r + 1) // S
+            e = np.exp(s[j0:j1] - s[j0:j1].max())
+            num, den = num + e @ vf[0, j0:j1], den + e.sum()
+        assert np.abs(num / den - ref[0]).max() > 1e-2
+
+
 # ------------------------------------------------------------------ the stack
 
 TINY = dict(hidden=128, layers=2, heads=4, kv_heads=2, head_dim=32, vocab=96, eps=1e-6,
