@@ -142,13 +142,30 @@ ModelLayout model_layout(const fmx_model_config& c, int64_t T, char* base) {
 
 int64_t packed_linear_bytes(int64_t N, int64_t K) { return (N / 16) * (K / 128) * kPackedBlockSingle; }
 
+// A decode projection's fused input norm (DenseArgs' nin fields; at most
+// kDenseNormMaxT rows: the input rows formed from nin (+ ndelta)), and res2
+// added to its residual first.
+struct FusedNorms {
+  const uint16_t* nin = nullptr;
+  const uint16_t* ndelta = nullptr;
+  const uint16_t* nin_w = nullptr;
+  const uint16_t* res2 = nullptr;
+  float eps = 0.0f;
+};
+
 // out = x . W^T (+ bias) (+ res) for T rows of a packed linear [N, K]: the
 // decode kernel for at most 16 rows, else the prefill GEMM grid on the fp16
 // copy of x (xh) with its range flag.
 int linear(const uint16_t* x, const uint16_t* xh, uint32_t* flag, int64_t T, const void* w, int64_t N,
-           int64_t K, const uint16_t* bias, const uint16_t* res, uint16_t* out, hipStream_t stream) {
+           int64_t K, const uint16_t* bias, const uint16_t* res, uint16_t* out, hipStream_t stream,
+           const FusedNorms& fn = FusedNorms()) {
   if (T <= kDenseDecMaxRows) {
     DenseArgs a{};
+    a.nin = fn.nin;
+    a.ndelta = fn.ndelta;
+    a.nin_w = fn.nin_w;
+    a.res2 = fn.res2;
+    a.eps = fn.eps;
     a.x = x;
     a.ldx = K;
     a.T = static_cast<int>(T);
@@ -339,6 +356,11 @@ int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weigh
       return fail(FMX_ERR_ARG, "layer %lld: weights incomplete", (long long)l);
     uint16_t* kc = static_cast<uint16_t*>(kv_cache) + l * layer_cache;
     uint16_t* vc = kc + layer_cache / 2;
+    // single-row forwards: the input norm runs in the q/k/v projection and
+    // the previous MoE output is added to the residual by the o projection
+    // (one kernel, with its cache write-back at the boundary, fewer per
+    // layer)
+    const bool fuse = T <= kDenseNormMaxT && rmsnorm_fits(d.H);
     // input norm (with the previous layer's MoE residual)
     NormArgs na{};
     na.x = M.h;
@@ -351,10 +373,19 @@ int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weigh
     na.out = M.normed;
     na.outh = many ? M.normed_h : nullptr;
     na.flag = M.flags + 2 * l;
-    FMX_HIP(launch_rmsnorm(na, static_cast<int>(T), stream));
+    FusedNorms fq, fo;
+    if (fuse) {
+      fq.nin = M.h;
+      fq.ndelta = na.delta;
+      fq.nin_w = na.w;
+      fq.eps = na.eps;
+      fo.res2 = na.delta;
+    } else {
+      FMX_HIP(launch_rmsnorm(na, static_cast<int>(T), stream));
+    }
     // q, k, v (+ biases)
     FMX_RC(linear(M.normed, M.normed_h, M.flags + 2 * l, T, lw.qkv, d.nqkv, d.H,
-                  static_cast<const uint16_t*>(lw.qkv_bias), nullptr, M.qkv, stream));
+                  static_cast<const uint16_t*>(lw.qkv_bias), nullptr, M.qkv, stream, fq));
     // RoPE, cache write, attention
     RopeArgs ra{};
     ra.qkv = M.qkv;
@@ -398,7 +429,7 @@ int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weigh
     FMX_HIP(launch_attn(aa, static_cast<int>(T), stream));
     // o_proj with the residual: h = h + attn . Wo^T
     FMX_RC(linear(M.attn, M.attn_h, M.flags + 2 * l + 1, T, lw.o, d.H, d.nh * d.hd, nullptr, M.h, M.h,
-                  stream));
+                  stream, fo));
     // post-attention norm, MoE block
     NormArgs nb = na;
     nb.delta = nullptr;

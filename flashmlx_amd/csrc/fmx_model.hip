@@ -37,18 +37,74 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 
 // ------------------------------------------------------------------ RMSNorm
 
+// RMSNorm arithmetic (mx::fast::rms_norm, model.cpp:486-488), shared by
+// rmsnorm_kernel and the decode projections' fused norms so that both give
+// the same bits: x = bf16(x + delta) element by element; the sum of squares
+// in fp64, each thread over its chunks c = tid + kNormThreads q in order,
+// then the wave's butterfly and the waves in order; r = 1 / sqrt(ss / H +
+// eps) in fp64; out = bf16(bf16(x * r) * w).
+__device__ inline u32x4_t norm_add(u32x4_t x, const u32x4_t& d) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = f32_to_bf16(bf16_to_f32(x[m] & 0xffffu) + bf16_to_f32(d[m] & 0xffffu));
+    const uint32_t hi = f32_to_bf16(bf16_to_f32(x[m] >> 16) + bf16_to_f32(d[m] >> 16));
+    x[m] = lo | (hi << 16);
+  }
+  return x;
+}
+__device__ inline double norm_sq(const u32x4_t& x, double ss) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const double lo = bf16_to_f32(x[m] & 0xffffu), hi = bf16_to_f32(x[m] >> 16);
+    ss += lo * lo;
+    ss += hi * hi;
+  }
+  return ss;
+}
+__device__ inline double norm_wave_sum(double ss) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  return ss;
+}
+__device__ inline double norm_r(const double* s_red_row, int H, float eps) {
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) tot += s_red_row[w];
+  return 1.0 / sqrt(tot / static_cast<double>(H) + static_cast<double>(eps));
+}
+__device__ inline u32x4_t norm_apply(const u32x4_t& x, const u32x4_t& wv, double r) {
+  u32x4_t o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint32_t e2[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const double xv = bf16_to_f32((x[m] >> (16 * hf)) & 0xffffu);
+      const uint16_t n = f64_to_bf16(xv * r);
+      e2[hf] = f64_to_bf16(static_cast<double>(bf16_to_f32(n)) *
+                           static_cast<double>(bf16_to_f32((wv[m] >> (16 * hf)) & 0xffffu)));
+    }
+    o[m] = e2[0] | (e2[1] << 16);
+  }
+  return o;
+}
+
 // One workgroup per output row i (input row i * row_mul + row_add): optionally
-// x = bf16(x + delta) first (written back: the residual stream), then
-// out = bf16(bf16(x * r) * w), r = 1 / sqrt(mean(x^2) + eps), the sum of
-// squares and r in fp64 (mx::fast::rms_norm, model.cpp:486-488). outh, when
-// given, receives out in fp16 (P8 layout) for the prefill GEMMs, and a value
-// outside fp16's range sets *flag.
+// x = bf16(x + delta) first (written back: the residual stream), then the
+// norm above. outh, when given, receives out in fp16 (P8 layout) for the
+// prefill GEMMs, and a value outside fp16's range sets *flag.
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(NormArgs a) {
   __shared__ double s_red[kNormThreads / kWave];
   const int i = blockIdx.x, tid = threadIdx.x;
   const int64_t xr = static_cast<int64_t>(i) * a.row_mul + a.row_add;
   const int nch = a.H / 8;
-  u32x4_t v[kNormMaxChunks];
+  u32x4_t v[kNormMaxChunks], wv[kNormMaxChunks];
+  // the weights' chunks are loaded with the row, not after the reduction
+#pragma unroll
+  for (int q = 0; q < kNormMaxChunks; ++q) {
+    const int c = tid + q * kNormThreads;
+    if (c < nch) wv[q] = reinterpret_cast<const u32x4_t*>(a.w)[c];
+  }
   double ss = 0.0;
 #pragma unroll
   for (int q = 0; q < kNormMaxChunks; ++q) {
@@ -56,50 +112,22 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(NormArgs a) {
     if (c >= nch) break;
     u32x4_t x = reinterpret_cast<const u32x4_t*>(a.x + xr * a.H)[c];
     if (a.delta) {
-      const u32x4_t d = reinterpret_cast<const u32x4_t*>(a.delta + xr * a.H)[c];
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        const uint32_t lo = f32_to_bf16(bf16_to_f32(x[m] & 0xffffu) + bf16_to_f32(d[m] & 0xffffu));
-        const uint32_t hi = f32_to_bf16(bf16_to_f32(x[m] >> 16) + bf16_to_f32(d[m] >> 16));
-        x[m] = lo | (hi << 16);
-      }
+      x = norm_add(x, reinterpret_cast<const u32x4_t*>(a.delta + xr * a.H)[c]);
       reinterpret_cast<u32x4_t*>(a.x_out + xr * a.H)[c] = x;
     }
     v[q] = x;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const double lo = bf16_to_f32(x[m] & 0xffffu), hi = bf16_to_f32(x[m] >> 16);
-      ss += lo * lo;
-      ss += hi * hi;
-    }
+    ss = norm_sq(x, ss);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = norm_wave_sum(ss);
   if ((tid & 63) == 0) s_red[tid >> 6] = ss;
   __syncthreads();
-  double tot = 0.0;
-#pragma unroll
-  for (int w = 0; w < kNormThreads / kWave; ++w) tot += s_red[w];
-  const double r = 1.0 / sqrt(tot / static_cast<double>(a.H) + static_cast<double>(a.eps));
+  const double r = norm_r(s_red, a.H, a.eps);
   bool ovf = false;
 #pragma unroll
   for (int q = 0; q < kNormMaxChunks; ++q) {
     const int c = tid + q * kNormThreads;
     if (c >= nch) break;
-    const u32x4_t wv = reinterpret_cast<const u32x4_t*>(a.w)[c];
-    u32x4_t o;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      uint32_t e2[2];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const double xv = bf16_to_f32((v[q][m] >> (16 * hf)) & 0xffffu);
-        const uint16_t n = f64_to_bf16(xv * r);
-        e2[hf] = f64_to_bf16(static_cast<double>(bf16_to_f32(n)) *
-                             static_cast<double>(bf16_to_f32((wv[m] >> (16 * hf)) & 0xffffu)));
-      }
-      o[m] = e2[0] | (e2[1] << 16);
-    }
+    const u32x4_t o = norm_apply(v[q], wv[q], r);
     reinterpret_cast<u32x4_t*>(a.out + static_cast<int64_t>(i) * a.H)[c] = o;
     if (a.outh) reinterpret_cast<u32x4_t*>(a.outh + static_cast<int64_t>(i) * a.H)[c] = bf16_chunk_to_f16_p8(o, ovf);
   }
@@ -115,15 +143,90 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(NormArgs a) {
 // added in wave order. Epilogue: bf16(acc), then + bias[col], then
 // res[t] + (each step rounded to bf16, as MLX's separate ops).
 constexpr int kDnBatch = 4;
+static_assert(kNormThreads == 256, "the fused norms run on the projection's 256 threads");
 
+// NIN: the row is formed in LDS by the input norm (every workgroup the
+// same, rmsnorm_kernel's arithmetic), for single-row forwards: one kernel
+// boundary fewer (a cache write-back and invalidation across the XCDs: the
+// norm kernel took ~5 us at batch 1, the fused norm adds ~2.7 us to the
+// projection; at 4 rows every workgroup's norms cost more than the kernel).
+template <bool NIN>
 __global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_dn[];  // NIN: the rows [T][K] bf16
   __shared__ f32x4_t s_acc[3][kWave];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ double s_red[kDenseNormMaxT][kNormThreads / kWave];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i16 = lane & 15, j = lane >> 4;
   const int tile = blockIdx.x;
+  const int K = a.nu * 128;
   const uint8_t* tb = a.w + static_cast<int64_t>(tile) * a.nu * kBlockSingle;
-  const uint16_t* xrow = a.x + static_cast<int64_t>(min(i16, a.T - 1)) * a.ldx + 8 * j;
+  const int col = tile * 16 + i16;
+  // the epilogue's bias and residual values, loaded by wave 0 ahead of the
+  // products (after them they would add a memory round trip)
+  uint16_t bias_v = 0, res_v[4] = {0, 0, 0, 0}, res2_v[4] = {0, 0, 0, 0};
+  if (wave == 0) {
+    if (a.bias) bias_v = a.bias[col];
+    if (a.res)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (4 * j + r < a.T) {
+          res_v[r] = a.res[static_cast<int64_t>(4 * j + r) * a.ldr + col];
+          if (a.res2) res2_v[r] = a.res2[static_cast<int64_t>(4 * j + r) * a.ldr + col];
+        }
+  }
+
+  const uint16_t* xrow;
+  if constexpr (NIN) {
+    // the input norm of the T rows, into LDS
+    const int nch = K / 8;
+    u32x4_t xv[kDenseNormMaxT][kNormMaxChunks], wv[kNormMaxChunks];
+    double ss[kDenseNormMaxT];
+#pragma unroll
+    for (int q = 0; q < kNormMaxChunks; ++q) {
+      const int c = tid + q * kNormThreads;
+      if (c < nch) wv[q] = reinterpret_cast<const u32x4_t*>(a.nin_w)[c];
+    }
+#pragma unroll
+    for (int t = 0; t < kDenseNormMaxT; ++t) {
+      ss[t] = 0.0;
+      if (t >= a.T) continue;
+#pragma unroll
+      for (int q = 0; q < kNormMaxChunks; ++q) {
+        const int c = tid + q * kNormThreads;
+        if (c >= nch) break;
+        u32x4_t x = reinterpret_cast<const u32x4_t*>(a.nin + static_cast<int64_t>(t) * a.ldx)[c];
+        if (a.ndelta)
+          x = norm_add(x, reinterpret_cast<const u32x4_t*>(a.ndelta + static_cast<int64_t>(t) * a.ldx)[c]);
+        xv[t][q] = x;
+        ss[t] = norm_sq(x, ss[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kDenseNormMaxT; ++t) {
+      if (t >= a.T) continue;
+      const double sw = norm_wave_sum(ss[t]);
+      if (lane == 0) s_red[t][wave] = sw;
+    }
+    __syncthreads();
+    u32x4_t* s_x = reinterpret_cast<u32x4_t*>(s_dn);
+#pragma unroll
+    for (int t = 0; t < kDenseNormMaxT; ++t) {
+      if (t >= a.T) continue;
+      const double r = norm_r(s_red[t], K, a.eps);
+#pragma unroll
+      for (int q = 0; q < kNormMaxChunks; ++q) {
+        const int c = tid + q * kNormThreads;
+        if (c >= nch) break;
+        s_x[t * nch + c] = norm_apply(xv[t][q], wv[q], r);
+      }
+    }
+    __syncthreads();
+    xrow = reinterpret_cast<const uint16_t*>(s_dn) + static_cast<int64_t>(min(i16, a.T - 1)) * K + 8 * j;
+  } else {
+    xrow = a.x + static_cast<int64_t>(min(i16, a.T - 1)) * a.ldx + 8 * j;
+  }
+
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = {0.f, 0.f, 0.f, 0.f};
   for (int u0 = wave; u0 < a.nu; u0 += 4 * kDnBatch) {
     PkUnit<false> L[kDnBatch];
@@ -141,18 +244,21 @@ __global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
   }
   if (wave > 0) s_acc[wave - 1][lane] = acc;
   __syncthreads();
-  if (wave != 0) return;
+  if (wave == 0) {
 #pragma unroll
-  for (int w = 0; w < 3; ++w) acc += s_acc[w][lane];
-  const int col = tile * 16 + i16;
+    for (int w = 0; w < 3; ++w) acc += s_acc[w][lane];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = 4 * j + r;
-    if (t >= a.T) continue;
-    uint16_t v = f32_to_bf16(acc[r]);
-    if (a.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(a.bias[col]));
-    if (a.res) v = f32_to_bf16(bf16_to_f32(a.res[static_cast<int64_t>(t) * a.ldr + col]) + bf16_to_f32(v));
-    a.out[static_cast<int64_t>(t) * a.ldo + col] = v;
+    for (int r = 0; r < 4; ++r) {
+      const int t = 4 * j + r;
+      uint16_t v = f32_to_bf16(acc[r]);
+      if (a.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(bias_v));
+      if (a.res) {
+        const float rv = a.res2 ? bf16_to_f32(f32_to_bf16(bf16_to_f32(res_v[r]) + bf16_to_f32(res2_v[r])))
+                                : bf16_to_f32(res_v[r]);
+        v = f32_to_bf16(rv + bf16_to_f32(v));
+      }
+      if (t < a.T) a.out[static_cast<int64_t>(t) * a.ldo + col] = v;
+    }
   }
 }
 
@@ -755,7 +861,14 @@ hipError_t launch_rmsnorm(const NormArgs& a, int n_rows, hipStream_t stream) {
 
 hipError_t launch_dense_dec(const DenseArgs& a, hipStream_t stream) {
   if (a.T == 0 || a.nt == 0) return hipSuccess;
-  hipLaunchKernelGGL(dense_dec_kernel, dim3(a.nt), dim3(256), 0, stream, a);
+  const bool nin = a.nin != nullptr;
+  if (nin && (a.T > kDenseNormMaxT || !a.nin_w || !rmsnorm_fits(a.nu * 128) || a.ldx % 8))
+    return hipErrorInvalidValue;
+  const size_t lds = nin ? static_cast<size_t>(a.T) * a.nu * 128 * 2 : 0;
+  if (nin)
+    hipLaunchKernelGGL(dense_dec_kernel<true>, dim3(a.nt), dim3(256), lds, stream, a);
+  else
+    hipLaunchKernelGGL(dense_dec_kernel<false>, dim3(a.nt), dim3(256), lds, stream, a);
   return hipGetLastError();
 }
 

