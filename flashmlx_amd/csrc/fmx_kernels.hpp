@@ -305,7 +305,8 @@ struct NhDecArgs {
   uint8_t* slots;              // [max_seg][16]: token t's slot for expert u, or 0xff
   uint16_t *h_hi, *h_lo;       // [T*k, Ip] relu^2 of fc1 as hi + lo bf16 (exact sum)
   uint16_t *hs_hi, *hs_lo;     // [T, Isp] the shared expert's
-  float* d;                    // [T*k, H] fc2 products, entry order
+  float* d;                    // [T*k, H] fc2 products, entry order (first K half)
+  float* d2;                   // [T*k, H] the same over the second K half
   float* sd_part;              // [kNhDecSdSplit][T][H] shared down, K-slice sums
   uint16_t* y;                 // [T, H]
   uint32_t* counter;           // D1 arrival counter: zero on entry and exit

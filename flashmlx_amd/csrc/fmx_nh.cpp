@@ -122,7 +122,7 @@ struct NhLayout {
   uint16_t* xh;        // [T, H] fp16 (P8)
   uint16_t *h, *hh;    // [n, Ip] relu^2 of fc1: bf16, fp16 (P8)
   uint16_t *hs, *hsh;  // [T, Isp] the shared expert's
-  float* d;            // [n, H] fc2 products, sorted rows (decode: entry order)
+  float* d;            // [n, H] fc2 products, sorted rows (decode: entry order, first K half)
   float* sd;           // [T, H] shared down
   // the decode kernels' (forwards of at most kDecMaxT tokens), sized for
   // min(T, kDecMaxT) at every T so that the layout only grows with T
@@ -130,6 +130,7 @@ struct NhLayout {
   uint32_t* seg;       // [1 + E]
   uint8_t* slots;      // [E][16]
   float* sd_part;      // [kNhDecSdSplit][Td][H]
+  float* d2;           // [Td * k][H] decode fc2 products over the second K half
   size_t total;
 };
 
@@ -171,6 +172,7 @@ NhLayout nh_layout(const fmx_nh_moe_config& c, int64_t T, char* base) {
   L.seg = static_cast<uint32_t*>(take((E + 1) * 4));
   L.slots = static_cast<uint8_t*>(take(E * kDecMaxT));
   L.sd_part = static_cast<float*>(take(P.Isp ? kNhDecSdSplit * Td * H * 4 : 0));
+  L.d2 = static_cast<float*>(take(Td * k * H * 4));
   L.total = used;
   return L;
 }
@@ -344,6 +346,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       da.hs_hi = L.hs;
       da.hs_lo = L.hsh;
       da.d = L.d;
+      da.d2 = L.d2;
       da.sd_part = L.sd_part;
       da.y = static_cast<uint16_t*>(y);
       da.counter = L.counters;

@@ -6,9 +6,9 @@
 //       limit, top-k, fp32 scores) and builds the routing tables
 //       |  the shared expert's up tiles + relu^2 (routing-independent,
 //       streaming meanwhile)
-//   D2  the routed fc1 tiles + relu^2, one 16-row tile per workgroup
-//   D3  fc2 of every selected expert (64 columns per workgroup) and the
-//       shared down projection in K slices, fp32 products
+//   D2  the routed fc1 tiles + relu^2, one or two 16-row tiles per workgroup
+//   D3  fc2 of every selected expert (64 columns and one K half per
+//       workgroup) and the shared down projection in K slices, fp32 products
 //   D4  the fp32 weighted sum and the shared add, rounded once to bf16
 //
 // Reference: server/src/nemotron_h.cpp:1010-1111 (moe_block), :54-63 (relu2).
@@ -30,8 +30,10 @@ namespace fmx {
 namespace {
 
 constexpr int kNhDnTiles = 4;     // 16-row tiles of H per D3 workgroup (one per wave)
-constexpr int kNhDnUnits = 16;    // D3's load ring: 128-k units per wave (routed fc2)
+constexpr int kNhDnSplit = 2;     // K halves of a routed fc2 tile (d, d2)
+constexpr int kNhDnUnits = 8;     // D3's load ring: 128-k units per wave (a routed fc2 K half)
 constexpr int kNhSdUnits = 8;     // the same for a shared down K slice
+constexpr int kNhD2PairGrid = 2048;  // D2 runs two tiles per workgroup from this many tiles
 
 // relu(bf16(acc))^2 as hi + lo bf16: v^2 of a bf16 v has at most 16
 // significant bits, so hi = bf16(v^2) and lo = v^2 - hi are both exact
@@ -209,10 +211,12 @@ __global__ __launch_bounds__(kDecThreads) void nh_d1(NhDecArgs a) {
 
 // ---------------------------------------------------------------- D2
 
-// Tile tp (fc1 rows 16 tp .. 16 tp + 15) of selected expert number u
-// (nemotron_h.cpp:1086-1090): h[t*k + slot, n] = relu(bf16(x_t . W1_e[n]))^2
-// for the tokens t whose slot `slot` selected expert e.
-template <int NU>
+// Tiles NT tp .. NT tp + NT - 1 (fc1 rows 16 tp ..) of selected expert
+// number u (nemotron_h.cpp:1086-1090): h[t*k + slot, n] = relu(bf16(x_t .
+// W1_e[n]))^2 for the tokens t whose slot `slot` selected expert e. Two tiles
+// per workgroup (large grids) share the routing-table reads and the staged
+// rows and put both tiles' loads in flight together.
+template <int NU, int NT>
 __global__ __launch_bounds__(kDecThreads) void nh_d2(NhDecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   float* s_red = reinterpret_cast<float*>(smem);
@@ -220,8 +224,8 @@ __global__ __launch_bounds__(kDecThreads) void nh_d2(NhDecArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, k = a.k, H = a.H, Ip = a.Ip, xs = xstride(H);
-  const int ntile = Ip / 16;
-  const int u = static_cast<int>(blockIdx.x) / ntile, tp = static_cast<int>(blockIdx.x) - u * ntile;
+  const int ntile = Ip / 16, ngrp = (ntile + NT - 1) / NT;
+  const int u = static_cast<int>(blockIdx.x) / ngrp, tp = (static_cast<int>(blockIdx.x) - u * ngrp) * NT;
   const int U = static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg)));
   if (u >= U) return;  // workgroup-uniform
   const int e = static_cast<int>(min(a.seg[1 + u], static_cast<uint32_t>(a.E - 1)));
@@ -237,23 +241,54 @@ __global__ __launch_bounds__(kDecThreads) void nh_d2(NhDecArgs a) {
   const int u0 = (nu * wave) / kDecWaves, u1 = (nu * (wave + 1)) / kDecWaves;
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
-  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  tile_units_lds<false, NU>(a.fc1 + static_cast<int64_t>(e) * a.fc1_es + static_cast<int64_t>(tp) * nu * kBlockSingle,
-                            u0, u1, xl, lane, acc0, acc1);
+  const uint8_t* eb = a.fc1 + static_cast<int64_t>(e) * a.fc1_es;
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;  // tile tp (and tp + 1)
+  if constexpr (NT == 1) {
+    tile_units_lds<false, NU>(eb + static_cast<int64_t>(tp) * nu * kBlockSingle, u0, u1, xl, lane, acc0, acc1);
+  } else {
+    // both tiles' units in flight, then the rows' DMA proven complete by
+    // their count (the DMA was issued before them)
+    PkUnit<false> L0[NU], L1[NU];
+    const uint8_t* b0 = eb + static_cast<int64_t>(tp) * nu * kBlockSingle;
+    const uint8_t* b1 = eb + static_cast<int64_t>(min(tp + 1, ntile - 1)) * nu * kBlockSingle;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < NU; ++d) L0[d] = pk_load<false>(b0 + min(u0 + d, u1 - 1) * kBlockSingle, lane);
+#pragma unroll
+    for (int d = 0; d < NU; ++d) L1[d] = pk_load<false>(b1 + min(u0 + d, u1 - 1) * kBlockSingle, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * NU * pk_load_insts<false>()>();
+    lds_dma_barrier();
+    f32x4_t unused = acc0;
+#pragma unroll
+    for (int d = 0; d < NU; ++d) {
+      if (u0 + d < u1) {
+        bf16x8_t A[4];
+        lds_a(xl + (u0 + d) * 128, A);
+        pk_unit<false>(L0[d], A, acc0, unused);
+        pk_unit<false>(L1[d], A, acc1, unused);
+      }
+    }
+  }
   quad_reduce(acc0, acc1, wave, lane, s_red);
   if (wave != 0) return;
   const uint32_t my_slots = __shfl(slot4, j);  // rows 4j .. 4j + 3
-  const int n = tp * 16 + m;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * j + i;
-    const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k)) {
-      uint16_t hi, lo;
-      relu2_split(acc0[i], hi, lo);
-      const int64_t o = static_cast<int64_t>(t * k + slot) * Ip + n;
-      a.h_hi[o] = hi;
-      a.h_lo[o] = lo;
+  for (int q = 0; q < NT; ++q) {
+    if (tp + q >= ntile) continue;
+    const f32x4_t& acc = q ? acc1 : acc0;
+    const int n = (tp + q) * 16 + m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * j + i;
+      const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
+      if (t < T && slot < static_cast<uint32_t>(k)) {
+        uint16_t hi, lo;
+        relu2_split(acc[i], hi, lo);
+        const int64_t o = static_cast<int64_t>(t * k + slot) * Ip + n;
+        a.h_hi[o] = hi;
+        a.h_lo[o] = lo;
+      }
     }
   }
 }
@@ -289,41 +324,47 @@ __device__ inline f32x4_t d3_tile(const uint8_t* tb, int nu, const uint16_t* xl_
 }
 
 // Selected expert number u, columns 64 cb .. 64 cb + 63 of H, one 16-row
-// tile per wave over all of Ip (nemotron_h.cpp:1091-1094): d[t*k + slot, n]
-// = h[t*k + slot] . W2_e[n] in fp32.
-__device__ void d3_routed(const NhDecArgs& a, int u, int cb, uint8_t* smem) {
+// tile per wave over K half ks of Ip (nemotron_h.cpp:1091-1094):
+// d[t*k + slot, n] (ks 0) or d2[..] (ks 1) = h[t*k + slot] . W2_e[n] over
+// the half, fp32. Halves keep a workgroup's staged rows (hi and lo) to half
+// of Ip, so that more workgroups share a CU.
+__device__ void d3_routed(const NhDecArgs& a, int u, int cb, int ks, uint8_t* smem) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int T = a.T, k = a.k, H = a.H, Ip = a.Ip, xs = xstride(Ip);
+  const int T = a.T, k = a.k, H = a.H, Ip = a.Ip;
   const int U = static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg)));
   if (u >= U) return;  // workgroup-uniform
   const int e = static_cast<int>(min(a.seg[1 + u], static_cast<uint32_t>(a.E - 1)));
   const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.slots + u * kDecMaxT);
   const uint32_t slot4 = srow[lane & 3];
+  const int nu_all = Ip / 128;
+  const int ub = (nu_all * ks) / kNhDnSplit, ue = (nu_all * (ks + 1)) / kNhDnSplit, nu = ue - ub;
+  const int kk = nu * 128, xs = xstride(kk);
   uint16_t* s_hi = reinterpret_cast<uint16_t*>(smem);
   uint16_t* s_lo = s_hi + T * xs;
-  const int nu = Ip / 128;
   const int tile = kNhDnTiles * cb + wave;
-  const uint8_t* tb = a.fc2 + static_cast<int64_t>(e) * a.fc2_es + static_cast<int64_t>(tile) * nu * kBlockSingle;
+  const uint8_t* tb =
+      a.fc2 + static_cast<int64_t>(e) * a.fc2_es + (static_cast<int64_t>(tile) * nu_all + ub) * kBlockSingle;
   const int m = lane & 15, j = lane >> 4;
   const int r = min(m, T - 1);
   const f32x4_t acc = d3_tile<kNhDnUnits>(tb, nu, s_hi + r * xs + 8 * j, s_lo + r * xs + 8 * j, lane, [&]() {
     for (int t = wave; t < T; t += kDecWaves) {
       const uint32_t slot = (__shfl(slot4, t >> 2) >> (8 * (t & 3))) & 0xffu;
       if (slot < static_cast<uint32_t>(k)) {
-        const int64_t o = static_cast<int64_t>(t * k + slot) * Ip;
-        dma_row(a.h_hi + o, Ip, s_hi + t * xs, lane);
-        dma_row(a.h_lo + o, Ip, s_lo + t * xs, lane);
+        const int64_t o = static_cast<int64_t>(t * k + slot) * Ip + ub * 128;
+        dma_row(a.h_hi + o, kk, s_hi + t * xs, lane);
+        dma_row(a.h_lo + o, kk, s_lo + t * xs, lane);
       }
     }
   });
+  float* const dst = ks ? a.d2 : a.d;
   const uint32_t my_slots = __shfl(slot4, j);
   const int n = tile * 16 + m;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
     const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k)) a.d[static_cast<int64_t>(t * k + slot) * H + n] = acc[i];
+    if (t < T && slot < static_cast<uint32_t>(k)) dst[static_cast<int64_t>(t * k + slot) * H + n] = acc[i];
   }
 }
 
@@ -356,13 +397,14 @@ __device__ void d3_shared(const NhDecArgs& a, int cb, int ks, uint8_t* smem) {
   }
 }
 
-// Workgroups [0, max_seg * H/64): routed fc2; then the shared down slices.
+// Workgroups [0, max_seg * H/64 * 2): routed fc2 (the two K halves of a
+// column block adjacent); then the shared down slices.
 __global__ __launch_bounds__(kDecThreads) void nh_d3(NhDecArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int ncb = a.H / (16 * kNhDnTiles);
-  const int b = blockIdx.x, nr = a.max_seg * ncb;
+  const int b = blockIdx.x, nr = a.max_seg * ncb * kNhDnSplit;
   if (b < nr)
-    d3_routed(a, b / ncb, b % ncb, smem);
+    d3_routed(a, b / (ncb * kNhDnSplit), (b / kNhDnSplit) % ncb, b % kNhDnSplit, smem);
   else
     d3_shared(a, (b - nr) / kNhDecSdSplit, (b - nr) % kNhDecSdSplit, smem);
 }
@@ -380,9 +422,11 @@ __global__ __launch_bounds__(kDecThreads) void nh_d4(NhDecArgs a) {
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < a.k; ++j) {
     const float s = a.scores[t * a.k + j];
-    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(a.d + static_cast<int64_t>(t * a.k + j) * a.H + o * 4);
+    const int64_t off = static_cast<int64_t>(t * a.k + j) * a.H + o * 4;
+    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(a.d + off);
+    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(a.d2 + off);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(v[i], s));
+    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(__fadd_rn(v0[i], v1[i]), s));
   }
   float out[4];
 #pragma unroll
@@ -410,9 +454,10 @@ size_t d1_lds(const NhDecArgs& a) {
 }
 size_t d2_lds(const NhDecArgs& a) { return d1_lds(a); }
 size_t d3_lds(const NhDecArgs& a) {
-  const int nu_s = a.Isp / 128;
+  const int nu_r = a.Ip / 128, nu_s = a.Isp / 128;
+  const int kk_r = ((nu_r + kNhDnSplit - 1) / kNhDnSplit) * 128;
   const int kk_s = ((nu_s + kNhDecSdSplit - 1) / kNhDecSdSplit) * 128;
-  return static_cast<size_t>(2) * a.T * xstride(std::max(a.Ip, kk_s)) * 2;
+  return static_cast<size_t>(2) * a.T * xstride(std::max(kk_r, kk_s)) * 2;
 }
 // units per wave of a D1 / D2 tile (K = H split in four)
 int d12_units(const NhDecArgs& a) { return (a.H / 128 + kDecWaves - 1) / kDecWaves; }
@@ -435,7 +480,8 @@ bool nh_decode_plan(NhDecArgs& a) {
   const int nu_s = a.Isp / 128;
   if (a.T < 1 || a.T > kDecMaxT || a.k < 1 || a.k > kDecMaxK || a.E < 1 || a.E > kNhDecMaxE || a.E > a.H ||
       a.H % 128 || a.H < 512 || a.H / 8 > 2 * kDecThreads || d12_units(a) > 8 || a.Ip % 128 ||
-      a.Ip / 128 > kNhDnUnits || a.H % (16 * kNhDnTiles) || a.Isp % 128 ||
+      a.Ip / 128 < kNhDnSplit || (a.Ip / 128 + kNhDnSplit - 1) / kNhDnSplit > kNhDnUnits ||
+      a.H % (16 * kNhDnTiles) || a.Isp % 128 ||
       (a.Isp > 0 && (nu_s < kNhDecSdSplit || (nu_s + kNhDecSdSplit - 1) / kNhDecSdSplit > kNhSdUnits)) ||
       a.n_group > kWave)
     return false;
@@ -461,20 +507,31 @@ hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const*
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if ((err = mark(1)) != hipSuccess) return err;
   {
-    const dim3 grid(a.max_seg * (a.Ip / 16)), block(kDecThreads);
+    const int ntile = a.Ip / 16;
+    const bool two = a.max_seg * ntile >= kNhD2PairGrid;
+    const dim3 grid(a.max_seg * (two ? (ntile + 1) / 2 : ntile)), block(kDecThreads);
     const int nu = d12_units(a);
-    if (nu <= 4)
-      hipLaunchKernelGGL(nh_d2<4>, grid, block, d2_lds(a), stream, a);
-    else if (nu <= 6)
-      hipLaunchKernelGGL(nh_d2<6>, grid, block, d2_lds(a), stream, a);
-    else
-      hipLaunchKernelGGL(nh_d2<8>, grid, block, d2_lds(a), stream, a);
+    if (two) {
+      if (nu <= 4)
+        hipLaunchKernelGGL((nh_d2<4, 2>), grid, block, d2_lds(a), stream, a);
+      else if (nu <= 6)
+        hipLaunchKernelGGL((nh_d2<6, 2>), grid, block, d2_lds(a), stream, a);
+      else
+        hipLaunchKernelGGL((nh_d2<8, 2>), grid, block, d2_lds(a), stream, a);
+    } else {
+      if (nu <= 4)
+        hipLaunchKernelGGL((nh_d2<4, 1>), grid, block, d2_lds(a), stream, a);
+      else if (nu <= 6)
+        hipLaunchKernelGGL((nh_d2<6, 1>), grid, block, d2_lds(a), stream, a);
+      else
+        hipLaunchKernelGGL((nh_d2<8, 1>), grid, block, d2_lds(a), stream, a);
+    }
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   if ((err = mark(2)) != hipSuccess) return err;
   {
     const int ncb = a.H / (16 * kNhDnTiles);
-    const int n = a.max_seg * ncb + (a.Isp > 0 ? ncb * kNhDecSdSplit : 0);
+    const int n = a.max_seg * ncb * kNhDnSplit + (a.Isp > 0 ? ncb * kNhDecSdSplit : 0);
     hipLaunchKernelGGL(nh_d3, dim3(n), dim3(kDecThreads), d3_lds(a), stream, a);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
