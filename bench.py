@@ -733,6 +733,121 @@ def stack_cpu_baseline(cfg, w, seconds: float):
                       f"prompt, on {cpu_model()}, {nproc} OpenMP threads"}
 
 
+# The standalone operators (fmx_gather_qmm, fmx_quantized_matmul: the drop-in
+# for switch_mlp's and shared_expert_mlp's MLX calls, model.cpp:703-721 and
+# :741-747) at the Qwen1.5-MoE-A2.7B shapes, on the MLX layout (their general
+# GEMM path). Decode cases stream their weights (GB/s), prefill cases are
+# priced in flops (TFLOP/s).
+def measure_ops(trials: int = 5, calls: int = 20) -> dict:
+    import ctypes as C
+
+    import torch
+
+    from flashmlx_amd import _lib
+    from flashmlx_amd import moe as Mo
+
+    lib = _lib.load()
+    H, E, I, Is, k = 2048, 60, 1408, 5632, 4
+    w = Mo.synth_normal_bf16_device((E, I, H), 11, 60, 0.0, 0.02)
+    gq, gs, gb = Mo.quantize(w)
+    del w
+    w = Mo.synth_normal_bf16_device((Is, H), 11, 61, 0.0, 0.02)
+    sq, ss, sb = Mo.quantize(w)
+    del w
+    gen = torch.Generator().manual_seed(5)
+
+    def graph_time(fn) -> float:
+        """GPU us per call: a HIP graph of `calls` calls, replayed."""
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(calls):
+                fn()
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(trials):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1000.0 / calls)
+        return statistics.median(ts)
+
+    def gather_case(x, rhs, sorted_idx: bool):
+        ax, aw, asc, abi, ar = Mo._arr(x), Mo._packed(gq), Mo._arr(gs), Mo._arr(gb), Mo._index(rhs)
+        shp = _lib.FmxArray()
+        _lib.check(lib.fmx_gather_qmm_out_shape(C.byref(ax), C.byref(aw), None, C.byref(ar), 1, 64, 4,
+                                                C.byref(shp)))
+        out = torch.empty(Mo._shape(shp), dtype=torch.bfloat16, device="cuda")
+        ao = Mo._arr(out)
+        wsz = lib.fmx_gather_qmm_workspace_size(C.byref(ax), C.byref(aw), None, C.byref(ar))
+        wbuf = torch.empty(max(wsz, 1), dtype=torch.uint8, device="cuda")
+        return lambda: _lib.check(lib.fmx_gather_qmm(
+            C.byref(ax), C.byref(aw), C.byref(asc), C.byref(abi), None, C.byref(ar), 1, 64, 4, b"affine",
+            int(sorted_idx), C.byref(ao), wbuf.data_ptr(), wsz, Mo._stream())), (x, rhs, out, wbuf)
+
+    def qmm_case(x):
+        ax, aw, asc, abi = Mo._arr(x), Mo._packed(sq), Mo._arr(ss), Mo._arr(sb)
+        shp = _lib.FmxArray()
+        _lib.check(lib.fmx_quantized_matmul_out_shape(C.byref(ax), C.byref(aw), 1, 64, 4, C.byref(shp)))
+        out = torch.empty(Mo._shape(shp), dtype=torch.bfloat16, device="cuda")
+        ao = Mo._arr(out)
+        wsz = lib.fmx_quantized_matmul_workspace_size(C.byref(ax), C.byref(aw))
+        wbuf = torch.empty(max(wsz, 1), dtype=torch.uint8, device="cuda")
+        return lambda: _lib.check(lib.fmx_quantized_matmul(
+            C.byref(ax), C.byref(aw), C.byref(asc), C.byref(abi), 1, 64, 4, b"affine", C.byref(ao),
+            wbuf.data_ptr(), wsz, Mo._stream())), (x, out, wbuf)
+
+    def rand_x(shape):
+        return torch.randn(shape, generator=gen).to(torch.bfloat16).cuda()
+
+    res = {}
+    # decode: switch_mlp's unsorted gate projection for 8 tokens x top-4
+    B = 8
+    inds = torch.stack([torch.randperm(E, generator=gen)[:k] for _ in range(B)]).to(torch.int32)
+    fn, keep = gather_case(rand_x((B, 1, 1, 1, H)), inds.reshape(B, 1, k).cuda(), False)
+    us = graph_time(fn)
+    U = int(torch.unique(inds).numel())
+    byts = U * I * H * 9 // 16 + B * H * 2 + B * k * I * 2
+    res["gather_qmm_decode_b8"] = {"shape": f"x [8,1,1,1,{H}], w [{E},{I},{H}/8], rhs [8,1,{k}]", "us": round(us, 2),
+                                   "algorithmic_bytes": byts, "GB_s": round(byts / us / 1e3, 1),
+                                   "hbm_frac": round(byts / us / 1e3 / 8000.0, 4)}
+    # prefill: the sorted call over 512 tokens x top-4 (rows already gathered)
+    n = 512 * k
+    rhs = torch.sort(torch.randint(0, E, (n,), generator=gen)).values.to(torch.int32)
+    fn, keep2 = gather_case(rand_x((n, 1, H)), rhs.cuda(), True)
+    us = graph_time(fn)
+    fl = 2.0 * n * I * H
+    res["gather_qmm_prefill_512"] = {"shape": f"x [{n},1,{H}] sorted, w [{E},{I},{H}/8]", "us": round(us, 2),
+                                     "flops": fl, "TFLOP_s": round(fl / us / 1e6, 2),
+                                     "mfma_frac": round(fl / us / 1e6 / 2500.0, 4)}
+    for T, name in ((8, "quantized_matmul_decode_b8"), (512, "quantized_matmul_prefill_512")):
+        fn, keep3 = qmm_case(rand_x((T, H)))
+        us = graph_time(fn)
+        if T <= 16:
+            byts = Is * H * 9 // 16 + T * H * 2 + T * Is * 2
+            res[name] = {"shape": f"x [{T},{H}], w [{Is},{H}/8]", "us": round(us, 2), "algorithmic_bytes": byts,
+                         "GB_s": round(byts / us / 1e3, 1), "hbm_frac": round(byts / us / 1e3 / 8000.0, 4)}
+        else:
+            fl = 2.0 * T * Is * H
+            res[name] = {"shape": f"x [{T},{H}], w [{Is},{H}/8]", "us": round(us, 2), "flops": fl,
+                         "TFLOP_s": round(fl / us / 1e6, 2), "mfma_frac": round(fl / us / 1e6 / 2500.0, 4)}
+        del keep3
+    for key, v in res.items():
+        log(f"op {key}: {v['us']} us")
+    return {"workload": "standalone fmx_gather_qmm / fmx_quantized_matmul on the MLX layout, "
+                        "Qwen1.5-MoE-A2.7B shapes, HIP graphs of 20 calls", "cases": res}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -753,6 +868,8 @@ def main():
                     help="decoder-stack configs measured in the same run: all, none or a comma list "
                          "(c4_stack_b1, c4_stack_b4, c4_stack_b8)")
     ap.add_argument("--stack-trials", type=int, default=5)
+    ap.add_argument("--ops", default="all", choices=["all", "none"],
+                    help="time the standalone fmx_gather_qmm / fmx_quantized_matmul")
     ap.add_argument("--nh", default="all",
                     help="Nemotron-H block configs measured in the same run: all, none or a comma list "
                          "(nh30b_decode_b1, nh30b_decode_b8, nh30b_prefill_512)")
@@ -808,6 +925,9 @@ def main():
         steps = 480 if T <= 16 else 48
         configs[key] = measure_nh(key, T, 8, steps, max(8, steps // 10), 5,
                                   0.0 if args.no_cpu_baseline else min(args.cpu_seconds, 6.0))
+
+    if args.ops == "all":
+        configs["ops_qwen15"] = measure_ops()
 
     cpu, parity = None, None
     if not args.no_cpu_baseline:

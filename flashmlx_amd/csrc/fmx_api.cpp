@@ -389,10 +389,66 @@ int fmx_quantized_matmul_out_shape(const fmx_array* x, const fmx_array* w, int t
   return ok();
 }
 
+namespace {
+
+// More than one MFMA tile of rows (16) goes to the prefill GEMM on the
+// MLX-layout weights (fmx_prefill.hip): K in whole 128-k units, N in whole
+// 16-row tiles; fewer rows, and other shapes, to the grouped GEMM
+// (fmx_qgemm.hip).
+bool op_uses_pf(int64_t rows, int64_t N, int64_t K) {
+  return rows > 16 && rows <= (1 << 20) && N % 16 == 0 && K % 128 == 0;
+}
+
+// the prefill GEMM's share of an op's workspace: the fp16 (Q8) copy of the
+// rows beside the bf16 (P8) one, and the overflow flag word
+void take_pf_rows(Arena& ar, int64_t x_rows, int64_t K, uint16_t** xq, uint32_t** flag) {
+  *xq = static_cast<uint16_t*>(ar.take(x_rows * K * 2));
+  *flag = static_cast<uint32_t*>(ar.take(4));
+}
+
+// One set of the prefill GEMM over MLX-layout weights [n_exp][N][K/8]
+// (scales / biases [n_exp][N][K/64]), output rows of N bf16.
+PfSet mlx_set(const fmx_array* w, const fmx_array* scales, const fmx_array* biases,
+              const uint16_t* xp, const uint16_t* xq, int64_t K, int64_t N, uint16_t* out) {
+  PfSet s{};
+  s.mw = static_cast<const uint32_t*>(w->data);
+  s.ms = static_cast<const uint16_t*>(scales->data);
+  s.mb = static_cast<const uint16_t*>(biases->data);
+  s.x = xp;
+  s.xh = xq;
+  s.ldx = K;
+  s.out = out;
+  s.ldo = N;
+  s.nt = static_cast<int>(N / 16);
+  s.nu = static_cast<int>(K / 128);
+  s.n_exp = 1;
+  return s;
+}
+
+hipError_t launch_mlx_pf(PfSet& s, uint32_t* flag, hipStream_t stream) {
+  PfArgs pa{};
+  pa.s1 = s;
+  pa.n_items1 = pf_items(pa.s1, false);
+  pa.f16_flag = flag;
+  pa.flag_in = 1u;
+  pa.flag_out = 0u;
+  return launch_pf(pa, false, stream);
+}
+
+}  // namespace
+
 size_t fmx_quantized_matmul_workspace_size(const fmx_array* x, const fmx_array* w) {
-  (void)w;
-  if (!x) return 0;
-  return static_cast<size_t>(align_up(numel(*x) * 2, 256));
+  if (!x || x->ndim < 1) return 0;
+  const int64_t K = x->shape[x->ndim - 1];
+  const int64_t rows = K ? numel(*x) / K : 0;
+  Arena ar;
+  ar.take(rows * K * 2);  // rows in the P8 layout
+  if (w && w->ndim == 2 && op_uses_pf(rows, w->shape[0], K)) {
+    uint16_t* xq;
+    uint32_t* flag;
+    take_pf_rows(ar, rows, K, &xq, &flag);
+  }
+  return ar.used;
 }
 
 int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
@@ -429,6 +485,17 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
                            fmx_quantized_matmul_workspace_size(x, w), stream)))
     return rc;
   uint16_t* xp = static_cast<uint16_t*>(ar.take(rows * K * 2));
+  if (op_uses_pf(rows, N, K)) {
+    uint16_t* xq;
+    uint32_t* flag;
+    take_pf_rows(ar, rows, K, &xq, &flag);
+    FMX_HIP(launch_fill_u32(flag, 1, 0u, stream));
+    FMX_HIP(launch_mlx_rows(static_cast<const uint16_t*>(x->data), rows, K, xp, xq, flag, 1u, stream));
+    PfSet s = mlx_set(w, scales, biases, xp, xq, K, N, static_cast<uint16_t*>(out->data));
+    s.rows_static = s.rows_max = s.x_rows = static_cast<int>(rows);
+    FMX_HIP(launch_mlx_pf(s, flag, stream));
+    return ok();
+  }
   FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), rows, K, xp, stream));
   QGemmProblem p{};
   p.x = xp;
@@ -522,6 +589,13 @@ size_t gather_ws(const GatherPlan& p) {
   ar.take((p.E + 1) * 4);              // seg_off
   ar.take(p.E * ((rows + 63) / 64) * 4);  // sort base
   ar.take(rows * 4);                   // row_map
+  if (op_uses_pf(rows, p.N, p.K)) {
+    ar.take(4);                                        // pass count
+    ar.take(static_cast<int64_t>(max_passes(rows, p.E)) * 8);  // pass table
+    uint16_t* xq;
+    uint32_t* flag;
+    take_pf_rows(ar, p.n_x * p.M, p.K, &xq, &flag);
+  }
   return ar.used;
 }
 
@@ -611,8 +685,19 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   uint32_t* seg_off = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
   uint32_t* sbase = static_cast<uint32_t*>(ar.take(p.E * ((rows + 63) / 64) * 4));
   uint32_t* row_map = static_cast<uint32_t*>(ar.take(rows * 4));
-
-  FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, stream));
+  const bool pf = op_uses_pf(rows, p.N, p.K);
+  uint32_t *pass_n = nullptr, *pass_tab = nullptr, *flag = nullptr;
+  uint16_t* xq = nullptr;
+  if (pf) {
+    pass_n = static_cast<uint32_t*>(ar.take(4));
+    pass_tab = static_cast<uint32_t*>(ar.take(static_cast<int64_t>(max_passes(rows, p.E)) * 8));
+    take_pf_rows(ar, p.n_x * p.M, p.K, &xq, &flag);
+    FMX_HIP(launch_fill_u32(flag, 1, 0u, stream));
+    FMX_HIP(launch_mlx_rows(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, xq, flag, 1u,
+                            stream));
+  } else {
+    FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, stream));
+  }
   BcastArgs bl{}, br{};
   fill_bcast(p, lhs, x->shape, x->ndim - 2, &bl);
   bl.dst = lhs_flat;
@@ -629,8 +714,25 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   so.seg_exp = seg_exp;
   so.seg_off = seg_off;
   so.base = sbase;
+  so.pass_n = pass_n;
+  so.pass_tab = pass_tab;
   FMX_HIP(launch_sort(keys, static_cast<int>(rows), 1, static_cast<int>(p.E), so, stream));
   FMX_HIP(launch_gather_maps(order, lhs_flat, rows, static_cast<int>(p.M), p.n_x, row_map, stream));
+  if (pf) {
+    // passes of at most 64 sorted rows of one expert; pass row r reads x row
+    // row_map[r] and writes output row order[r]
+    PfSet s = mlx_set(w, scales, biases, xp, xq, p.K, p.N, static_cast<uint16_t*>(out->data));
+    s.row_map = row_map;
+    s.out_map = order;
+    s.pass_n = pass_n;
+    s.pass_tab = pass_tab;
+    s.max_pass = max_passes(rows, p.E);
+    s.n_exp = static_cast<int>(p.E);
+    s.rows_max = static_cast<int>(rows);
+    s.x_rows = static_cast<int>(p.n_x * p.M);
+    FMX_HIP(launch_mlx_pf(s, flag, stream));
+    return ok();
+  }
 
   QGemmProblem q{};
   q.x = xp;

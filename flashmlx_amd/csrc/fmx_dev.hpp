@@ -388,6 +388,27 @@ __device__ inline u32x4_t bf16_chunk_to_f16_p8(u32x4_t v, bool& ovf) {
   return o;
 }
 
+// The same chunk as 8 fp16 in the Q8 layout (elements 0,2,4,6,1,3,5,7): the
+// order in which dq8_f16 delivers an MLX-layout word's weights (element i
+// at nibble position i).
+__device__ inline u32x4_t bf16_chunk_to_f16_q8(u32x4_t v, bool& ovf) {
+  uint32_t e[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    e[2 * i] = v[i] & 0xffffu;
+    e[2 * i + 1] = v[i] >> 16;
+  }
+  constexpr int q8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  u32x4_t o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = e[q8[2 * m]], hi = e[q8[2 * m + 1]];
+    ovf = ovf || bf16_f16_overflow(lo) || bf16_f16_overflow(hi);
+    o[m] = bf16_to_f16_bits(lo) | (bf16_to_f16_bits(hi) << 16);
+  }
+  return o;
+}
+
 template <bool DUAL>
 struct PkUnit {
   u32x4_t w0, w1;    // packed words (gate / up)

@@ -1,7 +1,7 @@
 // fmx_elem.hip -- small kernels around the GEMMs: the top-k weighted
 // combine with the gated shared expert, layout permutations, index
 // broadcasting for gather_qmm, and the affine quantizer.
-#include "fmx_kernels.hpp"
+#include "fmx_dev.hpp"
 
 namespace fmx {
 
@@ -147,6 +147,36 @@ hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_
   if (n_oct == 0) return hipSuccess;
   hipLaunchKernelGGL(permute_p8_kernel, dim3(grid_for(n_oct, kElemThreads)), dim3(kElemThreads),
                      0, stream, x, n_oct, xp);
+  return hipGetLastError();
+}
+
+// rows for the prefill GEMM on MLX-layout weights: a bf16 copy in the P8
+// layout (the exact path) and an fp16 copy in the Q8 layout; a value
+// outside fp16's range ORs bit into *flag
+__global__ __launch_bounds__(kElemThreads) void mlx_rows_kernel(const uint16_t* x, int64_t n_oct,
+                                                                uint16_t* xp, uint16_t* xq,
+                                                                uint32_t* flag, uint32_t bit) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
+  bool ovf = false;
+  if (o < n_oct) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(x + o * 8);
+    u32x4_t p;
+    p[0] = (v[0] & 0xffffu) | (v[2] << 16);
+    p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+    p[2] = (v[1] & 0xffffu) | (v[3] << 16);
+    p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+    *reinterpret_cast<u32x4_t*>(xp + o * 8) = p;
+    *reinterpret_cast<u32x4_t*>(xq + o * 8) = bf16_chunk_to_f16_q8(v, ovf);
+  }
+  if (__ballot(ovf) && (threadIdx.x & 63) == 0) atomicOr(flag, bit);
+}
+
+hipError_t launch_mlx_rows(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp, uint16_t* xq,
+                           uint32_t* flag, uint32_t bit, hipStream_t stream) {
+  const int64_t n_oct = rows * (K / 8);
+  if (n_oct == 0) return hipSuccess;
+  hipLaunchKernelGGL(mlx_rows_kernel, dim3(grid_for(n_oct, kElemThreads)), dim3(kElemThreads), 0,
+                     stream, x, n_oct, xp, xq, flag, bit);
   return hipGetLastError();
 }
 

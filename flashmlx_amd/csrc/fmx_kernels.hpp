@@ -227,6 +227,15 @@ struct PfSet {
   // out32 + ks * part_stride
   int ksplit;
   int64_t part_stride;
+  // single matrices in the MLX layout instead of w (mw set): mw [n_exp][nt*16]
+  // [K/8] u32, ms / mb [n_exp][nt*16][K/64] bf16 scales / biases; then x is
+  // the rows in the P8 layout (bf16) and xh in the Q8 layout (fp16), the
+  // orders in which an MLX word's nibbles convert. out_map (nullable): pass
+  // row r is written to output row out_map[r]
+  const uint32_t* mw;
+  const uint16_t* ms;
+  const uint16_t* mb;
+  const uint32_t* out_map;
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)
@@ -328,6 +337,11 @@ struct NhCombineArgs {
 };
 hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 
+// rows of K bf16 (natural order) -> xp: bf16 in the P8 layout, xq: fp16 in
+// the Q8 layout (fmx_dev.hpp), the two operand copies of the prefill GEMM on
+// MLX-layout weights; a value outside fp16's range ORs bit into *flag
+hipError_t launch_mlx_rows(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp, uint16_t* xq,
+                           uint32_t* flag, uint32_t bit, hipStream_t stream);
 hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
                              hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);

@@ -43,6 +43,17 @@
 // cost 0.5 % relative L2 error of the block output at 512 tokens and put
 // single elements outside the bf16 parity tolerance; fp16 weights cost
 // 0.06 %.)
+//
+// The single-matrix grid also reads weights in MLX's own layout (words of
+// 8 nibbles along K per row, scales and biases per row and group), for
+// quantized_matmul and gather_qmm with more than 16 rows: lane (i16, j)
+// moves words 4j..4j+3 of row i16 of the unit (the same 1 KB piece per
+// block), the (scale, bias) DMA takes each row's two 4-byte pairs from the
+// two arrays, and a lane reads its k-slice's word from the piece it sits in.
+// An MLX word's nibbles convert in another order than a packed word's, so
+// the rows come in matching copies: fp16 in the Q8 layout, bf16 in the P8
+// layout (fmx_dev.hpp), and out_map scatters the sorted rows of gather_qmm
+// back to their output rows.
 #include "fmx_dev.hpp"
 
 namespace fmx {
@@ -87,7 +98,7 @@ __device__ inline void dma4(const void* g, void* lds) {
 // weights, column group ng. MT (the 16-row tiles the rows fill) fixes how
 // many row pieces each wave moves per unit, so the pass's rows are moved
 // and multiplied once, without padding to kPassRows.
-template <bool DUAL, int MT, bool F16>
+template <bool DUAL, int MT, bool F16, bool MLX>
 __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, int row0, int rows,
                                                        int64_t e, int ks, uint8_t* s_pf,
                                                        uint32_t* flag, uint32_t flag_out) {
@@ -98,6 +109,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   constexpr int WB = pf_wave_bbytes<DUAL>(), SBO = NB * NM * 1024;  // wave's stage share, its sb offset
   constexpr int STAGE = pf_stage_bytes<DUAL>();
   static_assert(NB * NM * 128 == 256, "the blocks' (scale, bias) words fill one 4-byte DMA");
+  static_assert(!MLX || !DUAL, "MLX-layout weights: single matrices only");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -110,11 +122,19 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   // ---- sources: this wave's packed blocks (tiles past the matrix re-read
   // its last tile and are not stored) and its row pieces' lanes
   const int tile0 = (ng * kPfWaves + wave) * NB;
-  const uint8_t* wexp = P.w + e * P.es;
+  const uint8_t* wexp = MLX ? nullptr : P.w + e * P.es;
   const uint8_t* bsrc[NB];
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
-    bsrc[b] = wexp + (static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * P.nu + kb) * BB;
+  for (int b = 0; b < NB; ++b) {
+    if constexpr (MLX) {
+      // MLX layout: lane (i16, j) moves words 4j .. 4j + 3 of the unit in
+      // row i16 of the tile (64 contiguous bytes per row and unit)
+      const int64_t row = static_cast<int64_t>(e) * P.nt * 16 + min(tile0 + b, P.nt - 1) * 16 + i16;
+      bsrc[b] = reinterpret_cast<const uint8_t*>(P.mw + row * (P.nu * 16) + 16 * kb + 4 * j);
+    } else {
+      bsrc[b] = wexp + (static_cast<int64_t>(min(tile0 + b, P.nt - 1)) * P.nu + kb) * BB;
+    }
+  }
   const uint16_t* asrc[PA];
 #pragma unroll
   for (int pc = 0; pc < PA; ++pc) {
@@ -128,20 +148,36 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
   // the (scale, bias) piece: lane l fetches 4 bytes of block l / SBL's
   // 16 x 8 (single) or 2 x 16 x 8 (pair) bytes
   constexpr int SBL = kWave / NB;  // lanes per block
-  const uint8_t* sb_src = wexp + (static_cast<int64_t>(min(tile0 + lane / SBL, P.nt - 1)) * P.nu + kb) * BB +
-                          NM * 1024 + 4 * (lane % SBL);
+  const uint8_t* sb_src;
+  if constexpr (MLX) {
+    // the scale (even lanes) or bias (odd lanes) pair of groups 2u, 2u + 1
+    // of row (lane % 32) / 2 of block lane / 32, at the place of the
+    // packed block's (scale, bias) word
+    const int64_t row = static_cast<int64_t>(e) * P.nt * 16 + min(tile0 + lane / SBL, P.nt - 1) * 16 +
+                        (lane % SBL) / 2;
+    sb_src = reinterpret_cast<const uint8_t*>((lane & 1 ? P.mb : P.ms) + row * (P.nu * 2) + 2 * kb);
+  } else {
+    sb_src = wexp + (static_cast<int64_t>(min(tile0 + lane / SBL, P.nt - 1)) * P.nu + kb) * BB + NM * 1024 +
+             4 * (lane % SBL);
+  }
 
   auto issue = [&](int u, int st) {
     uint8_t* sa = s_pf + st * STAGE;
 #pragma unroll
     for (int pc = 0; pc < PA; ++pc) dma16(asrc[pc] + u * 128, sa + (pc * kPfWaves + wave) * 1024);
     uint8_t* sb = sa + kPfABytes + wave * WB;
-    const int64_t uo = static_cast<int64_t>(u) * BB;
+    if constexpr (MLX) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
+      for (int b = 0; b < NB; ++b) dma16(bsrc[b] + 64 * u, sb + b * 1024);
+      dma4(sb_src + 4 * u, sb + SBO);
+    } else {
+      const int64_t uo = static_cast<int64_t>(u) * BB;
 #pragma unroll
-      for (int m = 0; m < NM; ++m) dma16(bsrc[b] + uo + m * 1024 + 16 * lane, sb + (b * NM + m) * 1024);
-    dma4(sb_src + uo, sb + SBO);
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) dma16(bsrc[b] + uo + m * 1024 + 16 * lane, sb + (b * NM + m) * 1024);
+      dma4(sb_src + uo, sb + SBO);
+    }
   };
 
   f32x4_t acc[MT][NB][NM];
@@ -180,7 +216,14 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        W[b][m] = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
+        if constexpr (MLX) {
+          // word 4q + j of row i16 (k-slice q) sits in lane 16q + i16's piece
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            W[b][m][q] = *reinterpret_cast<const uint32_t*>(sb + b * 1024 + 256 * q + 16 * i16 + 4 * j);
+        } else {
+          W[b][m] = *reinterpret_cast<const u32x4_t*>(sb + (b * NM + m) * 1024 + 16 * lane);
+        }
         SB[b][m] = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
       }
     if constexpr (F16) {
@@ -281,7 +324,9 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mt + 4 * j + r;
         if (row >= rows) continue;
-        const int64_t orow = static_cast<int64_t>(row0 + row) * P.ldo;
+        const int64_t orow =
+            static_cast<int64_t>(P.out_map ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
+                                           : row0 + row) * P.ldo;
         if (DUAL) {
           const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
           P.out[orow + col] = v;
@@ -318,7 +363,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 // groups go round-robin and an XCD runs all passes of one group back to
 // back, so the group's weights are fetched once. Blocks past the work
 // (padding, passes the sort did not fill) exit.
-template <bool DUAL>
+template <bool DUAL, bool MLX>
 __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
   int b = blockIdx.x;
@@ -366,17 +411,17 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   const bool exact = __builtin_amdgcn_readfirstlane(*a.f16_flag & a.flag_in) != 0;
   if (exact) {
     switch ((rows + 15) / 16) {
-      case 1: pf_item<DUAL, 1, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      case 2: pf_item<DUAL, 2, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      case 3: pf_item<DUAL, 3, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      default: pf_item<DUAL, 4, false>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 1: pf_item<DUAL, 1, false, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, false, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, false, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, false, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
     }
   } else {
     switch ((rows + 15) / 16) {
-      case 1: pf_item<DUAL, 1, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      case 2: pf_item<DUAL, 2, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      case 3: pf_item<DUAL, 3, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
-      default: pf_item<DUAL, 4, true>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 1: pf_item<DUAL, 1, true, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 2: pf_item<DUAL, 2, true, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      case 3: pf_item<DUAL, 3, true, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
+      default: pf_item<DUAL, 4, true, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
     }
   }
 }
@@ -402,10 +447,15 @@ hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream) {
   // K slices only for static single-matrix sets with fp32 outputs
   for (const PfSet* s : {&a.s0, &a.s1})
     if (s->ksplit > 1 && (dual || s->pass_n || !s->out32 || s->ksplit > s->nu)) return hipErrorInvalidValue;
+  // MLX-layout weights: single matrices, every set with items in that layout
+  const bool mlx = (a.n_items0 ? a.s0.mw : a.s1.mw) != nullptr;
+  if (mlx && (dual || (a.n_items0 && !a.s0.mw) || (a.n_items1 && !a.s1.mw))) return hipErrorInvalidValue;
   if (dual)
-    hipLaunchKernelGGL(pf_gemm<true>, dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
+    hipLaunchKernelGGL((pf_gemm<true, false>), dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
+  else if (mlx)
+    hipLaunchKernelGGL((pf_gemm<false, true>), dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
   else
-    hipLaunchKernelGGL(pf_gemm<false>, dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
+    hipLaunchKernelGGL((pf_gemm<false, false>), dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
   return hipGetLastError();
 }
 

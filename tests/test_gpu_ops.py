@@ -4,7 +4,7 @@ tolerance), router top-k and the expert sort (bit-exact)."""
 import numpy as np
 import pytest
 
-from helpers import (assert_close, bf16_to_f32, from_dev_bf16, from_dev_u32, to_dev,
+from helpers import (assert_close, assert_close_rows, bf16_to_f32, from_dev_bf16, from_dev_u32, to_dev,
                      to_dev_u32)
 
 pytestmark = pytest.mark.gpu
@@ -40,8 +40,13 @@ def test_dequantize_matches_oracle(gpu, fmx, oracle):
     np.testing.assert_array_equal(from_dev_bf16(out), ref)
 
 
+# up to 16 rows, and shapes outside whole 128-k units or 16-row tiles, run
+# the grouped GEMM (exact dequantisation); more rows run the prefill GEMM on
+# the MLX-layout weights (fp16 weights, within 2^-11 relative of exact)
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (3, 200, 1408), (16, 128, 2048),
-                                   (37, 96, 768), (5, 2048, 5632)])
+                                   (37, 96, 768), (5, 2048, 5632), (17, 16, 128),
+                                   (64, 256, 1024), (200, 512, 2048), (40, 200, 1408),
+                                   (33, 64, 1344)])
 def test_quantized_matmul(gpu, fmx, oracle, M, N, K):
     rng = np.random.default_rng(M * 1000 + N + K)
     x = _rand_bf16(rng, (M, K))
@@ -51,11 +56,32 @@ def test_quantized_matmul(gpu, fmx, oracle, M, N, K):
     got = from_dev_bf16(out)
     ref = oracle.qmm_t(x, rq, rs, rb, oracle.ACC_A)
     e = assert_close(got, ref, f"qmm M={M} N={N} K={K}")
-    # also against the exact (fp64) value: the GPU dequantises exactly
+    # also against the exact (fp64) value
     ref64 = oracle.qmm_t(x, rq, rs, rb, oracle.ACC_F64)
     e64 = assert_close(got, ref64, "qmm vs fp64")
     assert e64["max_abs"] <= 2 * np.abs(bf16_to_f32(ref64)).max() * 2 ** -8 + 1e-6, e64
     print(f"qmm M={M} N={N} K={K}: vs A {e}, vs f64 {e64}")
+
+
+def test_quantized_matmul_prefill_fp16_overflow(gpu, fmx, oracle):
+    """Rows holding values outside fp16's range take the exact bf16 path of
+    the prefill GEMM (the copy kernel's flag); a second call on rows that fit
+    takes the fp16 path again (the flag is cleared per call)."""
+    rng = np.random.default_rng(23)
+    M, N, K = 48, 128, 512
+    w = _rand_bf16(rng, (N, K), 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    x = _rand_bf16(rng, (M, K))
+    big = x.copy()
+    big[5, 17] = oracle.f32_to_bf16_array(np.array([1.0e5], np.float32))[0]
+    big[40, 300] = oracle.f32_to_bf16_array(np.array([-7.0e4], np.float32))[0]
+    # a row with a 1e5 element sums products up to ~5000 (fp32 ulp 2^-11
+    # there) whose group sums cancel, so its elements are held to the row's
+    # scale: two bf16 ulps of the row's largest output (assert_close_rows)
+    for xi, what, check in ((big, "overflow rows", assert_close_rows), (x, "fp16 rows", assert_close)):
+        out = fmx.quantized_matmul(to_dev(xi), to_dev_u32(rq), to_dev(rs), to_dev(rb))
+        ref = oracle.qmm_t(xi, rq, rs, rb, oracle.ACC_A)
+        check(from_dev_bf16(out), ref, f"qmm {what}")
 
 
 def test_quantized_matmul_batch_dims(gpu, fmx, oracle):
@@ -117,6 +143,25 @@ def test_gather_qmm_broadcast_and_m_rows(gpu, fmx, oracle):
     R = np.broadcast_to(rhs, (2, 3)).reshape(-1)
     ref = oracle.gather_qmm(x, rq, rs, rb, L, R, oracle.ACC_A)
     assert_close(from_dev_bf16(out).reshape(6, M, N), ref, "gather broadcast")
+
+
+@pytest.mark.parametrize("T,k,E,N,K", [(75, 4, 16, 256, 1024), (300, 2, 8, 128, 512)])
+def test_gather_qmm_prefill_unsorted(gpu, fmx, oracle, T, k, E, N, K):
+    """switch_mlp's prefill call (model.cpp:681, :703) at prefill sizes: the
+    rows sorted by expert into passes of the prefill GEMM and scattered back
+    to their (token, slot) output rows; a skewed expert choice leaves
+    experts with no rows and others with several passes."""
+    rng = np.random.default_rng(T * k + E)
+    x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, T, 1)
+    p = np.exp(-np.arange(E) / (E / 4.0))
+    p /= p.sum()
+    inds = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.uint32)
+    out = fmx.gather_qmm(to_dev(x.reshape(T, 1, 1, K)), to_dev_u32(rq), to_dev(rs), to_dev(rb),
+                         rhs_indices=to_dev_u32(inds))
+    assert tuple(out.shape) == (T, k, 1, N)
+    lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
+    ref = oracle.gather_qmm(x, rq, rs, rb, lhs, inds.reshape(-1), oracle.ACC_A)
+    assert_close(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather prefill")
 
 
 def test_gather_qmm_defaults_one_hot(gpu, fmx, oracle):
