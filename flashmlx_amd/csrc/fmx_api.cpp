@@ -391,31 +391,46 @@ int fmx_quantized_matmul_out_shape(const fmx_array* x, const fmx_array* w, int t
 
 namespace {
 
-// More than one MFMA tile of rows (16) goes to the prefill GEMM on the
-// MLX-layout weights (fmx_prefill.hip): K in whole 128-k units, N in whole
-// 16-row tiles; fewer rows, and other shapes, to the grouped GEMM
-// (fmx_qgemm.hip).
-bool op_uses_pf(int64_t rows, int64_t N, int64_t K) {
-  return rows > 16 && rows <= (1 << 20) && N % 16 == 0 && K % 128 == 0;
+// Calls the standalone ops send to the prefill GEMM on the MLX-layout
+// weights (fmx_prefill.hip): K in whole 128-k units, N in whole 16-row
+// tiles, and at least min_rows rows; other calls go to the grouped GEMM
+// (fmx_qgemm.hip), which reads x as it is. Measured at Qwen1.5-MoE shapes
+// (K 2048): gather_qmm's passes are faster from 17 rows on (8 tokens x
+// top-4: 28 against 40 us; 512 x 4: 65 against 360 us), quantized_matmul's
+// from 32 rows (17-24 rows: 18.8 against 16.1-17.7 us).
+constexpr int64_t kQmmPfMinRows = 32;
+constexpr int64_t kGatherPfMinRows = 17;
+bool op_uses_pf(int64_t rows, int64_t N, int64_t K, int64_t min_rows) {
+  return rows >= min_rows && rows <= (1 << 20) && N % 16 == 0 && K % 128 == 0;
 }
 
-// the prefill GEMM's share of an op's workspace: the fp16 (Q8) copy of the
-// rows beside the bf16 (P8) one, and the overflow flag word
-void take_pf_rows(Arena& ar, int64_t x_rows, int64_t K, uint16_t** xq, uint32_t** flag) {
-  *xq = static_cast<uint16_t*>(ar.take(x_rows * K * 2));
-  *flag = static_cast<uint32_t*>(ar.take(4));
+// The prefill GEMM's operand copies of x_rows rows (bf16 P8, fp16 Q8) and
+// the copy blocks' overflow words.
+struct PfRows {
+  uint16_t* xp;
+  uint16_t* xq;
+  uint32_t* ovf;
+  int n_ovf;
+};
+PfRows take_pf_rows(Arena& ar, int64_t x_rows, int64_t K) {
+  PfRows r;
+  r.xp = static_cast<uint16_t*>(ar.take(x_rows * K * 2));
+  r.xq = static_cast<uint16_t*>(ar.take(x_rows * K * 2));
+  r.n_ovf = ops_prologue_ovf_words(x_rows * (K / 8));
+  r.ovf = static_cast<uint32_t*>(ar.take(static_cast<int64_t>(r.n_ovf) * 4));
+  return r;
 }
 
 // One set of the prefill GEMM over MLX-layout weights [n_exp][N][K/8]
 // (scales / biases [n_exp][N][K/64]), output rows of N bf16.
-PfSet mlx_set(const fmx_array* w, const fmx_array* scales, const fmx_array* biases,
-              const uint16_t* xp, const uint16_t* xq, int64_t K, int64_t N, uint16_t* out) {
+PfSet mlx_set(const fmx_array* w, const fmx_array* scales, const fmx_array* biases, const PfRows& xr,
+              int64_t K, int64_t N, uint16_t* out) {
   PfSet s{};
   s.mw = static_cast<const uint32_t*>(w->data);
   s.ms = static_cast<const uint16_t*>(scales->data);
   s.mb = static_cast<const uint16_t*>(biases->data);
-  s.x = xp;
-  s.xh = xq;
+  s.x = xr.xp;
+  s.xh = xr.xq;
   s.ldx = K;
   s.out = out;
   s.ldo = N;
@@ -425,11 +440,12 @@ PfSet mlx_set(const fmx_array* w, const fmx_array* scales, const fmx_array* bias
   return s;
 }
 
-hipError_t launch_mlx_pf(PfSet& s, uint32_t* flag, hipStream_t stream) {
+hipError_t launch_mlx_pf(const PfSet& s, const PfRows& xr, hipStream_t stream) {
   PfArgs pa{};
   pa.s1 = s;
   pa.n_items1 = pf_items(pa.s1, false);
-  pa.f16_flag = flag;
+  pa.f16_flag = xr.ovf;
+  pa.n_flag = xr.n_ovf;
   pa.flag_in = 1u;
   pa.flag_out = 0u;
   return launch_pf(pa, false, stream);
@@ -442,12 +458,7 @@ size_t fmx_quantized_matmul_workspace_size(const fmx_array* x, const fmx_array* 
   const int64_t K = x->shape[x->ndim - 1];
   const int64_t rows = K ? numel(*x) / K : 0;
   Arena ar;
-  ar.take(rows * K * 2);  // rows in the P8 layout
-  if (w && w->ndim == 2 && op_uses_pf(rows, w->shape[0], K)) {
-    uint16_t* xq;
-    uint32_t* flag;
-    take_pf_rows(ar, rows, K, &xq, &flag);
-  }
+  if (w && w->ndim == 2 && op_uses_pf(rows, w->shape[0], K, kQmmPfMinRows)) take_pf_rows(ar, rows, K);
   return ar.used;
 }
 
@@ -484,21 +495,23 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
   if ((rc = bind_workspace(ar, workspace, workspace_bytes,
                            fmx_quantized_matmul_workspace_size(x, w), stream)))
     return rc;
-  uint16_t* xp = static_cast<uint16_t*>(ar.take(rows * K * 2));
-  if (op_uses_pf(rows, N, K)) {
-    uint16_t* xq;
-    uint32_t* flag;
-    take_pf_rows(ar, rows, K, &xq, &flag);
-    FMX_HIP(launch_fill_u32(flag, 1, 0u, stream));
-    FMX_HIP(launch_mlx_rows(static_cast<const uint16_t*>(x->data), rows, K, xp, xq, flag, 1u, stream));
-    PfSet s = mlx_set(w, scales, biases, xp, xq, K, N, static_cast<uint16_t*>(out->data));
+  if (op_uses_pf(rows, N, K, kQmmPfMinRows)) {
+    const PfRows xr = take_pf_rows(ar, rows, K);
+    OpsPrologue pro{};
+    pro.x = static_cast<const uint16_t*>(x->data);
+    pro.n_oct = rows * (K / 8);
+    pro.xp = xr.xp;
+    pro.xq = xr.xq;
+    pro.ovf = xr.ovf;
+    FMX_HIP(launch_ops_prologue(pro, stream));
+    PfSet s = mlx_set(w, scales, biases, xr, K, N, static_cast<uint16_t*>(out->data));
     s.rows_static = s.rows_max = s.x_rows = static_cast<int>(rows);
-    FMX_HIP(launch_mlx_pf(s, flag, stream));
+    FMX_HIP(launch_mlx_pf(s, xr, stream));
     return ok();
   }
-  FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), rows, K, xp, stream));
   QGemmProblem p{};
-  p.x = xp;
+  p.x = static_cast<const uint16_t*>(x->data);
+  p.x_natural = 1;
   p.ldx = K;
   p.rows_static = static_cast<int>(rows);
   p.max_seg = 1;
@@ -575,27 +588,39 @@ void fill_bcast(const GatherPlan& p, const fmx_array* idx, const int64_t* dflt_s
   }
 }
 
-size_t gather_ws(const GatherPlan& p) {
+// gather_qmm's workspace, in the order fmx_gather_qmm takes it
+struct GatherWs {
+  uint32_t *lhs_flat, *rhs_flat, *keys, *order, *offsets, *seg_n, *seg_exp, *seg_off, *sbase, *row_map;
+  uint32_t *pass_n, *pass_tab, *flag;  // prefill GEMM only
+  PfRows xr;                           // prefill GEMM only
+};
+GatherWs take_gather_ws(Arena& ar, const GatherPlan& p, bool pf) {
   const int64_t rows = p.nb * p.M;
-  Arena ar;
-  ar.take(p.n_x * p.M * p.K * 2);      // xp
-  ar.take(p.nb * 4);                   // lhs flat
-  ar.take(p.nb * 4);                   // rhs flat
-  ar.take(rows * 4);                   // row keys
-  ar.take(rows * 4);                   // order
-  ar.take((p.E + 1) * 4);              // offsets
-  ar.take(4);                          // seg_n
-  ar.take(p.E * 4);                    // seg_exp
-  ar.take((p.E + 1) * 4);              // seg_off
-  ar.take(p.E * ((rows + 63) / 64) * 4);  // sort base
-  ar.take(rows * 4);                   // row_map
-  if (op_uses_pf(rows, p.N, p.K)) {
-    ar.take(4);                                        // pass count
-    ar.take(static_cast<int64_t>(max_passes(rows, p.E)) * 8);  // pass table
-    uint16_t* xq;
-    uint32_t* flag;
-    take_pf_rows(ar, p.n_x * p.M, p.K, &xq, &flag);
+  GatherWs g{};
+  g.lhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
+  g.rhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
+  g.keys = static_cast<uint32_t*>(ar.take(rows * 4));
+  g.order = static_cast<uint32_t*>(ar.take(rows * 4));
+  g.offsets = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
+  g.seg_n = static_cast<uint32_t*>(ar.take(4));
+  g.seg_exp = static_cast<uint32_t*>(ar.take(p.E * 4));
+  g.seg_off = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
+  g.sbase = static_cast<uint32_t*>(ar.take(p.E * ((rows + 63) / 64) * 4));
+  g.row_map = static_cast<uint32_t*>(ar.take(rows * 4));
+  if (pf) {
+    g.pass_n = static_cast<uint32_t*>(ar.take(4));
+    g.pass_tab = static_cast<uint32_t*>(ar.take(static_cast<int64_t>(max_passes(rows, p.E)) * 8));
+    g.xr = take_pf_rows(ar, p.n_x * p.M, p.K);
+    g.flag = static_cast<uint32_t*>(ar.take(4));
   }
+  return g;
+}
+
+bool gather_uses_pf(const GatherPlan& p) { return op_uses_pf(p.nb * p.M, p.N, p.K, kGatherPfMinRows); }
+
+size_t gather_ws(const GatherPlan& p) {
+  Arena ar;
+  take_gather_ws(ar, p, gather_uses_pf(p));
   return ar.used;
 }
 
@@ -674,74 +699,73 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   Arena ar;
   WsGuard guard(ar);
   if ((rc = bind_workspace(ar, workspace, workspace_bytes, gather_ws(p), stream))) return rc;
-  uint16_t* xp = static_cast<uint16_t*>(ar.take(p.n_x * p.M * p.K * 2));
-  uint32_t* lhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
-  uint32_t* rhs_flat = static_cast<uint32_t*>(ar.take(p.nb * 4));
-  uint32_t* keys = static_cast<uint32_t*>(ar.take(rows * 4));
-  uint32_t* order = static_cast<uint32_t*>(ar.take(rows * 4));
-  uint32_t* offsets = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
-  uint32_t* seg_n = static_cast<uint32_t*>(ar.take(4));
-  uint32_t* seg_exp = static_cast<uint32_t*>(ar.take(p.E * 4));
-  uint32_t* seg_off = static_cast<uint32_t*>(ar.take((p.E + 1) * 4));
-  uint32_t* sbase = static_cast<uint32_t*>(ar.take(p.E * ((rows + 63) / 64) * 4));
-  uint32_t* row_map = static_cast<uint32_t*>(ar.take(rows * 4));
-  const bool pf = op_uses_pf(rows, p.N, p.K);
-  uint32_t *pass_n = nullptr, *pass_tab = nullptr, *flag = nullptr;
-  uint16_t* xq = nullptr;
+  const bool pf = gather_uses_pf(p);
+  const GatherWs g = take_gather_ws(ar, p, pf);
+
+  // one launch: both index broadcasts (rhs also as per-row sort keys) and,
+  // for the prefill GEMM, the operand copies of x
+  OpsPrologue pro{};
+  fill_bcast(p, lhs, x->shape, x->ndim - 2, &pro.lhs);
+  pro.lhs.dst = g.lhs_flat;
+  fill_bcast(p, rhs, w->shape, w->ndim - 2, &pro.rhs);
+  pro.rhs.dst = g.rhs_flat;
+  pro.rhs.M = static_cast<int>(p.M);
+  pro.rhs.dst_rows = g.keys;
   if (pf) {
-    pass_n = static_cast<uint32_t*>(ar.take(4));
-    pass_tab = static_cast<uint32_t*>(ar.take(static_cast<int64_t>(max_passes(rows, p.E)) * 8));
-    take_pf_rows(ar, p.n_x * p.M, p.K, &xq, &flag);
-    FMX_HIP(launch_fill_u32(flag, 1, 0u, stream));
-    FMX_HIP(launch_mlx_rows(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, xq, flag, 1u,
-                            stream));
-  } else {
-    FMX_HIP(launch_permute_p8(static_cast<const uint16_t*>(x->data), p.n_x * p.M, p.K, xp, stream));
+    pro.x = static_cast<const uint16_t*>(x->data);
+    pro.n_oct = p.n_x * p.M * (p.K / 8);
+    pro.xp = g.xr.xp;
+    pro.xq = g.xr.xq;
+    pro.ovf = g.xr.ovf;
   }
-  BcastArgs bl{}, br{};
-  fill_bcast(p, lhs, x->shape, x->ndim - 2, &bl);
-  bl.dst = lhs_flat;
-  fill_bcast(p, rhs, w->shape, w->ndim - 2, &br);
-  br.dst = rhs_flat;
-  br.M = static_cast<int>(p.M);
-  br.dst_rows = keys;
-  FMX_HIP(launch_bcast_indices(bl, stream));
-  FMX_HIP(launch_bcast_indices(br, stream));
+  FMX_HIP(launch_ops_prologue(pro, stream));
   SortOut so{};
-  so.order = order;
-  so.offsets = offsets;
-  so.seg_n = seg_n;
-  so.seg_exp = seg_exp;
-  so.seg_off = seg_off;
-  so.base = sbase;
-  so.pass_n = pass_n;
-  so.pass_tab = pass_tab;
-  FMX_HIP(launch_sort(keys, static_cast<int>(rows), 1, static_cast<int>(p.E), so, stream));
-  FMX_HIP(launch_gather_maps(order, lhs_flat, rows, static_cast<int>(p.M), p.n_x, row_map, stream));
+  so.order = g.order;
+  so.offsets = g.offsets;
+  so.seg_n = g.seg_n;
+  so.seg_exp = g.seg_exp;
+  so.seg_off = g.seg_off;
+  so.base = g.sbase;
+  so.pass_n = g.pass_n;
+  so.pass_tab = g.pass_tab;
+  // sorted row r is entry order[r] = b * M + m: it reads x row
+  // row_map[r] = lhs[b] * M + m and writes output row order[r]
+  so.row_map = g.row_map;
+  so.row_lhs = g.lhs_flat;
+  so.row_m = static_cast<int>(p.M);
+  so.x_rows = static_cast<int>(p.n_x * p.M);
+  if (pf) {  // one overflow word for the GEMM from the copy blocks' words
+    so.ovf = g.xr.ovf;
+    so.n_ovf = g.xr.n_ovf;
+    so.flag = g.flag;
+  }
+  FMX_HIP(launch_sort(g.keys, static_cast<int>(rows), 1, static_cast<int>(p.E), so, stream));
+
   if (pf) {
-    // passes of at most 64 sorted rows of one expert; pass row r reads x row
-    // row_map[r] and writes output row order[r]
-    PfSet s = mlx_set(w, scales, biases, xp, xq, p.K, p.N, static_cast<uint16_t*>(out->data));
-    s.row_map = row_map;
-    s.out_map = order;
-    s.pass_n = pass_n;
-    s.pass_tab = pass_tab;
+    PfSet s = mlx_set(w, scales, biases, g.xr, p.K, p.N, static_cast<uint16_t*>(out->data));
+    s.row_map = g.row_map;
+    s.out_map = g.order;
+    s.pass_n = g.pass_n;
+    s.pass_tab = g.pass_tab;
     s.max_pass = max_passes(rows, p.E);
     s.n_exp = static_cast<int>(p.E);
     s.rows_max = static_cast<int>(rows);
     s.x_rows = static_cast<int>(p.n_x * p.M);
-    FMX_HIP(launch_mlx_pf(s, flag, stream));
+    PfRows one = g.xr;
+    one.ovf = g.flag;
+    one.n_ovf = 1;
+    FMX_HIP(launch_mlx_pf(s, one, stream));
     return ok();
   }
-
   QGemmProblem q{};
-  q.x = xp;
+  q.x = static_cast<const uint16_t*>(x->data);
+  q.x_natural = 1;
   q.ldx = p.K;
-  q.row_map = row_map;
-  q.out_map = order;
-  q.seg_n = seg_n;
-  q.seg_exp = seg_exp;
-  q.seg_off = seg_off;
+  q.row_map = g.row_map;
+  q.out_map = g.order;
+  q.seg_n = g.seg_n;
+  q.seg_exp = g.seg_exp;
+  q.seg_off = g.seg_off;
   q.max_seg = static_cast<int>(std::min<int64_t>(p.E, rows));
   q.w0 = static_cast<const uint32_t*>(w->data);
   q.s0 = static_cast<const uint16_t*>(scales->data);

@@ -1,6 +1,8 @@
 // fmx_elem.hip -- small kernels around the GEMMs: the top-k weighted
 // combine with the gated shared expert, layout permutations, index
 // broadcasting for gather_qmm, and the affine quantizer.
+#include <algorithm>
+
 #include "fmx_dev.hpp"
 
 namespace fmx {
@@ -150,36 +152,6 @@ hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_
   return hipGetLastError();
 }
 
-// rows for the prefill GEMM on MLX-layout weights: a bf16 copy in the P8
-// layout (the exact path) and an fp16 copy in the Q8 layout; a value
-// outside fp16's range ORs bit into *flag
-__global__ __launch_bounds__(kElemThreads) void mlx_rows_kernel(const uint16_t* x, int64_t n_oct,
-                                                                uint16_t* xp, uint16_t* xq,
-                                                                uint32_t* flag, uint32_t bit) {
-  const int64_t o = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
-  bool ovf = false;
-  if (o < n_oct) {
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(x + o * 8);
-    u32x4_t p;
-    p[0] = (v[0] & 0xffffu) | (v[2] << 16);
-    p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
-    p[2] = (v[1] & 0xffffu) | (v[3] << 16);
-    p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
-    *reinterpret_cast<u32x4_t*>(xp + o * 8) = p;
-    *reinterpret_cast<u32x4_t*>(xq + o * 8) = bf16_chunk_to_f16_q8(v, ovf);
-  }
-  if (__ballot(ovf) && (threadIdx.x & 63) == 0) atomicOr(flag, bit);
-}
-
-hipError_t launch_mlx_rows(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp, uint16_t* xq,
-                           uint32_t* flag, uint32_t bit, hipStream_t stream) {
-  const int64_t n_oct = rows * (K / 8);
-  if (n_oct == 0) return hipSuccess;
-  hipLaunchKernelGGL(mlx_rows_kernel, dim3(grid_for(n_oct, kElemThreads)), dim3(kElemThreads), 0,
-                     stream, x, n_oct, xp, xq, flag, bit);
-  return hipGetLastError();
-}
-
 __global__ __launch_bounds__(kElemThreads) void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
   if (i < n) p[i] = v;
@@ -192,32 +164,9 @@ hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t strea
   return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ gather_qmm maps
-__global__ __launch_bounds__(kElemThreads) void gather_maps_kernel(const uint32_t* order,
-                                                                   const uint32_t* lhs,
-                                                                   int64_t rows, int M,
-                                                                   int64_t n_x,
-                                                                   uint32_t* row_map) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
-  if (r >= rows) return;
-  const uint32_t o = order[r];  // o = b*M + m
-  const uint32_t b = o / static_cast<uint32_t>(M), m = o % static_cast<uint32_t>(M);
-  uint32_t l = lhs[b];
-  if (static_cast<int64_t>(l) >= n_x) l = static_cast<uint32_t>(n_x - 1);
-  row_map[r] = l * static_cast<uint32_t>(M) + m;
-}
-
-hipError_t launch_gather_maps(const uint32_t* order, const uint32_t* lhs, int64_t rows, int M,
-                              int64_t n_x, uint32_t* row_map, hipStream_t stream) {
-  if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(gather_maps_kernel, dim3(grid_for(rows, kElemThreads)), dim3(kElemThreads),
-                     0, stream, order, lhs, rows, M, n_x, row_map);
-  return hipGetLastError();
-}
-
-__global__ __launch_bounds__(kElemThreads) void bcast_kernel(BcastArgs a) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
-  if (i >= a.n) return;
+// ------------------------------------------------------------------ gather_qmm indices
+// MLX broadcasting of one index array: entry i of the flattened batch
+__device__ inline void bcast_one(const BcastArgs& a, int64_t i) {
   uint32_t v;
   if (!a.src) {
     int64_t rem = i, off = 0;
@@ -242,10 +191,49 @@ __global__ __launch_bounds__(kElemThreads) void bcast_kernel(BcastArgs a) {
     for (int m = 0; m < a.M; ++m) a.dst_rows[i * a.M + m] = v;
 }
 
-hipError_t launch_bcast_indices(const BcastArgs& a, hipStream_t stream) {
-  if (a.n == 0) return hipSuccess;
-  hipLaunchKernelGGL(bcast_kernel, dim3(grid_for(a.n, kElemThreads)), dim3(kElemThreads), 0,
-                     stream, a);
+// ------------------------------------------------------------------ ops prologue
+// Blocks [0, n_idx) broadcast the index arrays (one entry of each per
+// thread); the n_ovf blocks after them copy x in a grid-stride loop and
+// each writes its ovf word.
+__global__ __launch_bounds__(kElemThreads) void ops_prologue_kernel(OpsPrologue a, int n_idx,
+                                                                    int n_ovf) {
+  __shared__ uint32_t s_ovf;
+  if (static_cast<int>(blockIdx.x) < n_idx) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
+    if (i < a.lhs.n) bcast_one(a.lhs, i);
+    if (i < a.rhs.n) bcast_one(a.rhs, i);
+    return;
+  }
+  const int c = blockIdx.x - n_idx;
+  if (threadIdx.x == 0) s_ovf = 0u;
+  __syncthreads();
+  bool ovf = false;
+  for (int64_t o = static_cast<int64_t>(c) * kElemThreads + threadIdx.x; o < a.n_oct;
+       o += static_cast<int64_t>(n_ovf) * kElemThreads) {
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.x + o * 8);
+    u32x4_t p;
+    p[0] = (v[0] & 0xffffu) | (v[2] << 16);
+    p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+    p[2] = (v[1] & 0xffffu) | (v[3] << 16);
+    p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+    *reinterpret_cast<u32x4_t*>(a.xp + o * 8) = p;
+    *reinterpret_cast<u32x4_t*>(a.xq + o * 8) = bf16_chunk_to_f16_q8(v, ovf);
+  }
+  if (__ballot(ovf) && (threadIdx.x & 63) == 0) atomicOr(&s_ovf, 1u);
+  __syncthreads();
+  if (threadIdx.x == 0) a.ovf[c] = s_ovf;
+}
+
+int ops_prologue_ovf_words(int64_t n_oct) {
+  return static_cast<int>(std::min<int64_t>(kOvfBlocks, (n_oct + kElemThreads - 1) / kElemThreads));
+}
+
+hipError_t launch_ops_prologue(const OpsPrologue& a, hipStream_t stream) {
+  const int n_idx = static_cast<int>(grid_for(std::max(a.lhs.n, a.rhs.n), kElemThreads));
+  const int n_ovf = ops_prologue_ovf_words(a.n_oct);
+  if (n_idx + n_ovf == 0) return hipSuccess;
+  hipLaunchKernelGGL(ops_prologue_kernel, dim3(n_idx + n_ovf), dim3(kElemThreads), 0, stream, a, n_idx,
+                     n_ovf);
   return hipGetLastError();
 }
 

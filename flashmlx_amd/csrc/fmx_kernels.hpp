@@ -23,6 +23,17 @@ struct SortOut {
   // most kPassRows rows, in segment order (both nullable)
   uint32_t* pass_n;   // [1]   number of passes
   uint32_t* pass_tab; // [max_passes(n, E)][2]: first sorted row, key | rows << 16
+  // gather_qmm (row_map nullable): sorted position -> x row of its entry
+  // o = b * row_m + m, lhs[b] * row_m + m (lhs values clamped into the
+  // x_rows / row_m batches of x)
+  uint32_t* row_map;
+  const uint32_t* row_lhs;
+  int row_m, x_rows;
+  // (flag nullable) workgroup 0 also writes *flag = the OR of the n_ovf
+  // words at ovf (a copy kernel's per-block overflow words, n_ovf <= 1024)
+  const uint32_t* ovf;
+  int n_ovf;
+  uint32_t* flag;
 };
 
 constexpr int kPassRows = 64;
@@ -129,6 +140,8 @@ struct QGemmProblem {
   // by launch_qgemm from max_rows_per_seg, the most rows a segment can hold)
   int max_rows_per_seg;
   int rows_per_pass;
+  // x rows in natural order (permuted to P8 while staged)
+  int x_natural;
 };
 // Launch one or two independent problems in one grid (p1 may be null).
 hipError_t launch_qgemm(const QGemmProblem& p0, const QGemmProblem* p1, hipStream_t stream);
@@ -252,9 +265,13 @@ struct PfArgs {
   int n_items0, n_items1;
   // f16_flag & flag_in set: an input row holds a value outside fp16's range,
   // so the grid multiplies the bf16 rows exactly; gate/up ORs flag_out into
-  // it when one of its outputs does
+  // it when one of its outputs does. n_flag > 1: the input test ORs the
+  // n_flag (at most 256, 16-byte aligned) words at f16_flag (per-block
+  // words of a copy kernel; each wave reads them all, which costs a grid
+  // of many work items more than one word does)
   uint32_t* f16_flag;
   uint32_t flag_in, flag_out;
+  int n_flag;
 };
 constexpr uint32_t kF16FlagX = 1u;  // x (gate/up input)
 constexpr uint32_t kF16FlagH = 2u;  // h (down input)
@@ -337,20 +354,9 @@ struct NhCombineArgs {
 };
 hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 
-// rows of K bf16 (natural order) -> xp: bf16 in the P8 layout, xq: fp16 in
-// the Q8 layout (fmx_dev.hpp), the two operand copies of the prefill GEMM on
-// MLX-layout weights; a value outside fp16's range ORs bit into *flag
-hipError_t launch_mlx_rows(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp, uint16_t* xq,
-                           uint32_t* flag, uint32_t bit, hipStream_t stream);
 hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
                              hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
-
-// gather_qmm row maps: for sorted row r (of nb*M rows, sorted by rhs key),
-// x row = lhs[b]*M + m where b*M + m = order[r]; lhs values >= n_x are
-// clamped to n_x - 1.
-hipError_t launch_gather_maps(const uint32_t* order, const uint32_t* lhs, int64_t rows,
-                              int M, int64_t n_x, uint32_t* row_map, hipStream_t stream);
 
 // MLX broadcasting of index arrays to the common batch shape (up to 8 dims).
 struct BcastArgs {
@@ -364,7 +370,24 @@ struct BcastArgs {
   int M;
   uint32_t* dst_rows;           // nullable
 };
-hipError_t launch_bcast_indices(const BcastArgs& a, hipStream_t stream);
+
+// The standalone ops' first launch: gather_qmm's index broadcasts (lhs, and
+// rhs with its per-row key expansion; n == 0: none) and the two operand
+// copies of the rows for the prefill GEMM on MLX-layout weights (xp: bf16 in
+// the P8 layout, xq: fp16 in the Q8 layout, fmx_dev.hpp; n_oct == 0: none).
+// Copy block c writes ovf[c] = 1 when its rows hold a value outside fp16's
+// range, else 0: every word is written on every call, none needs clearing.
+struct OpsPrologue {
+  BcastArgs lhs, rhs;
+  const uint16_t* x;
+  int64_t n_oct;  // 8-element chunks of x
+  uint16_t* xp;
+  uint16_t* xq;
+  uint32_t* ovf;  // [ops_prologue_ovf_words(n_oct)]
+};
+constexpr int kOvfBlocks = 256;  // most copy blocks (ovf words)
+int ops_prologue_ovf_words(int64_t n_oct);
+hipError_t launch_ops_prologue(const OpsPrologue& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- quantization
 hipError_t launch_quantize(const uint16_t* w, int64_t n_groups, uint32_t* wq, uint16_t* s,

@@ -325,8 +325,8 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
         const int row = 16 * mt + 4 * j + r;
         if (row >= rows) continue;
         const int64_t orow =
-            static_cast<int64_t>(P.out_map ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
-                                           : row0 + row) * P.ldo;
+            static_cast<int64_t>((MLX && P.out_map) ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
+                                                    : row0 + row) * P.ldo;
         if (DUAL) {
           const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
           P.out[orow + col] = v;
@@ -364,8 +364,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
 // back, so the group's weights are fetched once. Blocks past the work
 // (padding, passes the sort did not fill) exit.
 template <bool DUAL, bool MLX>
-__global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
+__device__ __attribute__((always_inline)) void pf_grid(const PfArgs& a, uint8_t* s_pf) {
   int b = blockIdx.x;
   const bool second = b >= a.n_items0;
   if (second) b -= a.n_items0;
@@ -408,7 +407,19 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
   // one call site per tile count and arithmetic: each inlined copy is
   // compiled on its own
   static_assert(kPfMT == 4, "row-tile dispatch below covers passes of up to 4 tiles");
-  const bool exact = __builtin_amdgcn_readfirstlane(*a.f16_flag & a.flag_in) != 0;
+  bool exact;
+  if (MLX && a.n_flag > 1) {
+    // OR of the copy kernel's per-block words (at most 4 per lane: one load)
+    const int i = 4 * (threadIdx.x & 63);
+    uint32_t v = 0;
+    if (i < a.n_flag) {
+      const u32x4_t f = *reinterpret_cast<const u32x4_t*>(a.f16_flag + i);
+      v = f[0] | (i + 1 < a.n_flag ? f[1] : 0u) | (i + 2 < a.n_flag ? f[2] : 0u) | (i + 3 < a.n_flag ? f[3] : 0u);
+    }
+    exact = __ballot((v & a.flag_in) != 0) != 0;
+  } else {
+    exact = __builtin_amdgcn_readfirstlane(*a.f16_flag & a.flag_in) != 0;
+  }
   if (exact) {
     switch ((rows + 15) / 16) {
       case 1: pf_item<DUAL, 1, false, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
@@ -424,6 +435,19 @@ __global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
       default: pf_item<DUAL, 4, true, MLX>(P, ng, row0, rows, e, ks, s_pf, a.f16_flag, a.flag_out); break;
     }
   }
+}
+
+template <bool DUAL>
+__global__ __launch_bounds__(kPfThreads) void pf_gemm(PfArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
+  pf_grid<DUAL, false>(a, s_pf);
+}
+
+// MLX-layout weights: the lane's word reads and row-map scatter take a few
+// registers more, which would leave two waves per SIMD; held to three
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(3))) void pf_gemm_mlx(PfArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_pf[];
+  pf_grid<false, true>(a, s_pf);
 }
 
 }  // namespace
@@ -447,15 +471,18 @@ hipError_t launch_pf(const PfArgs& a, bool dual, hipStream_t stream) {
   // K slices only for static single-matrix sets with fp32 outputs
   for (const PfSet* s : {&a.s0, &a.s1})
     if (s->ksplit > 1 && (dual || s->pass_n || !s->out32 || s->ksplit > s->nu)) return hipErrorInvalidValue;
+  // per-block flag words: at most 4 per lane, 16-byte aligned
+  if (a.n_flag > 4 * kWave || (a.n_flag > 1 && (reinterpret_cast<uintptr_t>(a.f16_flag) & 15)))
+    return hipErrorInvalidValue;
   // MLX-layout weights: single matrices, every set with items in that layout
   const bool mlx = (a.n_items0 ? a.s0.mw : a.s1.mw) != nullptr;
   if (mlx && (dual || (a.n_items0 && !a.s0.mw) || (a.n_items1 && !a.s1.mw))) return hipErrorInvalidValue;
   if (dual)
-    hipLaunchKernelGGL((pf_gemm<true, false>), dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
+    hipLaunchKernelGGL(pf_gemm<true>, dim3(n), dim3(kPfThreads), pf_lds_bytes(true), stream, a);
   else if (mlx)
-    hipLaunchKernelGGL((pf_gemm<false, true>), dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
+    hipLaunchKernelGGL(pf_gemm_mlx, dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
   else
-    hipLaunchKernelGGL((pf_gemm<false, false>), dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
+    hipLaunchKernelGGL(pf_gemm<false>, dim3(n), dim3(kPfThreads), pf_lds_bytes(false), stream, a);
   return hipGetLastError();
 }
 

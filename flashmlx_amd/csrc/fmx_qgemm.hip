@@ -186,7 +186,14 @@ __device__ void qgemm_tile(const QGemmProblem& P, int seg, int nt, int ks, uint1
         const int64_t xrow = P.row_map
             ? static_cast<int64_t>(min(P.row_map[mb + rr], static_cast<uint32_t>(P.x_rows - 1)))
             : mb + rr;
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(P.x + xrow * P.ldx + kb * 128 + pc * 8);
+        u32x4_t v = *reinterpret_cast<const u32x4_t*>(P.x + xrow * P.ldx + kb * 128 + pc * 8);
+        if (P.x_natural) {  // natural order -> P8 (elements 0,4,1,5,2,6,3,7)
+          const u32x4_t n = v;
+          v[0] = (n[0] & 0xffffu) | (n[2] << 16);
+          v[1] = (n[0] >> 16) | (n[2] & 0xffff0000u);
+          v[2] = (n[1] & 0xffffu) | (n[3] << 16);
+          v[3] = (n[1] >> 16) | (n[3] & 0xffff0000u);
+        }
         *reinterpret_cast<u32x4_t*>(s_x + rr * xs + pc * 8) = v;
       }
     }

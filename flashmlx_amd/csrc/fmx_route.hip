@@ -63,6 +63,10 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
     s_mine[2] = u;
     s_mine[3] = p;
   }
+  if (e == 0 && o.flag) {
+    const int any = __syncthreads_or(tid < o.n_ovf ? static_cast<int>(o.ovf[tid] != 0u) : 0);
+    if (tid == 0) *o.flag = any ? 1u : 0u;
+  }
   if (e == 0) {
     if (tid < E) o.offsets[tid] = off;
     if (tid == 0) {
@@ -106,6 +110,11 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
     if (match) {
       const uint32_t pos = run + before + static_cast<uint32_t>(__popcll(b & lanes_below(lane)));
       if (o.order) o.order[pos] = static_cast<uint32_t>(i);
+      if (o.row_map) {
+        const uint32_t m = static_cast<uint32_t>(o.row_m), ui = static_cast<uint32_t>(i);
+        const uint32_t l = min(o.row_lhs[ui / m], static_cast<uint32_t>(o.x_rows / o.row_m - 1));
+        o.row_map[pos] = l * m + ui % m;
+      }
       if (o.inv) o.inv[i] = pos;
       if (o.src) o.src[pos] = static_cast<uint32_t>(i / k);
       if (o.idx) o.idx[pos] = static_cast<uint32_t>(e);
@@ -117,6 +126,8 @@ __global__ __launch_bounds__(kSortThreads) void sort_kernel(const uint32_t* keys
 
 hipError_t launch_sort(const uint32_t* keys, int n, int k, int E, const SortOut& o,
                        hipStream_t stream) {
+  if (o.row_map && (!o.row_lhs || o.row_m < 1 || o.x_rows < o.row_m)) return hipErrorInvalidValue;
+  if (o.flag && (!o.ovf || o.n_ovf > kSortThreads)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(sort_kernel, dim3(E), dim3(kSortThreads), 0, stream, keys, n, k, E, o);
   return hipGetLastError();
 }

@@ -40,9 +40,10 @@ def test_dequantize_matches_oracle(gpu, fmx, oracle):
     np.testing.assert_array_equal(from_dev_bf16(out), ref)
 
 
-# up to 16 rows, and shapes outside whole 128-k units or 16-row tiles, run
-# the grouped GEMM (exact dequantisation); more rows run the prefill GEMM on
-# the MLX-layout weights (fp16 weights, within 2^-11 relative of exact)
+# fewer than 32 rows, and shapes outside whole 128-k units or 16-row tiles,
+# run the grouped GEMM (exact dequantisation); more rows run the prefill
+# GEMM on the MLX-layout weights (fp16 weights, within 2^-11 relative of
+# exact)
 @pytest.mark.parametrize("M,N,K", [(1, 64, 256), (3, 200, 1408), (16, 128, 2048),
                                    (37, 96, 768), (5, 2048, 5632), (17, 16, 128),
                                    (64, 256, 1024), (200, 512, 2048), (40, 200, 1408),
@@ -129,9 +130,12 @@ def test_gather_qmm_sorted_layout(gpu, fmx, oracle):
     assert_close(from_dev_bf16(out), ref, "gather sorted")
 
 
-def test_gather_qmm_broadcast_and_m_rows(gpu, fmx, oracle):
+# 12 rows (grouped GEMM) and 18 rows (prefill GEMM): x rows found through
+# the broadcast lhs and the row within M on both
+@pytest.mark.parametrize("M", [2, 3])
+def test_gather_qmm_broadcast_and_m_rows(gpu, fmx, oracle, M):
     rng = np.random.default_rng(13)
-    E, N, K, n_x, M = 5, 64, 256, 4, 3
+    E, N, K, n_x = 5, 64, 256, 4
     x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, n_x, M)
     lhs = np.array([[3], [0]], dtype=np.int32)          # [2,1]
     rhs = np.array([[4, 1, 1]], dtype=np.uint32)         # [1,3]
@@ -145,14 +149,20 @@ def test_gather_qmm_broadcast_and_m_rows(gpu, fmx, oracle):
     assert_close(from_dev_bf16(out).reshape(6, M, N), ref, "gather broadcast")
 
 
-@pytest.mark.parametrize("T,k,E,N,K", [(75, 4, 16, 256, 1024), (300, 2, 8, 128, 512)])
-def test_gather_qmm_prefill_unsorted(gpu, fmx, oracle, T, k, E, N, K):
+@pytest.mark.parametrize("T,k,E,N,K,big", [(75, 4, 16, 256, 1024, False), (300, 2, 8, 128, 512, False),
+                                           (40, 4, 8, 128, 512, True)])
+def test_gather_qmm_prefill_unsorted(gpu, fmx, oracle, T, k, E, N, K, big):
     """switch_mlp's prefill call (model.cpp:681, :703) at prefill sizes: the
     rows sorted by expert into passes of the prefill GEMM and scattered back
     to their (token, slot) output rows; a skewed expert choice leaves
-    experts with no rows and others with several passes."""
+    experts with no rows and others with several passes. big: one token's
+    row scaled by 2^17 (values beyond fp16's range: the exact path), checked
+    to two bf16 ulps of each output row's largest value."""
     rng = np.random.default_rng(T * k + E)
     x, rq, rs, rb = _gather_case(rng, oracle, E, N, K, T, 1)
+    if big:
+        row = bf16_to_f32(x[7]) * np.float32(2.0 ** 17)
+        x[7] = oracle.f32_to_bf16_array(row)
     p = np.exp(-np.arange(E) / (E / 4.0))
     p /= p.sum()
     inds = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.uint32)
@@ -161,7 +171,8 @@ def test_gather_qmm_prefill_unsorted(gpu, fmx, oracle, T, k, E, N, K):
     assert tuple(out.shape) == (T, k, 1, N)
     lhs = np.repeat(np.arange(T, dtype=np.uint32), k)
     ref = oracle.gather_qmm(x, rq, rs, rb, lhs, inds.reshape(-1), oracle.ACC_A)
-    assert_close(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather prefill")
+    check = assert_close_rows if big else assert_close
+    check(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather prefill")
 
 
 def test_gather_qmm_defaults_one_hot(gpu, fmx, oracle):
