@@ -178,6 +178,8 @@ _SIGS = {
     "fmx_moe_forward_path": (C.c_int, [P(FmxMoEConfig), C.c_int64, C.c_int]),
     "fmx_moe_workspace_size": (C.c_size_t, [P(FmxMoEConfig), C.c_int64]),
     "fmx_moe_workspace_init": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p]),
+    "fmx_moe_workspace_status": (C.c_int, [C.c_void_p, C.c_size_t, P(C.c_uint32), C.c_int, C.c_void_p]),
+    "fmx_set_decode_wait_limit": (C.c_int64, [C.c_int64]),
     "fmx_moe_block_forward": (
         C.c_int,
         [P(FmxMoEConfig), P(FmxMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
@@ -280,6 +282,8 @@ _SIGS = {
     "fmx_nh_moe_workspace_routing": (
         C.c_int, [P(FmxNhMoEConfig), C.c_int64, C.c_void_p, P(C.c_void_p), P(C.c_void_p), P(C.c_void_p)]),
 }
+
+FMX_STATUS_WAIT_TIMEOUT = 1
 
 EXPORTED = tuple(_SIGS)
 

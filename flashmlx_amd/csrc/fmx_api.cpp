@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -140,7 +141,13 @@ constexpr int kSharedDownSplit = kDecSdSplit;
 constexpr size_t kRouterCounterWords = kMoEMaxTokens / kRouterTok + 64;
 constexpr size_t kCbCounterWords = static_cast<size_t>(kDecMaxColBlocks) * kDecCbStride;
 constexpr size_t kGuCounterWords = static_cast<size_t>(kDecMaxE) * kDecGuWords;
-constexpr size_t kCounterBytes = (kRouterCounterWords + kCbCounterWords + kGuCounterWords) * sizeof(uint32_t);
+// then the status word, on a line of its own
+constexpr size_t kStatusWords = 64;
+constexpr size_t kStatusOffsetWords = kRouterCounterWords + kCbCounterWords + kGuCounterWords;
+constexpr size_t kCounterBytes = (kStatusOffsetWords + kStatusWords) * sizeof(uint32_t);
+
+// bound of the decode down workgroups' wait (fmx_set_decode_wait_limit)
+std::atomic<int> g_wait_polls{kDecWaitPolls};
 
 struct MoELayout {
   uint32_t* counters;
@@ -920,6 +927,24 @@ int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream s
   return ok();
 }
 
+int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
+                             int clear, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  if (!workspace || !status) return fail(FMX_ERR_ARG, "workspace or status is NULL");
+  if (workspace_bytes < kCounterBytes)
+    return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, kCounterBytes);
+  uint32_t* word = static_cast<uint32_t*>(const_cast<void*>(workspace)) + kStatusOffsetWords;
+  FMX_HIP(hipStreamSynchronize(stream));
+  FMX_HIP(hipMemcpy(status, word, 4, hipMemcpyDeviceToHost));
+  if (clear) FMX_HIP(launch_fill_u32(word, 1, 0u, stream));
+  return ok();
+}
+
+int64_t fmx_set_decode_wait_limit(int64_t polls) {
+  const int v = static_cast<int>(std::max<int64_t>(std::min<int64_t>(polls, INT32_MAX), 0));
+  return g_wait_polls.exchange(polls < 0 ? kDecWaitPolls : v);
+}
+
 int fmx_moe_workspace_routing(const fmx_moe_config* cfg, int64_t n_tokens, const void* workspace,
                               const uint32_t** inds, const void** scores, const void** probs,
                               const uint32_t** order, const uint32_t** inv,
@@ -1129,6 +1154,8 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.counter = L.counters;
     da.cb_counter = L.counters + kRouterCounterWords;
     da.gu_counter = L.counters + kRouterCounterWords + kCbCounterWords;
+    da.status = L.counters + kStatusOffsetWords;
+    da.wait_polls = g_wait_polls.load(std::memory_order_relaxed);
     da.y = static_cast<uint16_t*>(y);
     if (decode_plan(da)) {
       FMX_HIP(mark(0));

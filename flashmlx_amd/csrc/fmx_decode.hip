@@ -576,12 +576,12 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
 // one copy of its expert's done flag, then every wave issues its weight
 // loads (they do not depend on h); loads complete in order, so the flag's
 // value is in while the weights are still in flight. Until the flag is set,
-// wave 0 polls it (s_sleep between reads, at most kDecWaitPolls reads: far
-// beyond any real wait, a guard against a hang) while the other waves wait at
-// a barrier. Then every wave fetches its h rows with device-scope DMA. A
-// wait that ran out stores NaN products, so that the failure shows in y
-// instead of stale rows passing for results.
-constexpr int kDecWaitPolls = 1 << 21;
+// wave 0 polls it (s_sleep between reads, at most a.wait_polls reads, by
+// default kDecWaitPolls: far beyond any real wait, a guard against a hang)
+// while the other waves wait at a barrier. Then every wave fetches its h rows
+// with device-scope DMA. A wait that ran out stores NaN products, so that the
+// failure shows in y instead of stale rows passing for results, and sets
+// kStatusWaitTimeout in the workspace's status word.
 
 template <int NU, int TPW>
 __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s_a) {
@@ -621,12 +621,15 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
     for (int d = 0; d < PER; ++d) L[c * PER + d] = pk_load<false>(tb[c] + min(d, nu - 1) * kBlockSingle, lane);
   __builtin_amdgcn_sched_barrier(0);
   if (wave == 0) {
-    done = __builtin_amdgcn_readfirstlane(done);
-    for (int poll = 1; done == 0 && poll < kDecWaitPolls; ++poll) {
+    done = a.wait_polls > 0 ? __builtin_amdgcn_readfirstlane(done) : 0u;
+    for (int poll = 1; done == 0 && poll < a.wait_polls; ++poll) {
       __builtin_amdgcn_s_sleep(16);
       done = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     }
-    if (lane == 0) s_timed_out = done == 0;
+    if (lane == 0) {
+      s_timed_out = done == 0;
+      if (done == 0) atomicOr(a.status, kStatusWaitTimeout);
+    }
     wait_lgkmcnt0();  // the LDS write lands before the barrier (the weights stay in flight)
   }
   lds_dma_barrier();  // wave 0 has seen the flag (no wait for the weights in flight)

@@ -199,11 +199,20 @@ struct DecodeArgs {
   uint32_t* gu_counter;     // [max_seg][kDecGuWords] K23: gate/up tiles finished per routed expert
                             //   and their done flags; K1 zeroes them for every forward
   uint16_t* y;              // [T, H] bf16
+  // status word (sticky: set bits stay until the caller clears them):
+  // kStatusWaitTimeout when a down workgroup's bounded wait for its expert's
+  // gate/up tiles ran out (its products are then NaN)
+  uint32_t* status;
+  int wait_polls;           // the wait's bound in flag reads; <= 0 gives up at once
   // launch shape (decode_plan)
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
   int max_seg, gu_tiles;    // K2: expert slots x gate/up tile pairs
   int k2_pairs, gu_wgs;     // K2: tile pairs per workgroup, workgroups per expert slot
 };
+constexpr uint32_t kStatusWaitTimeout = 1u;
+// default bound of the down workgroups' wait (flag reads, s_sleep 16 apart):
+// far beyond any real wait, a guard against a hang
+constexpr int kDecWaitPolls = 1 << 21;
 // Fills the launch shape; false when the shapes are outside the decode path.
 bool decode_plan(DecodeArgs& a);
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream);

@@ -362,6 +362,15 @@ class MoEBlock:
         self.forward_into(x, y)
         return y
 
+    def status(self, clear: bool = False) -> int:
+        """The workspace's status word after the queued forwards end (0, or
+        _lib.FMX_STATUS_WAIT_TIMEOUT when a decode forward's bounded wait
+        ran out and its products were written as NaN); clear resets it."""
+        st = C.c_uint32()
+        _lib.check(self.lib.fmx_moe_workspace_status(self.workspace.data_ptr(), self.ws_bytes,
+                                                     C.byref(st), int(clear), _stream()))
+        return st.value
+
     def routing(self) -> dict:
         """Views of the last forward's routing state inside the workspace."""
         T = self._last_T

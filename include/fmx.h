@@ -229,10 +229,28 @@ int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t n_tokens, int has_pa
  * tokens. */
 size_t fmx_moe_workspace_size(const fmx_moe_config* cfg, int64_t max_tokens);
 
-/* Prepares a fresh workspace: clears the completion counters kept in its
- * first bytes. Call once after allocating; every forward leaves them
- * cleared again, so a workspace is reusable across calls and sizes. */
+/* Prepares a fresh workspace: clears the completion counters and the
+ * status word kept in its first bytes. Call once after allocating; every
+ * forward leaves the counters cleared again, so a workspace is reusable
+ * across calls and sizes. */
 int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream stream);
+
+/* The workspace's status word, after the forwards queued on `stream` end
+ * (synchronises the stream): 0, or FMX_STATUS_WAIT_TIMEOUT when a decode
+ * forward's bounded wait (a down workgroup waiting for its expert's gate/up
+ * tiles) ran out and its products were written as NaN. Bits stay set until
+ * cleared (clear != 0 clears them after reading, in stream order). No
+ * counterpart in the reference: MLX's graph has no in-kernel waits. */
+#define FMX_STATUS_WAIT_TIMEOUT 1u
+int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
+                             int clear, fmx_stream stream);
+
+/* Bound of that wait, in flag reads s_sleep(16) apart (default 2^21, far
+ * beyond any real wait): applies to forwards launched after the call;
+ * polls = 0 gives up at once (a way to exercise the guard), polls < 0
+ * restores the default. Returns the previous bound. No counterpart in the
+ * reference. */
+int64_t fmx_set_decode_wait_limit(int64_t polls);
 
 /* y [T, H] bf16 = moe_block(x [T, H] bf16), T = B*L tokens. The workspace
  * must hold fmx_moe_workspace_size(cfg, T) bytes and have been initialised
@@ -249,7 +267,7 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
  * bytes that the library holds on every device it runs on until the process
  * ends. Forwards whose fmx_moe_workspace_size(cfg, n_tokens) exceeds that
  * return FMX_ERR_UNSUPPORTED before launching anything (8 MiB: every decode
- * batch of up to 16 tokens, and forwards of up to 69 tokens of the
+ * batch of up to 16 tokens, and forwards of up to 72 tokens of the
  * Qwen1.5-MoE-A2.7B shape or 104 of the Qwen3-30B-A3B shape). All calls on
  * one device share the array:
  * calls that overlap on one GPU (two streams, or two host threads) race and

@@ -193,6 +193,23 @@ def test_moe_workspace_size_nondecreasing(fmx):
         assert all(b >= a for a, b in zip(sizes, sizes[1:])), sizes
 
 
+def test_decode_wait_limit_hook(fmx):
+    """The bound of the decode kernels' wait: set, 0 (give up at once) and
+    the default restored by a negative value; each call returns the bound
+    it replaced. Host state only; status reads need no kernel either way."""
+    from flashmlx_amd import _lib
+    lib = _lib.load()
+    default = 1 << 21
+    assert lib.fmx_set_decode_wait_limit(5) == default
+    assert lib.fmx_set_decode_wait_limit(0) == 5
+    assert lib.fmx_set_decode_wait_limit(-1) == 0
+    assert lib.fmx_set_decode_wait_limit(-1) == default
+    st = C.c_uint32()
+    assert lib.fmx_moe_workspace_status(None, 0, C.byref(st), 0, None) == _lib.FMX_ERR_ARG
+    ws = (C.c_uint8 * 256)()
+    assert lib.fmx_moe_workspace_status(ws, 256, C.byref(st), 0, None) == _lib.FMX_ERR_WORKSPACE
+
+
 def test_packed_forward_arguments(fmx):
     """Packed forwards do not need the MLX-layout expert arrays, but the
     packed buffer must be 256-byte aligned and at least the config's packed

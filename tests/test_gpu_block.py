@@ -108,6 +108,36 @@ def test_block_parity_token_sweep(gpu, fmx, oracle, T):
     print(f"qwen15 T={T}: {e}")
 
 
+@pytest.mark.parametrize("wl_key", ["qwen15_decode_b8", "qwen3_decode_b1"])
+def test_block_decode_wait_guard(gpu, fmx, oracle, wl_key):
+    """The down workgroups' bounded wait for their expert's gate/up tiles,
+    made to give up at once from the host (fmx_set_decode_wait_limit(0)):
+    every kernel still ends, the products come out NaN and the workspace's
+    status word says so; with the default bound back and the word cleared,
+    the next forward gives the normal output again."""
+    import torch
+    from flashmlx_amd import _lib
+    from flashmlx_amd import workloads as W
+    from helpers import bf16_to_f32
+    lib = _lib.load()
+    wl = W.WORKLOADS[wl_key]
+    hi = W.host_inputs(wl)
+    block, xd = W.device_block(wl, hi)
+    y_ok = from_dev_bf16(block(xd))
+    assert block.status() == 0
+    assert lib.fmx_set_decode_wait_limit(0) == 1 << 21
+    try:
+        y_bad = block(xd)
+        torch.cuda.synchronize()
+    finally:
+        lib.fmx_set_decode_wait_limit(-1)
+    assert block.status(clear=True) == _lib.FMX_STATUS_WAIT_TIMEOUT
+    assert np.isnan(bf16_to_f32(from_dev_bf16(y_bad))).all()
+    assert block.status() == 0
+    np.testing.assert_array_equal(from_dev_bf16(block(xd)), y_ok)
+    assert block.status() == 0
+
+
 @pytest.mark.parametrize("wl_key", ["qwen3_decode_b8", "qwen15_decode_b8"])
 def test_block_deterministic_and_reusable(gpu, fmx, oracle, wl_key):
     """Same input twice -> identical bits; the workspace then serves a
