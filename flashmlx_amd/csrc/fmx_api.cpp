@@ -984,8 +984,10 @@ int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t T, int has_packed) {
 namespace {
 int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x, int64_t T,
                 void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_,
-                void* const* stage_events, int n_stages);
+                void* const* stage_events, int n_stages, const MoEInputNorm* nin = nullptr);
 }  // namespace
+
+
 
 int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x,
                           int64_t T, void* y, void* workspace, size_t workspace_bytes,
@@ -1069,7 +1071,7 @@ namespace {
 
 int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void* x, int64_t T,
                 void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_,
-                void* const* stage_events, int n_stages) {
+                void* const* stage_events, int n_stages, const MoEInputNorm* nin) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   auto mark = [&](int i) -> hipError_t {
     return stage_events ? hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream)
@@ -1089,6 +1091,9 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     return fail(FMX_ERR_ARG, "shared_expert_gate_w (or its scales/biases) NULL or misaligned");
   // packed weights: the forward reads the experts from there only
   const bool use_packed = w->packed != nullptr;
+  if (nin && (!use_packed || T > kDecNinMaxT || !nin->h || !nin->w || !aligned(nin->h, 16) || !aligned(nin->w, 16)))
+    return fail(FMX_ERR_UNSUPPORTED, "input norm in K1: decode forwards of up to %d tokens on packed weights",
+                kDecNinMaxT);
   if (use_packed) {
     if (!packable(c)) return fail(FMX_ERR_ARG, "packed weights given for a config that cannot be packed");
     if (!aligned(w->packed, 256)) return fail(FMX_ERR_ARG, "packed not 256-byte aligned");
@@ -1157,7 +1162,15 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.status = L.counters + kStatusOffsetWords;
     da.wait_polls = g_wait_polls.load(std::memory_order_relaxed);
     da.y = static_cast<uint16_t*>(y);
-    if (decode_plan(da)) {
+    if (nin) {
+      da.nin = nin->h;
+      da.nin_w = nin->w;
+      da.nin_eps = nin->eps;
+      da.x_out = static_cast<uint16_t*>(const_cast<void*>(x));
+    }
+    const bool dec = decode_plan(da);
+    if (nin && !dec) return fail(FMX_ERR_UNSUPPORTED, "input norm in K1: shapes outside the decode kernels");
+    if (dec) {
       FMX_HIP(mark(0));
       FMX_HIP(launch_decode_k1(da, stream));
       FMX_HIP(mark(1));
@@ -1478,3 +1491,9 @@ int fmx_moe_sort(const uint32_t* inds, int64_t T, int32_t k, int64_t E, uint32_t
 }
 
 }  // extern "C"
+
+int fmx::moe_block_forward_nin(const fmx_moe_config* cfg, const fmx_moe_weights* w, const MoEInputNorm& nin,
+                               void* x_out, int64_t T, void* y, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream) {
+  return moe_forward(cfg, w, x_out, T, y, workspace, workspace_bytes, stream, nullptr, 4, &nin);
+}

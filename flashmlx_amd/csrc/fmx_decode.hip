@@ -255,7 +255,7 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
 // and the four waves' in LDS. The last router workgroup to finish derives
 // the routing. NT: T rounded up to a power of two (the reduce-scatter's
 // width).
-template <int NPER, int NT>
+template <int NPER, int NT, bool NIN>
 __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   __shared__ int s_last;
   double* s_lp = reinterpret_cast<double*>(smem);
@@ -266,13 +266,26 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   const int H = a.H, T = a.T, E = a.E, xs = xstride(H);
   const int ncols = E + (a.wsg.w ? 1 : 0);
   const int nch = H / 8;
-  dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
+  if (!NIN) dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
   const RChunk wv = c < E ? load_rchunk(a.wr, c, H, min(tid, nch - 1))
                           : load_rchunk(a.wsg, 0, H, min(tid, nch - 1));
   const bool biased = c < E && a.lbias;
   const uint16_t lb = biased ? a.lbias[c] : 0;
-  wait_vmcnt0();
-  lds_dma_barrier();
+  if constexpr (NIN) {
+    // the input norm, in flight with the router row's loads; column 0 hands
+    // the rows on to K23
+    __shared__ double s_nred[kDecNinMaxT * (kNormThreads / kWave)];
+    norm_rows_lds<kDecNinMaxT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
+    if (c == 0)
+      for (int i = tid; i < T * nch; i += kDecThreads) {
+        const int t = i / nch, ch = i - t * nch;
+        reinterpret_cast<u32x4_t*>(a.x_out + static_cast<int64_t>(t) * H)[ch] =
+            *reinterpret_cast<const u32x4_t*>(s_x + t * xs + 8 * ch);
+      }
+  } else {
+    wait_vmcnt0();
+    lds_dma_barrier();
+  }
   double wd[8];
 #pragma unroll
   for (int q = 0; q < 8; ++q) wd[q] = tid < nch ? wv.get(q) : 0.0;
@@ -322,6 +335,7 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
 // Shared expert gate/up + SwiGLU for tile pair tp (model.cpp:741-747):
 // hs[t, n] = swiglu(x_t . Wg[n], x_t . Wu[n]) for every token; wave q
 // multiplies K quarter q.
+template <bool NIN>
 __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
@@ -333,9 +347,29 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
-  dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  tile_units_lds<true, kDecK2Units>(a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair, u0, u1, xl, lane,
-                                     acc0, acc1);
+  const uint8_t* tb = a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair;
+  if constexpr (NIN) {
+    // the tile's loads first, then the input norm (its barrier also waits
+    // for them), then the products
+    __shared__ double s_nred[kDecNinMaxT * (kNormThreads / kWave)];
+    PkUnit<true> L[kDecK2Units];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    norm_rows_lds<kDecNinMaxT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
+#pragma unroll
+    for (int d = 0; d < kDecK2Units; ++d) {
+      if (u0 + d < u1) {
+        bf16x8_t A[4];
+        lds_a(xl + (u0 + d) * 128, A);
+        pk_unit<true>(L[d], A, acc0, acc1);
+      }
+    }
+  } else {
+    dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
+    tile_units_lds<true, kDecK2Units>(tb, u0, u1, xl, lane, acc0, acc1);
+  }
   // Warm the device's last-level cache with this workgroup's share of the
   // shared expert's down weights, which K23 reads after the routing: K1's
   // HBM would otherwise idle while its router chain finishes. At most
@@ -368,14 +402,15 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
 }
 
 // Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
-template <int NPER, int NT>
+// NIN: the input norm formed here (single-row forwards of the decoder stack)
+template <int NPER, int NT, bool NIN>
 __global__ __launch_bounds__(kDecThreads) void dec_k1(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int w = blockIdx.x;
   if (w < a.n_rt)
-    dec_router<NPER, NT>(a, w, smem);
+    dec_router<NPER, NT, NIN>(a, w, smem);
   else
-    dec_shared_gu(a, w - a.n_rt, smem);
+    dec_shared_gu<NIN>(a, w - a.n_rt, smem);
 }
 
 // ---------------------------------------------------------------- K2: routed gate/up
@@ -742,6 +777,9 @@ static size_t k3_lds(const DecodeArgs& a) {
 
 bool decode_plan(DecodeArgs& a) {
   const int nu_i = a.I / 128, nu_s = a.Is / 128;
+  if (a.nin && (a.T > kDecNinMaxT || !a.nin_w || !a.x_out || a.H / 8 > kNormThreads * kNormMaxChunks ||
+                a.H / 128 > kDecK2Units * kDecWaves))
+    return false;
   if (a.T < 1 || a.T > kDecMaxT || a.k < 1 || a.k > kDecMaxK || a.E < 1 || a.E > kDecMaxE ||
       a.H % 512 || a.I % 128 || a.Is % 128 || a.H / 8 > kDecThreads ||
       a.H / 128 > 16 || nu_i > kDnMaxUnits ||
@@ -760,16 +798,19 @@ bool decode_plan(DecodeArgs& a) {
 template <int NPER>
 static void launch_k1_nt(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.n_rt + a.n_sgu), block(kDecThreads);
-  if (a.T <= 1)
-    hipLaunchKernelGGL((dec_k1<NPER, 1>), grid, block, k1_lds(a), stream, a);
+  static_assert(kDecNinMaxT == 1, "the input-norm K1 is instantiated for one row");
+  if (a.nin)
+    hipLaunchKernelGGL((dec_k1<NPER, 1, true>), grid, block, k1_lds(a), stream, a);
+  else if (a.T <= 1)
+    hipLaunchKernelGGL((dec_k1<NPER, 1, false>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 2)
-    hipLaunchKernelGGL((dec_k1<NPER, 2>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 2, false>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 4)
-    hipLaunchKernelGGL((dec_k1<NPER, 4>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 4, false>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 8)
-    hipLaunchKernelGGL((dec_k1<NPER, 8>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 8, false>), grid, block, k1_lds(a), stream, a);
   else
-    hipLaunchKernelGGL((dec_k1<NPER, 16>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 16, false>), grid, block, k1_lds(a), stream, a);
 }
 
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {

@@ -673,4 +673,110 @@ __device__ void nh_select_wave(const uint16_t* lrow, int E, int k, int norm, int
   }
 }
 
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxChunks = 4;  // 16-byte chunks per thread: H <= 8192
+
+// ------------------------------------------------------------------ RMSNorm
+//
+// RMSNorm arithmetic (mx::fast::rms_norm, model.cpp:486-488), shared by
+// rmsnorm_kernel, the decode projections' fused norms and K1's so that all
+// give the same bits (kNormThreads threads over a row): x = bf16(x + delta) element by element; the sum of squares
+// in fp64, each thread over its chunks c = tid + kNormThreads q in order,
+// then the wave's butterfly and the waves in order; r = 1 / sqrt(ss / H +
+// eps) in fp64; out = bf16(bf16(x * r) * w).
+__device__ inline u32x4_t norm_add(u32x4_t x, const u32x4_t& d) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t lo = f32_to_bf16(bf16_to_f32(x[m] & 0xffffu) + bf16_to_f32(d[m] & 0xffffu));
+    const uint32_t hi = f32_to_bf16(bf16_to_f32(x[m] >> 16) + bf16_to_f32(d[m] >> 16));
+    x[m] = lo | (hi << 16);
+  }
+  return x;
+}
+__device__ inline double norm_sq(const u32x4_t& x, double ss) {
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const double lo = bf16_to_f32(x[m] & 0xffffu), hi = bf16_to_f32(x[m] >> 16);
+    ss += lo * lo;
+    ss += hi * hi;
+  }
+  return ss;
+}
+__device__ inline double norm_wave_sum(double ss) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  return ss;
+}
+__device__ inline double norm_r(const double* s_red_row, int H, float eps) {
+  double tot = 0.0;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) tot += s_red_row[w];
+  return 1.0 / sqrt(tot / static_cast<double>(H) + static_cast<double>(eps));
+}
+__device__ inline u32x4_t norm_apply(const u32x4_t& x, const u32x4_t& wv, double r) {
+  u32x4_t o;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    uint32_t e2[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const double xv = bf16_to_f32((x[m] >> (16 * hf)) & 0xffffu);
+      const uint16_t n = f64_to_bf16(xv * r);
+      e2[hf] = f64_to_bf16(static_cast<double>(bf16_to_f32(n)) *
+                           static_cast<double>(bf16_to_f32((wv[m] >> (16 * hf)) & 0xffffu)));
+    }
+    o[m] = e2[0] | (e2[1] << 16);
+  }
+  return o;
+}
+
+// The norm of T <= MAXT rows (row stride ld) of H elements into LDS rows of
+// stride xs elements, by kNormThreads threads, chunk c of a row to thread c
+// mod kNormThreads as in rmsnorm_kernel (the same bits); s_red: MAXT x
+// (kNormThreads / kWave) doubles. Every thread calls; ends with a barrier.
+template <int MAXT>
+__device__ inline void norm_rows_lds(const uint16_t* x, int64_t ld, const uint16_t* w, float eps, int T, int H,
+                                     uint16_t* s_dst, int xs, double* s_red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = H / 8;
+  u32x4_t xv[MAXT][kNormMaxChunks], wv[kNormMaxChunks];
+  double ss[MAXT];
+#pragma unroll
+  for (int q = 0; q < kNormMaxChunks; ++q) {
+    const int c = tid + q * kNormThreads;
+    if (c < nch) wv[q] = reinterpret_cast<const u32x4_t*>(w)[c];
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    ss[t] = 0.0;
+    if (t >= T) continue;
+#pragma unroll
+    for (int q = 0; q < kNormMaxChunks; ++q) {
+      const int c = tid + q * kNormThreads;
+      if (c >= nch) break;
+      xv[t][q] = reinterpret_cast<const u32x4_t*>(x + static_cast<int64_t>(t) * ld)[c];
+      ss[t] = norm_sq(xv[t][q], ss[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    if (t >= T) continue;
+    const double sw = norm_wave_sum(ss[t]);
+    if (lane == 0) s_red[t * (kNormThreads / kWave) + wave] = sw;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < MAXT; ++t) {
+    if (t >= T) continue;
+    const double r = norm_r(s_red + t * (kNormThreads / kWave), H, eps);
+#pragma unroll
+    for (int q = 0; q < kNormMaxChunks; ++q) {
+      const int c = tid + q * kNormThreads;
+      if (c >= nch) break;
+      *reinterpret_cast<u32x4_t*>(s_dst + t * xs + 8 * c) = norm_apply(xv[t][q], wv[q], r);
+    }
+  }
+  __syncthreads();
+}
+
 }  // namespace fmx

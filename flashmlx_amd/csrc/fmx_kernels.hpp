@@ -3,6 +3,9 @@
 
 #include "fmx_common.hpp"
 
+struct fmx_moe_config;
+struct fmx_moe_weights;
+
 namespace fmx {
 
 // ---------------------------------------------------------------- sorting
@@ -208,8 +211,16 @@ struct DecodeArgs {
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
   int max_seg, gu_tiles;    // K2: expert slots x gate/up tile pairs
   int k2_pairs, gu_wgs;     // K2: tile pairs per workgroup, workgroups per expert slot
+  // input norm in K1 (nin non-null, T <= kDecNinMaxT): every K1 workgroup
+  // forms x = rmsnorm(nin) * nin_w in LDS itself (rmsnorm_kernel's bits),
+  // and router column 0 writes it to x_out (= x, read by K23)
+  const uint16_t* nin;
+  const uint16_t* nin_w;
+  float nin_eps;
+  uint16_t* x_out;
 };
 constexpr uint32_t kStatusWaitTimeout = 1u;
+constexpr int kDecNinMaxT = 1;  // rows K1 normalises itself (every workgroup: more cost more than a kernel)
 // default bound of the down workgroups' wait (flag reads, s_sleep 16 apart):
 // far beyond any real wait, a guard against a hang
 constexpr int kDecWaitPolls = 1 << 21;
@@ -404,4 +415,22 @@ hipError_t launch_quantize(const uint16_t* w, int64_t n_groups, uint32_t* wq, ui
 hipError_t launch_dequantize(const uint32_t* wq, const uint16_t* s, const uint16_t* b,
                              int64_t n_groups, uint16_t* out, hipStream_t stream);
 
+// ---------------------------------------------------------------- stack hook
+// The MoE block forward on the rows x = rmsnorm(h) * w (the decoder stack's
+// post-attention norm), for forwards the decode kernels take with at most
+// kDecNinMaxT tokens: K1 forms the rows itself and writes them to x_out.
+// Other forwards return FMX_ERR_UNSUPPORTED before launching anything (the
+// caller then runs the norm kernel and fmx_moe_block_forward).
+struct MoEInputNorm {
+  const uint16_t* h;
+  const uint16_t* w;
+  float eps;
+};
+
+}  // namespace fmx
+
+namespace fmx {
+int moe_block_forward_nin(const ::fmx_moe_config* cfg, const ::fmx_moe_weights* w, const MoEInputNorm& nin,
+                          void* x_out, int64_t T, void* y, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
 }  // namespace fmx

@@ -430,14 +430,24 @@ int fmx_model_forward_batched(const fmx_model_config* cfg, const fmx_model_weigh
     // o_proj with the residual: h = h + attn . Wo^T
     FMX_RC(linear(M.attn, M.attn_h, M.flags + 2 * l + 1, T, lw.o, d.H, d.nh * d.hd, nullptr, M.h, M.h,
                   stream, fo));
-    // post-attention norm, MoE block
-    NormArgs nb = na;
-    nb.delta = nullptr;
-    nb.w = static_cast<const uint16_t*>(lw.post_norm_w);
-    nb.outh = nullptr;
-    FMX_HIP(launch_rmsnorm(nb, static_cast<int>(T), stream));
-    FMX_RC(fmx_moe_block_forward(&cfg->moe, &lw.moe, M.normed, T, M.moe_out, M.moe_ws, M.moe_bytes,
-                                 stream_));
+    // post-attention norm, MoE block: single-row decode forwards form the
+    // norm inside the MoE block's first kernel (one kernel boundary fewer);
+    // otherwise the norm kernel, then the block
+    int mrc = FMX_ERR_UNSUPPORTED;
+    if (T <= kDecNinMaxT && rmsnorm_fits(d.H)) {
+      const MoEInputNorm mn{M.h, static_cast<const uint16_t*>(lw.post_norm_w), cfg->rms_norm_eps};
+      mrc = moe_block_forward_nin(&cfg->moe, &lw.moe, mn, M.normed, T, M.moe_out, M.moe_ws, M.moe_bytes, stream);
+      if (mrc != FMX_OK && mrc != FMX_ERR_UNSUPPORTED) return mrc;
+    }
+    if (mrc == FMX_ERR_UNSUPPORTED) {
+      NormArgs nb = na;
+      nb.delta = nullptr;
+      nb.w = static_cast<const uint16_t*>(lw.post_norm_w);
+      nb.outh = nullptr;
+      FMX_HIP(launch_rmsnorm(nb, static_cast<int>(T), stream));
+      FMX_RC(fmx_moe_block_forward(&cfg->moe, &lw.moe, M.normed, T, M.moe_out, M.moe_ws, M.moe_bytes,
+                                   stream_));
+    }
     if (routing) {
       const uint32_t* inds = nullptr;
       FMX_RC(fmx_moe_workspace_routing(&cfg->moe, T, M.moe_ws, &inds, nullptr, nullptr, nullptr, nullptr,

@@ -17,9 +17,6 @@ namespace fmx {
 
 namespace {
 
-constexpr int kNormThreads = 256;
-constexpr int kNormMaxChunks = 4;  // 16-byte chunks per thread: H <= 8192
-
 // ------------------------------------------------------------------ embedding
 
 // Row ids[t] of the bf16 table (ids outside [0, V) take the nearest row);
@@ -36,58 +33,6 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
 }
 
 // ------------------------------------------------------------------ RMSNorm
-
-// RMSNorm arithmetic (mx::fast::rms_norm, model.cpp:486-488), shared by
-// rmsnorm_kernel and the decode projections' fused norms so that both give
-// the same bits: x = bf16(x + delta) element by element; the sum of squares
-// in fp64, each thread over its chunks c = tid + kNormThreads q in order,
-// then the wave's butterfly and the waves in order; r = 1 / sqrt(ss / H +
-// eps) in fp64; out = bf16(bf16(x * r) * w).
-__device__ inline u32x4_t norm_add(u32x4_t x, const u32x4_t& d) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const uint32_t lo = f32_to_bf16(bf16_to_f32(x[m] & 0xffffu) + bf16_to_f32(d[m] & 0xffffu));
-    const uint32_t hi = f32_to_bf16(bf16_to_f32(x[m] >> 16) + bf16_to_f32(d[m] >> 16));
-    x[m] = lo | (hi << 16);
-  }
-  return x;
-}
-__device__ inline double norm_sq(const u32x4_t& x, double ss) {
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const double lo = bf16_to_f32(x[m] & 0xffffu), hi = bf16_to_f32(x[m] >> 16);
-    ss += lo * lo;
-    ss += hi * hi;
-  }
-  return ss;
-}
-__device__ inline double norm_wave_sum(double ss) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-  return ss;
-}
-__device__ inline double norm_r(const double* s_red_row, int H, float eps) {
-  double tot = 0.0;
-#pragma unroll
-  for (int w = 0; w < kNormThreads / kWave; ++w) tot += s_red_row[w];
-  return 1.0 / sqrt(tot / static_cast<double>(H) + static_cast<double>(eps));
-}
-__device__ inline u32x4_t norm_apply(const u32x4_t& x, const u32x4_t& wv, double r) {
-  u32x4_t o;
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    uint32_t e2[2];
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      const double xv = bf16_to_f32((x[m] >> (16 * hf)) & 0xffffu);
-      const uint16_t n = f64_to_bf16(xv * r);
-      e2[hf] = f64_to_bf16(static_cast<double>(bf16_to_f32(n)) *
-                           static_cast<double>(bf16_to_f32((wv[m] >> (16 * hf)) & 0xffffu)));
-    }
-    o[m] = e2[0] | (e2[1] << 16);
-  }
-  return o;
-}
 
 // One workgroup per output row i (input row i * row_mul + row_add): optionally
 // x = bf16(x + delta) first (written back: the residual stream), then the
