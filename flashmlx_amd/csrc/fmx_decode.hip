@@ -274,8 +274,8 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   if constexpr (NIN) {
     // the input norm, in flight with the router row's loads; column 0 hands
     // the rows on to K23
-    __shared__ double s_nred[kDecNinMaxT * (kNormThreads / kWave)];
-    norm_rows_lds<kDecNinMaxT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
+    __shared__ double s_nred[NT * (kNormThreads / kWave)];
+    norm_rows_lds<NT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
     if (c == 0)
       for (int i = tid; i < T * nch; i += kDecThreads) {
         const int t = i / nch, ch = i - t * nch;
@@ -335,7 +335,7 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
 // Shared expert gate/up + SwiGLU for tile pair tp (model.cpp:741-747):
 // hs[t, n] = swiglu(x_t . Wg[n], x_t . Wu[n]) for every token; wave q
 // multiplies K quarter q.
-template <bool NIN>
+template <int NT, bool NIN>
 __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
@@ -351,13 +351,13 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   if constexpr (NIN) {
     // the tile's loads first, then the input norm (its barrier also waits
     // for them), then the products
-    __shared__ double s_nred[kDecNinMaxT * (kNormThreads / kWave)];
+    __shared__ double s_nred[NT * (kNormThreads / kWave)];
     PkUnit<true> L[kDecK2Units];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
     __builtin_amdgcn_sched_barrier(0);
-    norm_rows_lds<kDecNinMaxT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
+    norm_rows_lds<NT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
       if (u0 + d < u1) {
@@ -410,7 +410,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_k1(DecodeArgs a) {
   if (w < a.n_rt)
     dec_router<NPER, NT, NIN>(a, w, smem);
   else
-    dec_shared_gu<NIN>(a, w - a.n_rt, smem);
+    dec_shared_gu<NT, NIN>(a, w - a.n_rt, smem);
 }
 
 // ---------------------------------------------------------------- K2: routed gate/up

@@ -733,13 +733,15 @@ __device__ inline u32x4_t norm_apply(const u32x4_t& x, const u32x4_t& wv, double
 // The norm of T <= MAXT rows (row stride ld) of H elements into LDS rows of
 // stride xs elements, by kNormThreads threads, chunk c of a row to thread c
 // mod kNormThreads as in rmsnorm_kernel (the same bits); s_red: MAXT x
-// (kNormThreads / kWave) doubles. Every thread calls; ends with a barrier.
+// (kNormThreads / kWave) doubles. The raw rows go to LDS with the sums of
+// squares and are normalised there in place (no row held in registers).
+// Every thread calls; ends with a barrier.
 template <int MAXT>
 __device__ inline void norm_rows_lds(const uint16_t* x, int64_t ld, const uint16_t* w, float eps, int T, int H,
                                      uint16_t* s_dst, int xs, double* s_red) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nch = H / 8;
-  u32x4_t xv[MAXT][kNormMaxChunks], wv[kNormMaxChunks];
+  u32x4_t wv[kNormMaxChunks];
   double ss[MAXT];
 #pragma unroll
   for (int q = 0; q < kNormMaxChunks; ++q) {
@@ -754,8 +756,9 @@ __device__ inline void norm_rows_lds(const uint16_t* x, int64_t ld, const uint16
     for (int q = 0; q < kNormMaxChunks; ++q) {
       const int c = tid + q * kNormThreads;
       if (c >= nch) break;
-      xv[t][q] = reinterpret_cast<const u32x4_t*>(x + static_cast<int64_t>(t) * ld)[c];
-      ss[t] = norm_sq(xv[t][q], ss[t]);
+      const u32x4_t v = reinterpret_cast<const u32x4_t*>(x + static_cast<int64_t>(t) * ld)[c];
+      *reinterpret_cast<u32x4_t*>(s_dst + t * xs + 8 * c) = v;
+      ss[t] = norm_sq(v, ss[t]);
     }
   }
 #pragma unroll
@@ -773,7 +776,8 @@ __device__ inline void norm_rows_lds(const uint16_t* x, int64_t ld, const uint16
     for (int q = 0; q < kNormMaxChunks; ++q) {
       const int c = tid + q * kNormThreads;
       if (c >= nch) break;
-      *reinterpret_cast<u32x4_t*>(s_dst + t * xs + 8 * c) = norm_apply(xv[t][q], wv[q], r);
+      u32x4_t* p = reinterpret_cast<u32x4_t*>(s_dst + t * xs + 8 * c);
+      *p = norm_apply(*p, wv[q], r);
     }
   }
   __syncthreads();

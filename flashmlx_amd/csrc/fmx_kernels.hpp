@@ -220,7 +220,10 @@ struct DecodeArgs {
   uint16_t* x_out;
 };
 constexpr uint32_t kStatusWaitTimeout = 1u;
-constexpr int kDecNinMaxT = 1;  // rows K1 normalises itself (every workgroup: more cost more than a kernel)
+// rows K1 normalises itself: every workgroup forms every row's norm, which
+// at 4 and 8 rows costs more than the norm kernel (stack decode step 1678 ->
+// 1825 us at batch 4, 1970 -> 2402 us at batch 8)
+constexpr int kDecNinMaxT = 1;
 // default bound of the down workgroups' wait (flag reads, s_sleep 16 apart):
 // far beyond any real wait, a guard against a hang
 constexpr int kDecWaitPolls = 1 << 21;
