@@ -481,12 +481,14 @@ def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_secon
         roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": load_traffic(key, dom),
                 "algorithmic_per_launch": grid_flops[dom]}
-    roof["stage"] = dom
+    # decode: D3's last contributors also form the combine, so the fc2 grid's
+    # time includes it (the combine stage is then empty)
+    roof["stage"] = dom + (" (D3, combine included)" if T <= 16 and dom == "fc2_grid" else "")
     roof["avg_launch_us"] = round(stage_ms[dom] * 1e3, 2)
     res = {
         "workload": (f"Nemotron-H MoE block (30B-A3B layer shape: H 2688, 128 experts top-6 sigmoid-routed "
                      f"with correction bias, I 1856, shared 3712, relu^2), {T} tokens, seed {NH_SEED}"),
-        "kernel_path": "decode kernels D1-D4" if T <= 16 else "router + sort + prefill GEMMs + combine",
+        "kernel_path": "decode kernels D1-D3" if T <= 16 else "router + sort + prefill GEMMs + combine",
         "key": key,
         "tokens": T,
         "value": round(T / (ms_step * 1e-3), 1),

@@ -359,8 +359,10 @@ struct NhDecArgs {
   float* sd_part;              // [kNhDecSdSplit][T][H] shared down, K-slice sums
   uint16_t* y;                 // [T, H]
   uint32_t* counter;           // D1 arrival counter: zero on entry and exit
+  uint32_t* cb_counter;        // [H / 64, stride kDecCbStride] D3 arrivals per column block: zero on entry and exit
   int max_seg, n_sup;          // launch shape: expert slots, shared up tiles
 };
+constexpr int kNhDecMaxColBlocks = 64;  // 64-column blocks of H (D3 arrival counters)
 bool nh_decode_plan(NhDecArgs& a);
 hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks);
 

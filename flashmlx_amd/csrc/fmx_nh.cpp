@@ -110,9 +110,14 @@ NhPacked nh_packed(const fmx_nh_moe_config& c) {
 // kRouterManyMin tokens: one per token tile and one more): zero on entry
 // and exit
 constexpr int64_t kNhCounterWords = 64;
+// then the flag word (a 64-word slot of its own), then D3's per-column-block
+// arrival counters: all cleared by the workspace's initialisation
+constexpr int64_t kNhCbCounterWords = static_cast<int64_t>(kNhDecMaxColBlocks) * kDecCbStride;
+constexpr int64_t kNhClearWords = kNhCounterWords + 64 + kNhCbCounterWords;
 
 struct NhLayout {
   uint32_t* counters;  // [kNhCounterWords]
+  uint32_t* cb_counter;  // [kNhDecMaxColBlocks][kDecCbStride]
   uint16_t* logits;    // [T, E + 1]
   uint32_t* inds;      // [n]
   float* scores;       // [n]
@@ -146,6 +151,7 @@ NhLayout nh_layout(const fmx_nh_moe_config& c, int64_t T, char* base) {
   NhLayout L{};
   L.counters = static_cast<uint32_t*>(take(kNhCounterWords * 4));
   L.f16_flag = static_cast<uint32_t*>(take(4));
+  L.cb_counter = static_cast<uint32_t*>(take(kNhCbCounterWords * 4));
   L.logits = static_cast<uint16_t*>(take(T * (E + 1) * 2));
   L.inds = static_cast<uint32_t*>(take(n * 4));
   L.scores = static_cast<float*>(take(n * 4));
@@ -235,10 +241,9 @@ int fmx_nh_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_strea
   if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
   if (!aligned(workspace, 256)) return fail(FMX_ERR_ARG, "workspace not 256-byte aligned");
   // the counters and the flag word that follows them (their own 256-byte slot)
-  if (workspace_bytes < (kNhCounterWords * 4 + 256))
+  if (workspace_bytes < static_cast<size_t>(kNhClearWords * 4))
     return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes is too small", workspace_bytes);
-  FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(workspace), kNhCounterWords + 64, 0u,
-                          static_cast<hipStream_t>(stream)));
+  FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(workspace), kNhClearWords, 0u, static_cast<hipStream_t>(stream)));
   return ok();
 }
 
@@ -302,7 +307,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
     FMX_HIP(hipMallocAsync(&p, need, stream));
     base = static_cast<char*>(p);
     owned = true;
-    const hipError_t e = launch_fill_u32(static_cast<uint32_t*>(p), kNhCounterWords + 64, 0u, stream);
+    const hipError_t e = launch_fill_u32(static_cast<uint32_t*>(p), kNhClearWords, 0u, stream);
     if (e != hipSuccess) {
       (void)hipFreeAsync(p, stream);
       return fail(FMX_ERR_HIP, "clearing the workspace: %s", hipGetErrorString(e));
@@ -350,6 +355,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       da.sd_part = L.sd_part;
       da.y = static_cast<uint16_t*>(y);
       da.counter = L.counters;
+      da.cb_counter = L.cb_counter;
       FMX_HIP(launch_nh_decode(da, stream, stage_events));
       return FMX_OK;
     }

@@ -8,8 +8,9 @@
 //       streaming meanwhile)
 //   D2  the routed fc1 tiles + relu^2, one or two 16-row tiles per workgroup
 //   D3  fc2 of every selected expert (64 columns and one K half per
-//       workgroup) and the shared down projection in K slices, fp32 products
-//   D4  the fp32 weighted sum and the shared add, rounded once to bf16
+//       workgroup) and the shared down projection in K slices, fp32
+//       products; the last contributor of each 64-column block forms its
+//       fp32 weighted sum and the shared add, rounded once to bf16
 //
 // Reference: server/src/nemotron_h.cpp:1010-1111 (moe_block), :54-63 (relu2).
 //
@@ -323,6 +324,80 @@ __device__ inline f32x4_t d3_tile(const uint8_t* tb, int nu, const uint16_t* xl_
   return acc;
 }
 
+// The weighted sum of column block cb (columns 64 cb .. 64 cb + 63) for
+// every token (nemotron_h.cpp:1096-1108): y = bf16(bf16(sum over slots of
+// (d + d2) * score) + shared), products and sums fp32, each rounded on its
+// own, slots in order, the shared expert's K slices added in order first.
+// The products were stored device-scope by the block's contributors in this
+// grid and are read with device-scope loads.
+// a pair of fp32 values by one device-scope 8-byte load
+__device__ inline void load2_dev(const float* p, float& lo, float& hi) {
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  lo = __uint_as_float(static_cast<uint32_t>(v));
+  hi = __uint_as_float(static_cast<uint32_t>(v >> 32));
+}
+
+__device__ void nh_combine_block(const NhDecArgs& a, int cb) {
+  const int T = a.T, k = a.k, H = a.H;
+  for (int g = threadIdx.x; g < T * 16; g += kDecThreads) {
+    const int t = g >> 4, c = cb * 64 + 4 * (g & 15);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; ++j) {
+      const float s = a.scores[t * k + j];
+      const int64_t off = static_cast<int64_t>(t * k + j) * H + c;
+      float v0[4], v1[4];
+      load2_dev(a.d + off, v0[0], v0[1]);
+      load2_dev(a.d + off + 2, v0[2], v0[3]);
+      load2_dev(a.d2 + off, v1[0], v1[1]);
+      load2_dev(a.d2 + off + 2, v1[2], v1[3]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(__fadd_rn(v0[i], v1[i]), s));
+    }
+    float out[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = round_bf16(acc[i]);
+    if (a.Isp > 0) {
+      float sd[4];
+      load2_dev(a.sd_part + static_cast<int64_t>(t) * H + c, sd[0], sd[1]);
+      load2_dev(a.sd_part + static_cast<int64_t>(t) * H + c + 2, sd[2], sd[3]);
+      for (int ks = 1; ks < kNhDecSdSplit; ++ks) {
+        float p[4];
+        const float* src = a.sd_part + (static_cast<int64_t>(ks) * T + t) * H + c;
+        load2_dev(src, p[0], p[1]);
+        load2_dev(src + 2, p[2], p[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sd[i] = __fadd_rn(sd[i], p[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out[i] = __fadd_rn(out[i], sd[i]);
+    }
+    u32x2_t w;
+    w[0] = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
+    w[1] = static_cast<uint32_t>(f32_to_bf16(out[2])) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
+    *reinterpret_cast<u32x2_t*>(a.y + static_cast<int64_t>(t) * H + c) = w;
+  }
+}
+
+// Counts a D3 workgroup's outputs for column block cb in, once every wave's
+// device-scope stores have completed; the last of the block's contributors
+// (the K halves of its U selected experts and the shared expert's K
+// slices) forms the block's sum and resets the count.
+__device__ void nh_arrive(const NhDecArgs& a, int cb, int U) {
+  __shared__ int s_last_cb;
+  wait_vmcnt0();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t target = static_cast<uint32_t>(U * kNhDnSplit + (a.Isp > 0 ? kNhDecSdSplit : 0));
+    s_last_cb = __hip_atomic_fetch_add(a.cb_counter + cb * kDecCbStride, 1u, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT) == target - 1;
+  }
+  __syncthreads();
+  if (!s_last_cb) return;
+  nh_combine_block(a, cb);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(a.cb_counter + cb * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Selected expert number u, columns 64 cb .. 64 cb + 63 of H, one 16-row
 // tile per wave over K half ks of Ip (nemotron_h.cpp:1091-1094):
 // d[t*k + slot, n] (ks 0) or d2[..] (ks 1) = h[t*k + slot] . W2_e[n] over
@@ -357,15 +432,18 @@ __device__ void d3_routed(const NhDecArgs& a, int u, int cb, int ks, uint8_t* sm
       }
     }
   });
-  float* const dst = ks ? a.d2 : a.d;
+  uint32_t* const dst = reinterpret_cast<uint32_t*>(ks ? a.d2 : a.d);
   const uint32_t my_slots = __shfl(slot4, j);
   const int n = tile * 16 + m;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
     const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
-    if (t < T && slot < static_cast<uint32_t>(k)) dst[static_cast<int64_t>(t * k + slot) * H + n] = acc[i];
+    if (t < T && slot < static_cast<uint32_t>(k))
+      __hip_atomic_store(dst + static_cast<int64_t>(t * k + slot) * H + n, __float_as_uint(acc[i]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  nh_arrive(a, cb, U);
 }
 
 // The shared down projection, columns 64 cb .. +63, K slice ks of
@@ -393,8 +471,11 @@ __device__ void d3_shared(const NhDecArgs& a, int cb, int ks, uint8_t* smem) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int t = 4 * j + i;
-    if (t < T) a.sd_part[(static_cast<int64_t>(ks) * T + t) * H + n] = acc[i];
+    if (t < T)
+      __hip_atomic_store(reinterpret_cast<uint32_t*>(a.sd_part) + (static_cast<int64_t>(ks) * T + t) * H + n,
+                         __float_as_uint(acc[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  nh_arrive(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
 }
 
 // Workgroups [0, max_seg * H/64 * 2): routed fc2 (the two K halves of a
@@ -407,44 +488,6 @@ __global__ __launch_bounds__(kDecThreads) void nh_d3(NhDecArgs a) {
     d3_routed(a, b / (ncb * kNhDnSplit), (b / kNhDnSplit) % ncb, b % kNhDnSplit, smem);
   else
     d3_shared(a, (b - nr) / kNhDecSdSplit, (b - nr) % kNhDecSdSplit, smem);
-}
-
-// ---------------------------------------------------------------- D4
-
-// y = bf16(bf16(sum over slots of d * score) + shared) (nemotron_h.cpp:
-// 1096-1108): products and sums fp32, each rounded on its own, slots in
-// order; the shared expert's K slices added in order first.
-__global__ __launch_bounds__(kDecThreads) void nh_d4(NhDecArgs a) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kDecThreads + threadIdx.x;
-  const int quads = a.H / 4;
-  if (gid >= static_cast<int64_t>(a.T) * quads) return;
-  const int t = static_cast<int>(gid / quads), o = static_cast<int>(gid % quads);
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < a.k; ++j) {
-    const float s = a.scores[t * a.k + j];
-    const int64_t off = static_cast<int64_t>(t * a.k + j) * a.H + o * 4;
-    const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(a.d + off);
-    const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(a.d2 + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], __fmul_rn(__fadd_rn(v0[i], v1[i]), s));
-  }
-  float out[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) out[i] = round_bf16(acc[i]);
-  if (a.Isp > 0) {
-    f32x4_t sd = *reinterpret_cast<const f32x4_t*>(a.sd_part + static_cast<int64_t>(t) * a.H + o * 4);
-    for (int ks = 1; ks < kNhDecSdSplit; ++ks) {
-      const f32x4_t p = *reinterpret_cast<const f32x4_t*>(a.sd_part + (static_cast<int64_t>(ks) * a.T + t) * a.H + o * 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sd[i] = __fadd_rn(sd[i], p[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out[i] = __fadd_rn(out[i], sd[i]);
-  }
-  u32x2_t w;
-  w[0] = static_cast<uint32_t>(f32_to_bf16(out[0])) | (static_cast<uint32_t>(f32_to_bf16(out[1])) << 16);
-  w[1] = static_cast<uint32_t>(f32_to_bf16(out[2])) | (static_cast<uint32_t>(f32_to_bf16(out[3])) << 16);
-  *reinterpret_cast<u32x2_t*>(a.y + static_cast<int64_t>(t) * a.H + o * 4) = w;
 }
 
 // ---------------------------------------------------------------- host side
@@ -483,7 +526,7 @@ bool nh_decode_plan(NhDecArgs& a) {
       a.Ip / 128 < kNhDnSplit || (a.Ip / 128 + kNhDnSplit - 1) / kNhDnSplit > kNhDnUnits ||
       a.H % (16 * kNhDnTiles) || a.Isp % 128 ||
       (a.Isp > 0 && (nu_s < kNhDecSdSplit || (nu_s + kNhDecSdSplit - 1) / kNhDecSdSplit > kNhSdUnits)) ||
-      a.n_group > kWave)
+      a.n_group > kWave || a.H / 64 > kNhDecMaxColBlocks)
     return false;
   a.max_seg = std::min(a.E, a.T * a.k);
   a.n_sup = a.Isp / 16;
@@ -491,6 +534,7 @@ bool nh_decode_plan(NhDecArgs& a) {
 }
 
 hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks) {
+  if (!a.cb_counter || !a.counter) return hipErrorInvalidValue;
   auto mark = [&](int i) -> hipError_t {
     return marks ? hipEventRecord(static_cast<hipEvent_t>(marks[i]), stream) : hipSuccess;
   };
@@ -535,13 +579,8 @@ hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const*
     hipLaunchKernelGGL(nh_d3, dim3(n), dim3(kDecThreads), d3_lds(a), stream, a);
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
+  // D3's last contributors have combined: the combine stage ends with it
   if ((err = mark(3)) != hipSuccess) return err;
-  {
-    const int64_t n = static_cast<int64_t>(a.T) * (a.H / 4);
-    hipLaunchKernelGGL(nh_d4, dim3(static_cast<unsigned>((n + kDecThreads - 1) / kDecThreads)), dim3(kDecThreads),
-                       0, stream, a);
-    if ((err = hipGetLastError()) != hipSuccess) return err;
-  }
   return mark(4);
 }
 
