@@ -279,6 +279,7 @@ struct PfSet {
   const uint32_t* pass_tab;  // [max_pass][2] (see SortOut)
   int max_pass;              // passes the grid covers
   int rows_static;           // rows of the static passes
+  int pass_rows;             // static passes: rows per pass (0: kPassRows; at most kPassRows)
   int n_exp;                 // experts in w (table values clamp to n_exp - 1)
   int rows_max;              // pass rows (table rows clamp to it)
   int x_rows;                // rows of x (row_map values clamp to x_rows - 1)

@@ -54,6 +54,8 @@
 // the rows come in matching copies: fp16 in the Q8 layout, bf16 in the P8
 // layout (fmx_dev.hpp), and out_map scatters the sorted rows of gather_qmm
 // back to their output rows.
+#include <algorithm>
+
 #include "fmx_dev.hpp"
 
 namespace fmx {
@@ -381,7 +383,8 @@ __device__ __attribute__((always_inline)) void pf_grid(const PfArgs& a, uint8_t*
     ng = l % P.ng;
   } else {
     // XCD x runs every pass and K slice of one column group back to back
-    const int np = (P.rows_static + kPassRows - 1) / kPassRows;
+    const int pr = P.pass_rows > 0 ? min(P.pass_rows, kPassRows) : kPassRows;
+    const int np = (P.rows_static + pr - 1) / pr;
     const int per = np * max(P.ksplit, 1);
     ng = x + kXcds * (l / per);
     pass = (l % per) % np;
@@ -400,8 +403,9 @@ __device__ __attribute__((always_inline)) void pf_grid(const PfArgs& a, uint8_t*
     rows = min(min(static_cast<int>(t[1] >> 16), kPassRows), P.rows_max - row0);
     e = min(static_cast<int>(t[1] & 0xffffu), P.n_exp - 1);
   } else {
-    row0 = pass * kPassRows;
-    rows = min(kPassRows, P.rows_static - row0);
+    const int pr = P.pass_rows > 0 ? min(P.pass_rows, kPassRows) : kPassRows;
+    row0 = pass * pr;
+    rows = min(pr, P.rows_static - row0);
   }
   if (rows <= 0) return;
   // one call site per tile count and arithmetic: each inlined copy is
@@ -457,7 +461,8 @@ int pf_items(PfSet& s, bool dual) {
   s.ng = (s.nt + per_group - 1) / per_group;
   if (s.pass_n)  // pass-major per XCD
     return kXcds * s.ng * ((s.max_pass + kXcds - 1) / kXcds);
-  const int np = (s.rows_static + kPassRows - 1) / kPassRows;  // group-major per XCD
+  const int pr = s.pass_rows > 0 ? std::min(s.pass_rows, kPassRows) : kPassRows;
+  const int np = (s.rows_static + pr - 1) / pr;  // group-major per XCD
   return kXcds * np * max(s.ksplit, 1) * ((s.ng + kXcds - 1) / kXcds);
 }
 
