@@ -52,11 +52,18 @@ def log(*a):
 
 
 def cpu_model() -> str:
+    """lscpu's model name, with its family / model / stepping numbers (a
+    virtual machine's CPU may name only the product line)."""
     try:
         out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        f = {}
         for ln in out.splitlines():
-            if ln.startswith("Model name"):
-                return ln.split(":", 1)[1].strip()
+            if ":" in ln:
+                k, v = ln.split(":", 1)
+                f.setdefault(k.strip(), v.strip())
+        if "Model name" in f:
+            ids = ", ".join(f"{k.lower()} {f[k]}" for k in ("CPU family", "Model", "Stepping") if f.get(k))
+            return f["Model name"] + (f" ({ids})" if ids else "")
     except OSError:
         pass
     return platform.processor() or "unknown"
