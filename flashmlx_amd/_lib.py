@@ -20,7 +20,7 @@ FMX_ERR_UNSUPPORTED = 4
 FMX_ERR_WORKSPACE = 5
 FMX_ERR_HIP = 6
 
-FMX_BF16, FMX_F32, FMX_U32, FMX_I32 = 0, 1, 2, 3
+FMX_BF16, FMX_F32, FMX_U32, FMX_I32, FMX_F16 = 0, 1, 2, 3, 4
 MAX_NDIM = 8
 
 

@@ -392,7 +392,7 @@ int fmx_quantized_matmul_out_shape(const fmx_array* x, const fmx_array* w, int t
   out->ndim = x->ndim;
   for (int i = 0; i < x->ndim - 1; ++i) out->shape[i] = x->shape[i];
   out->shape[x->ndim - 1] = w->shape[0];
-  out->dtype = FMX_BF16;
+  out->dtype = x->dtype == FMX_F16 ? FMX_F16 : FMX_BF16;
   return ok();
 }
 
@@ -465,7 +465,8 @@ size_t fmx_quantized_matmul_workspace_size(const fmx_array* x, const fmx_array* 
   const int64_t K = x->shape[x->ndim - 1];
   const int64_t rows = K ? numel(*x) / K : 0;
   Arena ar;
-  if (w && w->ndim == 2 && op_uses_pf(rows, w->shape[0], K, kQmmPfMinRows)) take_pf_rows(ar, rows, K);
+  const int64_t min_rows = x->dtype == FMX_F16 ? 1 : kQmmPfMinRows;
+  if (w && w->ndim == 2 && op_uses_pf(rows, w->shape[0], K, min_rows)) take_pf_rows(ar, rows, K);
   return ar.used;
 }
 
@@ -476,12 +477,14 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   int rc;
   if ((rc = check_quant_args(transpose, group_size, bits, mode))) return rc;
-  if ((rc = check_array(x, "x", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(x, "x", -1, 2))) return rc;
+  if (x->dtype != FMX_BF16 && x->dtype != FMX_F16) return fail(FMX_ERR_DTYPE, "x must be bfloat16 or float16");
+  const bool f16 = x->dtype == FMX_F16;
   if ((rc = check_array(w, "w", FMX_U32, 2))) return rc;
-  if ((rc = check_array(scales, "scales", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(scales, "scales", x->dtype, 2))) return rc;
   if (!biases) return fail(FMX_ERR_ARG, "affine mode requires biases");
-  if ((rc = check_array(biases, "biases", FMX_BF16, 2))) return rc;
-  if ((rc = check_array(out, "out", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(biases, "biases", x->dtype, 2))) return rc;
+  if ((rc = check_array(out, "out", x->dtype, 2))) return rc;
   if (w->ndim != 2) return fail(FMX_ERR_UNSUPPORTED, "w with batch dims (use gather_qmm)");
   const int64_t K = x->shape[x->ndim - 1], N = w->shape[0];
   if (K % 64) return fail(FMX_ERR_SHAPE, "K=%lld not a multiple of 64", static_cast<long long>(K));
@@ -502,16 +505,22 @@ int fmx_quantized_matmul(const fmx_array* x, const fmx_array* w, const fmx_array
   if ((rc = bind_workspace(ar, workspace, workspace_bytes,
                            fmx_quantized_matmul_workspace_size(x, w), stream)))
     return rc;
-  if (op_uses_pf(rows, N, K, kQmmPfMinRows)) {
+  // float16 rows run the prefill GEMM at every row count (its fp16 operands
+  // are the values themselves); other shapes are not taken in float16
+  if (f16 && !op_uses_pf(rows, N, K, 1))
+    return fail(FMX_ERR_UNSUPPORTED, "float16 quantized_matmul needs K %% 128 == 0 and N %% 16 == 0");
+  if (op_uses_pf(rows, N, K, f16 ? 1 : kQmmPfMinRows)) {
     const PfRows xr = take_pf_rows(ar, rows, K);
     OpsPrologue pro{};
     pro.x = static_cast<const uint16_t*>(x->data);
+    pro.x_f16 = f16 ? 1 : 0;
     pro.n_oct = rows * (K / 8);
     pro.xp = xr.xp;
     pro.xq = xr.xq;
     pro.ovf = xr.ovf;
     FMX_HIP(launch_ops_prologue(pro, stream));
     PfSet s = mlx_set(w, scales, biases, xr, K, N, static_cast<uint16_t*>(out->data));
+    s.io_f16 = f16 ? 1 : 0;
     s.rows_static = s.rows_max = s.x_rows = static_cast<int>(rows);
     // fewer work items than CUs: passes of 32 rows instead (twice the items,
     // each with half the rows; Qwen1.5 shared shape [5632, 2048]: 48-256 rows
@@ -628,11 +637,13 @@ GatherWs take_gather_ws(Arena& ar, const GatherPlan& p, bool pf) {
   return g;
 }
 
-bool gather_uses_pf(const GatherPlan& p) { return op_uses_pf(p.nb * p.M, p.N, p.K, kGatherPfMinRows); }
+bool gather_uses_pf(const GatherPlan& p, bool f16) {
+  return op_uses_pf(p.nb * p.M, p.N, p.K, f16 ? 1 : kGatherPfMinRows);
+}
 
-size_t gather_ws(const GatherPlan& p) {
+size_t gather_ws(const GatherPlan& p, bool f16) {
   Arena ar;
-  take_gather_ws(ar, p, gather_uses_pf(p));
+  take_gather_ws(ar, p, gather_uses_pf(p, f16));
   return ar.used;
 }
 
@@ -650,7 +661,7 @@ int fmx_gather_qmm_out_shape(const fmx_array* x, const fmx_array* w, const fmx_a
   for (int i = 0; i < p.ndim; ++i) out->shape[i] = p.batch[i];
   out->shape[p.ndim] = p.M;
   out->shape[p.ndim + 1] = p.N;
-  out->dtype = FMX_BF16;
+  out->dtype = x->dtype == FMX_F16 ? FMX_F16 : FMX_BF16;
   return ok();
 }
 
@@ -658,7 +669,7 @@ size_t fmx_gather_qmm_workspace_size(const fmx_array* x, const fmx_array* w,
                                      const fmx_array* lhs, const fmx_array* rhs) {
   GatherPlan p;
   if (gather_plan(x, w, lhs, rhs, &p)) return 0;
-  return gather_ws(p);
+  return gather_ws(p, x && x->dtype == FMX_F16);
 }
 
 int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scales,
@@ -670,12 +681,14 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   int rc;
   if ((rc = check_quant_args(transpose, group_size, bits, mode))) return rc;
-  if ((rc = check_array(x, "x", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(x, "x", -1, 2))) return rc;
+  if (x->dtype != FMX_BF16 && x->dtype != FMX_F16) return fail(FMX_ERR_DTYPE, "x must be bfloat16 or float16");
+  const bool f16 = x->dtype == FMX_F16;
   if ((rc = check_array(w, "w", FMX_U32, 2))) return rc;
-  if ((rc = check_array(scales, "scales", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(scales, "scales", x->dtype, 2))) return rc;
   if (!biases) return fail(FMX_ERR_ARG, "affine mode requires biases");
-  if ((rc = check_array(biases, "biases", FMX_BF16, 2))) return rc;
-  if ((rc = check_array(out, "out", FMX_BF16, 2))) return rc;
+  if ((rc = check_array(biases, "biases", x->dtype, 2))) return rc;
+  if ((rc = check_array(out, "out", x->dtype, 2))) return rc;
   if (lhs) {
     if ((rc = check_array(lhs, "lhs_indices", -1, 0))) return rc;
     if (lhs->dtype != FMX_U32 && lhs->dtype != FMX_I32)
@@ -710,8 +723,10 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
 
   Arena ar;
   WsGuard guard(ar);
-  if ((rc = bind_workspace(ar, workspace, workspace_bytes, gather_ws(p), stream))) return rc;
-  const bool pf = gather_uses_pf(p);
+  if (f16 && !gather_uses_pf(p, true))
+    return fail(FMX_ERR_UNSUPPORTED, "float16 gather_qmm needs K %% 128 == 0 and N %% 16 == 0");
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, gather_ws(p, f16), stream))) return rc;
+  const bool pf = gather_uses_pf(p, f16);
   const GatherWs g = take_gather_ws(ar, p, pf);
 
   // one launch: both index broadcasts (rhs also as per-row sort keys) and,
@@ -725,6 +740,7 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
   pro.rhs.dst_rows = g.keys;
   if (pf) {
     pro.x = static_cast<const uint16_t*>(x->data);
+    pro.x_f16 = f16 ? 1 : 0;
     pro.n_oct = p.n_x * p.M * (p.K / 8);
     pro.xp = g.xr.xp;
     pro.xq = g.xr.xq;
@@ -755,6 +771,7 @@ int fmx_gather_qmm(const fmx_array* x, const fmx_array* w, const fmx_array* scal
 
   if (pf) {
     PfSet s = mlx_set(w, scales, biases, g.xr, p.K, p.N, static_cast<uint16_t*>(out->data));
+    s.io_f16 = f16 ? 1 : 0;
     s.row_map = g.row_map;
     s.out_map = g.order;
     s.pass_n = g.pass_n;

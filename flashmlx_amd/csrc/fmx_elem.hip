@@ -211,6 +211,15 @@ __global__ __launch_bounds__(kElemThreads) void ops_prologue_kernel(OpsPrologue 
   for (int64_t o = static_cast<int64_t>(c) * kElemThreads + threadIdx.x; o < a.n_oct;
        o += static_cast<int64_t>(n_ovf) * kElemThreads) {
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.x + o * 8);
+    if (a.x_f16) {  // already fp16: the Q8 order only (elements 0,2,4,6,1,3,5,7)
+      u32x4_t q;
+      q[0] = (v[0] & 0xffffu) | (v[1] << 16);
+      q[1] = (v[2] & 0xffffu) | (v[3] << 16);
+      q[2] = (v[0] >> 16) | (v[1] & 0xffff0000u);
+      q[3] = (v[2] >> 16) | (v[3] & 0xffff0000u);
+      *reinterpret_cast<u32x4_t*>(a.xq + o * 8) = q;
+      continue;
+    }
     u32x4_t p;
     p[0] = (v[0] & 0xffffu) | (v[2] << 16);
     p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);

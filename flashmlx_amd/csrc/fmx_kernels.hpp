@@ -272,6 +272,7 @@ struct PfSet {
   const uint16_t* ms;
   const uint16_t* mb;
   const uint32_t* out_map;
+  int io_f16;                // MLX sets: ms / mb and out in float16 (not bf16)
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)
@@ -406,6 +407,7 @@ struct BcastArgs {
 struct OpsPrologue {
   BcastArgs lhs, rhs;
   const uint16_t* x;
+  int x_f16;      // x in float16: xq is x in the Q8 order, xp unused, ovf words 0
   int64_t n_oct;  // 8-element chunks of x
   uint16_t* xp;
   uint16_t* xq;

@@ -242,10 +242,17 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          sc[b][m][0] = f16_splat(__uint_as_float(SB[b][m][0] << 16));
-          sc[b][m][1] = f16_splat(__uint_as_float(SB[b][m][0] & 0xffff0000u));
-          bs[b][m][0] = f16_splat(__uint_as_float(SB[b][m][1] << 16));
-          bs[b][m][1] = f16_splat(__uint_as_float(SB[b][m][1] & 0xffff0000u));
+          if (MLX && P.io_f16) {  // float16 scales and biases: the values as they are
+            sc[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] & 0xffffu) * 0x10001u);
+            sc[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] >> 16) * 0x10001u);
+            bs[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] & 0xffffu) * 0x10001u);
+            bs[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] >> 16) * 0x10001u);
+          } else {
+            sc[b][m][0] = f16_splat(__uint_as_float(SB[b][m][0] << 16));
+            sc[b][m][1] = f16_splat(__uint_as_float(SB[b][m][0] & 0xffff0000u));
+            bs[b][m][0] = f16_splat(__uint_as_float(SB[b][m][1] << 16));
+            bs[b][m][1] = f16_splat(__uint_as_float(SB[b][m][1] & 0xffff0000u));
+          }
         }
       __builtin_amdgcn_sched_barrier(0);
       // k-slice q (32 k) of quantisation group q / 2: the weights dequantised
@@ -344,6 +351,8 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
           P.out[orow + col] = f32_to_bf16(av);
           ovf |= av >= 65504.0f;
           P.outh[orow + colh] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(av));
+        } else if (MLX && P.io_f16) {
+          P.out[orow + col] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[mt][b][0][r]));
         } else {
           uint16_t v = f32_to_bf16(acc[mt][b][0][r]);
           if (P.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(P.bias[col]));

@@ -18,7 +18,7 @@ import torch
 from . import _lib
 from ._lib import FMX_BF16, FMX_I32, FMX_U32, FmxArray, FmxMoEConfig, FmxMoEWeights, FmxQWeight
 
-_DT = {torch.bfloat16: FMX_BF16, torch.float32: 1, torch.int32: FMX_I32}
+_DT = {torch.bfloat16: FMX_BF16, torch.float32: 1, torch.int32: FMX_I32, torch.float16: 4}
 if hasattr(torch, "uint32"):
     _DT[torch.uint32] = FMX_U32
 
@@ -72,7 +72,7 @@ def quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4
     shp = FmxArray()
     _lib.check(lib.fmx_quantized_matmul_out_shape(C.byref(ax), C.byref(aw), int(transpose),
                                                   group_size, bits, C.byref(shp)))
-    out = torch.empty(_shape(shp), dtype=torch.bfloat16, device=x.device)
+    out = torch.empty(_shape(shp), dtype=x.dtype, device=x.device)
     ws = lib.fmx_quantized_matmul_workspace_size(C.byref(ax), C.byref(aw))
     wbuf = torch.empty(max(ws, 1), dtype=torch.uint8, device=x.device)
     _lib.check(lib.fmx_quantized_matmul(
@@ -91,7 +91,7 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
     shp = FmxArray()
     _lib.check(lib.fmx_gather_qmm_out_shape(C.byref(ax), C.byref(aw), _ref(al), _ref(ar),
                                             int(transpose), group_size, bits, C.byref(shp)))
-    out = torch.empty(_shape(shp), dtype=torch.bfloat16, device=x.device)
+    out = torch.empty(_shape(shp), dtype=x.dtype, device=x.device)
     ws = lib.fmx_gather_qmm_workspace_size(C.byref(ax), C.byref(aw), _ref(al), _ref(ar))
     wbuf = torch.empty(max(ws, 1), dtype=torch.uint8, device=x.device)
     _lib.check(lib.fmx_gather_qmm(

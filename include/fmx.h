@@ -53,7 +53,10 @@ typedef enum fmx_status {
   FMX_ERR_HIP = 6          /* HIP runtime error (launch, allocation)         */
 } fmx_status;
 
-typedef enum fmx_dtype { FMX_BF16 = 0, FMX_F32 = 1, FMX_U32 = 2, FMX_I32 = 3 } fmx_dtype;
+/* FMX_F16: float16 activations (a checkpoint whose norms are float16,
+ * model.cpp:208-214), taken by fmx_quantized_matmul and fmx_gather_qmm with
+ * float16 scales, biases and output. */
+typedef enum fmx_dtype { FMX_BF16 = 0, FMX_F32 = 1, FMX_U32 = 2, FMX_I32 = 3, FMX_F16 = 4 } fmx_dtype;
 
 #define FMX_MAX_NDIM 8
 

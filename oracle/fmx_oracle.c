@@ -252,6 +252,76 @@ static uint16_t qdot_row(const uint16_t* x, const uint32_t* wrow, const uint16_t
   return rb(b0 + b1);
 }
 
+/* IEEE binary16 <-> binary32: the activation dtype a float16 checkpoint
+ * runs in (model.cpp:208-214 detects it). Decoding is exact; encoding
+ * rounds to nearest even, with overflow to infinity. */
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sgn = (uint32_t)(h >> 15), ex = (h >> 10) & 31u, man = h & 1023u;
+  float v;
+  if (ex == 0)
+    v = ldexpf((float)man, -24);
+  else if (ex == 31)
+    v = man ? NAN : INFINITY;
+  else
+    v = ldexpf((float)(man | 1024u), (int)ex - 25);
+  return sgn ? -v : v;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sgn = (uint16_t)((u >> 16) & 0x8000u);
+  if (isnan(f)) return (uint16_t)(sgn | 0x7e00u);
+  const double a = fabs((double)f);
+  if (a >= 65520.0) return (uint16_t)(sgn | 0x7c00u); /* rounds past the largest finite */
+  /* a = m * 2^e exactly in double; the spacing of fp16 values near a */
+  int e;
+  (void)frexp(a, &e);                  /* a in [2^(e-1), 2^e) */
+  int step_exp = e - 11;               /* 10 fraction bits: spacing 2^(e-11) */
+  if (step_exp < -24) step_exp = -24;  /* subnormals: spacing 2^-24 */
+  const double q = a / ldexp(1.0, step_exp); /* exact: a power-of-two scale */
+  double r = nearbyint(q);             /* round half to even (default mode) */
+  double v = r * ldexp(1.0, step_exp);
+  /* v is now an fp16 value (or 65536 for inputs that round up past 65504) */
+  if (v >= 65536.0) return (uint16_t)(sgn | 0x7c00u);
+  int ve;
+  (void)frexp(v, &ve);
+  uint16_t bits;
+  if (v == 0.0)
+    bits = 0;
+  else if (ve - 1 < -14) /* subnormal */
+    bits = (uint16_t)(v * ldexp(1.0, 24));
+  else
+    bits = (uint16_t)(((ve - 1 + 15) << 10) | ((uint32_t)(v * ldexp(1.0, 11 - ve)) & 1023u));
+  return (uint16_t)(sgn | bits);
+}
+
+/* One output element in float16: x, scales and biases fp16; modes
+ * ORC_ACC_F64 (the mathematical value) and ORC_ACC_A (fp32 dequantisation
+ * s*q + b and sequential fp32 accumulation, as the bf16 form); the result
+ * rounded once to fp16. */
+static uint16_t qdot_row_f16(const uint16_t* x, const uint32_t* wrow, const uint16_t* srow,
+                             const uint16_t* brow, int64_t K, int mode) {
+  const int64_t G = K / 64;
+  double acc64 = 0.0;
+  float acc = 0.0f;
+  for (int64_t g = 0; g < G; ++g) {
+    const float s = orc_f16_to_f32(srow[g]), b = orc_f16_to_f32(brow[g]);
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t word = wrow[g * 8 + p];
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t q = (word >> (4 * j)) & 15u;
+        const float xv = orc_f16_to_f32(x[g * 64 + p * 8 + j]);
+        if (mode == ORC_ACC_F64)
+          acc64 += (double)xv * ((double)s * (double)q + (double)b);
+        else
+          acc += xv * (s * (float)q + b);
+      }
+    }
+  }
+  return orc_f32_to_f16(mode == ORC_ACC_F64 ? (float)acc64 : acc);
+}
+
 /* quantized_matmul(x, w, scales, biases, transpose=true, 64, 4):
  * model.cpp:476-480 (linear_fast), :741-747 (shared expert). */
 int orc_qmm_t(const uint16_t* x, int64_t M, int64_t K,
@@ -263,6 +333,19 @@ int orc_qmm_t(const uint16_t* x, int64_t M, int64_t K,
     for (int64_t n = 0; n < N; ++n)
       out[m * N + n] = qdot_row(x + m * K, w + n * (K / 8), scales + n * (K / 64),
                                 biases + n * (K / 64), K, mode);
+  return 0;
+}
+
+/* quantized_matmul on float16 x, scales, biases and output. */
+int orc_qmm_t_f16(const uint16_t* x, int64_t M, int64_t K,
+                  const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                  int64_t N, int mode, uint16_t* out) {
+  if (K % 64 != 0 || (mode != ORC_ACC_F64 && mode != ORC_ACC_A)) return -1;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int64_t m = 0; m < M; ++m)
+    for (int64_t n = 0; n < N; ++n)
+      out[m * N + n] = qdot_row_f16(x + m * K, w + n * (K / 8), scales + n * (K / 64),
+                                    biases + n * (K / 64), K, mode);
   return 0;
 }
 
@@ -286,6 +369,29 @@ int orc_gather_qmm(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
             qdot_row(x + ((int64_t)lhs[b] * M + m) * K, w + e * wstride + n * (K / 8),
                      scales + e * sstride + n * (K / 64), biases + e * sstride + n * (K / 64),
                      K, mode);
+      }
+  return 0;
+}
+
+/* gather_qmm on float16 x, scales, biases and output. */
+int orc_gather_qmm_f16(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
+                       const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                       int64_t E, int64_t N,
+                       const uint32_t* lhs, const uint32_t* rhs, int64_t nb,
+                       int mode, uint16_t* out) {
+  if (K % 64 != 0 || (mode != ORC_ACC_F64 && mode != ORC_ACC_A)) return -1;
+  for (int64_t b = 0; b < nb; ++b)
+    if ((int64_t)lhs[b] >= n_x || (int64_t)rhs[b] >= E) return -2;
+  const int64_t wstride = N * (K / 8), sstride = N * (K / 64);
+#pragma omp parallel for schedule(static) collapse(3)
+  for (int64_t b = 0; b < nb; ++b)
+    for (int64_t m = 0; m < M; ++m)
+      for (int64_t n = 0; n < N; ++n) {
+        const uint32_t e = rhs[b];
+        out[(b * M + m) * N + n] =
+            qdot_row_f16(x + ((int64_t)lhs[b] * M + m) * K, w + e * wstride + n * (K / 8),
+                         scales + e * sstride + n * (K / 64), biases + e * sstride + n * (K / 64),
+                         K, mode);
       }
   return 0;
 }

@@ -109,6 +109,19 @@ int orc_gather_qmm(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
                    const uint32_t* lhs, const uint32_t* rhs, int64_t nb,
                    int mode, uint16_t* out);
 
+/* float16 forms (activation dtype float16, model.cpp:208-214): x, scales,
+ * biases and out in IEEE binary16; modes ORC_ACC_F64 and ORC_ACC_A only. */
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+int orc_qmm_t_f16(const uint16_t* x, int64_t M, int64_t K,
+                  const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                  int64_t N, int mode, uint16_t* out);
+int orc_gather_qmm_f16(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
+                       const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
+                       int64_t E, int64_t N,
+                       const uint32_t* lhs, const uint32_t* rhs, int64_t nb,
+                       int mode, uint16_t* out);
+
 /* ---- router (model.cpp:757-775; renorm per moe-support-plan.md:319-322) -- */
 /* logits/probs [T,E] may be NULL. logit_bias [E] may be NULL (harness-only
  * extension: a per-expert logit offset added before softmax). */

@@ -97,6 +97,13 @@ def load() -> C.CDLL:
         lib.orc_quantize.argtypes = [_vp, i64, i64, C.c_int, C.c_int, _vp, _vp, _vp]
         lib.orc_dequantize.argtypes = [_vp, _vp, _vp, i64, i64, C.c_int, C.c_int, _vp]
         lib.orc_qmm_t.argtypes = [_vp, i64, i64, _vp, _vp, _vp, i64, C.c_int, _vp]
+        lib.orc_qmm_t_f16.argtypes = [_vp, i64, i64, _vp, _vp, _vp, i64, C.c_int, _vp]
+        lib.orc_gather_qmm_f16.argtypes = [_vp, i64, i64, i64, _vp, _vp, _vp, i64, i64, _vp, _vp, i64,
+                                           C.c_int, _vp]
+        lib.orc_f16_to_f32.restype = C.c_float
+        lib.orc_f16_to_f32.argtypes = [C.c_uint16]
+        lib.orc_f32_to_f16.restype = C.c_uint16
+        lib.orc_f32_to_f16.argtypes = [C.c_float]
         lib.orc_gather_qmm.argtypes = [_vp, i64, i64, i64, _vp, _vp, _vp, i64, i64, _vp, _vp, i64,
                                        C.c_int, _vp]
         lib.orc_router_topk.argtypes = [_vp, i64, i64, _vp, i64, _vp, C.c_int, C.c_int, _vp, _vp,
@@ -204,6 +211,32 @@ def qmm_t(x, wq, s, b, mode=ACC_A) -> np.ndarray:
     N = wq.shape[-2]
     out = np.empty(x.shape[:-1] + (N,), np.uint16)
     rc = load().orc_qmm_t(_p(x), M, K, _p(wq), _p(s), _p(b), N, mode, _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def qmm_t_f16(x, wq, s, b, mode=ACC_A) -> np.ndarray:
+    """quantized_matmul with float16 x, scales, biases and output (bit patterns as uint16)."""
+    x, wq, s, b = _c(x, np.uint16), _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    K = x.shape[-1]
+    M = x.size // K
+    N = wq.shape[-2]
+    out = np.empty(x.shape[:-1] + (N,), np.uint16)
+    rc = load().orc_qmm_t_f16(_p(x), M, K, _p(wq), _p(s), _p(b), N, mode, _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def gather_qmm_f16(x, wq, s, b, lhs, rhs, mode=ACC_A) -> np.ndarray:
+    """gather_qmm with float16 x, scales, biases and output."""
+    x, wq, s, b = _c(x, np.uint16), _c(wq, np.uint32), _c(s, np.uint16), _c(b, np.uint16)
+    lhs, rhs = _c(lhs, np.uint32), _c(rhs, np.uint32)
+    n_x, M, K = x.shape
+    E, N = wq.shape[0], wq.shape[1]
+    nb = lhs.size
+    out = np.empty((nb, M, N), np.uint16)
+    rc = load().orc_gather_qmm_f16(_p(x), n_x, M, K, _p(wq), _p(s), _p(b), E, N, _p(lhs), _p(rhs), nb,
+                                   mode, _p(out))
     assert rc == 0, rc
     return out
 

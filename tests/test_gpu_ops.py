@@ -290,3 +290,71 @@ def test_device_synth_matches_host(gpu, fmx, oracle, n, seed, stream, mean, std)
     torch.cuda.synchronize()
     h = fmx.synth_normal_bf16(n, seed, stream, mean, std)
     np.testing.assert_array_equal(from_dev_bf16(d), h)
+
+
+# ---------------------------------------------------------------- float16 activations
+
+def _f16_case(rng, oracle, shape_w, shape_x):
+    """float16 x and the oracle's quantization of w with its bf16 scales and
+    biases re-encoded as float16 (the same values: bf16 values in fp16 range)."""
+    w = _rand_bf16(rng, shape_w, 0.02)
+    rq, rs, rb = oracle.quantize(w)
+    to16 = lambda u: bf16_to_f32(u).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(shape_x).astype(np.float16).view(np.uint16)
+    return x, rq, to16(rs), to16(rb)
+
+
+def _to_dev_f16(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.float16)
+
+
+def _f16_close(got_u16, ref_u16, what):
+    g = got_u16.view(np.float16).astype(np.float64)
+    r = ref_u16.view(np.float16).astype(np.float64)
+    assert np.isfinite(g).all(), what
+    bad = np.abs(g - r) > 1e-2 + 2e-2 * np.abs(r)
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements outside rtol/atol"
+    l2 = np.linalg.norm(g - r) / max(np.linalg.norm(r), 1e-30)
+    assert l2 <= 1e-2, f"{what}: relative L2 {l2:.3g}"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (5, 2048, 5632), (37, 96, 768), (512, 256, 1024)])
+def test_quantized_matmul_f16(gpu, fmx, oracle, M, N, K):
+    """float16 x, scales, biases and output (a float16 checkpoint's
+    activations, model.cpp:208-214) against the oracle's float16 form; every
+    row count runs the prefill GEMM in its float16 mode."""
+    import torch
+    rng = np.random.default_rng(M + N + K + 16)
+    x, rq, s, b = _f16_case(rng, oracle, (N, K), (M, K))
+    out = fmx.quantized_matmul(_to_dev_f16(x), to_dev_u32(rq), _to_dev_f16(s), _to_dev_f16(b))
+    assert out.dtype == torch.float16
+    got = out.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    _f16_close(got, oracle.qmm_t_f16(x, rq, s, b, oracle.ACC_A), f"qmm f16 M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("T,k,E,N,K", [(6, 4, 8, 128, 512), (75, 4, 16, 256, 1024)])
+def test_gather_qmm_f16(gpu, fmx, oracle, T, k, E, N, K):
+    import torch
+    rng = np.random.default_rng(T * k + E + 16)
+    x, rq, s, b = _f16_case(rng, oracle, (E, N, K), (T, 1, K))
+    inds = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.uint32)
+    out = fmx.gather_qmm(_to_dev_f16(x.reshape(T, 1, 1, K)), to_dev_u32(rq), _to_dev_f16(s), _to_dev_f16(b),
+                         rhs_indices=to_dev_u32(inds))
+    assert tuple(out.shape) == (T, k, 1, N) and out.dtype == torch.float16
+    got = out.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1, 1, N)
+    ref = oracle.gather_qmm_f16(x, rq, s, b, np.repeat(np.arange(T, dtype=np.uint32), k), inds.reshape(-1),
+                                oracle.ACC_A)
+    _f16_close(got, ref, f"gather f16 T={T}")
+
+
+def test_f16_shapes_outside_the_gemm(gpu, fmx, oracle):
+    """float16 needs whole 128-k units and 16-row tiles: K % 128 == 64 is
+    refused (no bfloat16 fallback for float16 operands); mixed dtypes too."""
+    rng = np.random.default_rng(17)
+    x, rq, s, b = _f16_case(rng, oracle, (64, 1344), (3, 1344))
+    with pytest.raises(fmx.FmxError, match="UNSUPPORTED"):
+        fmx.quantized_matmul(_to_dev_f16(x), to_dev_u32(rq), _to_dev_f16(s), _to_dev_f16(b))
+    x, rq, s, b = _f16_case(rng, oracle, (64, 256), (3, 256))
+    with pytest.raises(fmx.FmxError, match="DTYPE"):
+        fmx.quantized_matmul(_to_dev_f16(x), to_dev_u32(rq), to_dev(np.zeros_like(s)), _to_dev_f16(b))

@@ -459,3 +459,67 @@ def test_moe_block_quantized_router_dense_formula(oracle):
     ref = _dense_block(oracle, cfg, w, hi.x)
     got = bf(y).astype(np.float64)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-2
+
+
+# ---------------------------------------------------------------- float16 forms
+
+def test_f16_decode_all_patterns(oracle):
+    """Every binary16 pattern decodes to numpy's value (NaNs as NaN)."""
+    lib = oracle.load()
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f16_encode_round_to_nearest_even(oracle):
+    """fp32 -> fp16 against numpy's conversion: random values over the whole
+    range, exact ties between neighbours (to even), subnormals, the
+    overflow edge (65504, 65519.996 -> 65504, 65520 -> inf) and signs."""
+    lib = oracle.load()
+    rng = np.random.default_rng(5)
+    f = np.concatenate([
+        (rng.standard_normal(20000) * np.exp2(rng.integers(-30, 17, 20000))).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e-8, 2.0 ** -24, 2.0 ** -25,
+                  3 * 2.0 ** -26, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, np.inf, -np.inf], np.float32)])
+    # ties: midpoints between consecutive fp16 values (exact in fp32)
+    h = rng.integers(0, 0x7bff, 3000).astype(np.uint16)
+    lo = h.view(np.float16).astype(np.float32)
+    hi = (h + 1).view(np.float16).astype(np.float32)
+    f = np.concatenate([f, (lo + (hi - lo) / 2).astype(np.float32)])
+    with np.errstate(over="ignore"):
+        ref = f.astype(np.float16).view(np.uint16)
+    got = np.array([lib.orc_f32_to_f16(float(v)) for v in f], np.uint16)
+    np.testing.assert_array_equal(got, ref)
+
+
+def _f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def test_qmm_f16_matches_float64_formula(oracle):
+    """The float16 quantized matmul in fp64 mode is fp16(x . (s q + b)) of
+    the decoded values (numpy float64), and mode A (fp32) stays within two
+    fp16 ulps of it; gather_qmm_f16 with one-hot indices equals it."""
+    rng = np.random.default_rng(6)
+    M, N, K = 5, 24, 256
+    x = _f16(rng.standard_normal((M, K)))
+    wq = rng.integers(0, 2 ** 32, (N, K // 8), dtype=np.uint64).astype(np.uint32)
+    s = _f16(rng.uniform(0.001, 0.01, (N, K // 64)))
+    b = _f16(rng.uniform(-0.05, 0.05, (N, K // 64)))
+    q = ((wq[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 15).reshape(N, K).astype(np.float64)
+    sf = np.repeat(s.view(np.float16).astype(np.float64), 64, axis=1)
+    bf = np.repeat(b.view(np.float16).astype(np.float64), 64, axis=1)
+    ref = x.view(np.float16).astype(np.float64) @ (sf * q + bf).T
+    got64 = oracle.qmm_t_f16(x, wq, s, b, oracle.ACC_F64)
+    np.testing.assert_array_equal(got64, ref.astype(np.float32).astype(np.float16).view(np.uint16))
+    gotA = oracle.qmm_t_f16(x, wq, s, b, oracle.ACC_A).view(np.float16).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(gotA - ref) <= 2 * ulp + 1e-6)
+    E = 3
+    wE = np.stack([wq] * E)
+    out = oracle.gather_qmm_f16(x.reshape(M, 1, K), wE, np.stack([s] * E), np.stack([b] * E),
+                                np.arange(M, dtype=np.uint32), np.array([0, 2, 1, 2, 0], np.uint32))
+    np.testing.assert_array_equal(out.reshape(M, N), oracle.qmm_t_f16(x, wq, s, b, oracle.ACC_A))
