@@ -596,6 +596,13 @@ def measure_stack(batches, trials: int, cpu_seconds: float):
     log(f"stack: 24-layer weights built in {time.perf_counter() - t0:.1f}s")
     rng = np.random.default_rng(STACK_SEED)
     res = {}
+    solo = M.DecoderModel(cfg, w, 1, STACK_PROMPT + STACK_NEW, STACK_PROMPT)
+
+    def alone(prompt):
+        """Each prompt row generated on its own at batch 1 (eager)."""
+        return torch.cat([solo.generate(prompt[b:b + 1].contiguous(), STACK_NEW)
+                          for b in range(prompt.shape[0])])
+
     for B in batches:
         max_seq = STACK_PROMPT + STACK_NEW
         dm = M.DecoderModel(cfg, w, B, max_seq, B * STACK_PROMPT)
@@ -668,21 +675,25 @@ def measure_stack(batches, trials: int, cpu_seconds: float):
                                  f"mean {np.mean(uniq):.1f}"},
         }
         log(f"stack B={B}: prefill {pm:.2f} ms, decode {step_ms * 1e3:.1f} us/step")
-        res[f"c4_stack_b{B}"]["scheduler"] = measure_scheduler(cfg, w, prompt, ref, max_seq)
+        res[f"c4_stack_b{B}"]["scheduler"] = measure_scheduler(
+            cfg, w, prompt, ref if B == 1 else alone(prompt), max_seq)
         del dm, gp, gs
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+    del solo
     if cpu_seconds > 0:
         res["c4_stack_b1"]["cpu_baseline"] = stack_cpu_baseline(cfg, w, cpu_seconds)
     return res
 
 
-def measure_scheduler(cfg, w, prompt, ref, max_seq: int) -> dict:
+def measure_scheduler(cfg, w, prompt, alone, max_seq: int) -> dict:
     """The same B requests through the native server loop (BatchScheduler:
     batch-1 prefills into pool slots, then batched decode steps with a host
     round trip per step): wall-clock tok/s of the whole run, the decode
     steps' mean wall time once every request is admitted, and whether each
-    request's tokens equal the batched generation's."""
+    request's tokens equal that prompt generated alone at batch 1 (`alone`
+    [B, n] int32: the property the scheduler guarantees, since every decode
+    kernel computes a row on its own for batches of up to 16)."""
     from flashmlx_amd import model as M
 
     B = prompt.shape[0]
@@ -704,11 +715,11 @@ def measure_scheduler(cfg, w, prompt, ref, max_seq: int) -> dict:
         sched.drain_completed()
         runs.append((wall, steps[1:], toks, ids))
     wall, dsteps, toks, ids = runs[-1]
-    want = ref.cpu().numpy()
+    want = alone.cpu().numpy()
     out["tok_s"] = round(B * STACK_NEW / wall, 1)
     out["wall_ms"] = round(wall * 1e3, 2)
     out["decode_ms_per_step_wall"] = round(1e3 * sum(dsteps) / max(len(dsteps), 1), 4)
-    out["tokens_equal_batched_generate"] = all(toks[i] == want[b].tolist() for b, i in enumerate(ids))
+    out["tokens_equal_alone_b1"] = all(toks[i] == want[b].tolist() for b, i in enumerate(ids))
     sched.close()
     log(f"scheduler B={B}: {out['tok_s']} tok/s, decode step {out['decode_ms_per_step_wall']} ms wall")
     return out
@@ -857,6 +868,45 @@ def measure_ops(trials: int = 5, calls: int = 20) -> dict:
                         "Qwen1.5-MoE-A2.7B shapes, HIP graphs of 20 calls", "cases": res}
 
 
+def _r(v, nd=4):
+    return None if v is None else round(float(v), nd)
+
+
+def compact_config(key: str, c: dict) -> dict:
+    """The headline figures of one measured configuration as a flat object:
+    throughput, per-layer (or per-step) time, the dominant kernel's roofline
+    fraction with the figures it is computed from, and the check results."""
+    if "cases" in c:  # the standalone operators
+        return {k: {"us": v["us"], "frac": v.get("hbm_frac", v.get("mfma_frac")),
+                    "bound": "hbm" if "hbm_frac" in v else "mfma"} for k, v in c["cases"].items()}
+    rf = c.get("roofline", {})
+    o = {"value": c.get("value"), "unit": c.get("unit")}
+    if "decode_ms_per_step" in c:  # decoder stack
+        sch = c.get("scheduler", {})
+        o.update(decode_ms_per_step=c["decode_ms_per_step"], prefill_ms=c.get("prefill_ms"),
+                 e2e_tok_s=c.get("e2e_tok_s"), frac=rf.get("frac"), achieved=rf.get("achieved"),
+                 algorithmic_per_step=rf.get("algorithmic_per_step"),
+                 graph_tokens_equal_eager=c.get("graph_tokens_equal_eager"),
+                 sched_tok_s=sch.get("tok_s"), sched_tokens_equal_alone_b1=sch.get("tokens_equal_alone_b1"))
+    else:
+        ly = c.get("layer", {})
+        o.update(us_per_layer=c.get("us_per_layer"), U=ly.get("unique_experts"), bound=rf.get("bound"),
+                 frac=rf.get("frac"), achieved=rf.get("achieved"), stage=rf.get("stage"),
+                 avg_launch_us=rf.get("avg_launch_us"), algorithmic_per_launch=rf.get("algorithmic_per_launch"),
+                 traffic=rf.get("traffic"))
+        if rf.get("bound") == "mfma" and "mfma_frac" in ly:
+            o["layer_mfma_frac"] = ly["mfma_frac"]
+        if "hbm_frac" in ly:
+            o["layer_hbm_frac"] = ly["hbm_frac"]
+    cb = c.get("cpu_baseline")
+    if cb:
+        o["cpu_tok_s"] = cb.get("value")
+        if "parity_rel_l2" in cb:
+            o["parity_rel_l2"] = _r(cb["parity_rel_l2"], 8)
+            o["routing_bitexact"] = cb.get("routing_bitexact")
+    return {k: v for k, v in o.items() if v is not None}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -879,6 +929,9 @@ def main():
     ap.add_argument("--stack-trials", type=int, default=5)
     ap.add_argument("--ops", default="all", choices=["all", "none"],
                     help="time the standalone fmx_gather_qmm / fmx_quantized_matmul")
+    ap.add_argument("--detail", default="",
+                    help="also write the full per-config results (stage times, bytes, samples) to this "
+                         "JSON file; the printed line holds each config's headline figures")
     ap.add_argument("--nh", default="all",
                     help="Nemotron-H block configs measured in the same run: all, none or a comma list "
                          "(nh30b_decode_b1, nh30b_decode_b8, nh30b_prefill_512)")
@@ -975,14 +1028,28 @@ def main():
             "parallelism": "single GPU",
         },
         "roofline": head["roofline"],
-        "layer": head["layer"],
-        "trial_ms": head["trial_ms"],
-        "wall_s": head["wall_s"],
-        "parity": parity,
         "cpu_baseline": cpu,
-        "configs": configs,
     }
-    print(json.dumps(out), flush=True)
+    lay = head["layer"]
+    out["layer"] = {"us": head["us_per_layer"], "U": lay["unique_experts"],
+                    "algorithmic_bytes": lay["algorithmic_bytes"], "hbm_frac": lay["hbm_frac"],
+                    "stage_us": lay["stage_us"], "trial_ms": head["trial_ms"]}
+    if parity:
+        out["parity"] = {k: (_r(v, 8) if isinstance(v, float) else v) for k, v in parity.items()}
+    out["configs"] = {k: compact_config(k, c) for k, c in configs.items()}
+    if args.detail:
+        full = dict(out, layer=head["layer"], trial_ms=head["trial_ms"], wall_s=head["wall_s"],
+                    parity=parity, configs=configs)
+        with open(args.detail, "w") as f:
+            json.dump(full, f, indent=1)
+        log(f"full results written to {args.detail}")
+    for k, c in configs.items():  # every config's full record on stderr, one line each
+        log(f"detail {k}: " + json.dumps(c))
+    for k, c in out["configs"].items():  # then a short line each
+        if "frac" in c:
+            t = f"{c['us_per_layer']} us/layer" if "us_per_layer" in c else f"{c['decode_ms_per_step']} ms/step"
+            log(f"summary {k}: {c['value']} {c['unit']}, {t}, roofline frac {c['frac']}")
+    print(json.dumps(out, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":
