@@ -208,6 +208,11 @@ _SIGS = {
         [P(FmxMoEConfig), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
          C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p],
     ),
+    "fmx_moe_router_topk_ex": (
+        C.c_int,
+        [P(FmxMoEConfig), C.c_void_p, C.c_int64, P(FmxMoEWeights), C.c_void_p, C.c_void_p, C.c_void_p,
+         C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p],
+    ),
     "fmx_moe_sort_workspace_size": (C.c_size_t, [C.c_int64, C.c_int32, C.c_int64]),
     "fmx_moe_sort": (
         C.c_int,

@@ -1479,6 +1479,42 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, con
                     static_cast<uint16_t*>(probs), nullptr, nullptr, false, nullptr, stream);
 }
 
+int fmx_moe_router_topk_ex(const fmx_moe_config* cfg, const void* x, int64_t T, const fmx_moe_weights* w,
+                           uint32_t* inds, void* scores, void* probs, void* shared_gate_out,
+                           void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  int rc;
+  if ((rc = check_moe_config(cfg))) return rc;
+  if (T < 0 || T > kMoEMaxTokens) return fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  if (T == 0) return ok();  // nothing to run: the buffers may be NULL (empty tensors)
+  if (!x || !w || !inds || !scores) return fail(FMX_ERR_ARG, "NULL argument");
+  if (!aligned(x, 16)) return fail(FMX_ERR_ARG, "x not 16-byte aligned");
+  const RouterRows wr = router_rows(*w);
+  if (!rows_ok(wr))
+    return fail(FMX_ERR_ARG, "router_w: bf16 rows 16-byte aligned, or 4-bit words with both "
+                             "router_scales and router_biases");
+  RouterRows wsg{nullptr, nullptr, nullptr};
+  if (shared_gate_out) {
+    wsg = RouterRows{w->shared_expert_gate_w, static_cast<const uint16_t*>(w->shared_expert_gate_scales),
+                     static_cast<const uint16_t*>(w->shared_expert_gate_biases)};
+    if (!rows_ok(wsg))
+      return fail(FMX_ERR_ARG, "shared_gate_out needs shared_expert_gate_w: a bf16 row 16-byte aligned, "
+                               "or 4-bit words with both scales and biases");
+  }
+  Arena ar;
+  WsGuard guard(ar);
+  const size_t need = moe_layout(*cfg, T, nullptr).total;
+  if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
+  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  const MoELayout L = moe_layout(*cfg, T, ar.base);
+  if ((rc = run_router(*cfg, L, x, T, wr, w->router_logit_bias, wsg, inds, static_cast<uint16_t*>(scores),
+                       static_cast<uint16_t*>(probs), shared_gate_out ? L.sgate : nullptr, nullptr, false,
+                       nullptr, stream)))
+    return rc;
+  if (shared_gate_out) FMX_HIP(launch_f32_bf16(L.sgate, T, static_cast<uint16_t*>(shared_gate_out), stream));
+  return FMX_OK;
+}
+
 size_t fmx_moe_sort_workspace_size(int64_t T, int32_t k, int64_t E) {
   if (T < 0 || k < 1 || E < 1) return 0;
   const int64_t n = T * k;

@@ -164,6 +164,19 @@ hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t strea
   return hipGetLastError();
 }
 
+// bf16-valued fp32 -> bf16 bits (the value's upper half: exact)
+__global__ __launch_bounds__(kElemThreads) void f32_bf16_kernel(const float* src, int64_t n, uint16_t* dst) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
+  if (i < n) dst[i] = static_cast<uint16_t>(__float_as_uint(src[i]) >> 16);
+}
+
+hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_bf16_kernel, dim3(grid_for(n, kElemThreads)), dim3(kElemThreads), 0, stream, src, n,
+                     dst);
+  return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ gather_qmm indices
 // MLX broadcasting of one index array: entry i of the flattened batch
 __device__ inline void bcast_one(const BcastArgs& a, int64_t i) {

@@ -384,6 +384,8 @@ hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
                              hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
+// dst[i] = bf16 bits of src[i], a value that is exactly a bf16
+hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream);
 
 // MLX broadcasting of index arrays to the common batch shape (up to 8 dims).
 struct BcastArgs {

@@ -396,9 +396,15 @@ class MoEBlock:
         }
 
 
-def router_topk(cfg: MoEConfig, x: torch.Tensor, router_w: torch.Tensor,
-                logit_bias: Optional[torch.Tensor] = None):
-    """Router alone: (inds [T,k] int32, scores [T,k] bf16, probs [T,E] bf16)."""
+def router_topk(cfg: MoEConfig, x: torch.Tensor, router_w,
+                logit_bias: Optional[torch.Tensor] = None, shared_expert_gate_w=None):
+    """Router alone (model.cpp:757-775): (inds [T,k] int32, scores [T,k]
+    bf16, probs [T,E] bf16), and with `shared_expert_gate_w` also the shared
+    expert's gate sigmoid(x . wsg^T) [T] bf16 (:787-803). router_w and
+    shared_expert_gate_w are bf16 tensors or QWeights (the quantized router
+    of :758-760)."""
+    if isinstance(router_w, QWeight) or shared_expert_gate_w is not None:
+        return _router_topk_ex(cfg, x, router_w, logit_bias, shared_expert_gate_w)
     lib = _lib.load()
     c = cfg.to_c()
     T = x.numel() // cfg.hidden_size
@@ -411,3 +417,21 @@ def router_topk(cfg: MoEConfig, x: torch.Tensor, router_w: torch.Tensor,
         logit_bias.data_ptr() if logit_bias is not None else None,
         inds.data_ptr(), scores.data_ptr(), probs.data_ptr(), None, 0, _stream()))
     return inds, scores, probs
+
+
+def _router_topk_ex(cfg: MoEConfig, x: torch.Tensor, router_w, logit_bias, shared_expert_gate_w):
+    lib = _lib.load()
+    c = cfg.to_c()
+    T = x.numel() // cfg.hidden_size
+    k, E = cfg.num_experts_per_tok, cfg.num_experts
+    w = MoEWeights(router_w=router_w, gate=None, up=None, down=None,
+                   shared_expert_gate_w=shared_expert_gate_w, router_logit_bias=logit_bias)
+    cw = w.to_c()
+    inds = torch.empty(T, k, dtype=torch.int32, device=x.device)
+    scores = torch.empty(T, k, dtype=torch.bfloat16, device=x.device)
+    probs = torch.empty(T, E, dtype=torch.bfloat16, device=x.device)
+    sg = torch.empty(T, dtype=torch.bfloat16, device=x.device) if shared_expert_gate_w is not None else None
+    _lib.check(lib.fmx_moe_router_topk_ex(
+        C.byref(c), x.data_ptr(), T, C.byref(cw), inds.data_ptr(), scores.data_ptr(), probs.data_ptr(),
+        _ptr(sg), None, 0, _stream()))
+    return (inds, scores, probs) if sg is None else (inds, scores, probs, sg)

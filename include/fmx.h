@@ -21,8 +21,10 @@
  *     crosses this boundary. fmx_last_error() gives the thread's last message.
  *   - Concurrency: calls are re-entrant for distinct (stream, workspace)
  *     pairs. Two calls sharing one workspace must be ordered on one stream.
- *   - Scope: affine mode, bits = 4, group_size = 64, transpose = true, bf16
- *     activations and bf16 scales/biases. Any other valid MLX argument returns
+ *   - Scope: affine mode, bits = 4, group_size = 64, transpose = true.
+ *     Activations and scales/biases are bf16 everywhere; fmx_quantized_matmul
+ *     and fmx_gather_qmm also take float16 ones (FMX_F16: x, scales, biases
+ *     and out all float16). Any other valid MLX argument returns
  *     FMX_ERR_UNSUPPORTED and computes nothing.
  *
  * Packed weight layout (MLX's, unchanged): for a logical [N, K] matrix
@@ -41,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FMX_ABI_VERSION 3
+#define FMX_ABI_VERSION 4
 
 typedef enum fmx_status {
   FMX_OK = 0,
@@ -322,6 +324,22 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t n_toke
                         const void* router_w, const void* router_logit_bias,
                         uint32_t* inds, void* scores, void* probs, void* workspace,
                         size_t workspace_bytes, fmx_stream stream);
+
+/* Router alone, with the router and the shared-expert gate in either form
+ * (model.cpp:757-775 + renorm, and the gate of :787-803). Reads from `w`
+ * only: router_w with router_scales / router_biases (NULL scales = bf16 rows
+ * [E, H], :762; given = 4-bit rows u32 [E, H/8] with bf16 scales and biases
+ * [E, H/64], the quantized_matmul of :758-760), router_logit_bias, and,
+ * when shared_gate_out is not NULL, shared_expert_gate_w with its scales and
+ * biases (bf16 [1, H], or u32 [1, H/8] + [1, H/64]). Logits are formed as
+ * fmx_moe_block_forward forms them (exact sums, one bf16 rounding), so inds,
+ * scores and probs are bit-identical to the block's routing.
+ *   inds [T,k] u32, scores [T,k] bf16, probs [T,E] bf16 (or NULL),
+ *   shared_gate_out [T] bf16 = sigmoid(x . shared_expert_gate^T) (or NULL). */
+int fmx_moe_router_topk_ex(const fmx_moe_config* cfg, const void* x, int64_t n_tokens,
+                           const fmx_moe_weights* w, uint32_t* inds, void* scores, void* probs,
+                           void* shared_gate_out, void* workspace, size_t workspace_bytes,
+                           fmx_stream stream);
 
 /* Sort / permutation alone (model.cpp:682-700): order = stable argsort of the
  * flattened inds, inv = argsort(order), src = order / k, idx = flat[order],

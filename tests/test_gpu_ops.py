@@ -216,6 +216,43 @@ def test_router_bitexact(gpu, fmx, oracle, T, E, k, norm, H, bias):
     np.testing.assert_array_equal(from_dev_bf16(scores), rsc)
 
 
+@pytest.mark.parametrize("T,E,k,norm,H,qr,qg", [(1, 60, 4, False, 2048, True, True),
+                                                 (8, 60, 4, False, 2048, True, False),
+                                                 (8, 128, 8, True, 2048, True, True),
+                                                 (40, 60, 4, False, 2048, False, True),
+                                                 (300, 128, 8, True, 512, True, True)])
+def test_router_topk_ex_bitexact(gpu, fmx, oracle, T, E, k, norm, H, qr, qg):
+    """fmx_moe_router_topk_ex: the router quantized (model.cpp:758-760) or
+    bf16 (:762), and the shared-expert gate (:787-803) quantized or bf16.
+    inds, scores and probs bit-exact against the oracle's router; the gate
+    equals bf16(sigmoid(v)) of the oracle's exactly rounded logit v, with the
+    sigmoid taken by numpy in float64."""
+    rng = np.random.default_rng(1000 + T + E + k)
+    x = _rand_bf16(rng, (T, H))
+    wr = _rand_bf16(rng, (E, H), 0.02)
+    wsg = _rand_bf16(rng, (1, H), 0.02)
+    rq = oracle.quantize(wr) if qr else None
+    gq = oracle.quantize(wsg) if qg else None
+    cfg = fmx.MoEConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k,
+                        moe_intermediate_size=64, norm_topk_prob=norm)
+    dev_r = fmx.QWeight(to_dev_u32(rq[0]), to_dev(rq[1]), to_dev(rq[2])) if qr else to_dev(wr)
+    dev_g = fmx.QWeight(to_dev_u32(gq[0]), to_dev(gq[1]), to_dev(gq[2])) if qg else to_dev(wsg)
+    inds, scores, probs, sg = fmx.router_topk(cfg, to_dev(x), dev_r, shared_expert_gate_w=dev_g)
+    _, rp, ri, rsc = oracle.router_topk(x, rq if qr else wr, k, norm)
+    np.testing.assert_array_equal(from_dev_bf16(probs), rp)
+    np.testing.assert_array_equal(from_dev_u32(inds), ri)
+    np.testing.assert_array_equal(from_dev_bf16(scores), rsc)
+    glog, _, _, _ = oracle.router_topk(x, gq if qg else wsg, 1)
+    v = bf16_to_f32(glog[:, 0]).astype(np.float64)
+    want = oracle.f64_to_bf16(1.0 / (1.0 + np.exp(-v)))
+    np.testing.assert_array_equal(from_dev_bf16(sg), want)
+    # the bf16-router form through the same entry point equals fmx_moe_router_topk
+    if not qr:
+        i2, s2, p2 = fmx.router_topk(cfg, to_dev(x), to_dev(wr))
+        np.testing.assert_array_equal(from_dev_u32(i2), from_dev_u32(inds))
+        np.testing.assert_array_equal(from_dev_bf16(p2), from_dev_bf16(probs))
+
+
 # (10001, 4, 60) and (8192, 8, 128): 40,004 and 65,536 entries, beyond the
 # 32,768 keys the sort holds in LDS (the rest are re-read from memory)
 @pytest.mark.parametrize("T,k,E", [(1, 4, 60), (8, 8, 128), (512, 4, 60), (1024, 8, 128),
