@@ -617,10 +617,12 @@ __device__ void nh_select_wave(const uint16_t* lrow, int E, int k, int norm, int
       }
       if (lane == g) my_gs = m1 + m2;
     }
+    // the topk_group groups that argpartition's (value asc, index asc) order
+    // leaves last stay: group score desc, then index desc (equal scores: the
+    // lower group is zeroed first)
     bool keep = false;
-    uint64_t gkey = lane < n_group
-                        ? (static_cast<uint64_t>(f32_key(my_gs)) << 32) | (0xffffffffu - static_cast<uint32_t>(lane))
-                        : 0ull;
+    uint64_t gkey = lane < n_group ? (static_cast<uint64_t>(f32_key(my_gs)) << 32) | static_cast<uint32_t>(lane + 1)
+                                   : 0ull;
     for (int r = 0; r < topk_group; ++r) {
       const uint64_t best = wave_max_u64(gkey);
       if (gkey == best && lane < n_group) {

@@ -703,14 +703,19 @@ static void nh_select(const orc_nh_cfg* c, const uint16_t* lg, const float* cbia
       }
       gs[g] = m1 + m2;
     }
-    /* the topk_group best groups stay (group score desc, index asc); the
-     * others' experts get selection score 0 (:1032-1039) */
+    /* argpartition(group_scores, n_group - topk_group - 1) zeroes the
+     * n_group - topk_group first groups in MLX's (value asc, index asc)
+     * order (:1032-1039), the comparator behind the top-k tie rule below:
+     * among equal group scores the lower index is zeroed first. So the
+     * topk_group groups that stay are the last ones in that order: group
+     * score desc, index desc. Their experts keep their selection scores;
+     * the others' get 0. */
     unsigned char keep[1024];
     memset(keep, 0, sizeof keep);
     for (int r = 0; r < c->topk_group; ++r) {
       int best = -1;
       for (int g = 0; g < c->n_group; ++g)
-        if (!keep[g] && (best < 0 || gs[g] > gs[best])) best = g;
+        if (!keep[g] && (best < 0 || gs[g] >= gs[best])) best = g;
       keep[best] = 1;
     }
     for (int g = 0; g < c->n_group; ++g)

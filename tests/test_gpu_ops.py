@@ -175,6 +175,46 @@ def test_gather_qmm_prefill_unsorted(gpu, fmx, oracle, T, k, E, N, K, big):
     check(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather prefill")
 
 
+@pytest.mark.parametrize("case", ["decode_8x4_unsorted", "prefill_2048_sorted"])
+def test_gather_qmm_timed_shapes(gpu, fmx, oracle, case):
+    """The calls the benchmark times, at their full size: switch_mlp's gate
+    projection of the Qwen1.5-MoE-A2.7B shape (E 60, N 1408, K 2048) for 8
+    tokens x top-4 unsorted (model.cpp:703, the grouped GEMM) and for 2048
+    sorted rows (:686-706, the prefill GEMM in its MLX mode). Weights from
+    the device generator and quantizer (the quantizer is bit-exact against
+    the oracle's), copied to the host for the oracle. Every output row of
+    the decode call and every 4th row of the prefill call (512 rows, all 60
+    experts' segments) against the oracle; the whole prefill output finite."""
+    import torch
+    E, N, K, k = 60, 1408, 2048, 4
+    w = fmx.synth_normal_bf16_device((E, N, K), 11, 60, 0.0, 0.02)
+    wq, ws, wb = fmx.quantize(w)
+    del w
+    hq = wq.cpu().numpy().view(np.uint32)
+    hs, hb = from_dev_bf16(ws), from_dev_bf16(wb)
+    rng = np.random.default_rng(77)
+    if case.startswith("decode"):
+        B = 8
+        x = _rand_bf16(rng, (B, 1, K))
+        inds = np.stack([rng.permutation(E)[:k] for _ in range(B)]).astype(np.uint32)
+        out = fmx.gather_qmm(to_dev(x.reshape(B, 1, 1, 1, K)), wq, ws, wb,
+                             rhs_indices=to_dev_u32(inds.reshape(B, 1, k)))
+        assert tuple(out.shape) == (B, 1, k, 1, N)
+        ref = oracle.gather_qmm(x, hq, hs, hb, np.repeat(np.arange(B, dtype=np.uint32), k), inds.reshape(-1),
+                                oracle.ACC_A)
+        assert_close(from_dev_bf16(out).reshape(-1, 1, N), ref, "gather_qmm 8x4")
+    else:
+        n = 2048
+        x = _rand_bf16(rng, (n, 1, K))
+        idx = np.sort(rng.integers(0, E, n)).astype(np.uint32)
+        out = fmx.gather_qmm(to_dev(x), wq, ws, wb, rhs_indices=to_dev_u32(idx), sorted_indices=True)
+        assert tuple(out.shape) == (n, 1, N)
+        assert bool(torch.isfinite(out.float()).all())
+        rows = np.arange(0, n, 4, dtype=np.uint32)
+        ref = oracle.gather_qmm(x, hq, hs, hb, rows, idx[rows], oracle.ACC_A)
+        assert_close(from_dev_bf16(out)[rows], ref, "gather_qmm 2048 sorted")
+
+
 def test_gather_qmm_defaults_one_hot(gpu, fmx, oracle):
     """No index arrays: out[e] = x[e] . W[e]^T, i.e. E independent quantized_matmuls."""
     rng = np.random.default_rng(14)

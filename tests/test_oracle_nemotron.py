@@ -139,11 +139,43 @@ def test_route_group_limit_masked_zero_outranks_negative(oracle):
     assert inds[0].tolist() == [8, 9]
 
 
-def test_route_group_ties_keep_lower_group(oracle):
-    """Equal group scores: the lower group index is kept."""
+def test_route_group_ties_zero_lower_group(oracle):
+    """Equal group scores: argpartition's (value asc, index asc) order puts
+    the lower group first among the zeroed ones, so the higher group stays
+    (the comparator that also sends top-k ties to the lower expert)."""
     cb = np.array([0.25, 0.25, 0, 0, 0.25, 0.25, 0, 0], np.float32)
     _, inds, _ = _const_route(oracle, cb, top_k=2, n_group=2, topk_group=1)
-    assert inds[0].tolist() == [0, 1]
+    assert inds[0].tolist() == [4, 5]
+
+
+def _argpartition_route(sel, n_group, topk_group, k):
+    """The group limit and top-k by numpy's ordering primitives: groups
+    zeroed = the first n_group - topk_group in (group score asc, index asc)
+    order (lexsort), experts chosen = the first k in (sel desc, index asc)."""
+    E = sel.size
+    G = E // n_group
+    sel = sel.astype(np.float32).copy()
+    if n_group > 1:
+        top2 = np.sort(sel.reshape(n_group, G), axis=1)[:, -2:]
+        gs = (top2[:, 1] + top2[:, 0]).astype(np.float32)
+        zero = np.lexsort((np.arange(n_group), gs))[:n_group - topk_group]
+        for g in zero:
+            sel[g * G:(g + 1) * G] = 0.0
+    return np.lexsort((np.arange(E), -sel))[:k]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_route_group_limit_matches_argpartition_order(oracle, seed):
+    """Many tied group scores (biases from a small dyadic set): the oracle's
+    choice equals the comparator's, run by numpy's lexsort."""
+    rng = np.random.default_rng(300 + seed)
+    E, n_group = 32, 8
+    for topk_group in (1, 3, 5, 7):
+        cb = rng.choice(np.array([-0.25, 0.0, 0.125, 0.25], np.float32), E)
+        _, inds, _ = _const_route(oracle, cb, top_k=4, n_group=n_group, topk_group=topk_group)
+        sel = (np.float32(0.5) + cb).astype(np.float32)
+        want = _argpartition_route(sel, n_group, topk_group, 4)
+        assert inds[0].tolist() == want.tolist(), (topk_group, cb)
 
 
 # ------------------------------------------------------------------ block
