@@ -290,6 +290,35 @@ def test_greedy_next(gpu, fmx, V):
     assert offs.cpu().tolist() == [3, 4, 5, 6, 7]
 
 
+def test_checkpoint_safetensors_fixture_matches_oracle(gpu, fmx):
+    """The committed checkpoint that the safetensors library wrote under the
+    reference's key names (tests/golden/make_checkpoint.py: quantized
+    router, quantized shared-expert gate, q/k/v biases, quantized embedding
+    and lm_head), loaded by fmx_model_load: the prefill of a 20-token prompt
+    (every position's logits: the prefill GEMMs and the MoE prefill path)
+    and three decode steps (the decode kernels) against the CPU oracle's
+    logits committed beside it."""
+    import pathlib
+
+    import torch
+    from flashmlx_amd import model as M
+    g = pathlib.Path(__file__).resolve().parent / "golden"
+    ref = np.load(g / "ckpt_tiny_logits.npz")
+    lm = M.load_checkpoint(str(g / "ckpt_tiny"))
+    cfg = lm.cfg
+    dm = M.DecoderModel(cfg, lm, 1, 32, 20)
+    prompt = torch.from_numpy(ref["prompt"]).cuda()
+    got = from_dev_bf16(dm.forward(prompt, 0, last_only=False)).reshape(20, -1)
+    e = assert_close(got, ref["prefill_logits"], "fixture prefill logits")
+    for i in range(ref["steps"].shape[0]):
+        s = torch.from_numpy(ref["steps"][i]).cuda()
+        assert_close(from_dev_bf16(dm.forward(s, 20 + i)), ref["step_logits"][i], f"fixture step {i} logits")
+    torch.cuda.synchronize()
+    print(f"safetensors fixture: prefill logits {e}")
+    del dm
+    lm.close()
+
+
 def test_checkpoint_load_matches_memory(gpu, fmx, tmp_path):
     """A tiny stack written as an MLX checkpoint (per-expert arrays, "model."
     prefix, two shards, config.json) and read back by fmx_model_load gives

@@ -70,3 +70,33 @@ def test_checkpoint_index(fmx, tmp_path):
     bad.write_bytes(len(hdr).to_bytes(8, "little") + hdr + b"\0" * 8)
     assert lib.fmx_checkpoint_tensor(str(tmp_path).encode(), b"x", dt, shape, C.byref(nd)) == _l.FMX_ERR_ARG
     assert b"inconsistent" in lib.fmx_last_error()
+
+
+def test_safetensors_fixture_index(fmx):
+    """The committed checkpoint written by the safetensors library
+    (tests/golden/make_checkpoint.py): config.json parses with its keys,
+    and the loader's index finds every tensor under the reference's names
+    with the library's dtypes and shapes (the quantized router and shared
+    gate included: mlp.gate.scales, mlp.shared_expert_gate.scales)."""
+    import ctypes as C
+    import pathlib
+
+    from flashmlx_amd.model import config_from_json
+    d = pathlib.Path(__file__).resolve().parent / "golden" / "ckpt_tiny"
+    cfg, tie = config_from_json(str(d / "config.json"))
+    assert (cfg.hidden_size, cfg.num_hidden_layers, cfg.num_attention_heads, cfg.num_key_value_heads,
+            cfg.vocab_size) == (512, 1, 4, 1, 64) and tie is False
+    assert (cfg.moe.num_experts, cfg.moe.num_experts_per_tok, cfg.moe.moe_intermediate_size,
+            cfg.moe.shared_expert_intermediate_size, cfg.moe.quant_bits) == (4, 2, 128, 128, 4)
+    _l, lib = _lib()
+    dt = C.create_string_buffer(8)
+    shape = (C.c_int64 * 8)()
+    nd = C.c_int32()
+    want = {"layers.0.mlp.gate.weight": ("U32", [4, 64]), "layers.0.mlp.gate.scales": ("BF16", [4, 8]),
+            "layers.0.mlp.experts.3.down_proj.weight": ("U32", [512, 16]),
+            "layers.0.mlp.shared_expert_gate.biases": ("BF16", [1, 8]),
+            "layers.0.self_attn.k_proj.bias": ("BF16", [128]), "embed_tokens.scales": ("BF16", [64, 8]),
+            "norm.weight": ("BF16", [512]), "lm_head.weight": ("U32", [64, 64])}
+    for name, (dtype, shp) in want.items():
+        assert lib.fmx_checkpoint_tensor(str(d).encode(), name.encode(), dt, shape, C.byref(nd)) == 0, name
+        assert dt.value.decode() == dtype and list(shape[:nd.value]) == shp, (name, dt.value, shape[:nd.value])
