@@ -14,6 +14,7 @@
 // (batch_kv_cache.cpp:10-91, scheduler.cpp:556-576, :658-678).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <deque>
@@ -87,9 +88,12 @@ struct fmx_scheduler {
   std::deque<std::pair<int64_t, Request>> pending;
   int64_t next_id = 0;
   // active requests by id (ids grow with submission, so this is also the
-  // batch order of a decode step); touched by step only
+  // batch order of a decode step) and the free slots: touched by step only.
+  // Other threads read the counts: n_live = requests submitted and not yet
+  // completed (pending, being prefilled or active), n_active = active.size()
   std::map<int64_t, Request> active;
   std::vector<int> free_slots;
+  std::atomic<int64_t> n_live{0}, n_active{0};
   std::mutex completed_mu;
   std::vector<int64_t> completed;
   // decode step of batch B (forward + argmax) as a HIP graph, captured on
@@ -191,7 +195,11 @@ int prefill(fmx_scheduler& s, Request& r) {
       s.pc_free.pop_back();
     }
     e.tokens = r.prompt;
-    FMX_HIP(launch_kv_copy(kv_copy_args(s, e.kv, r.slot, n - 1, 0), s.stream));
+    const hipError_t ce = launch_kv_copy(kv_copy_args(s, e.kv, r.slot, n - 1, 0), s.stream);
+    if (ce != hipSuccess) {
+      s.pc_free.push_back(e.kv);  // the evicted (or free) buffer stays the cache's
+      return fail(FMX_ERR_HIP, "launch_kv_copy: %s", hipGetErrorString(ce));
+    }
     s.pc.push_back(std::move(e));
   }
   FMX_HIP(hipStreamSynchronize(s.stream));
@@ -328,6 +336,7 @@ int fmx_scheduler_submit(fmx_scheduler* s, const int32_t* prompt, int64_t n, int
     std::lock_guard<std::mutex> lock(s->pending_mu);
     const int64_t id = s->next_id++;
     s->pending.emplace_back(id, std::move(r));
+    s->n_live.fetch_add(1);
     *request_id = id;
   }
   clear_error();
@@ -346,26 +355,39 @@ int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, 
     ++n;
   };
   std::vector<int64_t> done;
-  // 1. admit pending requests while slots are free (scheduler.cpp:28-42)
-  {
-    std::lock_guard<std::mutex> lock(s->pending_mu);
-    while (!s->pending.empty() && !s->free_slots.empty()) {
-      const int64_t id = s->pending.front().first;
-      Request r = std::move(s->pending.front().second);
+  // 1. admit pending requests while slots are free (scheduler.cpp:28-42):
+  // each is taken off the queue under the lock and prefilled outside it, so
+  // submit never waits for a prefill
+  while (!s->free_slots.empty()) {
+    int64_t id;
+    Request r;
+    {
+      std::lock_guard<std::mutex> lock(s->pending_mu);
+      if (s->pending.empty()) break;
+      id = s->pending.front().first;
+      r = std::move(s->pending.front().second);
       s->pending.pop_front();
-      r.slot = s->free_slots.back();
-      s->free_slots.pop_back();
-      const int rc = prefill(*s, r);
-      if (rc) {
-        s->free_slots.push_back(r.slot);
-        *n_new = n;
-        return rc;
-      }
-      emit(id, r.next);
-      // a request for one token is done after its prefill
-      if (r.generated >= r.max_tokens) done.push_back(id);
-      s->active.emplace(id, std::move(r));
     }
+    r.slot = s->free_slots.back();
+    s->free_slots.pop_back();
+    const int rc = prefill(*s, r);
+    if (rc) {
+      // the request goes back to the head of the queue, its slot back to
+      // the pool: a later step retries it, nothing is lost
+      s->free_slots.push_back(r.slot);
+      r.slot = -1;
+      {
+        std::lock_guard<std::mutex> lock(s->pending_mu);
+        s->pending.emplace_front(id, std::move(r));
+      }
+      *n_new = n;
+      return rc;
+    }
+    emit(id, r.next);
+    // a request for one token is done after its prefill
+    if (r.generated >= r.max_tokens) done.push_back(id);
+    s->active.emplace(id, std::move(r));
+    s->n_active.fetch_add(1);
   }
   // 2. one decode step of every request still decoding (scheduler.cpp:44-69)
   std::vector<Request*> live;
@@ -393,7 +415,9 @@ int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, 
       auto it = s->active.find(id);
       s->free_slots.push_back(it->second.slot);
       s->active.erase(it);
+      s->n_active.fetch_sub(1);
       s->completed.push_back(id);
+      s->n_live.fetch_sub(1);
     }
   }
   *n_new = n;
@@ -401,15 +425,9 @@ int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, 
   return FMX_OK;
 }
 
-int fmx_scheduler_has_work(fmx_scheduler* s) {
-  if (!s) return 0;
-  std::lock_guard<std::mutex> lock(s->pending_mu);
-  return !s->pending.empty() || !s->active.empty();
-}
+int fmx_scheduler_has_work(fmx_scheduler* s) { return s && s->n_live.load() > 0; }
 
-int64_t fmx_scheduler_active_count(const fmx_scheduler* s) {
-  return s ? static_cast<int64_t>(s->active.size()) : 0;
-}
+int64_t fmx_scheduler_active_count(const fmx_scheduler* s) { return s ? s->n_active.load() : 0; }
 
 int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_t capacity, int64_t* n) {
   if (!s || !n || (capacity > 0 && !request_ids)) return fail(FMX_ERR_ARG, "NULL argument");

@@ -211,14 +211,19 @@ int fmx_scheduler_submit(fmx_scheduler* s, const int32_t* prompt, int64_t n, int
  * i < *n_new (a request admitted in this step gets its first token and its
  * second); capacity >= 2 * n_slots. A request finishes with exactly
  * max_tokens tokens (the reference decodes one more past its first token
- * when max_tokens is 1). */
+ * when max_tokens is 1). One thread steps; a queued request is taken off
+ * the queue under its lock and prefilled outside it, so submit does not wait
+ * for prefills. A prefill that fails puts its request back at the head of
+ * the queue (its slot freed) and step returns the error; the tokens emitted
+ * before it in that step are in the outputs (*n_new). */
 int fmx_scheduler_step(fmx_scheduler* s, int64_t* request_ids, int32_t* tokens, int64_t capacity,
                        int64_t* n_new);
 
 /* BatchScheduler::has_work / active_count / drain_completed
- * (scheduler.cpp:87-101): queued or active requests (1/0); active requests;
- * ids of requests finished since the last drain (up to capacity, oldest
- * first). */
+ * (scheduler.cpp:87-101): requests submitted and not yet finished (1/0);
+ * active requests; ids of requests finished since the last drain (up to
+ * capacity, oldest first). Safe to call from any thread while another
+ * steps. */
 int fmx_scheduler_has_work(fmx_scheduler* s);
 int64_t fmx_scheduler_active_count(const fmx_scheduler* s);
 int fmx_scheduler_drain_completed(fmx_scheduler* s, int64_t* request_ids, int64_t capacity,

@@ -166,6 +166,54 @@ def test_scheduler_eight_slots(gpu, fmx):
     sched.close()
 
 
+def test_scheduler_submit_from_another_thread(gpu, fmx):
+    """submit, has_work and active_count from a second host thread while
+    the main thread steps (the reference's Python threads feed the engine
+    loop the same way): every request completes once, with the tokens of
+    the request generated alone."""
+    import threading
+    import time
+
+    import torch
+    from flashmlx_amd import model as M
+    cfg = _tiny_cfg()
+    w = M.synthetic_model(cfg, 49)
+    rng = np.random.default_rng(13)
+    reqs = [(rng.integers(0, cfg.vocab_size, size=int(rng.integers(1, 15))).tolist(), int(rng.integers(2, 7)))
+            for _ in range(10)]
+    sched = M.BatchScheduler(cfg, w, 4, 24, 14)
+    ids, seen_counts = {}, []
+    first = sched.submit(*reqs[0])
+    ids[first] = 0
+
+    def feeder():
+        for i in range(1, len(reqs)):
+            time.sleep(0.002)
+            ids[sched.submit(*reqs[i])] = i
+            seen_counts.append((sched.has_work(), sched.active_count()))
+
+    th = threading.Thread(target=feeder)
+    th.start()
+    toks, completed, t0 = {}, [], time.monotonic()
+    while th.is_alive() or sched.has_work():
+        assert time.monotonic() - t0 < 60
+        if not sched.has_work():
+            time.sleep(0.0005)  # the feeder is between submissions
+            continue
+        for rid, t in sched.step().items():
+            toks.setdefault(rid, []).extend(t)
+        completed += sched.drain_completed()
+    th.join()
+    completed += sched.drain_completed()
+    torch.cuda.synchronize()
+    assert sorted(completed) == sorted(ids) and len(ids) == len(reqs)
+    assert len(seen_counts) == len(reqs) - 1 and all(0 <= a <= 4 for _, a in seen_counts)
+    for rid, i in ids.items():
+        p, n = reqs[i]
+        assert toks[rid] == _alone(cfg, w, p, n, 24), (i, p, n)
+    sched.close()
+
+
 def test_scheduler_refusals(gpu, fmx):
     """Sampling, over-long prompts, budgets past the context and tokens
     outside the vocabulary are refused at submit; nothing is queued."""
