@@ -157,6 +157,7 @@ def cpu_baseline(wl, y_gpu, inds_gpu, seconds: float):
         "cores": nproc,
         "kind": "port",
         "sample": sample,
+        "short_sample": f"oracle MoE block, {per_call}-token calls",
         "single_thread_value": round(n1 * per_call / e1, 3),
         "cpu_model": model,
         "nproc": os.cpu_count(),
@@ -907,6 +908,38 @@ def compact_config(key: str, c: dict) -> dict:
     return {k: v for k, v in o.items() if v is not None}
 
 
+ROW_FIELDS = {
+    "moe": "us/layer, kernel frac, layer frac (HBM decode, MFMA prefill), U",
+    "stack": "ms/step, HBM frac, tok/s, tokens ok",
+    "nemotron": "us/layer, frac, rel L2, routing exact",
+    "ops": "us/call",
+}
+
+
+def config_row(c: dict):
+    """A compact config record (compact_config) as the short array that
+    ROW_FIELDS describes."""
+    if "us_per_layer" not in c and "decode_ms_per_step" not in c:  # the standalone operators
+        short = lambda k: k.replace("quantized_matmul", "qmm").replace("gather_qmm", "gqmm").replace(  # noqa: E731
+            "_decode", "").replace("_prefill", "")
+        return {short(k): v["us"] for k, v in c.items()}
+    if "decode_ms_per_step" in c:
+        return [c["decode_ms_per_step"], c.get("frac"), c["value"],
+                bool(c.get("graph_tokens_equal_eager")) and bool(c.get("sched_tokens_equal_alone_b1"))]
+    if "routing_bitexact" in c:
+        return [c["us_per_layer"], c.get("frac"), _r(c.get("parity_rel_l2"), 6), bool(c["routing_bitexact"])]
+    return [c["us_per_layer"], c.get("frac"), c.get("layer_mfma_frac", c.get("layer_hbm_frac")), c.get("U")]
+
+
+def short_cpu(cpu):
+    """The CPU baseline object of the printed line (the full one, with the
+    single-thread figure and the sample's counts, goes to stderr)."""
+    if not cpu:
+        return cpu
+    return {"value": cpu["value"], "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"],
+            "sample": cpu["short_sample"], "single_thread_value": cpu["single_thread_value"]}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -991,11 +1024,12 @@ def main():
     if args.ops == "all":
         configs["ops_qwen15"] = measure_ops()
 
-    cpu, parity = None, None
+    cpu, parity, full_cpu = None, None, None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle")
         try:
             cpu, parity = cpu_baseline(wl, y_head, inds_head, args.cpu_seconds)
+            full_cpu = cpu
         except Exception as e:  # noqa: BLE001
             log(f"CPU baseline failed: {e}")
 
@@ -1011,44 +1045,40 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) bf16 activations, N(0,0.02) weights quantized affine 4-bit g64",
+        "data": "synthetic: seeded N(0,1) bf16 x, N(0,0.02) weights quantized affine 4-bit g64",
         "config": {
             "workload": head["workload"],
             "key": wl.key,
             "tokens": wl.tokens,
-            "hidden": wl.model["hidden"],
-            "experts": wl.model["n_experts"],
-            "top_k": wl.model["top_k"],
-            "moe_intermediate": wl.model["inter"],
-            "shared_intermediate": wl.model["shared_inter"],
             "seed": wl.seed,
             "layer_copies": R,
-            "hip_graph": True,
-            "timing": f"median of {args.trials} trials of {K} steps, every graph replayed first",
-            "parallelism": "single GPU",
+            "timing": f"HIP graphs, median of {args.trials} trials of {K} steps",
         },
         "roofline": head["roofline"],
-        "cpu_baseline": cpu,
+        "cpu_baseline": short_cpu(cpu),
     }
     lay = head["layer"]
-    out["layer"] = {"us": head["us_per_layer"], "U": lay["unique_experts"],
-                    "algorithmic_bytes": lay["algorithmic_bytes"], "hbm_frac": lay["hbm_frac"],
-                    "stage_us": lay["stage_us"], "trial_ms": head["trial_ms"]}
+    out["layer"] = {"us": head["us_per_layer"], "U": lay["unique_experts"], "hbm_frac": lay["hbm_frac"]}
     if parity:
-        out["parity"] = {k: (_r(v, 8) if isinstance(v, float) else v) for k, v in parity.items()}
-    out["configs"] = {k: compact_config(k, c) for k, c in configs.items()}
+        out["parity"] = {"rel_l2": _r(parity["rel_l2"], 6), "max_abs": _r(parity["max_abs"], 6),
+                         "within_tol": parity["within_rtol_2e-2_atol_1e-2"],
+                         "routing_bitexact": parity["routing_bitexact"]}
+    compact = {k: compact_config(k, c) for k, c in configs.items()}
+    # every other config's headline figures as short arrays (fields in ROW_FIELDS), so that the
+    # whole line stays within about 2 KB
+    out["configs"] = {k: config_row(c) for k, c in compact.items()}
+    out["config_fields"] = ROW_FIELDS
     if args.detail:
         full = dict(out, layer=head["layer"], trial_ms=head["trial_ms"], wall_s=head["wall_s"],
-                    parity=parity, configs=configs)
+                    parity=parity, configs=configs, cpu_baseline_full=full_cpu)
         with open(args.detail, "w") as f:
             json.dump(full, f, indent=1)
         log(f"full results written to {args.detail}")
     for k, c in configs.items():  # every config's full record on stderr, one line each
         log(f"detail {k}: " + json.dumps(c))
-    for k, c in out["configs"].items():  # then a short line each
-        if "frac" in c:
-            t = f"{c['us_per_layer']} us/layer" if "us_per_layer" in c else f"{c['decode_ms_per_step']} ms/step"
-            log(f"summary {k}: {c['value']} {c['unit']}, {t}, roofline frac {c['frac']}")
+    log("detail cpu_baseline: " + json.dumps(full_cpu))
+    for k, c in compact.items():  # then a short line each
+        log(f"summary {k}: " + json.dumps(c, separators=(",", ":")))
     print(json.dumps(out, separators=(",", ":")), flush=True)
 
 
