@@ -258,6 +258,11 @@ _SIGS = {
     "fmx_greedy_next": (
         C.c_int,
         [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p]),
+    "fmx_rope_table": (C.c_int, [C.c_void_p, C.c_int64, C.c_int64, C.c_float, C.c_void_p]),
+    "fmx_attention_decode": (
+        C.c_int,
+        [C.c_void_p, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
+         C.c_int64, C.c_void_p, C.c_float, C.c_void_p, C.c_void_p]),
     "fmx_scheduler_create": (
         C.c_int,
         [P(FmxModelConfig), P(FmxModelWeights), C.c_int64, C.c_int64, C.c_int64, C.c_void_p,

@@ -267,20 +267,7 @@ int fmx_model_workspace_init(const fmx_model_config* cfg, void* workspace, size_
   const ModelLayout M = model_layout(*cfg, 1, static_cast<char*>(workspace));
   if (workspace_bytes < M.total) return fail(FMX_ERR_WORKSPACE, "workspace smaller than one token's");
   const Dims d = dims(*cfg);
-  // (cos, sin) of p * theta^(-2i/hd) in fp64, rounded to fp32
-  const int64_t half = d.hd / 2;
-  std::vector<float> cs(static_cast<size_t>(d.P * half * 2));
-  for (int64_t i = 0; i < half; ++i) {
-    const double inv = std::pow(static_cast<double>(cfg->rope_theta), -(2.0 * static_cast<double>(i)) /
-                                                                          static_cast<double>(d.hd));
-    for (int64_t p = 0; p < d.P; ++p) {
-      const double th = static_cast<double>(p) * inv;
-      cs[(p * half + i) * 2] = static_cast<float>(std::cos(th));
-      cs[(p * half + i) * 2 + 1] = static_cast<float>(std::sin(th));
-    }
-  }
-  FMX_HIP(hipMemcpyAsync(M.rope, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, stream));
-  FMX_HIP(hipStreamSynchronize(stream));  // the host table is released on return
+  FMX_RC(fmx_rope_table(M.rope, d.P, d.hd, cfg->rope_theta, stream_));
   FMX_RC(fmx_moe_workspace_init(M.moe_ws, workspace_bytes - (static_cast<char*>(M.moe_ws) -
                                                              static_cast<char*>(workspace)),
                                 stream_));
@@ -483,6 +470,59 @@ int fmx_model_workspace_hidden(const fmx_model_config* cfg, int64_t n_tokens, co
   if (!workspace || !hidden) return fail(FMX_ERR_ARG, "NULL argument");
   if (n_tokens < 1 || n_tokens > 65536) return fail(FMX_ERR_SHAPE, "n_tokens=%lld", (long long)n_tokens);
   *hidden = model_layout(*cfg, n_tokens, static_cast<char*>(const_cast<void*>(workspace))).h;
+  return ok();
+}
+
+int fmx_rope_table(float* rope_cs, int64_t n_pos, int64_t head_dim, float rope_theta, fmx_stream stream_) {
+  if (n_pos < 1 || n_pos > kMaxPositions || head_dim < 2 || head_dim % 2 || head_dim > kAttnMaxHd)
+    return fail(FMX_ERR_SHAPE, "n_pos must be in [1, %lld], head_dim even and at most %d",
+                (long long)kMaxPositions, kAttnMaxHd);
+  if (!rope_cs) return fail(FMX_ERR_ARG, "NULL table");
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  // (cos, sin) of p * theta^(-2i/hd) in fp64, rounded to fp32
+  const int64_t half = head_dim / 2;
+  std::vector<float> cs(static_cast<size_t>(n_pos * half * 2));
+  for (int64_t i = 0; i < half; ++i) {
+    const double inv = std::pow(static_cast<double>(rope_theta), -(2.0 * static_cast<double>(i)) /
+                                                                     static_cast<double>(head_dim));
+    for (int64_t p = 0; p < n_pos; ++p) {
+      const double th = static_cast<double>(p) * inv;
+      cs[(p * half + i) * 2] = static_cast<float>(std::cos(th));
+      cs[(p * half + i) * 2 + 1] = static_cast<float>(std::sin(th));
+    }
+  }
+  FMX_HIP(hipMemcpyAsync(rope_cs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice, stream));
+  FMX_HIP(hipStreamSynchronize(stream));  // the host table is released on return
+  return ok();
+}
+
+int fmx_attention_decode(const void* qkv, int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                         const float* rope_cs, void* k_cache, void* v_cache, int64_t max_seq,
+                         const int32_t* offsets, float scale, void* out, fmx_stream stream_) {
+  if (batch < 0 || batch > 65535 || n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads || n_heads > 65535 ||
+      head_dim < 8 || max_seq < 1)
+    return fail(FMX_ERR_SHAPE, "batch, heads (n_heads a multiple of n_kv_heads), head_dim or max_seq");
+  if (head_dim > kAttnSplitMaxHd || head_dim % 8 || kWave % (head_dim / 8) || max_seq > kAttnMaxSeq)
+    return fail(FMX_ERR_UNSUPPORTED, "head_dim must be at most %d with 64 %% (head_dim / 8) == 0 and max_seq "
+                "at most %lld", kAttnSplitMaxHd, (long long)kAttnMaxSeq);
+  if (batch == 0) return ok();
+  if (!qkv || !rope_cs || !k_cache || !v_cache || !offsets || !out) return fail(FMX_ERR_ARG, "NULL buffer");
+  AttnArgs aa{};
+  aa.qkv = static_cast<const uint16_t*>(qkv);
+  aa.cs = rope_cs;
+  aa.L = 1;
+  aa.nh = static_cast<int>(n_heads);
+  aa.nkv = static_cast<int>(n_kv_heads);
+  aa.hd = static_cast<int>(head_dim);
+  aa.kc = static_cast<uint16_t*>(k_cache);
+  aa.vc = static_cast<uint16_t*>(v_cache);
+  aa.max_seq = max_seq;
+  aa.offs = offsets;
+  aa.n_slots = static_cast<int>(batch);
+  aa.scale = scale;
+  aa.out = static_cast<uint16_t*>(out);
+  aa.ldo = n_heads * head_dim;
+  FMX_HIP(launch_attn(aa, static_cast<int>(batch), static_cast<hipStream_t>(stream_)));
   return ok();
 }
 

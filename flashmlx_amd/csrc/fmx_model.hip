@@ -415,11 +415,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
 // workgroup per (token t, q head h), the keys 0 .. p in S = min(
 // kAttnSplitMax, ceil((p + 1) / kAttnSplitKeys)) contiguous ranges
 // [nk s / S, nk (s + 1) / S), wave s taking range s. At batch 1 the
-// kernel's time is one workgroup's chain of memory round trips, so a wave
-// issues everything its first 64 keys need at once, in the order it uses
-// them (the rotation's inputs, 64 key rows, then 16-byte value chunks of 32
-// keys: 29 loads, within the 63 a wave can have outstanding; the next 32
-// keys' values follow the scores), all as whole rows. In range s:
+// kernel's time is one workgroup's chain of memory round trips, so the
+// ranges are short (up to 16 waves, 32 keys each up to 512 keys) and a wave
+// issues everything its first 32 keys need at once, in the order it uses
+// them (the rotation's inputs, then key rows and 16-byte value chunks: at
+// most 21 loads), all as whole rows: one round trip before the arithmetic.
+// In range s:
 //   s_j = scale * (((P_0 + P_1) + ...) + P_{hd/8-1}), P_c = sum_{d in chunk
 //         c} q_d k_jd (8 dimensions in order; exact bf16 products in fp32):
 //         lane (key, c) forms P_c, an LDS transpose hands a key's P_c to one
@@ -439,8 +440,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_kernel(AttnArgs a) {
 // value (position p, the last key of the last range) are used from LDS, and
 // the first q head of each kv group writes them into the caches (no
 // workgroup reads position p from the cache in this launch).
-constexpr int kAttnValKeys = 8;  // keys per class and value batch (32 keys a batch)
+constexpr int kAttnRound = 32;   // keys per score round and per value batch
+constexpr int kAttnValKeys = kAttnRound / 4;  // keys per class in a value batch
 constexpr int kAttnPcStride = 17;  // LDS floats per key of a round's chunk sums (16 + 1: no bank conflicts)
+static_assert(kAttnSplitKeys == kAttnRound, "a range of the minimum length is one round");
 
 __device__ inline int attn_splits(int nk) {
   return min(kAttnSplitMax, (nk + kAttnSplitKeys - 1) / kAttnSplitKeys);
@@ -454,13 +457,27 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
   __shared__ double s_f[kAttnSplitMax];
   const int t = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const int rep = a.nh / a.nkv, g = h / rep;
+  const int half = a.hd / 2, nch = a.hd / 8;
+
+  // 1. the rotation's inputs that do not depend on the position: thread
+  // i < hd takes pair i mod hd/2 of q (i < hd/2) or of the new key; thread
+  // d < hd the new value's element d
+  const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
+  const bool rot = tid < a.hd;
+  const int hd_i = tid % half;
+  uint16_t rx1 = 0, rx2 = 0, rv = 0;
+  if (rot) {
+    const uint16_t* src = row + (tid < half ? h : a.nh + g) * a.hd;
+    rx1 = src[hd_i];
+    rx2 = src[hd_i + half];
+    rv = row[(a.nh + a.nkv + g) * a.hd + tid];
+  }
   const int p = token_pos(a.offs, a.off, t, 0, a.max_seq);
   const int nk = p + 1, S = attn_splits(nk);
-  const int rep = a.nh / a.nkv, g = h / rep;
   const int64_t cbase = (cache_slot(a.slots, a.n_slots, t) * a.nkv + g) * a.max_seq * a.hd;
   uint16_t* kb = a.kc + cbase;
   uint16_t* vb = a.vc + cbase;
-  const int half = a.hd / 2, nch = a.hd / 8;
   // this wave's range; keys before jg come from the cache (p, the last key
   // of the last range, from LDS)
   const bool active = wave < S;
@@ -469,47 +486,38 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
   const bool last = wave == S - 1;
   const int jg = last ? j1 - 1 : j1;
   const int jclamp = max(jg - 1, 0);  // loads past the range re-read its last cached key
-
-  // 1. the rotation's inputs: thread i < hd takes pair i mod hd/2 of q
-  // (i < hd/2) or of the new key; thread d < hd the new value's element d
-  const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
-  const bool rot = tid < a.hd;
-  const int hd_i = tid % half;
-  uint16_t rx1 = 0, rx2 = 0, rv = 0;
   float rc = 0.0f, rsn = 0.0f;
   if (rot) {
-    const uint16_t* src = row + (tid < half ? h : a.nh + g) * a.hd;
     const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
-    rx1 = src[hd_i];
-    rx2 = src[hd_i + half];
     rc = cs[2 * hd_i];
     rsn = cs[2 * hd_i + 1];
-    rv = row[(a.nh + a.nkv + g) * a.hd + tid];
   }
-  // 2. the first key round (64 keys: instruction c brings keys c * kpi +
+  // 2. the first key round (32 keys: instruction c brings keys c * kpi +
   // lane / nch, chunk lane mod nch) and value batch (lane (c, i): keys j0 +
   // c + 4u, chunk i)
   const int kc = lane >> 4, dc = lane & 15;
   const bool vlane = dc < nch;
-  const int kpi = kWave / nch;                   // keys per load instruction
-  const int kk = lane / nch, kch = lane % nch;  // this lane's key in it, its chunk
-  u32x4_t kv[16], vv[kAttnValKeys], vw[kAttnValKeys];
+  const int kpi = kWave / nch;                    // keys per load instruction
+  const int kk = lane / nch, kch = lane % nch;   // this lane's key in it, its chunk
+  const int nkin = max(1, kAttnRound / kpi);     // load instructions per round
+  constexpr int kMaxKin = kAttnRound * kAttnSplitMaxHd / 8 / kWave;
+  u32x4_t kv[kMaxKin], vv[kAttnValKeys];
   auto load_keys = [&](int jb) {
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-      if (c < nch)
+    for (int c = 0; c < kMaxKin; ++c)
+      if (c < nkin)
         kv[c] = *reinterpret_cast<const u32x4_t*>(kb + static_cast<int64_t>(min(jb + c * kpi + kk, jclamp)) * a.hd +
                                                   8 * kch);
   };
-  auto load_values = [&](u32x4_t* V, int jb) {
+  auto load_values = [&](int jb) {
 #pragma unroll
     for (int u = 0; u < kAttnValKeys; ++u)
-      V[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(min(jb + kc + 4 * u, jclamp)) * a.hd +
-                                               8 * min(dc, nch - 1));
+      vv[u] = *reinterpret_cast<const u32x4_t*>(vb + static_cast<int64_t>(min(jb + kc + 4 * u, jclamp)) * a.hd +
+                                                8 * min(dc, nch - 1));
   };
   if (active && j0 < jg) {
     load_keys(j0);
-    load_values(vv, j0);
+    load_values(j0);
   }
 
   // 3. rotation (one rounding of the fp64 value), the new value
@@ -534,37 +542,38 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
   }
 
   // 4. scores (LDS per wave: the range's fp64 weights, its fp32 scores,
-  // and the chunk sums of one 64-key round)
-  const int kmax = max(kAttnSplitKeys, static_cast<int>((a.max_seq + kAttnSplitMax - 1) / kAttnSplitMax));
+  // and the chunk sums of one 32-key round)
+  const int kmax = attn_split_range_keys(a.max_seq);
   double* s_e = reinterpret_cast<double*>(s_at) + static_cast<size_t>(wave) * kmax;
   float* s_s = reinterpret_cast<float*>(s_at + static_cast<size_t>(kAttnSplitMax) * kmax * 8) +
                static_cast<size_t>(wave) * kmax;
   float* s_pc = reinterpret_cast<float*>(s_at + static_cast<size_t>(kAttnSplitMax) * kmax * 12) +
-                static_cast<size_t>(wave) * kWave * kAttnPcStride;
+                static_cast<size_t>(wave) * kAttnRound * kAttnPcStride;
   float m = -__builtin_huge_valf();
   if (active) {
     // this lane's chunk of q, 8 dimensions
     float qc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) qc[e] = s_q[8 * kch + e];
-    for (int jb = j0; jb < jg; jb += kWave) {
+    for (int jb = j0; jb < jg; jb += kAttnRound) {
       if (jb != j0) load_keys(jb);
 #pragma unroll
-      for (int c = 0; c < 16; ++c) {
-        if (c < nch) {
+      for (int c = 0; c < kMaxKin; ++c) {
+        const int key = c * kpi + kk;
+        if (c < nkin && key < kAttnRound) {
           float pc = 0.0f;
 #pragma unroll
           for (int mm = 0; mm < 4; ++mm) {
             pc = __builtin_fmaf(qc[2 * mm], bf16_to_f32(kv[c][mm] & 0xffffu), pc);
             pc = __builtin_fmaf(qc[2 * mm + 1], bf16_to_f32(kv[c][mm] >> 16), pc);
           }
-          s_pc[(c * kpi + kk) * kAttnPcStride + kch] = pc;
+          s_pc[key * kAttnPcStride + kch] = pc;
         }
       }
       // the wave's LDS operations complete in order: each lane now sums its
       // key's chunks as the other lanes wrote them
       __builtin_amdgcn_wave_barrier();
-      if (jb + lane < jg) {
+      if (lane < kAttnRound && jb + lane < jg) {
         float acc = s_pc[lane * kAttnPcStride];
         for (int c = 1; c < nch; ++c) acc += s_pc[lane * kAttnPcStride + c];
         const float sc = acc * a.scale;
@@ -573,7 +582,7 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
       }
       __builtin_amdgcn_wave_barrier();
     }
-    if (last && lane == (p - j0) % kWave) {  // the new key, from LDS (the lane that takes key p below)
+    if (last && lane == (p - j0) % kAttnRound) {  // the new key, from LDS (the lane that takes key p below)
       float acc = 0.0f;
       for (int c = 0; c < nch; ++c) {
         float pc = 0.0f;
@@ -584,13 +593,12 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
       s_s[p - j0] = sc;
       m = fmaxf(m, sc);
     }
-    // the next value batch, in flight during the softmax
-    if (j0 + 4 * kAttnValKeys < jg) load_values(vw, j0 + 4 * kAttnValKeys);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     // each lane reads back only the scores it wrote
-    for (int jk = j0 + lane; jk < j1; jk += kWave)
-      s_e[jk - j0] = exp_det(static_cast<double>(s_s[jk - j0]) - static_cast<double>(m));
+    if (lane < kAttnRound)
+      for (int jk = j0 + lane; jk < j1; jk += kAttnRound)
+        s_e[jk - j0] = exp_det(static_cast<double>(s_s[jk - j0]) - static_cast<double>(m));
   }
   __syncthreads();
 
@@ -599,7 +607,8 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
     double nv[8], dv = 0.0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) nv[i] = 0.0;
-    auto accum = [&](const u32x4_t* V, int jb) {
+    for (int jb = j0; jb < jg; jb += kAttnRound) {
+      if (jb != j0) load_values(jb);
 #pragma unroll
       for (int u = 0; u < kAttnValKeys; ++u) {
         const int j = jb + kc + 4 * u;
@@ -608,23 +617,13 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
           dv += e;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            nv[2 * q] = __builtin_fma(e, static_cast<double>(bf16_to_f32(V[u][q] & 0xffffu)), nv[2 * q]);
-            nv[2 * q + 1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(V[u][q] >> 16)), nv[2 * q + 1]);
+            nv[2 * q] = __builtin_fma(e, static_cast<double>(bf16_to_f32(vv[u][q] & 0xffffu)), nv[2 * q]);
+            nv[2 * q + 1] = __builtin_fma(e, static_cast<double>(bf16_to_f32(vv[u][q] >> 16)), nv[2 * q + 1]);
           }
         }
         // one key's fp64 conversions at a time (converting a batch ahead
         // would need more registers than the kernel has)
         __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    for (int jb = j0; jb < jg; jb += 4 * kAttnValKeys) {
-      if (jb == j0) {
-        accum(vv, jb);
-      } else if (jb == j0 + 4 * kAttnValKeys) {
-        accum(vw, jb);
-      } else {
-        load_values(vv, jb);
-        accum(vv, jb);
       }
     }
     if (last && kc == (p - j0) % 4) {  // the new key's value, last of its class
@@ -692,8 +691,10 @@ __global__ __launch_bounds__(1024) void greedy_kernel(GreedyArgs a) {
   float best = -__builtin_huge_valf();
   int64_t bi = a.V;
   // a thread takes 16-byte chunks c = tid, tid + 1024, ... (index order, so
-  // the first maximum it sees is its lowest), loads of 4 chunks in flight;
-  // rows that are not 16-byte aligned or a multiple of 8 take the scalar loop
+  // the first maximum it sees is its lowest), loads of 4 chunks in flight
+  // (20 in flight measured no faster: one workgroup's row is bound by what
+  // one CU draws from HBM, about 25 GB/s); rows that are not 16-byte aligned
+  // or a multiple of 8 take the scalar loop
   const bool vec = (a.ld % 8 == 0) && (a.V % 8 == 0) && (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0);
   if (vec) {
     const u32x4_t* rv = reinterpret_cast<const u32x4_t*>(row);
@@ -830,9 +831,9 @@ hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream) {
   if (a.qkv) {
     if (a.L != 1 || a.hd > kAttnSplitMaxHd || a.hd % 8 || kWave % (a.hd / 8)) return hipErrorInvalidValue;
     // LDS: per wave, a range's fp64 weights and fp32 scores, one round's chunk sums
-    const int64_t keys = std::max<int64_t>(kAttnSplitKeys, (a.max_seq + kAttnSplitMax - 1) / kAttnSplitMax);
+    const int64_t keys = attn_split_range_keys(a.max_seq);
     hipLaunchKernelGGL(attn_split_kernel, dim3(T, a.nh), dim3(kWave * kAttnSplitMax),
-                       static_cast<size_t>(kAttnSplitMax * (keys * 12 + kWave * kAttnPcStride * 4)), stream, a);
+                       static_cast<size_t>(kAttnSplitMax * (keys * 12 + kAttnRound * kAttnPcStride * 4)), stream, a);
     return hipGetLastError();
   }
   const dim3 grid(T, a.nh);

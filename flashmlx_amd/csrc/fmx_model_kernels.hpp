@@ -100,9 +100,14 @@ struct AttnArgs {
 // single-token forwards (qkv set; head size at most kAttnSplitMaxHd): a
 // query's keys in min(kAttnSplitMax, ceil(keys / kAttnSplitKeys))
 // contiguous ranges, one wave each
-constexpr int kAttnSplitMax = 8;
-constexpr int kAttnSplitKeys = 64;
+constexpr int kAttnSplitMax = 16;
+constexpr int kAttnSplitKeys = 32;
 constexpr int kAttnSplitMaxHd = 128;
+// the longest range of a cache of max_seq positions
+__host__ __device__ inline int attn_split_range_keys(int64_t max_seq) {
+  const int64_t r = (max_seq + kAttnSplitMax - 1) / kAttnSplitMax;
+  return static_cast<int>(r > kAttnSplitKeys ? r : kAttnSplitKeys);
+}
 size_t attn_lds_bytes(int64_t max_seq);
 hipError_t launch_attn(const AttnArgs& a, int T, hipStream_t stream);
 

@@ -251,6 +251,32 @@ void fmx_scheduler_free(fmx_scheduler* s);
 int fmx_greedy_next(const void* logits, int64_t batch, int64_t vocab, int64_t row_stride,
                     int32_t* ids, int32_t* offsets, int32_t advance, fmx_stream stream);
 
+/* RoPE table of the decode attention: rope_cs [n_pos][head_dim / 2][2] fp32
+ * on the device, (cos, sin) of p * theta^(-2i / head_dim) computed in fp64
+ * and rounded to fp32 (the table fmx_model_workspace_init builds; the
+ * frequencies of mx::fast::rope with base theta, model.cpp:875-876).
+ * Synchronises the stream before it returns. */
+int fmx_rope_table(float* rope_cs, int64_t n_pos, int64_t head_dim, float rope_theta, fmx_stream stream);
+
+/* Single-token attention of a decode step, as the decoder stack runs it
+ * (model.cpp:874-884: mx::fast::rope of q and k at the sequence's cache
+ * offset, traditional = false; the KV-cache append; mx::fast::
+ * scaled_dot_product_attention with no mask): for each sequence b at
+ * position p = offsets[b], q and the new key are rotated, the new key and
+ * value go to cache position p of slot b, and out[b] = softmax(q K^T scale) V
+ * over positions 0 .. p for every query head (its kv head: head /
+ * (n_heads / n_kv_heads)). qkv [batch, (n_heads + 2 n_kv_heads) head_dim]
+ * bf16 (the q heads, then k, then v; unrotated); rope_cs from
+ * fmx_rope_table with at least max_seq rows; k_cache, v_cache [batch]
+ * [n_kv_heads][max_seq][head_dim] bf16; offsets [batch] int32 on the device
+ * (clamped to [0, max_seq)); out [batch, n_heads head_dim] bf16.
+ * head_dim <= 128 with 64 % (head_dim / 8) == 0, max_seq <= 4096; other
+ * shapes: FMX_ERR_UNSUPPORTED. */
+int fmx_attention_decode(const void* qkv, int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                         int64_t head_dim, const float* rope_cs, void* k_cache, void* v_cache,
+                         int64_t max_seq, const int32_t* offsets, float scale, void* out,
+                         fmx_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

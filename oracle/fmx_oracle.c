@@ -1030,8 +1030,8 @@ int orc_sdpa(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const uint16_
 }
 
 /* The single-token attention of libfmx's split kernel (attn_split_kernel):
- * query l's keys 0 .. nk - 1 (nk = q_off + l + 1) in S = min(8, ceil(nk /
- * 64)) contiguous ranges [nk s / S, nk (s + 1) / S); in range s, m_s = the
+ * query l's keys 0 .. nk - 1 (nk = q_off + l + 1) in S = min(16, ceil(nk /
+ * 32)) contiguous ranges [nk s / S, nk (s + 1) / S); in range s, m_s = the
  * largest fp32 score, e_j = exp(s_j - m_s) in fp64 with the deterministic
  * exp, and over the key classes c = (j - j0) mod 4 (each in key order)
  * den_s = ((D_0 + D_1) + D_2) + D_3, D_c = sum e_j, and num_s likewise
@@ -1052,8 +1052,8 @@ int orc_sdpa_split(const uint16_t* q, int64_t L, int64_t nh, int64_t hd, const u
       const uint16_t* qv = q + (l * nh + h) * hd;
       const uint16_t* kb = kc + g * max_seq * hd;
       const uint16_t* vb = vc + g * max_seq * hd;
-      int64_t S = (nk + 63) / 64;
-      if (S > 8) S = 8;
+      int64_t S = (nk + 31) / 32;
+      if (S > 16) S = 16;
       float* s = (float*)malloc(sizeof(float) * nk);
       double* ms = (double*)malloc(sizeof(double) * S);
       double* dens = (double*)malloc(sizeof(double) * S);

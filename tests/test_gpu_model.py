@@ -81,7 +81,7 @@ def test_stack_tiny_single_sequence_decode(gpu, fmx, oracle):
     """One sequence (single-row decode steps: the q/k/v projection forms its
     input norm itself and the o projection adds the previous MoE output to
     the residual; attention in the split kernel's key ranges, a 70-token
-    context spanning two ranges): each step's logits against the oracle, and
+    context spanning three ranges): each step's logits against the oracle, and
     the residual stream after a final prefill-path step."""
     import torch
     from flashmlx_amd import model as M

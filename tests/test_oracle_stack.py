@@ -204,7 +204,7 @@ def _numpy_attn(q, kc, vc, nk, scale, nkv):
 
 def test_sdpa_split_one_key_and_equal_keys(oracle):
     """The split order keeps the closed forms: one key gives its value, equal
-    keys the fp64 mean of the values (here over 3 ranges: 150 keys)."""
+    keys the fp64 mean of the values (here over 5 ranges: 150 keys)."""
     kc, vc = _cache(oracle, 2, 8, 64, 1)
     q = to_bf16(oracle, RNG.standard_normal((1, 4, 64)))
     out = oracle.sdpa_split(q, kc, vc, 0, 0.125)
@@ -220,9 +220,9 @@ def test_sdpa_split_one_key_and_equal_keys(oracle):
     assert (np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6).all()
 
 
-@pytest.mark.parametrize("nk", [1, 63, 64, 65, 129, 512, 513, 2500])
+@pytest.mark.parametrize("nk", [1, 31, 32, 33, 65, 300, 481, 512, 513, 2500])
 def test_sdpa_split_matches_numpy(oracle, nk):
-    """At range-count boundaries (1 range up to 64 keys, 8 from 449) and
+    """At range-count boundaries (1 range up to 32 keys, 16 from 481) and
     with one key's score far above the rest in the first range (every other
     range's sums then carry f_s << 1): within one bf16 ulp of numpy's fp64
     softmax and of the four-quarter order. A planted mistake (the ranges'
@@ -238,9 +238,9 @@ def test_sdpa_split_matches_numpy(oracle, nk):
     assert (np.abs(got - ref) <= np.abs(ref) * 2.0 ** -8 + 1e-6).all()
     quart = bf(oracle.sdpa(q, kc, vc, nk - 1, scale)[0]).astype(np.float64)
     assert (np.abs(got - quart) <= np.abs(quart) * 2.0 ** -8 + 1e-6).all()
-    if nk > 64:  # the planted mistake: unscaled range sums
+    if nk > 32:  # the planted mistake: unscaled range sums
         qf, kf, vf = (bf(a).astype(np.float64) for a in (q, kc, vc))
-        S = min(8, (nk + 63) // 64)
+        S = min(16, (nk + 31) // 32)
         s = kf[0, :nk] @ qf[0, 0] * scale
         num = den = 0.0
         for r in range(S):
