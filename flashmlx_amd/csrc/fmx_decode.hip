@@ -89,46 +89,48 @@ __device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0,
 // lower expert index, slots ordered (probability desc, index asc). The
 // tokens' dependent fp64 chains are interleaved; tokens ts[n] >= T are
 // computed on padding and not written. s_lg: every token's E (+1) logits.
+// Lane l takes the experts e = r + 64 i, r the 6-bit reverse of l: lane l
+// accumulates r's partial normaliser, and the DPP tree (adjacent lanes
+// first) then adds the partials r and r xor 32 first, r xor 16 next, .., the
+// association of the oracle's butterfly (w = 32, 16, .., 1).
 template <int NPER, int NT>
 __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uint16_t* s_lg, int lane,
                              uint32_t* s_inds) {
   const int E = a.E, ld = E + 1;
-  double lv[NT][NPER], ex[NT][NPER], m[NT], s[NT];
+  const int r = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(lane)) >> 26);
+  double ex[NT][NPER], m[NT], s[NT];
+  float lf[NT][NPER];
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int t = min(ts[n], a.T - 1);
-    m[n] = -__builtin_huge_val();
+    float mf = -__builtin_huge_valf();
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-      const int e = lane + 64 * i;
-      lv[n][i] = e < E ? static_cast<double>(bf16_to_f32(s_lg[t * ld + e])) : -__builtin_huge_val();
-      m[n] = fmax(m[n], lv[n][i]);
+      const int e = r + 64 * i;
+      lf[n][i] = e < E ? bf16_to_f32(s_lg[t * ld + e]) : -__builtin_huge_valf();
+      mf = fmaxf(mf, lf[n][i]);
     }
+    // bf16 logits are exact in fp32: the fp32 maximum is the fp64 one
+    m[n] = static_cast<double>(wave_max_f32(mf));
   }
-#pragma unroll
-  for (int n = 0; n < NT; ++n) m[n] = __ockl_wfred_max_f64(m[n]);
-  // lane l sums e = l, l + 64, ... in turn; six butterfly steps then give
-  // every lane the same total
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     s[n] = 0.0;
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-      const int e = lane + 64 * i;
-      ex[n][i] = e < E ? exp_det(lv[n][i] - m[n]) : 0.0;
+      const int e = r + 64 * i;
+      ex[n][i] = e < E ? exp_det(static_cast<double>(lf[n][i]) - m[n]) : 0.0;
       s[n] += ex[n][i];
     }
   }
 #pragma unroll
-  for (int w = 32; w >= 1; w >>= 1)
-#pragma unroll
-    for (int n = 0; n < NT; ++n) s[n] += __shfl_xor(s[n], w);
+  for (int n = 0; n < NT; ++n) s[n] = wave_sum_f64(s[n]);
   uint32_t key[NT][NPER];
 #pragma unroll
   for (int n = 0; n < NT; ++n)
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-      const int e = lane + 64 * i;
+      const int e = r + 64 * i;
       key[n][i] = 0u;
       if (e < E) {
         const uint16_t p = f64_to_bf16(ex[n][i] / s[n]);
@@ -153,7 +155,7 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
       for (int i = 0; i < NPER; ++i) best[n] = max(best[n], key[n][i]);
     }
 #pragma unroll
-    for (int n = 0; n < NT; ++n) best[n] = __ockl_wfred_max_u32(best[n]);
+    for (int n = 0; n < NT; ++n) best[n] = wave_max_u32(best[n]);
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
 #pragma unroll
@@ -183,11 +185,13 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
 }
 
 // The last router workgroup: routing of every token, the ascending list of
-// routed experts (seg) and each expert's token -> slot row (slots).
+// routed experts (seg) and each expert's token -> slot row (slots). Up to
+// four tokens take a wave each, more two per wave; the tables are then built
+// by wave 0 alone (its LDS operations complete in order, so no workgroup
+// barrier follows the routing's).
 template <int NPER>
 __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   __shared__ uint32_t s_inds[kDecMaxT * kDecMaxK];
-  __shared__ uint32_t s_seg[kDecMaxE + 1];
   __shared__ uint16_t s_segof[kDecMaxE];
   __shared__ uint8_t s_used[kDecMaxE];
   __shared__ uint8_t s_slot[kDecMaxE * kDecMaxT];
@@ -206,44 +210,50 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
     s_lg[t * ld + c] = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   }
   for (int e = tid; e < E; e += kDecThreads) s_used[e] = 0;
+  for (int i = tid; i < E * kDecMaxT / 4; i += kDecThreads) reinterpret_cast<uint32_t*>(s_slot)[i] = 0xffffffffu;
   lds_barrier();
-  // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
-  for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
-    const int ts[2] = {t0, t0 + kDecWaves};
-    route_tokens<NPER, 2>(a, ts, s_lg, lane, s_inds);
-  }
-  lds_barrier();
-  for (int i = tid; i < n; i += kDecThreads) s_used[s_inds[i]] = 1;
-  lds_barrier();
-  if (wave == 0) {
-    uint32_t U = 0;
-    for (int e0 = 0; e0 < E; e0 += 64) {
-      const int e = e0 + lane;
-      const bool used = e < E && s_used[e];
-      const uint64_t b = __ballot(used);
-      if (used) {
-        const uint32_t u = U + static_cast<uint32_t>(__popcll(b & lanes_below(lane)));
-        s_seg[1 + u] = static_cast<uint32_t>(e);
-        s_segof[e] = static_cast<uint16_t>(u);
-      }
-      U += static_cast<uint32_t>(__popcll(b));
+  if (T <= kDecWaves) {
+    if (wave < T) {
+      const int ts[1] = {wave};
+      route_tokens<NPER, 1>(a, ts, s_lg, lane, s_inds);
     }
-    if (lane == 0) s_seg[0] = U;
+  } else {
+    // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
+    for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
+      const int ts[2] = {t0, t0 + kDecWaves};
+      route_tokens<NPER, 2>(a, ts, s_lg, lane, s_inds);
+    }
   }
-  for (int i = tid; i < E * kDecMaxT; i += kDecThreads) s_slot[i] = 0xff;
   lds_barrier();
-  const int U = static_cast<int>(s_seg[0]);
-  for (int i = tid; i <= U; i += kDecThreads) a.seg[i] = s_seg[i];
+  if (wave != 0) {
+    // K23's per-expert gate/up counters and done flags start the next grid
+    // at zero (stores that drain with the kernel, off the chain)
+    for (int i = tid - kWave; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads - kWave)
+      __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  for (int i = lane; i < n; i += kWave) s_used[s_inds[i]] = 1;
+  __builtin_amdgcn_wave_barrier();
+  uint32_t U = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + lane;
+    const bool used = e < E && s_used[e];
+    const uint64_t b = __ballot(used);
+    if (used) {
+      const uint32_t u = U + static_cast<uint32_t>(__popcll(b & lanes_below(lane)));
+      a.seg[1 + u] = static_cast<uint32_t>(e);
+      s_segof[e] = static_cast<uint16_t>(u);
+    }
+    U += static_cast<uint32_t>(__popcll(b));
+  }
+  if (lane == 0) a.seg[0] = U;
+  __builtin_amdgcn_wave_barrier();
   // slot table, one byte per (expert u, token t): entry (t, j) marks its
   // expert's row, then the rows go out as whole words
-  for (int i = tid; i < n; i += kDecThreads) s_slot[s_segof[s_inds[i]] * kDecMaxT + i / k] = static_cast<uint8_t>(i % k);
-  lds_barrier();
-  for (int i = tid; i < U * (kDecMaxT / 4); i += kDecThreads)
+  for (int i = lane; i < n; i += kWave) s_slot[s_segof[s_inds[i]] * kDecMaxT + i / k] = static_cast<uint8_t>(i % k);
+  __builtin_amdgcn_wave_barrier();
+  for (int i = lane; i < static_cast<int>(U) * (kDecMaxT / 4); i += kWave)
     reinterpret_cast<uint32_t*>(a.slots)[i] = reinterpret_cast<const uint32_t*>(s_slot)[i];
-  // K23's per-expert gate/up counters and done flags start the next grid at
-  // zero (stores issued last: they drain with the kernel, off the chain)
-  for (int i = tid; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads)
-    __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Router column c (column E: the shared-expert gate row) for every token,
@@ -302,10 +312,10 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
       }
     }
   }
-  // lane l then holds the wave's total of token l / (64 / NT)
+  // the last lane of each block of 64 / NT then holds the wave's total of token l / (64 / NT)
   constexpr int kLanesPerToken = kWave / NT;
   const double r = reduce_scatter64<NT>(part, lane);
-  if ((lane & (kLanesPerToken - 1)) == 0) s_lp[wave * kDecMaxT + lane / kLanesPerToken] = r;
+  if (rs64_holder<NT>(lane)) s_lp[wave * kDecMaxT + lane / kLanesPerToken] = r;
   __syncthreads();
   // The logits go out as device-scope stores (written through to the
   // device's coherence point) from wave 0; once they have completed, thread

@@ -146,9 +146,74 @@ __device__ void sort_block(const uint32_t* keys, int n, int k, int E, const Sort
 
 // ------------------------------------------------------------------ exact dot products
 
-// Butterfly reduce-scatter of N = 2^P doubles over the 64 lanes of a wave:
-// afterwards lane l holds the wave-wide total of value index l >> (6 - P).
-// The router's partial sums are exact, so the association order is free.
+// Row moves of the DPP (gfx9 encodings): row_shr:n (lane i of a 16-lane row
+// takes lane i - n of its row), row_bcast:15 (lane 15 of each row to the
+// next row), row_bcast:31 (lane 31 to rows 2 and 3); the row mask selects
+// the rows written. Lanes without a source, and rows outside the mask, keep
+// `old`.
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr4 = 0x114, kDppRowShr8 = 0x118;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
+template <int CTRL, int ROWS = 0xf>
+__device__ inline uint32_t dpp_mov(uint32_t old, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(old), static_cast<int>(v), CTRL, ROWS, 0xf, false));
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ inline float dpp_mov(float old, float v) {
+  return __uint_as_float(dpp_mov<CTRL, ROWS>(__float_as_uint(old), __float_as_uint(v)));
+}
+template <int CTRL, int ROWS = 0xf>
+__device__ inline double dpp_mov(double old, double v) {
+  const uint64_t o = static_cast<uint64_t>(__double_as_longlong(old));
+  const uint64_t x = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = dpp_mov<CTRL, ROWS>(static_cast<uint32_t>(o), static_cast<uint32_t>(x));
+  const uint32_t hi = dpp_mov<CTRL, ROWS>(static_cast<uint32_t>(o >> 32), static_cast<uint32_t>(x >> 32));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Pairwise tree over each block of B consecutive lanes (B a power of two,
+// 1..64), adjacent lanes first: the block's result lands in its last lane
+// (the other lanes hold partial values). op(v, ident) must be v. For a sum
+// over 64 lanes this is the association of the butterfly s_l <- s_l +
+// s_(l xor w), w = 1, 2, .., 32: every pair's operands are the same.
+template <int B, typename T, typename Op>
+__device__ inline T tree_to_last(T v, T ident, Op op) {
+  static_assert(B >= 1 && B <= 64 && (B & (B - 1)) == 0, "B: a power of two <= 64");
+  if constexpr (B >= 2) v = op(v, dpp_mov<kDppRowShr1>(ident, v));
+  if constexpr (B >= 4) v = op(v, dpp_mov<kDppRowShr2>(ident, v));
+  if constexpr (B >= 8) v = op(v, dpp_mov<kDppRowShr4>(ident, v));
+  if constexpr (B >= 16) v = op(v, dpp_mov<kDppRowShr8>(ident, v));
+  if constexpr (B >= 32) v = op(v, dpp_mov<kDppRowBcast15, 0xa>(ident, v));
+  if constexpr (B >= 64) v = op(v, dpp_mov<kDppRowBcast31, 0xc>(ident, v));
+  return v;
+}
+
+__device__ inline double readlane_f64(double v, int l) {
+  const uint64_t x = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(x), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(x >> 32), l);
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+// Wave-wide results of the tree, in every lane
+__device__ inline float wave_max_f32(float v) {
+  v = tree_to_last<64>(v, -__builtin_huge_valf(), [](float a, float b) { return fmaxf(a, b); });
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+}
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+  v = tree_to_last<64>(v, 0u, [](uint32_t a, uint32_t b) { return max(a, b); });
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+__device__ inline double wave_sum_f64(double v) {
+  return readlane_f64(tree_to_last<64>(v, 0.0, [](double a, double b) { return a + b; }), 63);
+}
+
+// Reduce-scatter of N = 2^P doubles over the 64 lanes of a wave: butterfly
+// steps w = 32, 16, .. pair the values up, then a DPP tree sums each block
+// of 64 / N lanes; afterwards the last lane of block b (lane
+// (b + 1) * 64 / N - 1) holds the wave-wide total of value b. The router's
+// partial sums are exact, so the association order is free.
 template <int N>
 __device__ inline double reduce_scatter64(double (&v)[N], int lane) {
   constexpr int P = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
@@ -172,10 +237,13 @@ __device__ inline double reduce_scatter64(double (&v)[N], int lane) {
       }
     }
   }
-  double r = v[0];
-#pragma unroll
-  for (int w = 32 >> P; w >= 1; w >>= 1) r += __shfl_xor(r, w);
-  return r;
+  return tree_to_last<(64 >> P)>(v[0], 0.0, [](double a, double b) { return a + b; });
+}
+
+// Whether lane holds a reduce_scatter64<N> total
+template <int N>
+__device__ inline bool rs64_holder(int lane) {
+  return (lane & (64 / N - 1)) == 64 / N - 1;
 }
 
 // ------------------------------------------------------------------ router rows

@@ -145,9 +145,9 @@ __device__ void d1_router(const NhDecArgs& a, int c, uint8_t* smem) {
       }
     }
   }
-  // lane l then holds the wave's total of token l >> 2
+  // lane 4t + 3 then holds the wave's total of token t
   const double r = reduce_scatter64<kDecMaxT>(part, lane);
-  if ((lane & 3) == 0) s_lp[wave * kDecMaxT + (lane >> 2)] = r;
+  if (rs64_holder<kDecMaxT>(lane)) s_lp[wave * kDecMaxT + (lane >> 2)] = r;
   __syncthreads();
   if (wave == 0) {
     if (tid < T) {

@@ -211,7 +211,7 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
   }
   const double r = reduce_scatter64<NV>(acc, lane);
   constexpr int SH = NV == 1 ? 6 : NV == 2 ? 5 : NV == 4 ? 4 : NV == 8 ? 3 : NV == 16 ? 2 : NV == 32 ? 1 : 0;
-  if ((lane & ((1 << SH) - 1)) == 0) {
+  if (rs64_holder<NV>(lane)) {
     const int idx = lane >> SH;
     const int t = tt * kRouterTok + idx / CE, c = c0 + idx % CE;
     if (t < a.T && c < ncols) {
