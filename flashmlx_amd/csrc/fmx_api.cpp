@@ -144,7 +144,26 @@ constexpr size_t kGuCounterWords = static_cast<size_t>(kDecMaxE) * kDecGuWords;
 // then the status word, on a line of its own
 constexpr size_t kStatusWords = 64;
 constexpr size_t kStatusOffsetWords = kRouterCounterWords + kCbCounterWords + kGuCounterWords;
-constexpr size_t kCounterBytes = (kStatusOffsetWords + kStatusWords) * sizeof(uint32_t);
+// then the decode router's epoch word (a line of its own) and its logit
+// words (64-bit: epoch and logit), which nothing else writes
+constexpr size_t kEpochOffsetWords = kStatusOffsetWords + kStatusWords;
+constexpr size_t kLgxOffsetWords = kEpochOffsetWords + 64;
+constexpr size_t kLgxWords = 2 * static_cast<size_t>(kDecMaxT) * (kDecMaxE + 1);
+constexpr size_t kCounterBytes = (kLgxOffsetWords + kLgxWords) * sizeof(uint32_t);
+
+// Zeroes a workspace's counter block, then starts the decode router's epoch
+// at 1: zeroed logit words carry epoch 0 and are never taken for a forward's.
+hipError_t clear_counters(void* base, hipStream_t stream) {
+  uint32_t* w = static_cast<uint32_t*>(base);
+  const hipError_t e = launch_fill_u32(w, kCounterBytes / 4, 0u, stream);
+  return e != hipSuccess ? e : launch_fill_u32(w + kEpochOffsetWords, 1, 1u, stream);
+}
+
+// The decode router's logit words and epoch back to their initial state
+hipError_t clear_lgx(uint32_t* base, hipStream_t stream) {
+  const hipError_t e = launch_fill_u32(base + kLgxOffsetWords, kLgxWords, 0u, stream);
+  return e != hipSuccess ? e : launch_fill_u32(base + kEpochOffsetWords, 1, 1u, stream);
+}
 
 // bound of the decode down workgroups' wait (fmx_set_decode_wait_limit)
 std::atomic<int> g_wait_polls{kDecWaitPolls};
@@ -945,7 +964,7 @@ int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream s
   if (!workspace) return fail(FMX_ERR_ARG, "workspace is NULL");
   if (workspace_bytes < kCounterBytes)
     return fail(FMX_ERR_WORKSPACE, "workspace %zu bytes < %zu", workspace_bytes, kCounterBytes);
-  FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(workspace), kCounterBytes / 4, 0u, stream));
+  FMX_HIP(clear_counters(workspace, stream));
   return ok();
 }
 
@@ -958,7 +977,13 @@ int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint
   uint32_t* word = static_cast<uint32_t*>(const_cast<void*>(workspace)) + kStatusOffsetWords;
   FMX_HIP(hipStreamSynchronize(stream));
   FMX_HIP(hipMemcpy(status, word, 4, hipMemcpyDeviceToHost));
-  if (clear) FMX_HIP(launch_fill_u32(word, 1, 0u, stream));
+  if (clear) {
+    // after a wait that ran out, late router columns may have tagged their
+    // logit words with the next epoch: a fresh epoch and cleared words make
+    // the next forward start clean
+    FMX_HIP(launch_fill_u32(word, 1, 0u, stream));
+    FMX_HIP(clear_lgx(static_cast<uint32_t*>(const_cast<void*>(workspace)), stream));
+  }
   return ok();
 }
 
@@ -1061,7 +1086,7 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
     void* p = nullptr;
     FMX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     if (!p) return fail(FMX_ERR_HIP, "hipGetSymbolAddress(scratch) gave NULL");
-    FMX_HIP(launch_fill_u32(static_cast<uint32_t*>(p), kCounterBytes / 4, 0u, stream));
+    FMX_HIP(clear_counters(p, stream));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -1140,7 +1165,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
   WsGuard guard(ar);
   const size_t need = moe_layout(c, T, nullptr).total;
   if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
-  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  if (ar.owned) FMX_HIP(clear_counters(ar.base, stream));
   const MoELayout L = moe_layout(c, T, ar.base);
 
   // decode batches (T <= 16) on packed weights: two kernels, combine included
@@ -1182,6 +1207,8 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.cb_counter = L.counters + kRouterCounterWords;
     da.gu_counter = L.counters + kRouterCounterWords + kCbCounterWords;
     da.status = L.counters + kStatusOffsetWords;
+    da.epoch = L.counters + kEpochOffsetWords;
+    da.lgx = reinterpret_cast<uint64_t*>(L.counters + kLgxOffsetWords);
     da.wait_polls = g_wait_polls.load(std::memory_order_relaxed);
     da.y = static_cast<uint16_t*>(y);
     if (nin) {
@@ -1472,7 +1499,7 @@ int fmx_moe_router_topk(const fmx_moe_config* cfg, const void* x, int64_t T, con
   WsGuard guard(ar);
   const size_t need = moe_layout(*cfg, T, nullptr).total;
   if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
-  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  if (ar.owned) FMX_HIP(clear_counters(ar.base, stream));
   const MoELayout L = moe_layout(*cfg, T, ar.base);
   return run_router(*cfg, L, x, T, RouterRows{router_w, nullptr, nullptr}, lbias,
                     RouterRows{nullptr, nullptr, nullptr}, inds, static_cast<uint16_t*>(scores),
@@ -1505,7 +1532,7 @@ int fmx_moe_router_topk_ex(const fmx_moe_config* cfg, const void* x, int64_t T, 
   WsGuard guard(ar);
   const size_t need = moe_layout(*cfg, T, nullptr).total;
   if ((rc = bind_workspace(ar, workspace, workspace_bytes, need, stream))) return rc;
-  if (ar.owned) FMX_HIP(launch_fill_u32(reinterpret_cast<uint32_t*>(ar.base), kCounterBytes / 4, 0u, stream));
+  if (ar.owned) FMX_HIP(clear_counters(ar.base, stream));
   const MoELayout L = moe_layout(*cfg, T, ar.base);
   if ((rc = run_router(*cfg, L, x, T, wr, w->router_logit_bias, wsg, inds, static_cast<uint16_t*>(scores),
                        static_cast<uint16_t*>(probs), shared_gate_out ? L.sgate : nullptr, nullptr, false,

@@ -42,7 +42,11 @@ namespace fmx {
 namespace {
 
 constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
-constexpr int kDecWarmLoads = 8;  // K1's cache warming: 16-byte loads per thread (32 KB per workgroup)
+// K1's cache warming: LDS DMA instructions per wave (1 KB each, into a
+// throwaway LDS piece), at least a shared tile pair's share of the shared
+// down weights (9 H bytes per workgroup, H <= 2048)
+constexpr int kDecWarmDma = 5;
+constexpr int kDecWarmLdsBytes = kWave * 16;
 // Gate/up tile pairs per K2 workgroup (their loads in flight together, the
 // routing tables and staged rows shared): two when the grid has at least
 // kDecK2PairGrid tile pairs (about two resident grids of one-pair
@@ -55,6 +59,12 @@ constexpr int kDecK2PairGrid = 2 * 4 * 256;
 constexpr int kDecK1LpBytes = kDecWaves * kDecMaxT * 8;              // router partials per wave
 
 constexpr int kDecK1LgBytes = kDecMaxT * (kDecMaxE + 1) * 2;         // every token's logits
+// K1's LDS: the router's partials and logits, or the shared tiles' quarter
+// reduction; then the staged rows (the warming's throwaway piece follows)
+__host__ __device__ inline int k1_lds_main(int T, int H) {
+  return (kDecQuadRedBytes > kDecK1LpBytes + kDecK1LgBytes ? kDecQuadRedBytes : kDecK1LpBytes + kDecK1LgBytes) +
+         T * xstride(H) * 2;
+}
 
 // tile_units_lds for NP tile pairs at once: every pair's loads are issued
 // before the one wait, then the pairs are multiplied in turn.
@@ -180,17 +190,21 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
       a.inds[t * a.k + lane] = e;
       a.scores[t * a.k + lane] = sc;
     }
-    if (lane == 0 && a.wsg.w) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
   }
 }
 
-// The last router workgroup: routing of every token, the ascending list of
-// routed experts (seg) and each expert's token -> slot row (slots). Up to
-// four tokens take a wave each, more two per wave; the tables are then built
-// by wave 0 alone (its LDS operations complete in order, so no workgroup
-// barrier follows the routing's).
+// Router column 0, once its own logit is out: the routing of every token,
+// the ascending list of routed experts (seg) and each expert's token -> slot
+// row (slots). Every column's logits come from the words of this epoch
+// (device-scope loads, repeated until all are in: at most a.wait_polls
+// rounds; a wait that runs out sets kStatusWaitTimeout and reads the missing
+// logits as 0), then the epoch advances. Up to four tokens take a wave each,
+// more two per wave; the tables are built by wave 0 alone (its LDS
+// operations complete in order, so no workgroup barrier follows the
+// routing's), the other waves form the shared gate's sigmoid and reset K23's
+// counters meanwhile.
 template <int NPER>
-__device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
+__device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg, uint32_t ep) {
   __shared__ uint32_t s_inds[kDecMaxT * kDecMaxK];
   __shared__ uint16_t s_segof[kDecMaxE];
   __shared__ uint8_t s_used[kDecMaxE];
@@ -199,19 +213,39 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, E = a.E, k = a.k, n = T * k;
   const int ld = E + 1;
-  // every token's logits -> LDS in one round trip (device-scope loads: the
-  // other router workgroups' device-scope stores completed before their
-  // arrivals were counted). The barriers below order LDS only: the global
-  // stores of this workgroup (routing, tables, counters) stay in flight and
-  // drain at the kernel's end.
   const int ncols = E + (a.wsg.w ? 1 : 0);
-  for (int i = tid; i < ncols * T; i += kDecThreads) {
-    const int c = i / T, t = i - c * T;
-    s_lg[t * ld + c] = static_cast<uint16_t>(__hip_atomic_load(a.lgw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  }
+  const int nw = ncols * T;
   for (int e = tid; e < E; e += kDecThreads) s_used[e] = 0;
   for (int i = tid; i < E * kDecMaxT / 4; i += kDecThreads) reinterpret_cast<uint32_t*>(s_slot)[i] = 0xffffffffu;
-  lds_barrier();
+  for (int poll = 0;; ++poll) {
+    int mine = 1;
+    for (int i0 = tid; i0 < nw; i0 += 4 * kDecThreads) {
+      uint64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kDecThreads;
+        v[u] = i < nw ? __hip_atomic_load(a.lgx + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * kDecThreads;
+        if (i < nw) {
+          const int c = i / T, t = i - c * T;
+          const bool in = static_cast<uint32_t>(v[u] >> 32) == ep;
+          mine &= in ? 1 : 0;
+          s_lg[t * ld + c] = in ? static_cast<uint16_t>(v[u]) : 0;
+        }
+      }
+    }
+    if (__syncthreads_and(mine)) break;
+    if (poll + 1 >= a.wait_polls) {
+      if (tid == 0) atomicOr(a.status, kStatusWaitTimeout);
+      __syncthreads();
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (tid == 0) *a.epoch = ep + 1;  // every column of this epoch has stored its logits
   if (T <= kDecWaves) {
     if (wave < T) {
       const int ts[1] = {wave};
@@ -226,9 +260,12 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
   }
   lds_barrier();
   if (wave != 0) {
+    const int w = tid - kWave;
+    if (a.wsg.w)
+      for (int t = w; t < T; t += kDecThreads - kWave) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
     // K23's per-expert gate/up counters and done flags start the next grid
     // at zero (stores that drain with the kernel, off the chain)
-    for (int i = tid - kWave; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads - kWave)
+    for (int i = w; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads - kWave)
       __hip_atomic_store(a.gu_counter + i * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
@@ -267,15 +304,14 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg) {
 // width).
 template <int NPER, int NT, bool NIN>
 __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
-  __shared__ int s_last;
   double* s_lp = reinterpret_cast<double*>(smem);
   uint16_t* s_lg = reinterpret_cast<uint16_t*>(smem + kDecK1LpBytes);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecK1LpBytes + kDecK1LgBytes);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int H = a.H, T = a.T, E = a.E, xs = xstride(H);
-  const int ncols = E + (a.wsg.w ? 1 : 0);
   const int nch = H / 8;
+  const uint32_t ep = __builtin_amdgcn_readfirstlane(*a.epoch);
   if (!NIN) dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
   const RChunk wv = c < E ? load_rchunk(a.wr, c, H, min(tid, nch - 1))
                           : load_rchunk(a.wsg, 0, H, min(tid, nch - 1));
@@ -318,28 +354,21 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   if (rs64_holder<NT>(lane)) s_lp[wave * kDecMaxT + lane / kLanesPerToken] = r;
   __syncthreads();
   // The logits go out as device-scope stores (written through to the
-  // device's coherence point) from wave 0; once they have completed, thread
-  // 0 counts this workgroup in. The last one reads them with device-scope
-  // loads: no cache-wide write-back or invalidation is needed on either side.
-  if (wave == 0) {
-    if (tid < T) {
-      double v = 0.0;
+  // device's coherence point), tagged with this forward's epoch; router
+  // column 0 reads them with device-scope loads: no cache-wide write-back,
+  // invalidation or arrival count on either side.
+  if (wave == 0 && tid < T) {
+    double v = 0.0;
 #pragma unroll
-      for (int q = 0; q < kDecWaves; ++q) v += s_lp[q * kDecMaxT + tid];
-      uint16_t l = f64_to_bf16(v);
-      if (biased) l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(lb)));
-      __hip_atomic_store(a.lgw + c * T + tid, static_cast<uint32_t>(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      a.logits[tid * (E + 1) + c] = l;  // the routing accessor's copy
-    }
-    wait_vmcnt0();
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               static_cast<uint32_t>(ncols - 1);
+    for (int q = 0; q < kDecWaves; ++q) v += s_lp[q * kDecMaxT + tid];
+    uint16_t l = f64_to_bf16(v);
+    if (biased) l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(lb)));
+    __hip_atomic_store(a.lgx + c * T + tid, (static_cast<uint64_t>(ep) << 32) | l, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    a.logits[tid * (E + 1) + c] = l;  // the routing accessor's copy
   }
-  __syncthreads();
-  if (!s_last) return;
-  route_finish<NPER>(a, s_lg);
-  if (tid == 0) *a.counter = 0u;  // every router workgroup has arrived
+  if (c != 0) return;
+  route_finish<NPER>(a, s_lg, ep);
 }
 
 // Shared expert gate/up + SwiGLU for tile pair tp (model.cpp:741-747):
@@ -358,9 +387,27 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   const uint8_t* tb = a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair;
+  // Warming of the device's last-level cache with this workgroup's share of
+  // the shared expert's down weights, which K23 reads after the routing (K1's
+  // HBM would otherwise idle while its router chain finishes): exactly
+  // kDecWarmDma LDS DMA instructions per wave, issued right behind the tile's
+  // loads into a throwaway LDS piece (no registers held; addresses past the
+  // share re-read its last piece), drained before the workgroup ends.
+  uint8_t* s_warm = smem + k1_lds_main(T, H);
+  const int64_t total = static_cast<int64_t>(a.H / 16) * (a.Is / 128) * kBlockSingle;
+  const int64_t per = (total + a.n_sgu - 1) / a.n_sgu;
+  const int64_t b0 = min(static_cast<int64_t>(tp) * per, total - 16), b1 = min(b0 + per, total);
+  auto warm = [&]() {
+#pragma unroll
+    for (int i = 0; i < kDecWarmDma; ++i) {
+      const int64_t off = min(b0 + ((static_cast<int64_t>(wave) * kDecWarmDma + i) * kWave + lane) * 16, b1 - 16);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.sdn + off),
+                                       (__attribute__((address_space(3))) void*)s_warm, 16, 0, 0);
+    }
+  };
   if constexpr (NIN) {
     // the tile's loads first, then the input norm (its barrier also waits
-    // for them), then the products
+    // for them), then the warming, then the products
     __shared__ double s_nred[NT * (kNormThreads / kWave)];
     PkUnit<true> L[kDecK2Units];
     __builtin_amdgcn_sched_barrier(0);
@@ -368,6 +415,7 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
     for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
     __builtin_amdgcn_sched_barrier(0);
     norm_rows_lds<NT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
+    warm();
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
       if (u0 + d < u1) {
@@ -378,37 +426,36 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
     }
   } else {
     dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-    tile_units_lds<true, kDecK2Units>(tb, u0, u1, xl, lane, acc0, acc1);
-  }
-  // Warm the device's last-level cache with this workgroup's share of the
-  // shared expert's down weights, which K23 reads after the routing: K1's
-  // HBM would otherwise idle while its router chain finishes. At most
-  // kDecWarmLoads 16-byte loads per thread, all in flight together; the
-  // values are dropped.
-  {
-    const int64_t total = static_cast<int64_t>(a.H / 16) * (a.Is / 128) * kBlockSingle;
-    const int64_t per = (total + a.n_sgu - 1) / a.n_sgu;
-    const int64_t b0 = static_cast<int64_t>(tp) * per, b1 = min(b0 + per, total);
-    uint32_t sink = 0;
+    PkUnit<true> L[kDecK2Units];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < kDecWarmLoads; ++i) {
-      const int64_t off = b0 + (static_cast<int64_t>(i) * kDecThreads + threadIdx.x) * 16;
-      if (off + 16 <= b1) {
-        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.sdn + off);
-        sink ^= v[0];
+    for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
+    warm();
+    __builtin_amdgcn_sched_barrier(0);
+    // vector memory operations complete in order: the rows' DMA, issued
+    // before the tile's loads and the warming, has landed at this count
+    wait_vmcnt<kDecK2Units * pk_load_insts<true>() + kDecWarmDma>();
+    lds_dma_barrier();
+#pragma unroll
+    for (int d = 0; d < kDecK2Units; ++d) {
+      if (u0 + d < u1) {
+        bf16x8_t A[4];
+        lds_a(xl + (u0 + d) * 128, A);
+        pk_unit<true>(L[d], A, acc0, acc1);
       }
     }
-    asm volatile("" ::"v"(sink));
   }
   quad_reduce(acc0, acc1, wave, lane, s_red);
-  if (wave != 0) return;
-  const int n = tp * 16 + m;
+  if (wave == 0) {
+    const int n = tp * 16 + m;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 4 * j + i;
-    if (t < T)
-      a.hs[static_cast<int64_t>(t) * Is + n] = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * j + i;
+      if (t < T)
+        a.hs[static_cast<int64_t>(t) * Is + n] = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
+    }
   }
+  wait_vmcnt0();  // the warming's LDS writes land before the workgroup's LDS is released
 }
 
 // Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
@@ -770,9 +817,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
 
 // ---------------------------------------------------------------- host side
 
-static size_t k1_lds(const DecodeArgs& a) {
-  return std::max(kDecQuadRedBytes, kDecK1LpBytes + kDecK1LgBytes) + static_cast<size_t>(a.T) * xstride(a.H) * 2;
-}
+static size_t k1_lds(const DecodeArgs& a) { return k1_lds_main(a.T, a.H) + kDecWarmLdsBytes; }
 
 // K2: the quarter reduction, then the staged rows
 static size_t k2_lds(const DecodeArgs& a) {

@@ -198,15 +198,21 @@ struct DecodeArgs {
   uint32_t* seg;            // [1 + max_seg]: U, then the routed experts ascending
   uint8_t* slots;           // [max_seg][16]: slot of token t for routed expert u, or 0xff
   uint32_t* counter;        // router arrival counter: zero on entry, zero on exit
+  // K1's logit handoff: column c stores (epoch << 32) | logit of token t in
+  // lgx[c * T + t]; router column 0 accepts words of the current epoch only
+  // and advances the epoch once it has them all
+  uint64_t* lgx;            // [kDecMaxT * (kDecMaxE + 1)]
+  uint32_t* epoch;
   uint32_t* cb_counter;     // [H / 64, stride kDecCbStride] K3 arrivals per column block: zero on entry and exit
   uint32_t* gu_counter;     // [max_seg][kDecGuWords] K23: gate/up tiles finished per routed expert
                             //   and their done flags; K1 zeroes them for every forward
   uint16_t* y;              // [T, H] bf16
   // status word (sticky: set bits stay until the caller clears them):
   // kStatusWaitTimeout when a down workgroup's bounded wait for its expert's
-  // gate/up tiles ran out (its products are then NaN)
+  // gate/up tiles ran out (its products are then NaN), or router column 0's
+  // wait for the other columns' logits (missing logits then read as 0)
   uint32_t* status;
-  int wait_polls;           // the wait's bound in flag reads; <= 0 gives up at once
+  int wait_polls;           // the waits' bound in flag reads; <= 0 gives up at once
   // launch shape (decode_plan)
   int n_rt, n_sgu;          // K1: router columns, shared gate/up tile pairs (one each per workgroup)
   int max_seg, gu_tiles;    // K2: expert slots x gate/up tile pairs

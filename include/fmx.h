@@ -242,9 +242,12 @@ int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream s
 
 /* The workspace's status word, after the forwards queued on `stream` end
  * (synchronises the stream): 0, or FMX_STATUS_WAIT_TIMEOUT when a decode
- * forward's bounded wait (a down workgroup waiting for its expert's gate/up
- * tiles) ran out and its products were written as NaN. Bits stay set until
- * cleared (clear != 0 clears them after reading, in stream order). No
+ * forward's bounded wait ran out (a down workgroup waiting for its expert's
+ * gate/up tiles: its products are written as NaN; or the router waiting for
+ * the other router columns' logits: missing logits are read as 0). Bits
+ * stay set until cleared (clear != 0 clears them after reading, in stream
+ * order, and resets the router's logit exchange, which a forward whose wait
+ * ran out may leave holding late logits: clear before the next forward). No
  * counterpart in the reference: MLX's graph has no in-kernel waits. */
 #define FMX_STATUS_WAIT_TIMEOUT 1u
 int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
@@ -273,7 +276,7 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
  * ends. Forwards whose fmx_moe_workspace_size(cfg, n_tokens) exceeds that
  * return FMX_ERR_UNSUPPORTED before launching anything (8 MiB: every decode
  * batch of up to 16 tokens, and forwards of up to 72 tokens of the
- * Qwen1.5-MoE-A2.7B shape or 104 of the Qwen3-30B-A3B shape). All calls on
+ * Qwen1.5-MoE-A2.7B shape or 103 of the Qwen3-30B-A3B shape). All calls on
  * one device share the array:
  * calls that overlap on one GPU (two streams, or two host threads) race and
  * must be ordered by the caller. Each forward leaves the array's completion
