@@ -34,6 +34,13 @@ STAGE_OF = [
     (r"qgemm_kernel<true", "gate_up"),
     (r"qgemm_kernel<false", "down"),
     (r"combine_kernel", "combine"),
+    # the decoder stack's kernels (fmx_model)
+    (r"attn_split_kernel", "attention (single token)"),
+    (r"attn_kernel", "attention (several tokens)"),
+    (r"dense_dec_kernel<true", "q/k/v with input norm"),
+    (r"dense_dec_kernel<false", "o_proj, lm_head"),
+    (r"greedy_kernel", "argmax"),
+    (r"rmsnorm_kernel", "norm"),
 ]
 
 
