@@ -387,11 +387,12 @@ __device__ inline bf16x8_t nib8(uint32_t w) {
 //
 // The prefill GEMMs multiply in fp16: a weight s*q + b rounded once to fp16
 // (11 significant bits) is within 2^-11 relative of its exact value, an
-// eighth of bf16's rounding error, and a bf16 activation converts to fp16
-// exactly when its magnitude is below 65536 (values under 2^-14 keep an
-// absolute error below 2^-25 on fp16's subnormal grid). Activations at or
-// above 65536 (and inf/NaN) raise a flag that sends the GEMM to the exact
-// bf16 path instead.
+// eighth of bf16's rounding error. A bf16 activation converts to fp16
+// exactly when its magnitude lies in [2^-14, 65536); below 2^-14 fp16 is
+// subnormal (steps of 2^-24), so smaller values round to that grid (an
+// absolute error of at most 2^-25; magnitudes under 2^-25 become 0).
+// Activations at or above 65536 (and inf/NaN) raise a flag that sends the
+// GEMM to the exact bf16 path instead.
 //
 // P8 layout (p8_slot): the 8 elements e0..e7 of a 16-byte activation chunk are
 // stored as e0 e4 e1 e5 e2 e6 e3 e7, the order in which dq8_f16 delivers the
@@ -433,7 +434,8 @@ __device__ inline f32x4_t mfma_f16(const f16x8_t& a, const f16x8_t& b, const f32
 // |v| >= 65536 (or inf/NaN) for a bf16 bit pattern: outside fp16's range
 __device__ inline bool bf16_f16_overflow(uint32_t h) { return (h & 0x7fffu) >= 0x4780u; }
 
-// fp16 bits of a bf16 value (round to nearest even; exact below 65536)
+// fp16 bits of a bf16 value (round to nearest even: exact for magnitudes in
+// [2^-14, 65536), on fp16's subnormal grid below)
 __device__ inline uint32_t bf16_to_f16_bits(uint32_t h) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(__uint_as_float(h << 16)));
 }

@@ -33,8 +33,9 @@
 // Arithmetic: the weights are dequantised once per pass into fp16 (s*q + b
 // rounded once, 2^-11 relative) and multiplied with
 // v_mfma_f32_16x16x32_f16 against fp16 copies of the activation rows
-// (exact for bf16 values below 65536; the copies are written in the P8
-// layout, fmx_dev.hpp, by the router for x and by this gate/up grid for h).
+// (exact for bf16 magnitudes in [2^-14, 65536); smaller ones round to
+// fp16's subnormal grid, at most 2^-25 off; the copies are written in the
+// P8 layout, fmx_dev.hpp, by the router for x and by this gate/up grid for h).
 // When a row holds a value outside fp16's range (the forward's flag word
 // says so) the grid takes the exact bf16 path instead: nibbles become the
 // bf16 values 128 + q, the MFMA forms P = x.(128+q) and X = x.1 per
