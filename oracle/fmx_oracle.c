@@ -267,12 +267,12 @@ float orc_f16_to_f32(uint16_t h) {
   return sgn ? -v : v;
 }
 
-uint16_t orc_f32_to_f16(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  const uint16_t sgn = (uint16_t)((u >> 16) & 0x8000u);
+/* One rounding to nearest even from a double (every float converts to a
+ * double exactly, so orc_f32_to_f16 is the same rounding of a float). */
+uint16_t orc_f64_to_f16(double f) {
+  const uint16_t sgn = signbit(f) ? 0x8000u : 0u;
   if (isnan(f)) return (uint16_t)(sgn | 0x7e00u);
-  const double a = fabs((double)f);
+  const double a = fabs(f);
   if (a >= 65520.0) return (uint16_t)(sgn | 0x7c00u); /* rounds past the largest finite */
   /* a = m * 2^e exactly in double; the spacing of fp16 values near a */
   int e;
@@ -294,6 +294,20 @@ uint16_t orc_f32_to_f16(float f) {
   else
     bits = (uint16_t)(((ve - 1 + 15) << 10) | ((uint32_t)(v * ldexp(1.0, 11 - ve)) & 1023u));
   return (uint16_t)(sgn | bits);
+}
+
+uint16_t orc_f32_to_f16(float f) { return orc_f64_to_f16((double)f); }
+
+/* The block's activation dtype (a float16 checkpoint runs the whole block
+ * in float16, model.cpp:208-214): loads, roundings from fp32 and fp64 */
+static inline float ld_dt(int f16, uint16_t h) { return f16 ? orc_f16_to_f32(h) : orc_bf16_to_f32(h); }
+static inline uint16_t rnd_dt(int f16, float f) { return f16 ? orc_f32_to_f16(f) : orc_f32_to_bf16(f); }
+static inline uint16_t rnd64_dt(int f16, double d) { return f16 ? orc_f64_to_f16(d) : orc_f64_to_bf16(d); }
+
+/* fp16(sigmoid(g)) of a float16 g: fp64, rounded once */
+float orc_sigmoid_f16(uint16_t g) {
+  const double v = (double)orc_f16_to_f32(g);
+  return orc_f16_to_f32(orc_f64_to_f16(1.0 / (1.0 + exp(-v))));
 }
 
 /* One output element in float16: x, scales and biases fp16; modes
@@ -435,6 +449,27 @@ static uint16_t row_dot_exact(const uint16_t* x, const void* w, const uint16_t* 
                       b + row * (H / 64), H);
 }
 
+/* row_dot_exact in the block's activation dtype: float16 x, row, scales
+ * and biases (their products with x are exact in fp64 as well), one
+ * rounding to float16 */
+static uint16_t row_dot_exact_dt(int f16, const uint16_t* x, const void* w, const uint16_t* s,
+                                 const uint16_t* b, int64_t row, int64_t H) {
+  if (!f16) return row_dot_exact(x, w, s, b, row, H);
+  double acc = 0.0;
+  if (!s) {
+    const uint16_t* wr = (const uint16_t*)w + row * H;
+    for (int64_t i = 0; i < H; ++i) acc += (double)ld_dt(1, x[i]) * (double)ld_dt(1, wr[i]);
+  } else {
+    const uint32_t* wq = (const uint32_t*)w + row * (H / 8);
+    const uint16_t *sr = s + row * (H / 64), *br = b + row * (H / 64);
+    for (int64_t i = 0; i < H; ++i) {
+      const double q = (double)((wq[i / 8] >> (4 * (i % 8))) & 15u);
+      acc += (double)ld_dt(1, x[i]) * ((double)ld_dt(1, sr[i / 64]) * q + (double)ld_dt(1, br[i / 64]));
+    }
+  }
+  return orc_f64_to_f16(acc);
+}
+
 /* Softmax normaliser in a fixed summation order (MLX's own order is an
  * implementation detail of its CPU kernel): 64 partial sums, partial l
  * taking ex[l], ex[l+64], ... in turn, then six butterfly rounds
@@ -469,6 +504,14 @@ int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
                       const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
                       const uint16_t* logit_bias, int k, int norm_topk,
                       uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores) {
+  return orc_router_topk_dt(x, T, H, wr, wr_s, wr_b, E, logit_bias, k, norm_topk, 0, logits, probs,
+                            inds, scores);
+}
+
+int orc_router_topk_dt(const uint16_t* x, int64_t T, int64_t H,
+                       const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
+                       const uint16_t* logit_bias, int k, int norm_topk, int f16,
+                       uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores) {
   if (k <= 0 || k > E || E > 65535) return -1;
   if (wr_s && (!wr_b || H % 64)) return -1;
   int rc = 0;
@@ -485,21 +528,22 @@ int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
 #pragma omp for schedule(static)
       for (int64_t t = 0; t < T; ++t) {
         for (int64_t e = 0; e < E; ++e) {
-          uint16_t l = row_dot_exact(x + t * H, wr, wr_s, wr_b, e, H);
-          if (logit_bias) l = orc_f64_to_bf16((double)bf(l) + (double)bf(logit_bias[e]));
+          uint16_t l = row_dot_exact_dt(f16, x + t * H, wr, wr_s, wr_b, e, H);
+          if (logit_bias) l = rnd64_dt(f16, (double)ld_dt(f16, l) + (double)ld_dt(f16, logit_bias[e]));
           lg[e] = l;
         }
         double m = -INFINITY;
-        for (int64_t e = 0; e < E; ++e) m = fmax(m, (double)bf(lg[e]));
-        for (int64_t e = 0; e < E; ++e) ex[e] = orc_exp((double)bf(lg[e]) - m);
+        for (int64_t e = 0; e < E; ++e) m = fmax(m, (double)ld_dt(f16, lg[e]));
+        for (int64_t e = 0; e < E; ++e) ex[e] = orc_exp((double)ld_dt(f16, lg[e]) - m);
         const double sum = softmax_den(ex, E);
-        for (int64_t e = 0; e < E; ++e) pb[e] = orc_f64_to_bf16(ex[e] / sum);
+        for (int64_t e = 0; e < E; ++e) pb[e] = rnd64_dt(f16, ex[e] / sum);
         memset(taken, 0, E);
         for (int j = 0; j < k; ++j) {
           int64_t best = -1;
           for (int64_t e = 0; e < E; ++e) {
             if (taken[e]) continue;
-            if (best < 0 || bf(pb[e]) > bf(pb[best])) best = e; /* strict: ties keep lower index */
+            /* strict: ties keep lower index */
+            if (best < 0 || ld_dt(f16, pb[e]) > ld_dt(f16, pb[best])) best = e;
           }
           taken[best] = 1;
           inds[t * k + j] = (uint32_t)best;
@@ -507,11 +551,11 @@ int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
         }
         if (norm_topk) {
           float s = 0.0f;
-          for (int j = 0; j < k; ++j) s += bf(scores[t * k + j]);
-          uint16_t sb = rb(s);
+          for (int j = 0; j < k; ++j) s += ld_dt(f16, scores[t * k + j]);
+          uint16_t sb = rnd_dt(f16, s);
           for (int j = 0; j < k; ++j) {
-            float q = (float)((double)bf(scores[t * k + j]) / (double)bf(sb));
-            scores[t * k + j] = rb(q);
+            float q = (float)((double)ld_dt(f16, scores[t * k + j]) / (double)ld_dt(f16, sb));
+            scores[t * k + j] = rnd_dt(f16, q);
           }
         }
         if (logits) memcpy(logits + t * E, lg, sizeof(uint16_t) * E);
@@ -564,19 +608,21 @@ int orc_moe_sort(const uint32_t* inds, int64_t T, int k, int64_t E,
 /* ------------------------------------------------------------------------ */
 
 /* compiled SwiGLU (model.cpp:14-25): multiply(multiply(g, sigmoid(g)), u),
- * each op producing bf16. */
-static uint16_t swiglu_bf16(uint16_t g, uint16_t u) {
-  float sg = orc_sigmoid_bf16(g);
-  uint16_t t = rb(bf(g) * sg);
-  return rb(bf(t) * bf(u));
+ * each op producing the activation dtype (bf16, or fp16 when f16). */
+static uint16_t swiglu_dt(int f16, uint16_t g, uint16_t u) {
+  float sg = f16 ? orc_sigmoid_f16(g) : orc_sigmoid_bf16(g);
+  uint16_t t = rnd_dt(f16, ld_dt(f16, g) * sg);
+  return rnd_dt(f16, ld_dt(f16, t) * ld_dt(f16, u));
 }
 
-/* dense out[n] = x . deq(W[n]) for n < N, bf16 */
-static void qmv(const uint16_t* x, int64_t K, const uint32_t* w, const uint16_t* s,
+/* dense out[n] = x . deq(W[n]) for n < N, in the activation dtype (fp16
+ * supports modes ORC_ACC_A and ORC_ACC_F64) */
+static void qmv(int f16, const uint16_t* x, int64_t K, const uint32_t* w, const uint16_t* s,
                 const uint16_t* b, int64_t N, int mode, uint16_t* out) {
 #pragma omp parallel for schedule(static)
   for (int64_t n = 0; n < N; ++n)
-    out[n] = qdot_row(x, w + n * (K / 8), s + n * (K / 64), b + n * (K / 64), K, mode);
+    out[n] = f16 ? qdot_row_f16(x, w + n * (K / 8), s + n * (K / 64), b + n * (K / 64), K, mode)
+                 : qdot_row(x, w + n * (K / 8), s + n * (K / 64), b + n * (K / 64), K, mode);
 }
 
 static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
@@ -585,7 +631,9 @@ static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
                           uint16_t* y, uint32_t* inds_out, uint16_t* scores_out) {
   const int64_t H = cfg->hidden, E = cfg->n_experts, I = cfg->inter, Is = cfg->shared_inter;
   const int k = cfg->top_k;
+  const int f16 = cfg->act_f16;
   if (cfg->group_size != 64 || cfg->bits != 4 || H % 64 || I % 64 || (Is && Is % 64)) return -1;
+  if (f16 && mode != ORC_ACC_A && mode != ORC_ACC_F64) return -1;
   uint32_t* inds = (uint32_t*)malloc(sizeof(uint32_t) * T * k);
   uint16_t* scores = (uint16_t*)malloc(sizeof(uint16_t) * T * k);
   int64_t Imax = I > Is ? I : Is;
@@ -598,8 +646,8 @@ static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
 
   uint16_t* probs = forced ? (uint16_t*)malloc(sizeof(uint16_t) * T * E) : NULL;
   if (forced && !probs) return -3;
-  int rc = orc_router_topk_q(x, T, H, w->router_w, w->router_s, w->router_b, E, w->router_bias, k,
-                             cfg->norm_topk, NULL, probs, inds, scores);
+  int rc = orc_router_topk_dt(x, T, H, w->router_w, w->router_s, w->router_b, E, w->router_bias, k,
+                              cfg->norm_topk, f16, NULL, probs, inds, scores);
   if (rc) return rc;
   if (forced) {
     /* the given expert choice, with this router's probabilities as scores
@@ -613,10 +661,11 @@ static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
       }
       if (cfg->norm_topk) {
         float sum = 0.0f;
-        for (int j = 0; j < k; ++j) sum += bf(scores[t * k + j]);
-        const uint16_t sb = rb(sum);
+        for (int j = 0; j < k; ++j) sum += ld_dt(f16, scores[t * k + j]);
+        const uint16_t sb = rnd_dt(f16, sum);
         for (int j = 0; j < k; ++j)
-          scores[t * k + j] = rb((float)((double)bf(scores[t * k + j]) / (double)bf(sb)));
+          scores[t * k + j] =
+              rnd_dt(f16, (float)((double)ld_dt(f16, scores[t * k + j]) / (double)ld_dt(f16, sb)));
       }
     }
     free(probs);
@@ -633,28 +682,29 @@ static int moe_block_impl(const orc_moe_cfg* cfg, const orc_moe_weights* w,
      * SwiGLU, gather_qmm down (model.cpp:703-721) */
     for (int j = 0; j < k; ++j) {
       const int64_t e = inds[t * k + j];
-      qmv(xt, H, w->gate_w + e * wst_gu, w->gate_s + e * sst_gu, w->gate_b + e * sst_gu, I, mode, g);
-      qmv(xt, H, w->up_w + e * wst_gu, w->up_s + e * sst_gu, w->up_b + e * sst_gu, I, mode, u);
-      for (int64_t i = 0; i < I; ++i) a[i] = swiglu_bf16(g[i], u[i]);
-      qmv(a, I, w->down_w + e * wst_d, w->down_s + e * sst_d, w->down_b + e * sst_d, H, mode, d);
+      qmv(f16, xt, H, w->gate_w + e * wst_gu, w->gate_s + e * sst_gu, w->gate_b + e * sst_gu, I, mode, g);
+      qmv(f16, xt, H, w->up_w + e * wst_gu, w->up_s + e * sst_gu, w->up_b + e * sst_gu, I, mode, u);
+      for (int64_t i = 0; i < I; ++i) a[i] = swiglu_dt(f16, g[i], u[i]);
+      qmv(f16, a, I, w->down_w + e * wst_d, w->down_s + e * sst_d, w->down_b + e * sst_d, H, mode, d);
       /* y = sum(y * scores[..., None], -2) (model.cpp:782-784): the product
-       * is bf16, the k-sum accumulates in fp32 in slot order */
-      const float sc = bf(scores[t * k + j]);
-      for (int64_t h = 0; h < H; ++h) acc[h] += bf(rb(bf(d[h]) * sc));
+       * is in the activation dtype, the k-sum accumulates in fp32 in slot
+       * order */
+      const float sc = ld_dt(f16, scores[t * k + j]);
+      for (int64_t h = 0; h < H; ++h) acc[h] += ld_dt(f16, rnd_dt(f16, ld_dt(f16, d[h]) * sc));
     }
-    for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(acc[h]);
+    for (int64_t h = 0; h < H; ++h) y[t * H + h] = rnd_dt(f16, acc[h]);
     if (Is > 0) {
       /* shared_expert_mlp (model.cpp:736-748) and its sigmoid gate (:787-803) */
-      uint16_t gl = row_dot_exact(xt, w->sh_expert_gate_w, w->sh_expert_gate_s,
-                                  w->sh_expert_gate_b, 0, H);
-      float gv = orc_sigmoid_bf16(gl);
-      qmv(xt, H, w->sh_gate_w, w->sh_gate_s, w->sh_gate_b, Is, mode, g);
-      qmv(xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, u);
-      for (int64_t i = 0; i < Is; ++i) a[i] = swiglu_bf16(g[i], u[i]);
-      qmv(a, Is, w->sh_down_w, w->sh_down_s, w->sh_down_b, H, mode, d);
+      uint16_t gl = row_dot_exact_dt(f16, xt, w->sh_expert_gate_w, w->sh_expert_gate_s,
+                                     w->sh_expert_gate_b, 0, H);
+      float gv = f16 ? orc_sigmoid_f16(gl) : orc_sigmoid_bf16(gl);
+      qmv(f16, xt, H, w->sh_gate_w, w->sh_gate_s, w->sh_gate_b, Is, mode, g);
+      qmv(f16, xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, u);
+      for (int64_t i = 0; i < Is; ++i) a[i] = swiglu_dt(f16, g[i], u[i]);
+      qmv(f16, a, Is, w->sh_down_w, w->sh_down_s, w->sh_down_b, H, mode, d);
       for (int64_t h = 0; h < H; ++h) {
-        uint16_t sh = rb(gv * bf(d[h]));
-        y[t * H + h] = rb(bf(y[t * H + h]) + bf(sh));
+        uint16_t sh = rnd_dt(f16, gv * ld_dt(f16, d[h]));
+        y[t * H + h] = rnd_dt(f16, ld_dt(f16, y[t * H + h]) + ld_dt(f16, sh));
       }
     }
   }
@@ -869,7 +919,7 @@ int orc_nh_moe_block(const orc_nh_cfg* c, const orc_nh_weights* w, const uint16_
     /* switch_mlp: fc1 -> relu2 -> fc2 (:1086-1094), the weighted sum (:1098-1099) */
     for (int j = 0; j < k; ++j) {
       const int64_t e = inds[t * k + j];
-      qmv(xt, H, w->fc1_w + e * wst1, w->fc1_s + e * sst1, w->fc1_b + e * sst1, I, mode, hb);
+      qmv(0, xt, H, w->fc1_w + e * wst1, w->fc1_s + e * sst1, w->fc1_b + e * sst1, I, mode, hb);
       relu2_row(hb, I, a);
       qmv_f32(a, I, w->fc2_w + e * wst2, w->fc2_s + e * sst2, w->fc2_b + e * sst2, H, mode, d);
       const float sc = scores[t * k + j];
@@ -881,7 +931,7 @@ int orc_nh_moe_block(const orc_nh_cfg* c, const orc_nh_weights* w, const uint16_
     for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(acc[h]);
     if (Is > 0) {
       /* shared expert (:1102-1108): up -> relu2 -> down, added in fp32 */
-      qmv(xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, hb);
+      qmv(0, xt, H, w->sh_up_w, w->sh_up_s, w->sh_up_b, Is, mode, hb);
       relu2_row(hb, Is, a);
       qmv_f32(a, Is, w->sh_down_w, w->sh_down_s, w->sh_down_b, H, mode, d);
       for (int64_t h = 0; h < H; ++h) y[t * H + h] = rb(bf(y[t * H + h]) + d[h]);

@@ -113,6 +113,8 @@ int orc_gather_qmm(const uint16_t* x, int64_t n_x, int64_t M, int64_t K,
  * biases and out in IEEE binary16; modes ORC_ACC_F64 and ORC_ACC_A only. */
 float orc_f16_to_f32(uint16_t h);
 uint16_t orc_f32_to_f16(float f);
+uint16_t orc_f64_to_f16(double d);  /* one rounding to nearest even */
+float orc_sigmoid_f16(uint16_t g);  /* fp16(sigmoid(g)) as float (fp64, one rounding) */
 int orc_qmm_t_f16(const uint16_t* x, int64_t M, int64_t K,
                   const uint32_t* w, const uint16_t* scales, const uint16_t* biases,
                   int64_t N, int mode, uint16_t* out);
@@ -137,6 +139,13 @@ int orc_router_topk_q(const uint16_t* x, int64_t T, int64_t H,
                       const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
                       const uint16_t* logit_bias, int k, int norm_topk,
                       uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores);
+/* The same in the block's activation dtype: f16 = 1 takes x, the router
+ * rows (or their scales and biases), logit_bias and every output in float16
+ * (logits and probabilities rounded once to fp16, the top-k on fp16 values). */
+int orc_router_topk_dt(const uint16_t* x, int64_t T, int64_t H,
+                       const void* wr, const uint16_t* wr_s, const uint16_t* wr_b, int64_t E,
+                       const uint16_t* logit_bias, int k, int norm_topk, int f16,
+                       uint16_t* logits, uint16_t* probs, uint32_t* inds, uint16_t* scores);
 
 /* ---- sort / permutation (model.cpp:682-700) ---------------------------- */
 /* order = stable argsort(flat inds); inv = argsort(order); src = order / k;
@@ -155,6 +164,8 @@ typedef struct {
   int     norm_topk;     /* renormalise the k scores */
   int     group_size;    /* 64 */
   int     bits;          /* 4 */
+  int     act_f16;       /* 1: float16 activations, scales, biases and router (a float16
+                            checkpoint, model.cpp:208-214); 0: bfloat16 */
 } orc_moe_cfg;
 
 typedef struct {

@@ -40,6 +40,7 @@ class _Cfg(C.Structure):
         ("norm_topk", C.c_int),
         ("group_size", C.c_int),
         ("bits", C.c_int),
+        ("act_f16", C.c_int),
     ]
 
 
@@ -110,6 +111,12 @@ def load() -> C.CDLL:
                                         _vp, _vp]
         lib.orc_router_topk_q.argtypes = [_vp, i64, i64, _vp, _vp, _vp, i64, _vp, C.c_int, C.c_int,
                                           _vp, _vp, _vp, _vp]
+        lib.orc_router_topk_dt.argtypes = [_vp, i64, i64, _vp, _vp, _vp, i64, _vp, C.c_int, C.c_int,
+                                           C.c_int, _vp, _vp, _vp, _vp]
+        lib.orc_f64_to_f16.restype = C.c_uint16
+        lib.orc_f64_to_f16.argtypes = [C.c_double]
+        lib.orc_sigmoid_f16.restype = C.c_float
+        lib.orc_sigmoid_f16.argtypes = [C.c_uint16]
         lib.orc_moe_sort.argtypes = [_vp, i64, C.c_int, i64, _vp, _vp, _vp, _vp, _vp]
         lib.orc_moe_block.argtypes = [C.POINTER(_Cfg), C.POINTER(_W), _vp, i64, C.c_int, _vp, i64,
                                       _vp, _vp, _vp]
@@ -255,9 +262,10 @@ def gather_qmm(x, wq, s, b, lhs, rhs, mode=ACC_A) -> np.ndarray:
     return out
 
 
-def router_topk(x, wr, k, norm_topk=False, logit_bias=None):
+def router_topk(x, wr, k, norm_topk=False, logit_bias=None, f16=False):
     """-> logits [T,E], probs [T,E] (bf16 bits), inds [T,k] u32, scores [T,k] bf16.
-    wr: bf16 [E, H], or a quantized (wq u32 [E, H/8], scales, biases) tuple."""
+    wr: bf16 [E, H], or a quantized (wq u32 [E, H/8], scales, biases) tuple.
+    f16: every input and output in float16 instead (orc_router_topk_dt)."""
     x = _c(x, np.uint16)
     if isinstance(wr, tuple):
         wq, ws, wb = _c(wr[0], np.uint32), _c(wr[1], np.uint16), _c(wr[2], np.uint16)
@@ -271,8 +279,8 @@ def router_topk(x, wr, k, norm_topk=False, logit_bias=None):
     probs = np.empty((T, E), np.uint16)
     inds = np.empty((T, k), np.uint32)
     scores = np.empty((T, k), np.uint16)
-    rc = load().orc_router_topk_q(_p(x), T, H, _p(wq), _p(ws), _p(wb), E, _p(lb), k,
-                                  int(norm_topk), _p(logits), _p(probs), _p(inds), _p(scores))
+    rc = load().orc_router_topk_dt(_p(x), T, H, _p(wq), _p(ws), _p(wb), E, _p(lb), k,
+                                   int(norm_topk), int(f16), _p(logits), _p(probs), _p(inds), _p(scores))
     assert rc == 0, rc
     return logits, probs, inds, scores
 
@@ -289,7 +297,9 @@ def moe_sort(inds, E):
 
 
 def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None, inds=None):
-    """cfg keys: hidden, n_experts, top_k, inter, shared_inter, norm_topk.
+    """cfg keys: hidden, n_experts, top_k, inter, shared_inter, norm_topk,
+    act_f16 (float16 activations, scales, biases and router: every array in
+    and out is then fp16 bits; modes ACC_A and ACC_F64).
     w keys: router_w (bf16, or a quantized (wq, s, b) tuple), router_bias?,
     gate/up/down (wq, s, b) tuples, shared_gate/shared_up/shared_down tuples?,
     shared_expert_gate_w? (bf16 or a quantized tuple).
@@ -301,7 +311,7 @@ def moe_block(cfg: dict, w: dict, x, mode=ACC_A, tokens=None, inds=None):
     T = x.size // H
     k = cfg["top_k"]
     c = _Cfg(H, cfg["n_experts"], k, cfg["inter"], cfg.get("shared_inter", 0),
-             int(cfg.get("norm_topk", False)), 64, 4)
+             int(cfg.get("norm_topk", False)), 64, 4, int(cfg.get("act_f16", False)))
     keep = []
 
     def ptr(a, dt):
