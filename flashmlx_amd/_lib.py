@@ -43,6 +43,7 @@ class FmxMoEConfig(C.Structure):
         ("shared_expert_intermediate_size", C.c_int64),
         ("quant_bits", C.c_int32),
         ("quant_group_size", C.c_int32),
+        ("activation_dtype", C.c_int32),
     ]
 
 

@@ -249,6 +249,8 @@ int check_moe_config(const fmx_moe_config* c) {
   if (c->num_experts_per_tok < 1 || c->num_experts_per_tok > 16 ||
       c->num_experts_per_tok > c->num_experts)
     return fail(FMX_ERR_UNSUPPORTED, "num_experts_per_tok=%d (1..min(16, E))", c->num_experts_per_tok);
+  if (c->activation_dtype != FMX_BF16 && c->activation_dtype != FMX_F16)
+    return fail(FMX_ERR_DTYPE, "activation_dtype=%d (FMX_BF16 or FMX_F16)", c->activation_dtype);
   return FMX_OK;
 }
 
@@ -308,6 +310,7 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
                uint16_t* scores, uint16_t* probs, float* sgate, uint16_t* xp, bool want_sort,
                bool* sorted_in_router, hipStream_t stream, bool want_f16 = false) {
   RouterArgs a{};
+  a.f16 = c.activation_dtype == FMX_F16 ? 1 : 0;
   a.x = static_cast<const uint16_t*>(x);
   a.wr = wr;
   a.lbias = static_cast<const uint16_t*>(lbias);
@@ -1017,6 +1020,8 @@ int fmx_moe_forward_path(const fmx_moe_config* cfg, int64_t T, int has_packed) {
   int rc;
   if ((rc = check_moe_config(cfg))) return -rc;
   if (T < 0 || T > kMoEMaxTokens) return -fail(FMX_ERR_SHAPE, "n_tokens out of range");
+  if (cfg->activation_dtype == FMX_F16 && (!has_packed || !packable(*cfg)))
+    return -fail(FMX_ERR_UNSUPPORTED, "float16 blocks run on packed weights");
   if (!has_packed || !packable(*cfg)) return 0;
   DecodeArgs da{};
   da.T = static_cast<int>(T);
@@ -1138,6 +1143,9 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     return fail(FMX_ERR_ARG, "shared_expert_gate_w (or its scales/biases) NULL or misaligned");
   // packed weights: the forward reads the experts from there only
   const bool use_packed = w->packed != nullptr;
+  const bool f16 = c.activation_dtype == FMX_F16;
+  if (f16 && !use_packed) return fail(FMX_ERR_UNSUPPORTED, "float16 blocks run on packed weights");
+  if (f16 && nin) return fail(FMX_ERR_UNSUPPORTED, "the input norm in K1 is bf16 only");
   if (nin && (!use_packed || T > kDecNinMaxT || !nin->h || !nin->w || !aligned(nin->h, 16) || !aligned(nin->w, 16)))
     return fail(FMX_ERR_UNSUPPORTED, "input norm in K1: decode forwards of up to %d tokens on packed weights",
                 kDecNinMaxT);
@@ -1180,6 +1188,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.I = static_cast<int>(I);
     da.Is = static_cast<int>(Is);
     da.norm = c.norm_topk_prob ? 1 : 0;
+    da.f16 = f16 ? 1 : 0;
     da.x = static_cast<const uint16_t*>(x);
     da.wr = wr;
     da.lbias = static_cast<const uint16_t*>(w->router_logit_bias);
@@ -1274,6 +1283,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       s.n_exp = static_cast<int>(E);
       s.rows_max = static_cast<int>(n);
       s.x_rows = static_cast<int>(row_map ? T : n);
+      s.io_f16 = f16 ? 1 : 0;
       return s;
     };
     auto shared = [&](const uint8_t* wp, const uint16_t* xr, const uint16_t* xrh, int64_t ldx,
@@ -1290,6 +1300,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
       s.nu = static_cast<int>(K / 128);
       s.rows_static = s.rows_max = s.x_rows = static_cast<int>(T);
       s.n_exp = 1;
+      s.io_f16 = f16 ? 1 : 0;
       return s;
     };
     const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -1302,9 +1313,10 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
         pa.s0 = shared(pk + PL.sgu, xb, L.xh, H, L.hs, L.hsh, Is, Is, H);
         pa.n_items0 = pf_items(pa.s0, true);
       }
+      // a float16 block's rows are fp16 already: no range flag, no exact path
       pa.f16_flag = L.f16_flag;
-      pa.flag_in = kF16FlagX;
-      pa.flag_out = kF16FlagH;
+      pa.flag_in = f16 ? 0u : kF16FlagX;
+      pa.flag_out = f16 ? 0u : kF16FlagH;
       FMX_HIP(launch_pf(pa, true, stream));
     }
     FMX_HIP(mark(2));
@@ -1331,7 +1343,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
         sd_split = pa.s0.ksplit;
       }
       pa.f16_flag = L.f16_flag;
-      pa.flag_in = kF16FlagH;
+      pa.flag_in = f16 ? 0u : kF16FlagH;
       pa.flag_out = 0u;
       FMX_HIP(launch_pf(pa, false, stream));
     }
@@ -1348,6 +1360,7 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     cb.T = static_cast<int>(T);
     cb.k = static_cast<int>(k);
     cb.H = static_cast<int>(H);
+    cb.f16 = f16 ? 1 : 0;
     FMX_HIP(launch_combine(cb, stream));
     FMX_HIP(mark(4));
     return ok();
@@ -1538,7 +1551,9 @@ int fmx_moe_router_topk_ex(const fmx_moe_config* cfg, const void* x, int64_t T, 
                        static_cast<uint16_t*>(probs), shared_gate_out ? L.sgate : nullptr, nullptr, false,
                        nullptr, stream)))
     return rc;
-  if (shared_gate_out) FMX_HIP(launch_f32_bf16(L.sgate, T, static_cast<uint16_t*>(shared_gate_out), stream));
+  if (shared_gate_out)
+    FMX_HIP(launch_f32_bf16(L.sgate, T, static_cast<uint16_t*>(shared_gate_out), stream,
+                            cfg->activation_dtype == FMX_F16));
   return FMX_OK;
 }
 

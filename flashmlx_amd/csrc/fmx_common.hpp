@@ -98,6 +98,72 @@ __device__ inline uint16_t swiglu_bf16(float g_bf, float u_bf) {
   return f32_to_bf16(t * u_bf);
 }
 
+// ---- float16 activations (a float16 checkpoint, model.cpp:208-214)
+
+__host__ __device__ inline float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// round to nearest even (the conversion instruction's default mode)
+__device__ inline uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+__device__ inline float round_f16(float f) { return f16_to_f32(f32_to_f16(f)); }
+
+// Single round-to-nearest-even from fp64 to fp16, on the integer image of
+// the double: keep the top 10 fraction bits of a normal result, or scale the
+// value onto fp16's subnormal grid (exact power-of-two multiply, then rint);
+// from 65520 (the midpoint past the largest finite value) it is infinite.
+__device__ inline uint16_t f64_to_f16(double d) {
+  const uint64_t u = static_cast<uint64_t>(__double_as_longlong(d));
+  const uint16_t sign = static_cast<uint16_t>((u >> 48) & 0x8000u);
+  const uint64_t a = u & 0x7fffffffffffffffull;
+  if (a > 0x7ff0000000000000ull) return sign | 0x7e00u;               // NaN
+  if (a >= 0x40effe0000000000ull) return sign | 0x7c00u;              // >= 65520: inf
+  if (a < 0x3f10000000000000ull)                                      // < 2^-14: subnormal
+    return sign | static_cast<uint16_t>(rint(fabs(d) * 0x1p24));      // 0..1024
+  const uint64_t r = (a + 0x000001ffffffffffull + ((a >> 42) & 1u)) >> 42;
+  return sign | static_cast<uint16_t>(r - (static_cast<uint64_t>(1023 - 15) << 10));
+}
+
+// fp16(sigmoid(v)) for an fp16-valued v, computed in fp64 and rounded once
+__device__ inline float sigmoid_f16(float v) {
+  const double s = 1.0 / (1.0 + exp(-static_cast<double>(v)));
+  return f16_to_f32(f64_to_f16(s));
+}
+
+// MLX's compiled SwiGLU on float16 arrays: every op rounded to fp16
+__device__ inline uint16_t swiglu_f16(float g_h, float u_h) {
+  const float e = __builtin_amdgcn_exp2f(-g_h * 1.4426950408889634f);
+  const float sg = round_f16(__builtin_amdgcn_rcpf(1.0f + e));
+  const float t = round_f16(g_h * sg);
+  return f32_to_f16(t * u_h);
+}
+
+// The activation dtype's loads and roundings: Act<false> bf16, Act<true>
+// fp16; lo / hi load the low / high element of a 32-bit pair
+template <bool F16>
+struct Act {
+  static __device__ inline float ld(uint16_t h) { return bf16_to_f32(h); }
+  static __device__ inline float lo(uint32_t v) { return __uint_as_float(v << 16); }
+  static __device__ inline float hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+  static __device__ inline uint16_t st(float f) { return f32_to_bf16(f); }
+  static __device__ inline float rnd(float f) { return round_bf16(f); }
+  static __device__ inline uint16_t from64(double d) { return f64_to_bf16(d); }
+  static __device__ inline float sigmoid(float v) { return sigmoid_bf16(v); }
+  static __device__ inline uint16_t swiglu(float g, float u) { return swiglu_bf16(g, u); }
+};
+template <>
+struct Act<true> {
+  static __device__ inline float ld(uint16_t h) { return f16_to_f32(h); }
+  static __device__ inline float lo(uint32_t v) { return f16_to_f32(static_cast<uint16_t>(v)); }
+  static __device__ inline float hi(uint32_t v) { return f16_to_f32(static_cast<uint16_t>(v >> 16)); }
+  static __device__ inline uint16_t st(float f) { return f32_to_f16(f); }
+  static __device__ inline float rnd(float f) { return round_f16(f); }
+  static __device__ inline uint16_t from64(double d) { return f64_to_f16(d); }
+  static __device__ inline float sigmoid(float v) { return sigmoid_f16(v); }
+  static __device__ inline uint16_t swiglu(float g, float u) { return swiglu_f16(g, u); }
+};
+
 // Octet permutation of activation rows ("P8 layout"). Within each run of 8
 // consecutive elements, element i is stored at slot p8_slot(i):
 // 0,4,1,5,2,6,3,7 -> slots 0..7. A packed weight word's nibble pairs

@@ -68,7 +68,7 @@ __host__ __device__ inline int k1_lds_main(int T, int H) {
 
 // tile_units_lds for NP tile pairs at once: every pair's loads are issued
 // before the one wait, then the pairs are multiplied in turn.
-template <int NP, int NU>
+template <int NP, int NU, bool F16>
 __device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0, int u1, const uint16_t* xl,
                                        int lane, f32x4_t (&acc)[NP][2]) {
   PkUnit<true> L[NP][NU];
@@ -83,10 +83,10 @@ __device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0,
 #pragma unroll
   for (int d = 0; d < NU; ++d) {
     if (u0 + d < u1) {
-      bf16x8_t A[4];
-      lds_a(xl + (u0 + d) * 128, A);
+      act8_t<F16> A[4];
+      lds_a<F16>(xl + (u0 + d) * 128, A);
 #pragma unroll
-      for (int p = 0; p < NP; ++p) pk_unit<true>(L[p][d], A, acc[p][0], acc[p][1]);
+      for (int p = 0; p < NP; ++p) pk_unit<true, F16>(L[p][d], A, acc[p][0], acc[p][1]);
     }
   }
 }
@@ -102,8 +102,10 @@ __device__ inline void pairs_units_lds(const uint8_t* const (&base)[NP], int u0,
 // Lane l takes the experts e = r + 64 i, r the 6-bit reverse of l: lane l
 // accumulates r's partial normaliser, and the DPP tree (adjacent lanes
 // first) then adds the partials r and r xor 32 first, r xor 16 next, .., the
-// association of the oracle's butterfly (w = 32, 16, .., 1).
-template <int NPER, int NT>
+// association of the oracle's butterfly (w = 32, 16, .., 1). F16: logits,
+// probabilities and scores in fp16 (nonnegative fp16 patterns order like
+// their values too).
+template <int NPER, int NT, bool F16>
 __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uint16_t* s_lg, int lane,
                              uint32_t* s_inds) {
   const int E = a.E, ld = E + 1;
@@ -117,10 +119,10 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
       const int e = r + 64 * i;
-      lf[n][i] = e < E ? bf16_to_f32(s_lg[t * ld + e]) : -__builtin_huge_valf();
+      lf[n][i] = e < E ? Act<F16>::ld(s_lg[t * ld + e]) : -__builtin_huge_valf();
       mf = fmaxf(mf, lf[n][i]);
     }
-    // bf16 logits are exact in fp32: the fp32 maximum is the fp64 one
+    // bf16 (fp16) logits are exact in fp32: the fp32 maximum is the fp64 one
     m[n] = static_cast<double>(wave_max_f32(mf));
   }
 #pragma unroll
@@ -143,7 +145,7 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
       const int e = r + 64 * i;
       key[n][i] = 0u;
       if (e < E) {
-        const uint16_t p = f64_to_bf16(ex[n][i] / s[n]);
+        const uint16_t p = Act<F16>::from64(ex[n][i] / s[n]);
         if (a.probs && ts[n] < a.T) a.probs[static_cast<int64_t>(ts[n]) * E + e] = p;
         // probabilities are >= 0: their bf16 patterns order like their values
         key[n][i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
@@ -171,7 +173,7 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
 #pragma unroll
       for (int i = 0; i < NPER; ++i)
         if (key[n][i] == best[n]) key[n][i] = 0u;
-      sc_sum[n] += bf16_to_f32(static_cast<uint16_t>(best[n] >> 16));  // fp32, slot order
+      sc_sum[n] += Act<F16>::ld(static_cast<uint16_t>(best[n] >> 16));  // fp32, slot order
       if (lane == j) my_key[n] = best[n];
     }
   }
@@ -183,8 +185,8 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
       const uint32_t e = 0xffffu - (my_key[n] & 0xffffu);
       uint16_t sc = static_cast<uint16_t>(my_key[n] >> 16);
       if (a.norm) {
-        const double den = static_cast<double>(round_bf16(sc_sum[n]));
-        sc = f32_to_bf16(static_cast<float>(static_cast<double>(bf16_to_f32(sc)) / den));
+        const double den = static_cast<double>(Act<F16>::rnd(sc_sum[n]));
+        sc = Act<F16>::st(static_cast<float>(static_cast<double>(Act<F16>::ld(sc)) / den));
       }
       s_inds[t * a.k + lane] = e;
       a.inds[t * a.k + lane] = e;
@@ -203,7 +205,7 @@ __device__ void route_tokens(const DecodeArgs& a, const int (&ts)[NT], const uin
 // operations complete in order, so no workgroup barrier follows the
 // routing's), the other waves form the shared gate's sigmoid and reset K23's
 // counters meanwhile.
-template <int NPER>
+template <int NPER, bool F16>
 __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg, uint32_t ep) {
   __shared__ uint32_t s_inds[kDecMaxT * kDecMaxK];
   __shared__ uint16_t s_segof[kDecMaxE];
@@ -249,20 +251,20 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg, uint32_t ep) {
   if (T <= kDecWaves) {
     if (wave < T) {
       const int ts[1] = {wave};
-      route_tokens<NPER, 1>(a, ts, s_lg, lane, s_inds);
+      route_tokens<NPER, 1, F16>(a, ts, s_lg, lane, s_inds);
     }
   } else {
     // tokens wave, wave + 4 (, wave + 8, wave + 12) interleaved in one wave
     for (int t0 = wave; t0 < T; t0 += 2 * kDecWaves) {
       const int ts[2] = {t0, t0 + kDecWaves};
-      route_tokens<NPER, 2>(a, ts, s_lg, lane, s_inds);
+      route_tokens<NPER, 2, F16>(a, ts, s_lg, lane, s_inds);
     }
   }
   lds_barrier();
   if (wave != 0) {
     const int w = tid - kWave;
     if (a.wsg.w)
-      for (int t = w; t < T; t += kDecThreads - kWave) a.sgate[t] = sigmoid_bf16(bf16_to_f32(s_lg[t * ld + E]));
+      for (int t = w; t < T; t += kDecThreads - kWave) a.sgate[t] = Act<F16>::sigmoid(Act<F16>::ld(s_lg[t * ld + E]));
     // K23's per-expert gate/up counters and done flags start the next grid
     // at zero (stores that drain with the kernel, off the chain)
     for (int i = w; i < a.max_seg * (1 + kDecGuFlags); i += kDecThreads - kWave)
@@ -302,7 +304,7 @@ __device__ void route_finish(const DecodeArgs& a, uint16_t* s_lg, uint32_t ep) {
 // and the four waves' in LDS. The last router workgroup to finish derives
 // the routing. NT: T rounded up to a power of two (the reduce-scatter's
 // width).
-template <int NPER, int NT, bool NIN>
+template <int NPER, int NT, bool NIN, bool F16>
 __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   double* s_lp = reinterpret_cast<double*>(smem);
   uint16_t* s_lg = reinterpret_cast<uint16_t*>(smem + kDecK1LpBytes);
@@ -313,8 +315,8 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   const int nch = H / 8;
   const uint32_t ep = __builtin_amdgcn_readfirstlane(*a.epoch);
   if (!NIN) dma_rows(a.x, H, T, H, s_x, xs, wave, kDecWaves, lane);
-  const RChunk wv = c < E ? load_rchunk(a.wr, c, H, min(tid, nch - 1))
-                          : load_rchunk(a.wsg, 0, H, min(tid, nch - 1));
+  const RChunk wv = c < E ? load_rchunk<F16>(a.wr, c, H, min(tid, nch - 1))
+                          : load_rchunk<F16>(a.wsg, 0, H, min(tid, nch - 1));
   const bool biased = c < E && a.lbias;
   const uint16_t lb = biased ? a.lbias[c] : 0;
   if constexpr (NIN) {
@@ -334,7 +336,7 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
   }
   double wd[8];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) wd[q] = tid < nch ? wv.get(q) : 0.0;
+  for (int q = 0; q < 8; ++q) wd[q] = tid < nch ? wv.template get<F16>(q) : 0.0;
   double part[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -343,8 +345,8 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
       const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(s_x + t * xs + min(tid, nch - 1) * 8);
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        part[t] = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] << 16)), wd[2 * q], part[t]);
-        part[t] = __builtin_fma(static_cast<double>(__uint_as_float(xv[q] & 0xffff0000u)), wd[2 * q + 1], part[t]);
+        part[t] = __builtin_fma(static_cast<double>(Act<F16>::lo(xv[q])), wd[2 * q], part[t]);
+        part[t] = __builtin_fma(static_cast<double>(Act<F16>::hi(xv[q])), wd[2 * q + 1], part[t]);
       }
     }
   }
@@ -361,20 +363,20 @@ __device__ void dec_router(const DecodeArgs& a, int c, uint8_t* smem) {
     double v = 0.0;
 #pragma unroll
     for (int q = 0; q < kDecWaves; ++q) v += s_lp[q * kDecMaxT + tid];
-    uint16_t l = f64_to_bf16(v);
-    if (biased) l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(lb)));
+    uint16_t l = Act<F16>::from64(v);
+    if (biased) l = Act<F16>::from64(static_cast<double>(Act<F16>::ld(l)) + static_cast<double>(Act<F16>::ld(lb)));
     __hip_atomic_store(a.lgx + c * T + tid, (static_cast<uint64_t>(ep) << 32) | l, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
     a.logits[tid * (E + 1) + c] = l;  // the routing accessor's copy
   }
   if (c != 0) return;
-  route_finish<NPER>(a, s_lg, ep);
+  route_finish<NPER, F16>(a, s_lg, ep);
 }
 
 // Shared expert gate/up + SwiGLU for tile pair tp (model.cpp:741-747):
 // hs[t, n] = swiglu(x_t . Wg[n], x_t . Wu[n]) for every token; wave q
 // multiplies K quarter q.
-template <int NT, bool NIN>
+template <int NT, bool NIN, bool F16>
 __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + kDecQuadRedBytes);
@@ -419,9 +421,9 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
       if (u0 + d < u1) {
-        bf16x8_t A[4];
-        lds_a(xl + (u0 + d) * 128, A);
-        pk_unit<true>(L[d], A, acc0, acc1);
+        act8_t<F16> A[4];
+        lds_a<F16>(xl + (u0 + d) * 128, A);
+        pk_unit<true, F16>(L[d], A, acc0, acc1);
       }
     }
   } else {
@@ -439,9 +441,9 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
       if (u0 + d < u1) {
-        bf16x8_t A[4];
-        lds_a(xl + (u0 + d) * 128, A);
-        pk_unit<true>(L[d], A, acc0, acc1);
+        act8_t<F16> A[4];
+        lds_a<F16>(xl + (u0 + d) * 128, A);
+        pk_unit<true, F16>(L[d], A, acc0, acc1);
       }
     }
   }
@@ -452,7 +454,7 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
     for (int i = 0; i < 4; ++i) {
       const int t = 4 * j + i;
       if (t < T)
-        a.hs[static_cast<int64_t>(t) * Is + n] = swiglu_bf16(round_bf16(acc0[i]), round_bf16(acc1[i]));
+        a.hs[static_cast<int64_t>(t) * Is + n] = Act<F16>::swiglu(Act<F16>::rnd(acc0[i]), Act<F16>::rnd(acc1[i]));
     }
   }
   wait_vmcnt0();  // the warming's LDS writes land before the workgroup's LDS is released
@@ -460,14 +462,16 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
 
 // Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
 // NIN: the input norm formed here (single-row forwards of the decoder stack)
-template <int NPER, int NT, bool NIN>
+// F16: the float16 block (no input norm)
+template <int NPER, int NT, bool NIN, bool F16>
 __global__ __launch_bounds__(kDecThreads) void dec_k1(DecodeArgs a) {
+  static_assert(!(NIN && F16), "the input norm is formed in bf16");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int w = blockIdx.x;
   if (w < a.n_rt)
-    dec_router<NPER, NT, NIN>(a, w, smem);
+    dec_router<NPER, NT, NIN, F16>(a, w, smem);
   else
-    dec_shared_gu<NT, NIN>(a, w - a.n_rt, smem);
+    dec_shared_gu<NT, NIN, F16>(a, w - a.n_rt, smem);
 }
 
 // ---------------------------------------------------------------- K2: routed gate/up
@@ -494,7 +498,7 @@ __device__ void dec_sort(const DecodeArgs& a) {
 // workgroup runs the sort for the routing accessors. SIGNAL (in K23): the h
 // values go out as device-scope stores and, once they have completed, the
 // tile is counted in on its expert's gate/up counter.
-template <bool SIGNAL, int NP>
+template <bool SIGNAL, int NP, bool F16>
 __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
   float* s_red = reinterpret_cast<float*>(smem);
   uint16_t* s_x = reinterpret_cast<uint16_t*>(smem + NP * kDecQuadRedBytes);
@@ -532,7 +536,7 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
     acc[p][1] = acc[p][0];
     base[p] = a.gu + static_cast<int64_t>(e) * a.gu_es + static_cast<int64_t>(tp0 + p) * nu * kBlockPair;
   }
-  pairs_units_lds<NP, kDecK2Units>(base, u0, u1, xl, lane, acc);
+  pairs_units_lds<NP, kDecK2Units, F16>(base, u0, u1, xl, lane, acc);
 #pragma unroll
   for (int p = 0; p < NP; ++p)
     quad_reduce(acc[p][0], acc[p][1], wave, lane, s_red + p * (kDecQuadRedBytes / 4));
@@ -548,7 +552,7 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
       const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
       if (t < T && slot < static_cast<uint32_t>(k)) {
         uint16_t* dst = a.h + static_cast<int64_t>(t * k + slot) * I + n;
-        const uint16_t v = swiglu_bf16(round_bf16(acc[p][0][i]), round_bf16(acc[p][1][i]));
+        const uint16_t v = Act<F16>::swiglu(Act<F16>::rnd(acc[p][0][i]), Act<F16>::rnd(acc[p][1][i]));
         if (SIGNAL)
           __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
@@ -571,10 +575,10 @@ __device__ void dec_gu_tile(const DecodeArgs& a, int b, uint8_t* smem) {
 }
 
 // K2 alone (forwards that stop after the gate/up stage)
-template <int NP>
+template <int NP, bool F16>
 __global__ __launch_bounds__(kDecThreads) void dec_k2(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  dec_gu_tile<false, NP>(a, blockIdx.x, smem);
+  dec_gu_tile<false, NP, F16>(a, blockIdx.x, smem);
 }
 
 // ---------------------------------------------------------------- K3: down projections
@@ -586,8 +590,10 @@ constexpr int kDnSmallUnits = 12;  // a ring this short leaves room for four wor
 // The top-k weighted combine of column block cb (columns 64 cb .. 64 cb + 63)
 // for every token (model.cpp:782-803): y = bf16(sum over slots, fp32 in slot
 // order, of bf16(d * score)) + bf16(sigmoid(gate) * bf16(shared down, K
-// slices added in order)). d and the shared slices were written by other
-// workgroups with device-scope stores; they are read with device-scope loads.
+// slices added in order)) (F16: every rounding to fp16). d and the shared
+// slices were written by other workgroups with device-scope stores; they are
+// read with device-scope loads.
+template <bool F16>
 __device__ void dec_combine(const DecodeArgs& a, int cb) {
   const int T = a.T, k = a.k, H = a.H;
   for (int g = threadIdx.x; g < T * 32; g += kDecThreads) {
@@ -615,12 +621,13 @@ __device__ void dec_combine(const DecodeArgs& a, int cb) {
 #pragma unroll
     for (int q = 0; q < kDecMaxK; ++q) {
       if (q < k) {
-        const float sc = bf16_to_f32(sv[q]);
+        const float sc = Act<F16>::ld(sv[q]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i] += round_bf16(bf16_to_f32(static_cast<uint16_t>(dv[2 * q + i])) * sc);
+        for (int i = 0; i < 2; ++i)
+          acc[i] += Act<F16>::rnd(Act<F16>::ld(static_cast<uint16_t>(dv[2 * q + i])) * sc);
       }
     }
-    float yv[2] = {round_bf16(acc[0]), round_bf16(acc[1])};
+    float yv[2] = {Act<F16>::rnd(acc[0]), Act<F16>::rnd(acc[1])};
     if (a.Is > 0) {
       const float gt = a.sgate[t];
 #pragma unroll
@@ -628,11 +635,11 @@ __device__ void dec_combine(const DecodeArgs& a, int cb) {
         float sd = 0.f;
 #pragma unroll
         for (int ks = 0; ks < kDecSdSplit; ++ks) sd += __uint_as_float(sp[2 * ks + i]);
-        yv[i] += round_bf16(gt * round_bf16(sd));
+        yv[i] += Act<F16>::rnd(gt * Act<F16>::rnd(sd));
       }
     }
     *reinterpret_cast<uint32_t*>(a.y + static_cast<int64_t>(t) * H + c) =
-        static_cast<uint32_t>(f32_to_bf16(yv[0])) | (static_cast<uint32_t>(f32_to_bf16(yv[1])) << 16);
+        static_cast<uint32_t>(Act<F16>::st(yv[0])) | (static_cast<uint32_t>(Act<F16>::st(yv[1])) << 16);
   }
 }
 
@@ -640,6 +647,7 @@ __device__ void dec_combine(const DecodeArgs& a, int cb) {
 // device-scope stores have completed; the last of the block's contributors
 // (its U routed experts and the shared expert's K slices) combines the block
 // and resets the count.
+template <bool F16>
 __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
   __shared__ int s_last_cb;
   wait_vmcnt0();
@@ -651,7 +659,7 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
   }
   __syncthreads();
   if (!s_last_cb) return;
-  dec_combine(a, cb);
+  dec_combine<F16>(a, cb);
   if (threadIdx.x == 0)
     __hip_atomic_store(a.cb_counter + cb * kDecCbStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -675,7 +683,7 @@ __device__ void dec_arrive(const DecodeArgs& a, int cb, int U) {
 // failure shows in y instead of stale rows passing for results, and sets
 // kStatusWaitTimeout in the workspace's status word.
 
-template <int NU, int TPW>
+template <int NU, int TPW, bool F16>
 __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s_a) {
   // TPW column blocks of 64 (cb = TPW*cbp + c), one 16-row tile of each per wave
   static_assert(TPW == 1 || TPW == 2, "one or two column blocks per workgroup");
@@ -735,10 +743,10 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
 #pragma unroll
   for (int d = 0; d < PER; ++d) {
     if (d < nu) {
-      bf16x8_t A[4];
-      lds_a(xl + d * 128, A);
+      act8_t<F16> A[4];
+      lds_a<F16>(xl + d * 128, A);
 #pragma unroll
-      for (int c = 0; c < TPW; ++c) pk_unit<false>(L[c * PER + d], A, acc[c], unused);
+      for (int c = 0; c < TPW; ++c) pk_unit<false, F16>(L[c * PER + d], A, acc[c], unused);
     }
   }
   if (s_timed_out) {
@@ -754,17 +762,17 @@ __device__ void dec_down_routed(const DecodeArgs& a, int u, int cbp, uint16_t* s
       const int t = 4 * j + i;
       const uint32_t slot = (my_slots >> (8 * i)) & 0xffu;
       if (t < T && slot < static_cast<uint32_t>(k))
-        __hip_atomic_store(a.dw + static_cast<int64_t>(t * k + slot) * H + n, static_cast<uint32_t>(f32_to_bf16(acc[c][i])),
+        __hip_atomic_store(a.dw + static_cast<int64_t>(t * k + slot) * H + n, static_cast<uint32_t>(Act<F16>::st(acc[c][i])),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 #pragma unroll
-  for (int c = 0; c < TPW; ++c) dec_arrive(a, TPW * cbp + c, U);
+  for (int c = 0; c < TPW; ++c) dec_arrive<F16>(a, TPW * cbp + c, U);
 }
 
 // Shared expert down projection, columns 64*cb .. +63, K slice ks of
 // kDecSdSplit (model.cpp:746-747): fp32 partial sums sd_part[ks][t][n].
-template <int NU>
+template <int NU, bool F16>
 __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s_a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -778,7 +786,7 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
   const int m = lane & 15, j = lane >> 4;
   const uint16_t* xl = s_a + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = acc;
-  tile_units_lds<false, NU>(tb, 0, nu, xl, lane, acc, unused);
+  tile_units_lds<false, NU, F16>(tb, 0, nu, xl, lane, acc, unused);
   const int n = tile * 16 + m;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -787,7 +795,7 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
       __hip_atomic_store(reinterpret_cast<uint32_t*>(a.sd_part) + (static_cast<int64_t>(ks) * T + t) * H + n,
                          __float_as_uint(acc[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  dec_arrive(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
+  dec_arrive<F16>(a, cb, static_cast<int>(min(a.seg[0], static_cast<uint32_t>(a.max_seg))));
 }
 
 // K23 in dispatch order: K2's workgroups (the gate/up tiles, expert-major,
@@ -797,7 +805,7 @@ __device__ void dec_down_shared(const DecodeArgs& a, int cb, int ks, uint16_t* s
 // (Dispatching an expert's down workgroups right behind its tiles, about one
 // resident grid later, measured slower: their waits hold slots that the
 // tiles still need.)
-template <int NU, int NP, int TPW>
+template <int NU, int NP, int TPW, bool F16>
 __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t* s_a = reinterpret_cast<uint16_t*>(smem);
@@ -806,11 +814,11 @@ __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
   const int n_shared = a.Is > 0 ? (a.H / (16 * kDnTiles)) * kDecSdSplit : 0;
   const int b = blockIdx.x;
   if (b < n_gu)
-    dec_gu_tile<true, NP>(a, b, smem);
+    dec_gu_tile<true, NP, F16>(a, b, smem);
   else if (b - n_gu < n_shared)
-    dec_down_shared<NU>(a, (b - n_gu) / kDecSdSplit, (b - n_gu) % kDecSdSplit, s_a);
+    dec_down_shared<NU, F16>(a, (b - n_gu) / kDecSdSplit, (b - n_gu) % kDecSdSplit, s_a);
   else
-    dec_down_routed<NU, TPW>(a, (b - n_gu - n_shared) / D, (b - n_gu - n_shared) % D, s_a);
+    dec_down_routed<NU, TPW, F16>(a, (b - n_gu - n_shared) / D, (b - n_gu - n_shared) % D, s_a);
 }
 
 }  // namespace
@@ -850,40 +858,52 @@ bool decode_plan(DecodeArgs& a) {
   return k1_lds(a) <= 160 * 1024 && k2_lds(a) <= 160 * 1024 && k3_lds(a) <= 160 * 1024;
 }
 
-template <int NPER>
+template <int NPER, bool F16>
 static void launch_k1_nt(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.n_rt + a.n_sgu), block(kDecThreads);
   static_assert(kDecNinMaxT == 1, "the input-norm K1 is instantiated for one row");
-  if (a.nin)
-    hipLaunchKernelGGL((dec_k1<NPER, 1, true>), grid, block, k1_lds(a), stream, a);
-  else if (a.T <= 1)
-    hipLaunchKernelGGL((dec_k1<NPER, 1, false>), grid, block, k1_lds(a), stream, a);
+  if constexpr (!F16) {
+    if (a.nin) {
+      hipLaunchKernelGGL((dec_k1<NPER, 1, true, false>), grid, block, k1_lds(a), stream, a);
+      return;
+    }
+  }
+  if (a.T <= 1)
+    hipLaunchKernelGGL((dec_k1<NPER, 1, false, F16>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 2)
-    hipLaunchKernelGGL((dec_k1<NPER, 2, false>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 2, false, F16>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 4)
-    hipLaunchKernelGGL((dec_k1<NPER, 4, false>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 4, false, F16>), grid, block, k1_lds(a), stream, a);
   else if (a.T <= 8)
-    hipLaunchKernelGGL((dec_k1<NPER, 8, false>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 8, false, F16>), grid, block, k1_lds(a), stream, a);
   else
-    hipLaunchKernelGGL((dec_k1<NPER, 16, false>), grid, block, k1_lds(a), stream, a);
+    hipLaunchKernelGGL((dec_k1<NPER, 16, false, F16>), grid, block, k1_lds(a), stream, a);
+}
+
+template <bool F16>
+static void launch_k1_dt(const DecodeArgs& a, hipStream_t stream) {
+  if (a.E <= 64)
+    launch_k1_nt<1, F16>(a, stream);
+  else if (a.E <= 128)
+    launch_k1_nt<2, F16>(a, stream);
+  else
+    launch_k1_nt<4, F16>(a, stream);
 }
 
 hipError_t launch_decode_k1(const DecodeArgs& a, hipStream_t stream) {
-  if (a.E <= 64)
-    launch_k1_nt<1>(a, stream);
-  else if (a.E <= 128)
-    launch_k1_nt<2>(a, stream);
+  if (a.f16)
+    launch_k1_dt<true>(a, stream);
   else
-    launch_k1_nt<4>(a, stream);
+    launch_k1_dt<false>(a, stream);
   return hipGetLastError();
 }
 
 hipError_t launch_decode_k2(const DecodeArgs& a, hipStream_t stream) {
   const dim3 grid(a.max_seg * a.gu_wgs + 1);
   if (a.k2_pairs == 2)
-    hipLaunchKernelGGL(dec_k2<2>, grid, dim3(kDecThreads), k2_lds(a), stream, a);
+    hipLaunchKernelGGL((a.f16 ? dec_k2<2, true> : dec_k2<2, false>), grid, dim3(kDecThreads), k2_lds(a), stream, a);
   else
-    hipLaunchKernelGGL(dec_k2<1>, grid, dim3(kDecThreads), k2_lds(a), stream, a);
+    hipLaunchKernelGGL((a.f16 ? dec_k2<1, true> : dec_k2<1, false>), grid, dim3(kDecThreads), k2_lds(a), stream, a);
   return hipGetLastError();
 }
 
@@ -912,7 +932,10 @@ static int k3_workgroups(const DecodeArgs& a) {
 
 template <int NU, int NP, int TPW>
 static void launch_k23(const DecodeArgs& a, int n, size_t lds, hipStream_t stream) {
-  hipLaunchKernelGGL((dec_k23<NU, NP, TPW>), dim3(n), dim3(kDecThreads), lds, stream, a);
+  if (a.f16)
+    hipLaunchKernelGGL((dec_k23<NU, NP, TPW, true>), dim3(n), dim3(kDecThreads), lds, stream, a);
+  else
+    hipLaunchKernelGGL((dec_k23<NU, NP, TPW, false>), dim3(n), dim3(kDecThreads), lds, stream, a);
 }
 
 template <int NU, int NP>

@@ -2,6 +2,8 @@
 // (library-internal).
 #pragma once
 
+#include <type_traits>
+
 #include "fmx_kernels.hpp"
 
 extern "C" __device__ __attribute__((const)) double __ockl_wfred_max_f64(double);
@@ -253,26 +255,30 @@ __device__ inline bool rs64_holder(int lane) {
 // scale and bias (RouterRows). get(j) is weight j as an exact double: for the
 // quantized form s*q + b of bf16 s, b and q in 0..15 (MLX's dequantised
 // value, model.cpp:758-760), whose product and sum are exact in fp64.
+// F16: the row, or the scales and biases, in float16 (s*q + b of fp16 s, b
+// is exact in fp64 too).
 struct RChunk {
-  u32x4_t v;  // the bf16 chunk, or v[0] = the 4-bit word
+  u32x4_t v;  // the bf16 (fp16) chunk, or v[0] = the 4-bit word
   float s, b;
   bool q;
+  template <bool F16 = false>
   __device__ inline double get(int j) const {
     if (q) return __builtin_fma(static_cast<double>(s), static_cast<double>((v[0] >> (4 * j)) & 15u),
                                 static_cast<double>(b));
     const uint32_t w = v[j >> 1];
-    return static_cast<double>(__uint_as_float((j & 1) ? (w & 0xffff0000u) : (w << 16)));
+    return static_cast<double>((j & 1) ? Act<F16>::hi(w) : Act<F16>::lo(w));
   }
 };
 
+template <bool F16 = false>
 __device__ inline RChunk load_rchunk(const RouterRows& r, int64_t row, int H, int ch) {
   RChunk c;
   c.q = r.s != nullptr;
   if (c.q) {
     c.v = u32x4_t{static_cast<const uint32_t*>(r.w)[row * (H / 8) + ch], 0u, 0u, 0u};
     const int64_t g = row * (H / 64) + ch / 8;
-    c.s = bf16_to_f32(r.s[g]);
-    c.b = bf16_to_f32(r.b[g]);
+    c.s = Act<F16>::ld(r.s[g]);
+    c.b = Act<F16>::ld(r.b[g]);
   } else {
     c.v = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(r.w) + row * H + ch * 8);
     c.s = c.b = 0.0f;
@@ -479,6 +485,45 @@ __device__ inline u32x4_t bf16_chunk_to_f16_q8(u32x4_t v, bool& ovf) {
   return o;
 }
 
+// ------------------------------------------------------------------ operands of either dtype
+//
+// Decode tiles multiply in the activation dtype: bf16 operands on
+// v_mfma_f32_16x16x32_bf16, or fp16 ones (a float16 block) on
+// v_mfma_f32_16x16x32_f16, with the same exact dequantisation. The nibble
+// operands 128 + q are exact in fp16 too (0x5800 | q << 3), and so is a
+// product x.(128 + q) of an fp16 x (11 + 8 significant bits) in fp32.
+
+template <bool F16>
+using act8_t = typename std::conditional<F16, f16x8_t, bf16x8_t>::type;
+
+__device__ inline f32x4_t mfma16(const bf16x8_t& a, const bf16x8_t& b, const f32x4_t& c) { return mfma_bf16(a, b, c); }
+__device__ inline f32x4_t mfma16(const f16x8_t& a, const f16x8_t& b, const f32x4_t& c) { return mfma_f16(a, b, c); }
+
+// nib8 with fp16 pairs
+__device__ inline f16x8_t nib8_f16(uint32_t w) {
+  u32x4_t d;
+  d[0] = ((w << 3) & 0x00780078u) | 0x58005800u;
+  d[1] = ((w >> 1) & 0x00780078u) | 0x58005800u;
+  d[2] = ((w >> 5) & 0x00780078u) | 0x58005800u;
+  d[3] = ((w >> 9) & 0x00780078u) | 0x58005800u;
+  return __builtin_bit_cast(f16x8_t, d);
+}
+
+template <bool F16>
+__device__ inline act8_t<F16> nib8_dt(uint32_t w) {
+  if constexpr (F16)
+    return nib8_f16(w);
+  else
+    return nib8(w);
+}
+
+// eight ones (bf16 0x3f80, fp16 0x3c00)
+template <bool F16>
+__device__ inline act8_t<F16> ones8() {
+  const uint32_t o = F16 ? 0x3c003c00u : 0x3f803f80u;
+  return __builtin_bit_cast(act8_t<F16>, u32x4_t{o, o, o, o});
+}
+
 template <bool DUAL>
 struct PkUnit {
   u32x4_t w0, w1;    // packed words (gate / up)
@@ -504,12 +549,14 @@ __device__ inline PkUnit<DUAL> pk_load(const uint8_t* blk, int lane) {
   return L;
 }
 
-// acc[i] += s0 P0 + (b0 - 128 s0) X0 + s1 P1 + (b1 - 128 s1) X1
+// acc[i] += s0 P0 + (b0 - 128 s0) X0 + s1 P1 + (b1 - 128 s1) X1 (scales and
+// biases in the activation dtype)
+template <bool F16 = false>
 __device__ inline void pk_epi(f32x4_t& acc, const u32x2_t& sb, const f32x4_t& P0, const f32x4_t& P1,
                               const f32x4_t& X0, const f32x4_t& X1) {
-  const float s0 = __uint_as_float(sb[0] << 16), s1 = __uint_as_float(sb[0] & 0xffff0000u);
-  const float c0 = __builtin_fmaf(-128.0f, s0, __uint_as_float(sb[1] << 16));
-  const float c1 = __builtin_fmaf(-128.0f, s1, __uint_as_float(sb[1] & 0xffff0000u));
+  const float s0 = Act<F16>::lo(sb[0]), s1 = Act<F16>::hi(sb[0]);
+  const float c0 = __builtin_fmaf(-128.0f, s0, Act<F16>::lo(sb[1]));
+  const float c1 = __builtin_fmaf(-128.0f, s1, Act<F16>::hi(sb[1]));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     acc[i] = __builtin_fmaf(s0, P0[i], acc[i]);
@@ -521,31 +568,31 @@ __device__ inline void pk_epi(f32x4_t& acc, const u32x2_t& sb, const f32x4_t& P0
 
 // One unit: A[a] (a = 0..3) are the lane's activation operands for k =
 // 32a + 8j .. +7 (P8 order); accumulates into acc0 (and acc1 for a pair).
-template <bool DUAL>
-__device__ inline void pk_unit(const PkUnit<DUAL>& L, const bf16x8_t (&A)[4], f32x4_t& acc0,
+template <bool DUAL, bool F16 = false>
+__device__ inline void pk_unit(const PkUnit<DUAL>& L, const act8_t<F16> (&A)[4], f32x4_t& acc0,
                                f32x4_t& acc1) {
   const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
-  const f32x4_t X0 = mfma_bf16(A[1], ones, mfma_bf16(A[0], ones, zero));
-  const f32x4_t X1 = mfma_bf16(A[3], ones, mfma_bf16(A[2], ones, zero));
+  const act8_t<F16> ones = ones8<F16>();
+  const f32x4_t X0 = mfma16(A[1], ones, mfma16(A[0], ones, zero));
+  const f32x4_t X1 = mfma16(A[3], ones, mfma16(A[2], ones, zero));
   {
-    const f32x4_t P0 = mfma_bf16(A[1], nib8(L.w0[1]), mfma_bf16(A[0], nib8(L.w0[0]), zero));
-    const f32x4_t P1 = mfma_bf16(A[3], nib8(L.w0[3]), mfma_bf16(A[2], nib8(L.w0[2]), zero));
-    pk_epi(acc0, L.sb0, P0, P1, X0, X1);
+    const f32x4_t P0 = mfma16(A[1], nib8_dt<F16>(L.w0[1]), mfma16(A[0], nib8_dt<F16>(L.w0[0]), zero));
+    const f32x4_t P1 = mfma16(A[3], nib8_dt<F16>(L.w0[3]), mfma16(A[2], nib8_dt<F16>(L.w0[2]), zero));
+    pk_epi<F16>(acc0, L.sb0, P0, P1, X0, X1);
   }
   if (DUAL) {
-    const f32x4_t P0 = mfma_bf16(A[1], nib8(L.w1[1]), mfma_bf16(A[0], nib8(L.w1[0]), zero));
-    const f32x4_t P1 = mfma_bf16(A[3], nib8(L.w1[3]), mfma_bf16(A[2], nib8(L.w1[2]), zero));
-    pk_epi(acc1, L.sb1, P0, P1, X0, X1);
+    const f32x4_t P0 = mfma16(A[1], nib8_dt<F16>(L.w1[1]), mfma16(A[0], nib8_dt<F16>(L.w1[0]), zero));
+    const f32x4_t P1 = mfma16(A[3], nib8_dt<F16>(L.w1[3]), mfma16(A[2], nib8_dt<F16>(L.w1[2]), zero));
+    pk_epi<F16>(acc1, L.sb1, P0, P1, X0, X1);
   }
 }
 
 // The four A operands of one unit from an LDS row (P8 layout): xu points at
 // the unit's first element of the lane's row, plus 8*j.
-__device__ inline void lds_a(const uint16_t* xu, bf16x8_t (&A)[4]) {
+template <bool F16 = false>
+__device__ inline void lds_a(const uint16_t* xu, act8_t<F16> (&A)[4]) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a) A[a] = *reinterpret_cast<const bf16x8_t*>(xu + 32 * a);
+  for (int a = 0; a < 4; ++a) A[a] = *reinterpret_cast<const act8_t<F16>*>(xu + 32 * a);
 }
 
 // ------------------------------------------------------------------ decode tiles
@@ -565,7 +612,7 @@ constexpr int kDecQuadRedBytes = (kDecWaves - 1) * 8 * kWave * 4;  // quad_reduc
 // memory operation before this call: right after the weight loads, vmcnt
 // (their count) proves the DMA complete while they stay in flight, and
 // the units are multiplied as their loads land.
-template <bool DUAL, int NU>
+template <bool DUAL, int NU, bool F16 = false>
 __device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, const uint16_t* xl,
                                       int lane, f32x4_t& acc0, f32x4_t& acc1) {
   constexpr int BB = DUAL ? kBlockPair : kBlockSingle;
@@ -579,9 +626,9 @@ __device__ inline void tile_units_lds(const uint8_t* tile_base, int u0, int u1, 
 #pragma unroll
   for (int d = 0; d < NU; ++d) {
     if (u0 + d < u1) {
-      bf16x8_t A[4];
-      lds_a(xl + (u0 + d) * 128, A);
-      pk_unit<DUAL>(L[d], A, acc0, acc1);
+      act8_t<F16> A[4];
+      lds_a<F16>(xl + (u0 + d) * 128, A);
+      pk_unit<DUAL, F16>(L[d], A, acc0, acc1);
     }
   }
 }

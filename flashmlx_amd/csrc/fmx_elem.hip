@@ -16,8 +16,9 @@ static inline unsigned grid_for(int64_t n, int per_block) {
 // ------------------------------------------------------------------ combine
 // y = sum(d_sorted[inv] * scores[..., None], -2)            model.cpp:782-784
 //   + sigmoid(x . w_sg) * shared_expert(x)                   model.cpp:787-803
-// Every MLX op's bf16 result is rounded as MLX rounds it; the k-sum
-// accumulates in fp32 in slot order.
+// Every MLX op's bf16 (F16: fp16) result is rounded as MLX rounds it; the
+// k-sum accumulates in fp32 in slot order.
+template <bool F16>
 __global__ __launch_bounds__(kElemThreads) void combine_kernel(CombineArgs a) {
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
   const int oct = a.H / 8;
@@ -27,17 +28,17 @@ __global__ __launch_bounds__(kElemThreads) void combine_kernel(CombineArgs a) {
   for (int j = 0; j < a.k; ++j) {
     const int64_t ent = static_cast<int64_t>(t) * a.k + j;
     const uint32_t row = min(a.inv[ent], static_cast<uint32_t>(a.T * a.k - 1));
-    const float s = bf16_to_f32(a.scores[ent]);
+    const float s = Act<F16>::ld(a.scores[ent]);
     const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.d + static_cast<int64_t>(row) * a.H + o * 8);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc[2 * i] += round_bf16(__uint_as_float(v[i] << 16) * s);
-      acc[2 * i + 1] += round_bf16(__uint_as_float(v[i] & 0xffff0000u) * s);
+      acc[2 * i] += Act<F16>::rnd(Act<F16>::lo(v[i]) * s);
+      acc[2 * i + 1] += Act<F16>::rnd(Act<F16>::hi(v[i]) * s);
     }
   }
   uint16_t outv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) outv[i] = f32_to_bf16(acc[i]);
+  for (int i = 0; i < 8; ++i) outv[i] = Act<F16>::st(acc[i]);
   if (a.sd || a.sd_part) {
     const float g = a.sgate[t];
     float sdv[8];
@@ -56,19 +57,19 @@ __global__ __launch_bounds__(kElemThreads) void combine_kernel(CombineArgs a) {
         }
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) sdv[i] = round_bf16(sdv[i]);
+      for (int i = 0; i < 8; ++i) sdv[i] = Act<F16>::rnd(sdv[i]);
     } else {
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(a.sd + static_cast<int64_t>(t) * a.H + o * 8);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sdv[2 * i] = __uint_as_float(v[i] << 16);
-        sdv[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+        sdv[2 * i] = Act<F16>::lo(v[i]);
+        sdv[2 * i + 1] = Act<F16>::hi(v[i]);
       }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float sh = round_bf16(g * sdv[i]);
-      outv[i] = f32_to_bf16(bf16_to_f32(outv[i]) + sh);
+      const float sh = Act<F16>::rnd(g * sdv[i]);
+      outv[i] = Act<F16>::st(Act<F16>::ld(outv[i]) + sh);
     }
   }
   u32x4_t w;
@@ -81,8 +82,8 @@ __global__ __launch_bounds__(kElemThreads) void combine_kernel(CombineArgs a) {
 hipError_t launch_combine(const CombineArgs& a, hipStream_t stream) {
   const int64_t n = static_cast<int64_t>(a.T) * (a.H / 8);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3(grid_for(n, kElemThreads)), dim3(kElemThreads), 0,
-                     stream, a);
+  hipLaunchKernelGGL((a.f16 ? combine_kernel<true> : combine_kernel<false>), dim3(grid_for(n, kElemThreads)),
+                     dim3(kElemThreads), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -164,16 +165,18 @@ hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t strea
   return hipGetLastError();
 }
 
-// bf16-valued fp32 -> bf16 bits (the value's upper half: exact)
-__global__ __launch_bounds__(kElemThreads) void f32_bf16_kernel(const float* src, int64_t n, uint16_t* dst) {
+// bf16-valued fp32 -> bf16 bits (the value's upper half: exact); F16:
+// fp16-valued fp32 -> fp16 bits (exact)
+template <bool F16>
+__global__ __launch_bounds__(kElemThreads) void f32_half_kernel(const float* src, int64_t n, uint16_t* dst) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kElemThreads + threadIdx.x;
-  if (i < n) dst[i] = static_cast<uint16_t>(__float_as_uint(src[i]) >> 16);
+  if (i < n) dst[i] = F16 ? f32_to_f16(src[i]) : static_cast<uint16_t>(__float_as_uint(src[i]) >> 16);
 }
 
-hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream) {
+hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream, bool f16) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(f32_bf16_kernel, dim3(grid_for(n, kElemThreads)), dim3(kElemThreads), 0, stream, src, n,
-                     dst);
+  hipLaunchKernelGGL((f16 ? f32_half_kernel<true> : f32_half_kernel<false>), dim3(grid_for(n, kElemThreads)),
+                     dim3(kElemThreads), 0, stream, src, n, dst);
   return hipGetLastError();
 }
 

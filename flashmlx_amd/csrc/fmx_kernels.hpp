@@ -79,6 +79,7 @@ struct RouterArgs {
   const uint16_t* lbias;   // [E] bf16 or null
   RouterRows wsg;          // [1, H] shared-expert gate (wsg.w null: none)
   int T, H, E, k, norm;
+  int f16;                 // 1: x, the rows, logits, probabilities and scores in float16
   uint16_t* logits;        // [T, E+1] bf16 scratch (column E: shared gate logit)
   uint16_t* probs;         // [T, E] bf16 or null
   uint32_t* inds;          // [T, k]
@@ -173,6 +174,8 @@ constexpr int kPackedBlockPair = 2304;    // gate + up
 
 struct DecodeArgs {
   int T, H, E, k, I, Is, norm;
+  int f16;                  // 1: x, y, the router rows and every scale and bias are
+                            //   float16, and the block rounds in fp16 throughout
   const uint16_t* x;        // [T, H] bf16
   RouterRows wr;            // [E, H] router
   const uint16_t* lbias;    // [E] bf16 router logit bias or null
@@ -278,7 +281,9 @@ struct PfSet {
   const uint16_t* ms;
   const uint16_t* mb;
   const uint32_t* out_map;
-  int io_f16;                // MLX sets: ms / mb and out in float16 (not bf16)
+  int io_f16;                // scales, biases and out in float16 (not bf16): MLX sets of
+                             //   an fp16 x, and every set of a float16 MoE block (gate/up
+                             //   then writes fp16 SwiGLU rows, the exact path is never taken)
   int nt;                    // 16-row tiles of the weight matrix (pairs: of gate)
   int nu;                    // 128-k units of K
   int ng;                    // column groups (kPfWaves * blocks per wave tiles each)
@@ -333,6 +338,7 @@ struct CombineArgs {
   const float* sgate;      // [T] or null
   uint16_t* y;             // [T, H] bf16
   int T, k, H;
+  int f16;                 // d, scores, sd and y float16, every rounding to fp16
 };
 hipError_t launch_combine(const CombineArgs& a, hipStream_t stream);
 
@@ -390,8 +396,9 @@ hipError_t launch_nh_combine(const NhCombineArgs& a, hipStream_t stream);
 hipError_t launch_permute_p8(const uint16_t* x, int64_t rows, int64_t K, uint16_t* xp,
                              hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t stream);
-// dst[i] = bf16 bits of src[i], a value that is exactly a bf16
-hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream);
+// dst[i] = bf16 bits of src[i], a value that is exactly a bf16 (f16: fp16
+// bits of an fp16 value)
+hipError_t launch_f32_bf16(const float* src, int64_t n, uint16_t* dst, hipStream_t stream, bool f16 = false);
 
 // MLX broadcasting of index arrays to the common batch shape (up to 8 dims).
 struct BcastArgs {

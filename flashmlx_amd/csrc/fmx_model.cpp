@@ -88,6 +88,9 @@ int check_config(const fmx_model_config* c) {
     return fail(FMX_ERR_UNSUPPORTED, "max_position_embeddings=%lld (1..%lld)", (long long)d.P,
                 (long long)kMaxPositions);
   if (c->moe.hidden_size != d.H) return fail(FMX_ERR_SHAPE, "moe.hidden_size != hidden_size");
+  if (c->moe.activation_dtype != FMX_BF16)
+    return fail(FMX_ERR_UNSUPPORTED, "moe.activation_dtype=%d: the decoder stack runs in bf16",
+                c->moe.activation_dtype);
   if (fmx_moe_workspace_size(&c->moe, 1) == 0) return fail(FMX_ERR_ARG, "invalid moe config");
   if (fmx_moe_packed_size(&c->moe) == 0)
     return fail(FMX_ERR_UNSUPPORTED, "the MoE block's shapes are outside the packed layout");

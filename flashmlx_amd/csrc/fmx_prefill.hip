@@ -44,6 +44,8 @@
 // cost 0.5 % relative L2 error of the block output at 512 tokens and put
 // single elements outside the bf16 parity tolerance; fp16 weights cost
 // 0.06 %.)
+// A float16 block (io_f16) brings fp16 rows, scales and biases: the same
+// fp16 arithmetic, SwiGLU and outputs rounded to fp16, never the exact path.
 //
 // The single-matrix grid also reads weights in MLX's own layout (words of
 // 8 nibbles along K per row, scales and biases per row and group), for
@@ -243,7 +245,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
-          if (MLX && P.io_f16) {  // float16 scales and biases: the values as they are
+          if (P.io_f16) {  // float16 scales and biases: the values as they are
             sc[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] & 0xffffu) * 0x10001u);
             sc[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] >> 16) * 0x10001u);
             bs[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] & 0xffffu) * 0x10001u);
@@ -337,7 +339,11 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
         const int64_t orow =
             static_cast<int64_t>((MLX && P.out_map) ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
                                                     : row0 + row) * P.ldo;
-        if (DUAL) {
+        if (DUAL && P.io_f16) {  // a float16 block: fp16 SwiGLU, both copies fp16
+          const uint16_t v = swiglu_f16(round_f16(acc[mt][b][0][r]), round_f16(acc[mt][b][NM - 1][r]));
+          P.out[orow + col] = v;
+          P.outh[orow + colh] = v;
+        } else if (DUAL) {
           const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
           P.out[orow + col] = v;
           ovf |= bf16_f16_overflow(v);
@@ -352,7 +358,7 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
           P.out[orow + col] = f32_to_bf16(av);
           ovf |= av >= 65504.0f;
           P.outh[orow + colh] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(av));
-        } else if (MLX && P.io_f16) {
+        } else if (P.io_f16) {
           P.out[orow + col] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[mt][b][0][r]));
         } else {
           uint16_t v = f32_to_bf16(acc[mt][b][0][r]);

@@ -161,8 +161,9 @@ constexpr int kRouterWaves = kRouterThreads / kWave;
 
 // Phase 1 of the router: each wave forms the logits of TT tokens x CE
 // consecutive columns. Lanes take interleaved 8-element chunks of H
-// (coalesced 16-byte loads); products of bf16 values are exact in fp64.
-template <int TT, int CE>
+// (coalesced 16-byte loads); products of bf16 values are exact in fp64, and
+// so are those of fp16 values (F16: a float16 block, logits rounded to fp16).
+template <int TT, int CE, bool F16>
 __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int lane) {
   const int H = a.H, E = a.E;
   const int ncols = E + (a.wsg.w ? 1 : 0);
@@ -186,7 +187,7 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
     u32x4_t xv[TT];
 #pragma unroll
     for (int c = 0; c < CE; ++c)
-      wv[c] = col[c] < E ? load_rchunk(a.wr, col[c], H, ch) : load_rchunk(a.wsg, 0, H, ch);
+      wv[c] = col[c] < E ? load_rchunk<F16>(a.wr, col[c], H, ch) : load_rchunk<F16>(a.wsg, 0, H, ch);
 #pragma unroll
     for (int t = 0; t < TT; ++t) xv[t] = *reinterpret_cast<const u32x4_t*>(xrow[t] + ch * 8);
 #pragma unroll
@@ -194,13 +195,13 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
       double w0[CE], w1[CE];
 #pragma unroll
       for (int c = 0; c < CE; ++c) {
-        w0[c] = wv[c].get(2 * i);
-        w1[c] = wv[c].get(2 * i + 1);
+        w0[c] = wv[c].template get<F16>(2 * i);
+        w1[c] = wv[c].template get<F16>(2 * i + 1);
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
-        const double x0 = __uint_as_float(xv[t][i] << 16);
-        const double x1 = __uint_as_float(xv[t][i] & 0xffff0000u);
+        const double x0 = Act<F16>::lo(xv[t][i]);
+        const double x1 = Act<F16>::hi(xv[t][i]);
 #pragma unroll
         for (int c = 0; c < CE; ++c) {
           acc[t * CE + c] = __builtin_fma(x0, w0[c], acc[t * CE + c]);
@@ -215,10 +216,10 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
     const int idx = lane >> SH;
     const int t = tt * kRouterTok + idx / CE, c = c0 + idx % CE;
     if (t < a.T && c < ncols) {
-      uint16_t l = f64_to_bf16(r);
+      uint16_t l = Act<F16>::from64(r);
       if (c < E && a.lbias)
-        l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) +
-                        static_cast<double>(bf16_to_f32(a.lbias[c])));
+        l = Act<F16>::from64(static_cast<double>(Act<F16>::ld(l)) +
+                             static_cast<double>(Act<F16>::ld(a.lbias[c])));
       a.logits[static_cast<int64_t>(t) * (E + 1) + c] = l;
     }
   }
@@ -227,7 +228,8 @@ __device__ void router_logits(const RouterArgs& a, int ct, int tt, int wave, int
 // Phase 2: softmax (fp64, exp_det) and top-k of one token, by one wave.
 // The normaliser is summed in a fixed order: lane l adds e = l, l+64, ...
 // in turn, then six butterfly steps s_l += s_{l^w} (w = 32..1) leave the
-// same total in every lane.
+// same total in every lane. F16: logits, probabilities and scores in fp16.
+template <bool F16>
 __device__ void router_token(const RouterArgs& a, int t, int lane) {
   const int E = a.E;
   const int nblk = (E + kWave - 1) / kWave;  // 64-expert blocks (wave-uniform)
@@ -239,7 +241,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
     const int e = lane + 64 * i;
     lv[i] = -__builtin_huge_val();
     if (i < nblk) {
-      if (e < E) lv[i] = static_cast<double>(bf16_to_f32(lrow[e]));
+      if (e < E) lv[i] = static_cast<double>(Act<F16>::ld(lrow[e]));
       m = fmax(m, lv[i]);
     }
   }
@@ -262,7 +264,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
   for (int i = 0; i < kMaxExpertsPerLane; ++i) {
     const int e = lane + 64 * i;
     if (i < nblk && e < E) {
-      const uint16_t p = f64_to_bf16(ex[i] / s);
+      const uint16_t p = Act<F16>::from64(ex[i] / s);
       if (a.probs) a.probs[static_cast<int64_t>(t) * E + e] = p;
       key[i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
     } else {
@@ -270,7 +272,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
     }
   }
   // top-k, (prob desc, expert asc): probabilities are >= 0, so their bf16
-  // bit patterns order like their values. Slot j's winner stays in lane j.
+  // (fp16) bit patterns order like their values. Slot j's winner stays in lane j.
   float sc_sum = 0.0f;
   uint16_t my_sc = 0;
   for (int j = 0; j < a.k; ++j) {
@@ -284,7 +286,7 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
     for (int i = 0; i < kMaxExpertsPerLane; ++i)
       if (i < nblk && key[i] == best) key[i] = 0u;
     const uint16_t p = static_cast<uint16_t>(best >> 16);
-    sc_sum += bf16_to_f32(p);  // fp32, slot order
+    sc_sum += Act<F16>::ld(p);  // fp32, slot order
     if (lane == j) {
       my_sc = p;
       a.inds[static_cast<int64_t>(t) * a.k + j] = e;
@@ -293,12 +295,12 @@ __device__ void router_token(const RouterArgs& a, int t, int lane) {
   if (lane < a.k) {
     uint16_t out = my_sc;
     if (a.norm) {
-      const double den = static_cast<double>(round_bf16(sc_sum));
-      out = f32_to_bf16(static_cast<float>(static_cast<double>(bf16_to_f32(my_sc)) / den));
+      const double den = static_cast<double>(Act<F16>::rnd(sc_sum));
+      out = Act<F16>::st(static_cast<float>(static_cast<double>(Act<F16>::ld(my_sc)) / den));
     }
     a.scores[static_cast<int64_t>(t) * a.k + lane] = out;
   }
-  if (lane == 0 && a.wsg.w && a.sgate) a.sgate[t] = sigmoid_bf16(bf16_to_f32(lrow[E]));
+  if (lane == 0 && a.wsg.w && a.sgate) a.sgate[t] = Act<F16>::sigmoid(Act<F16>::ld(lrow[E]));
 }
 
 // The Nemotron-H selection of token t (nh_select_wave) from the logits row
@@ -408,6 +410,7 @@ constexpr int kLgBatch = 8;  // 16-byte chunks of x and w in flight per lane
 
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
+template <bool F16>
 __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   __shared__ double s_red[(kLgWaves - 1) * 4 * kWave];
   // the forward's fp16-range flag starts clear (topk_kernel and the gate/up
@@ -437,7 +440,7 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
     for (int b = 0; b < kLgBatch; ++b) {
       const int ch = min(base + kLgStep * b + 4 * wave + kk, nch - 1);
       xv[b] = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
-      wv[b] = load_rchunk(wrows, wrow, H, ch);
+      wv[b] = load_rchunk<F16>(wrows, wrow, H, ch);
     }
 #pragma unroll
     for (int b = 0; b < kLgBatch; ++b) {
@@ -445,8 +448,8 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
         xv[b] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const double x0 = __uint_as_float(xv[b][i] << 16), x1 = __uint_as_float(xv[b][i] & 0xffff0000u);
-        const double w0 = wv[b].get(2 * i), w1 = wv[b].get(2 * i + 1);
+        const double x0 = Act<F16>::lo(xv[b][i]), x1 = Act<F16>::hi(xv[b][i]);
+        const double w0 = wv[b].template get<F16>(2 * i), w1 = wv[b].template get<F16>(2 * i + 1);
         acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
       }
@@ -471,44 +474,63 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   for (int r = 0; r < 4; ++r) {
     const int t = t0 + kk + 4 * r;
     if (t >= a.T) continue;
-    uint16_t l = f64_to_bf16(acc[r]);
+    uint16_t l = Act<F16>::from64(acc[r]);
     if (c < E && a.lbias)
-      l = f64_to_bf16(static_cast<double>(bf16_to_f32(l)) + static_cast<double>(bf16_to_f32(a.lbias[c])));
+      l = Act<F16>::from64(static_cast<double>(Act<F16>::ld(l)) + static_cast<double>(Act<F16>::ld(a.lbias[c])));
     a.logits[static_cast<int64_t>(t) * (E + 1) + c] = l;
   }
 }
 
+// elements e0..e7 of a 16-byte chunk -> P8 slots 0,2,4,6 (e0..e3) and
+// 1,3,5,7 (e4..e7)
+__device__ inline u32x4_t p8_chunk(const u32x4_t& v) {
+  u32x4_t p;
+  p[0] = (v[0] & 0xffffu) | (v[2] << 16);
+  p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+  p[2] = (v[1] & 0xffffu) | (v[3] << 16);
+  p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+  return p;
+}
+
 // The token's row of x in fp16 (P8 layout) for the prefill GEMMs; a
-// value outside fp16's range sets kF16FlagX.
+// value outside fp16's range sets kF16FlagX. F16: x is fp16 already (the
+// copy only permutes it).
+template <bool F16>
 __device__ void f16_row(const RouterArgs& a, int t, int lane) {
   const u32x4_t* src = reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(t) * a.H);
   u32x4_t* dst = reinterpret_cast<u32x4_t*>(a.xh + static_cast<int64_t>(t) * a.H);
-  bool ovf = false;
-  for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = bf16_chunk_to_f16_p8(src[ch], ovf);
-  if (__ballot(ovf) && lane == 0) atomicOr(a.f16_flag, kF16FlagX);
+  if constexpr (F16) {
+    for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = p8_chunk(src[ch]);
+  } else {
+    bool ovf = false;
+    for (int ch = lane; ch < a.H / 8; ch += kWave) dst[ch] = bf16_chunk_to_f16_p8(src[ch], ovf);
+    if (__ballot(ovf) && lane == 0) atomicOr(a.f16_flag, kF16FlagX);
+  }
 }
 
+template <bool F16>
 __global__ __launch_bounds__(kRouterThreads) void topk_kernel(RouterArgs a) {
   const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= a.T) return;
   if (a.mode == 1)
     router_token_nh(a, t, threadIdx.x & 63);
   else
-    router_token(a, t, threadIdx.x & 63);
-  if (a.xh) f16_row(a, t, threadIdx.x & 63);
+    router_token<F16>(a, t, threadIdx.x & 63);
+  if (a.xh) f16_row<F16>(a, t, threadIdx.x & 63);
 }
 
 hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream) {
   const int ncols = a.E + (a.wsg.w ? 1 : 0);
-  hipLaunchKernelGGL(logits_kernel, dim3((ncols + 15) / 16, (a.T + 15) / 16), dim3(kLgThreads), 0,
-                     stream, a);
+  hipLaunchKernelGGL((a.f16 ? logits_kernel<true> : logits_kernel<false>), dim3((ncols + 15) / 16, (a.T + 15) / 16),
+                     dim3(kLgThreads), 0, stream, a);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(topk_kernel, dim3((a.T + kRouterWaves - 1) / kRouterWaves), dim3(kRouterThreads),
-                     0, stream, a);
+  hipLaunchKernelGGL((a.f16 ? topk_kernel<true> : topk_kernel<false>), dim3((a.T + kRouterWaves - 1) / kRouterWaves),
+                     dim3(kRouterThreads), 0, stream, a);
   return hipGetLastError();
 }
 
+template <bool F16>
 __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_cnt[kRouterSortCnt];
   __shared__ uint8_t s_rank[kRouterSortMaxN];
@@ -522,11 +544,11 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 
   // ---- phase 1: logits of this token tile x column tile
   if (a.cols_per_wave == 4)
-    router_logits<kRouterTok, 4>(a, ct, tt, wave, lane);
+    router_logits<kRouterTok, 4, F16>(a, ct, tt, wave, lane);
   else if (a.T == 1)
-    router_logits<1, 1>(a, ct, tt, wave, lane);
+    router_logits<1, 1, F16>(a, ct, tt, wave, lane);
   else
-    router_logits<kRouterTok, 1>(a, ct, tt, wave, lane);
+    router_logits<kRouterTok, 1, F16>(a, ct, tt, wave, lane);
   // P8 copy of the tile's x rows, once per token tile
   if (ct == 0 && a.xp) {
     const int oct = H / 8;
@@ -536,13 +558,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
       if (tok >= a.T) continue;
       const u32x4_t v =
           *reinterpret_cast<const u32x4_t*>(a.x + static_cast<int64_t>(tok) * H + oc * 8);
-      // elements e0..e7 -> slots 0,2,4,6 (e0..e3) and 1,3,5,7 (e4..e7)
-      u32x4_t p;
-      p[0] = (v[0] & 0xffffu) | (v[2] << 16);
-      p[1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
-      p[2] = (v[1] & 0xffffu) | (v[3] << 16);
-      p[3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
-      *reinterpret_cast<u32x4_t*>(a.xp + static_cast<int64_t>(tok) * H + oc * 8) = p;
+      *reinterpret_cast<u32x4_t*>(a.xp + static_cast<int64_t>(tok) * H + oc * 8) = p8_chunk(v);
     }
   }
   // fp16 copy (P8 layout) of the tile's x rows for the prefill GEMMs, once
@@ -551,7 +567,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
   if (ct == 0 && a.xh) {
     for (int tl = wave; tl < kRouterTok; tl += kRouterWaves) {
       const int tok = tt * kRouterTok + tl;
-      if (tok < a.T) f16_row(a, tok, lane);
+      if (tok < a.T) f16_row<F16>(a, tok, lane);
     }
   }
   if (!arrive_last(&a.counters[tt], static_cast<uint32_t>(a.n_ct), &s_flag)) return;
@@ -564,7 +580,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
     if (a.mode == 1)
       router_token_nh(a, t, lane);
     else
-      router_token(a, t, lane);
+      router_token<F16>(a, t, lane);
   }
   if (tid == 0) a.counters[tt] = 0u;  // every column tile of this token tile has arrived
 
@@ -585,7 +601,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_kernel(RouterArgs a) {
 }
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(router_kernel, dim3(a.n_ct, a.n_tt), dim3(kRouterThreads), 0, stream, a);
+  hipLaunchKernelGGL((a.f16 ? router_kernel<true> : router_kernel<false>), dim3(a.n_ct, a.n_tt), dim3(kRouterThreads),
+                     0, stream, a);
   return hipGetLastError();
 }
 

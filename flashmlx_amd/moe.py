@@ -175,6 +175,9 @@ class MoEConfig:
     norm_topk_prob: bool = False
     quant_bits: int = 4
     quant_group_size: int = 64
+    # ModelConfig::activation_dtype (model.h:34): torch.bfloat16 or
+    # torch.float16 (x, y, router rows, scales and biases all of it)
+    activation_dtype: torch.dtype = torch.bfloat16
 
     def to_c(self) -> FmxMoEConfig:
         c = FmxMoEConfig()
@@ -186,6 +189,9 @@ class MoEConfig:
         c.shared_expert_intermediate_size = self.shared_expert_intermediate_size
         c.quant_bits = self.quant_bits
         c.quant_group_size = self.quant_group_size
+        if self.activation_dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("activation_dtype must be torch.bfloat16 or torch.float16")
+        c.activation_dtype = _lib.FMX_F16 if self.activation_dtype == torch.float16 else _lib.FMX_BF16
         return c
 
 
@@ -356,8 +362,8 @@ class MoEBlock:
         self._last_T = T
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        if x.dtype != torch.bfloat16 or not x.is_contiguous():
-            raise ValueError("x must be a contiguous bf16 tensor [..., H]")
+        if x.dtype != self.cfg.activation_dtype or not x.is_contiguous():
+            raise ValueError(f"x must be a contiguous {self.cfg.activation_dtype} tensor [..., H]")
         y = torch.empty_like(x)
         self.forward_into(x, y)
         return y
@@ -386,8 +392,8 @@ class MoEBlock:
 
         return {
             "inds": view(ptrs[0], T * k, torch.int32, 4).view(T, k),
-            "scores": view(ptrs[1], T * k, torch.bfloat16, 2).view(T, k),
-            "probs": view(ptrs[2], T * E, torch.bfloat16, 2).view(T, E),
+            "scores": view(ptrs[1], T * k, self.cfg.activation_dtype, 2).view(T, k),
+            "probs": view(ptrs[2], T * E, self.cfg.activation_dtype, 2).view(T, E),
             "order": view(ptrs[3], T * k, torch.int32, 4),
             "inv": view(ptrs[4], T * k, torch.int32, 4),
             "src": view(ptrs[5], T * k, torch.int32, 4),
@@ -402,7 +408,8 @@ def router_topk(cfg: MoEConfig, x: torch.Tensor, router_w,
     bf16, probs [T,E] bf16), and with `shared_expert_gate_w` also the shared
     expert's gate sigmoid(x . wsg^T) [T] bf16 (:787-803). router_w and
     shared_expert_gate_w are bf16 tensors or QWeights (the quantized router
-    of :758-760)."""
+    of :758-760). With cfg.activation_dtype float16, every bf16 here is
+    float16."""
     if isinstance(router_w, QWeight) or shared_expert_gate_w is not None:
         return _router_topk_ex(cfg, x, router_w, logit_bias, shared_expert_gate_w)
     lib = _lib.load()
@@ -410,8 +417,8 @@ def router_topk(cfg: MoEConfig, x: torch.Tensor, router_w,
     T = x.numel() // cfg.hidden_size
     k, E = cfg.num_experts_per_tok, cfg.num_experts
     inds = torch.empty(T, k, dtype=torch.int32, device=x.device)
-    scores = torch.empty(T, k, dtype=torch.bfloat16, device=x.device)
-    probs = torch.empty(T, E, dtype=torch.bfloat16, device=x.device)
+    scores = torch.empty(T, k, dtype=cfg.activation_dtype, device=x.device)
+    probs = torch.empty(T, E, dtype=cfg.activation_dtype, device=x.device)
     _lib.check(lib.fmx_moe_router_topk(
         C.byref(c), x.data_ptr(), T, router_w.data_ptr(),
         logit_bias.data_ptr() if logit_bias is not None else None,
@@ -428,9 +435,9 @@ def _router_topk_ex(cfg: MoEConfig, x: torch.Tensor, router_w, logit_bias, share
                    shared_expert_gate_w=shared_expert_gate_w, router_logit_bias=logit_bias)
     cw = w.to_c()
     inds = torch.empty(T, k, dtype=torch.int32, device=x.device)
-    scores = torch.empty(T, k, dtype=torch.bfloat16, device=x.device)
-    probs = torch.empty(T, E, dtype=torch.bfloat16, device=x.device)
-    sg = torch.empty(T, dtype=torch.bfloat16, device=x.device) if shared_expert_gate_w is not None else None
+    scores = torch.empty(T, k, dtype=cfg.activation_dtype, device=x.device)
+    probs = torch.empty(T, E, dtype=cfg.activation_dtype, device=x.device)
+    sg = torch.empty(T, dtype=cfg.activation_dtype, device=x.device) if shared_expert_gate_w is not None else None
     _lib.check(lib.fmx_moe_router_topk_ex(
         C.byref(c), x.data_ptr(), T, C.byref(cw), inds.data_ptr(), scores.data_ptr(), probs.data_ptr(),
         _ptr(sg), None, 0, _stream()))

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FMX_ABI_VERSION 4
+#define FMX_ABI_VERSION 5
 
 typedef enum fmx_status {
   FMX_OK = 0,
@@ -57,7 +57,8 @@ typedef enum fmx_status {
 
 /* FMX_F16: float16 activations (a checkpoint whose norms are float16,
  * model.cpp:208-214), taken by fmx_quantized_matmul and fmx_gather_qmm with
- * float16 scales, biases and output. */
+ * float16 scales, biases and output, and by the MoE block
+ * (fmx_moe_config.activation_dtype). */
 typedef enum fmx_dtype { FMX_BF16 = 0, FMX_F32 = 1, FMX_U32 = 2, FMX_I32 = 3, FMX_F16 = 4 } fmx_dtype;
 
 #define FMX_MAX_NDIM 8
@@ -164,6 +165,15 @@ typedef struct fmx_moe_config {
   int64_t shared_expert_intermediate_size; /* Is; 0 = no shared expert   */
   int32_t quant_bits;                      /* 4                          */
   int32_t quant_group_size;                /* 64                         */
+  /* ModelConfig::activation_dtype (model.h:34, set at model.cpp:208-214):
+   * FMX_BF16 (0) or FMX_F16. With FMX_F16, x, y, the router and shared-gate
+   * rows (or their scales and biases), the logit bias and every expert scale
+   * and bias are float16, and the block rounds in fp16 where the bf16 block
+   * rounds in bf16 (logits, probabilities, scores, SwiGLU, expert outputs,
+   * the combine). Float16 blocks run on packed weights (decode and prefill
+   * kernels); without them the forward returns FMX_ERR_UNSUPPORTED, and so
+   * does the input norm of the decoder stack. */
+  int32_t activation_dtype;
 } fmx_moe_config;
 
 typedef struct fmx_qweight {
@@ -260,7 +270,8 @@ int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint
  * reference. */
 int64_t fmx_set_decode_wait_limit(int64_t polls);
 
-/* y [T, H] bf16 = moe_block(x [T, H] bf16), T = B*L tokens. The workspace
+/* y [T, H] = moe_block(x [T, H]), T = B*L tokens, in the config's activation
+ * dtype (bf16 or float16). The workspace
  * must hold fmx_moe_workspace_size(cfg, T) bytes and have been initialised
  * once with fmx_moe_workspace_init. T = 0 runs nothing and returns FMX_OK
  * (x and y may then be NULL, as for empty tensors). */

@@ -87,3 +87,32 @@ def assert_close_rows(got_u16, ref_u16, what="", rtol=RTOL, atol=ATOL, rel_l2=RE
     assert not bad.any(), f"{what}: {int(bad.sum())} elements outside the row tolerance; {e}"
     assert e["rel_l2"] <= rel_l2, f"{what}: relative L2 error {e['rel_l2']:.3g} > {rel_l2}; {e}"
     return e
+
+
+# ---- float16 blocks (a float16 checkpoint, model.cpp:208-214)
+
+def f16_bits(a):
+    """fp16 bit patterns of values (one rounding from fp64)."""
+    return np.asarray(a, np.float64).astype(np.float16).view(np.uint16)
+
+
+def f16_vals(h):
+    return np.asarray(h, np.uint16).view(np.float16).astype(np.float64)
+
+
+def f16_inputs(oracle, hi, model, router_quant=False):
+    """(cfg, weights, x) for oracle.moe_block in float16 from HostInputs:
+    x and the router rows converted, the experts (and a quantized router)
+    quantized by the oracle with their bf16 scales and biases re-encoded as
+    float16 (the same values)."""
+    tof = lambda u: f16_bits(bf16_to_f32(u))  # noqa: E731
+    q = lambda a: (lambda r: (r[0], tof(r[1]), tof(r[2])))(oracle.quantize(a))  # noqa: E731
+    rq = q if router_quant else tof
+    cfg = dict(hidden=model["hidden"], n_experts=model["n_experts"], top_k=model["top_k"],
+               inter=model["inter"], shared_inter=model["shared_inter"], norm_topk=model["norm_topk"])
+    w = dict(router_w=rq(hi.router_w), router_bias=None if hi.router_bias is None else tof(hi.router_bias),
+             gate=q(hi.gate), up=q(hi.up), down=q(hi.down))
+    if model["shared_inter"]:
+        w.update(shared_gate=q(hi.shared_gate), shared_up=q(hi.shared_up), shared_down=q(hi.shared_down),
+                 shared_expert_gate_w=rq(hi.shared_expert_gate_w))
+    return cfg, w, tof(hi.x)

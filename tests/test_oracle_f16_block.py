@@ -107,22 +107,9 @@ def test_router_f16_against_numpy(oracle, norm):
 
 
 def _f16_inputs(oracle, wl):
-    """A workload's inputs in float16: x and the router rows converted, the
-    experts quantized by the oracle and their bf16 scales and biases
-    re-encoded as float16 (the same values)."""
     from flashmlx_amd import workloads as W
-    hi = W.host_inputs(wl)
-    tof = lambda u: _f16(oracle.bf16_to_f32(u))  # noqa: E731
-    q = lambda a: (lambda r: (r[0], tof(r[1]), tof(r[2])))(oracle.quantize(a))  # noqa: E731
-    m = wl.model
-    cfg = dict(hidden=m["hidden"], n_experts=m["n_experts"], top_k=m["top_k"], inter=m["inter"],
-               shared_inter=m["shared_inter"], norm_topk=m["norm_topk"])
-    w = dict(router_w=tof(hi.router_w), router_bias=None if hi.router_bias is None else tof(hi.router_bias),
-             gate=q(hi.gate), up=q(hi.up), down=q(hi.down))
-    if m["shared_inter"]:
-        w.update(shared_gate=q(hi.shared_gate), shared_up=q(hi.shared_up), shared_down=q(hi.shared_down),
-                 shared_expert_gate_w=tof(hi.shared_expert_gate_w))
-    return cfg, w, tof(hi.x)
+    from helpers import f16_inputs
+    return f16_inputs(oracle, W.host_inputs(wl), wl.model)
 
 
 def _nibbles(wq):
