@@ -22,9 +22,11 @@
  *   - Concurrency: calls are re-entrant for distinct (stream, workspace)
  *     pairs. Two calls sharing one workspace must be ordered on one stream.
  *   - Scope: affine mode, bits = 4, group_size = 64, transpose = true.
- *     Activations and scales/biases are bf16 everywhere; fmx_quantized_matmul
- *     and fmx_gather_qmm also take float16 ones (FMX_F16: x, scales, biases
- *     and out all float16). Any other valid MLX argument returns
+ *     Activations and scales/biases are bf16 or float16: fmx_quantized_matmul
+ *     and fmx_gather_qmm take float16 ones (FMX_F16: x, scales, biases and
+ *     out all float16), and so do the MoE block and router entry points when
+ *     fmx_moe_config.activation_dtype is FMX_F16; the decoder stack and the
+ *     Nemotron-H block are bf16. Any other valid MLX argument returns
  *     FMX_ERR_UNSUPPORTED and computes nothing.
  *
  * Packed weight layout (MLX's, unchanged): for a logical [N, K] matrix
@@ -191,7 +193,8 @@ typedef struct fmx_qweight {
  * dequantised s*q + b) and rounded once to bf16, in either form.
  * When `packed` is given, the forward reads the expert weights from there
  * only: gate/up/down and shared_gate/up/down may then be NULL (the caller may
- * free the MLX-layout copies after fmx_pack_expert_weights). */
+ * free the MLX-layout copies after fmx_pack_expert_weights). Every bf16
+ * below is float16 in a float16 block (fmx_moe_config.activation_dtype). */
 typedef struct fmx_moe_weights {
   const void* router_w;          /* bf16 [E, H], or u32 [E, H/8] when router_scales */
   const void* router_logit_bias; /* bf16 [E] added to the logits before softmax, or
