@@ -171,7 +171,8 @@ std::atomic<int> g_wait_polls{kDecWaitPolls};
 struct MoELayout {
   uint32_t* counters;
   uint16_t* logits;
-  uint32_t* lgw;
+  double* lg_part;   // the prefill router's fp64 partial logits: aliases d (written later)
+  int64_t lg_cap;    // doubles lg_part holds
   uint16_t* probs;
   uint32_t* inds;
   uint16_t* scores;
@@ -196,7 +197,6 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   const int64_t n = T * k;
   L.counters = static_cast<uint32_t*>(ar.take(kCounterBytes));
   L.logits = static_cast<uint16_t*>(ar.take(T * (E + 1) * 2));
-  L.lgw = static_cast<uint32_t*>(ar.take(T * (E + 1) * 4));
   L.probs = static_cast<uint16_t*>(ar.take(T * E * 2));
   L.inds = static_cast<uint32_t*>(ar.take(n * 4));
   L.scores = static_cast<uint16_t*>(ar.take(n * 2));
@@ -218,6 +218,8 @@ MoELayout moe_layout(const fmx_moe_config& c, int64_t T, char* base) {
   L.h = static_cast<uint16_t*>(ar.take(n * I * 2));
   L.hs = static_cast<uint16_t*>(ar.take(T * Is * 2));
   L.d = static_cast<uint16_t*>(ar.take(n * H * 2));
+  L.lg_part = reinterpret_cast<double*>(L.d);  // consumed by the top-k kernel before d is written
+  L.lg_cap = n * H * 2 / 8;
   L.sd_part = static_cast<float*>(ar.take(Is ? kSharedDownSplit * T * H * 4 : 0));
   L.f16_flag = static_cast<uint32_t*>(ar.take(4));
   L.xh = static_cast<uint16_t*>(ar.take(T * H * 2));
@@ -346,6 +348,8 @@ int run_router(const fmx_moe_config& c, const MoELayout& L, const void* x, int64
   a.sort.base = L.sort_base;
   a.sort.pass_n = L.pass_n;
   a.sort.pass_tab = L.pass_tab;
+  a.lg_part = L.lg_part;
+  a.lg_split = router_lg_split(T, c.num_experts, L.lg_cap);
   if (want_f16) {  // the prefill GEMMs' fp16 copy of x and its range flag
     a.xh = L.xh;
     a.f16_flag = L.f16_flag;
@@ -1200,7 +1204,6 @@ int moe_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w, const void*
     da.sgu = pk + PL.sgu;
     da.sdn = pk + PL.sdn;
     da.logits = L.logits;
-    da.lgw = L.lgw;
     da.hs = L.hs;
     da.h = L.h;
     da.dw = L.dw;

@@ -88,6 +88,11 @@ struct RouterArgs {
   uint16_t* xp;            // [T, H] P8 copy of x or null
   uint16_t* xh;            // [T, H] fp16 copy of x in P8 layout (topk_kernel) or null
   uint32_t* f16_flag;      // zeroed by logits_kernel; topk_kernel ORs in kF16FlagX (or null)
+  // launch_router_many: logits_kernel splits H into lg_split slices (1..4)
+  // and, with more than one, writes fp64 partial sums lg_part[slice][t][c]
+  // that topk_kernel adds in slice order and rounds (router_lg_split)
+  double* lg_part;
+  int lg_split;
   uint32_t* counters;      // [n_tt + 1], zero on entry, zero on exit
   int n_tt, n_ct;          // token tiles, column tiles (4 * cols_per_wave columns each)
   int cols_per_wave;       // 1 (one token tile: decode) or 4 (prefill)
@@ -106,6 +111,10 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t stream);
 // Forwards of more than kRouterManyMin tokens: logits on fp64 MFMA tiles,
 // then softmax/top-k per token, in two launches (no xp copy, no sort).
 constexpr int kRouterManyMin = 16;
+constexpr int64_t kLgPartMax = 262144;  // doubles of lg_part
+// H slices of logits_kernel for T tokens and E experts: about 1024
+// workgroups, at most 4, with lg_split * T * (E + 1) <= min(kLgPartMax, cap)
+int router_lg_split(int64_t T, int64_t E, int64_t cap);
 hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream);
 
 // ---------------------------------------------------------------- grouped GEMM
@@ -187,7 +196,6 @@ struct DecodeArgs {
   const uint8_t* sgu;       // packed shared gate/up pair
   const uint8_t* sdn;       // packed shared down
   uint16_t* logits;         // [T, E+1] bf16 (column E: shared gate logit)
-  uint32_t* lgw;            // [E+1][T] the same logits (low halves), between K1 workgroups
   uint16_t* hs;             // [T, Is] shared SwiGLU output
   uint16_t* h;              // [T*k, I] routed SwiGLU output, entry order
   uint32_t* dw;             // [T*k, H] routed down projections, entry order, bf16 in the

@@ -99,6 +99,166 @@ __device__ inline void dma4(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
+// One unit's products: the pass's rows in LDS at sa (16-byte chunks
+// XOR-swizzled by row), the wave's packed words W and (scale, bias) pairs
+// SB, accumulated into acc.
+template <bool DUAL, int MT, bool F16, bool MLX>
+__device__ __attribute__((always_inline)) void pf_unit(const PfSet& P, const uint8_t* sa,
+                                                       const u32x4_t (&W)[pf_nb<DUAL>()][pf_nm<DUAL>()],
+                                                       const u32x2_t (&SB)[pf_nb<DUAL>()][pf_nm<DUAL>()],
+                                                       f32x4_t (&acc)[MT][pf_nb<DUAL>()][pf_nm<DUAL>()], int i16,
+                                                       int j) {
+  constexpr int NB = pf_nb<DUAL>(), NM = pf_nm<DUAL>();
+  if constexpr (F16) {
+    // every activation operand of the unit is read up front (one LDS round
+    // trip per unit, not one per k-slice)
+    f16x8_t A[4][MT];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        A[q][mt] = *reinterpret_cast<const f16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+    f16x2_t sc[NB][NM][2], bs[NB][NM][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        if (P.io_f16) {  // float16 scales and biases: the values as they are
+          sc[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] & 0xffffu) * 0x10001u);
+          sc[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] >> 16) * 0x10001u);
+          bs[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] & 0xffffu) * 0x10001u);
+          bs[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] >> 16) * 0x10001u);
+        } else {
+          sc[b][m][0] = f16_splat(__uint_as_float(SB[b][m][0] << 16));
+          sc[b][m][1] = f16_splat(__uint_as_float(SB[b][m][0] & 0xffff0000u));
+          bs[b][m][0] = f16_splat(__uint_as_float(SB[b][m][1] << 16));
+          bs[b][m][1] = f16_splat(__uint_as_float(SB[b][m][1] & 0xffff0000u));
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    // k-slice q (32 k) of quantisation group q / 2: the weights dequantised
+    // once, multiplied against every 16-row tile of the pass
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          const f16x8_t B = dq8_f16(W[b][m][q], sc[b][m][q >> 1], bs[b][m][q >> 1]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][b][m] = mfma_f16(A[q][mt], B, acc[mt][b][m]);
+        }
+  } else {
+    float sc[NB][NM][2], cb[NB][NM][2];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        sc[b][m][0] = __uint_as_float(SB[b][m][0] << 16);
+        sc[b][m][1] = __uint_as_float(SB[b][m][0] & 0xffff0000u);
+        cb[b][m][0] = __builtin_fmaf(-128.0f, sc[b][m][0], __uint_as_float(SB[b][m][1] << 16));
+        cb[b][m][1] = __builtin_fmaf(-128.0f, sc[b][m][1], __uint_as_float(SB[b][m][1] & 0xffff0000u));
+      }
+    // exact dequantisation, one quantisation group (two k-slices) at a time:
+    // P = x.(128+q) and X = x.1 by MFMA, then acc += s P + (b - 128 s) X
+    // (the group's activation operands only are held, which keeps this
+    // path within the register budget of the fp16 path)
+    const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+    const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      bf16x8_t A[4][MT];
+#pragma unroll
+      for (int q = 2 * g; q < 2 * g + 2; ++q)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
+      f32x4_t X[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) X[mt] = mfma_bf16(A[2 * g + 1][mt], ones, mfma_bf16(A[2 * g][mt], ones, zero));
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          const bf16x8_t B0 = nib8(W[b][m][2 * g]), B1 = nib8(W[b][m][2 * g + 1]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const f32x4_t Pg = mfma_bf16(A[2 * g + 1][mt], B1, mfma_bf16(A[2 * g][mt], B0, zero));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[mt][b][m][i] = __builtin_fmaf(sc[b][m][g], Pg[i], acc[mt][b][m][i]);
+              acc[mt][b][m][i] = __builtin_fmaf(cb[b][m][g], X[mt][i], acc[mt][b][m][i]);
+            }
+          }
+        }
+    }
+  }
+}
+
+// The work item's outputs from acc (rows [row0, row0 + rows), the wave's
+// tiles from tile0, K slice ks).
+template <bool DUAL, int MT, bool MLX>
+__device__ __attribute__((always_inline)) void pf_epilogue(const PfSet& P,
+                                                           f32x4_t (&acc)[MT][pf_nb<DUAL>()][pf_nm<DUAL>()],
+                                                           int tile0, int row0, int rows, int ks, int i16, int j,
+                                                           int lane, uint32_t* flag, uint32_t flag_out) {
+  constexpr int NB = pf_nb<DUAL>(), NM = pf_nm<DUAL>();
+  // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile,
+  // column i16; gate/up (and a relu^2 up projection) also writes its rows
+  // in fp16 (P8 layout) for the down grid and flags values outside fp16's
+  // range
+  bool ovf = false;
+  float* const out32 = P.out32 ? P.out32 + ks * P.part_stride : nullptr;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int t = tile0 + b;
+      if (t >= P.nt) continue;
+      const int col = t * 16 + i16;
+      const int colh = (col & ~7) | p8_slot(col & 7);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mt + 4 * j + r;
+        if (row >= rows) continue;
+        const int64_t orow =
+            static_cast<int64_t>((MLX && P.out_map) ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
+                                                    : row0 + row) * P.ldo;
+        if (DUAL && P.io_f16) {  // a float16 block: fp16 SwiGLU, both copies fp16
+          const uint16_t v = swiglu_f16(round_f16(acc[mt][b][0][r]), round_f16(acc[mt][b][NM - 1][r]));
+          P.out[orow + col] = v;
+          P.outh[orow + colh] = v;
+        } else if (DUAL) {
+          const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
+          P.out[orow + col] = v;
+          ovf |= bf16_f16_overflow(v);
+          P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
+        } else if (out32) {
+          out32[orow + col] = acc[mt][b][0][r];
+        } else if (P.act) {
+          // relu^2 of the bf16 product (Nemotron-H, nemotron_h.cpp:54-63):
+          // exact in fp32; bf16 and fp16 copies for the down grid
+          const float hv = fmaxf(round_bf16(acc[mt][b][0][r]), 0.0f);
+          const float av = hv * hv;
+          P.out[orow + col] = f32_to_bf16(av);
+          ovf |= av >= 65504.0f;
+          P.outh[orow + colh] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(av));
+        } else if (P.io_f16) {
+          P.out[orow + col] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[mt][b][0][r]));
+        } else {
+          uint16_t v = f32_to_bf16(acc[mt][b][0][r]);
+          if (P.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(P.bias[col]));
+          if (P.res)
+            v = f32_to_bf16(bf16_to_f32(P.res[static_cast<int64_t>(row0 + row) * P.ldr + col]) + bf16_to_f32(v));
+          P.out[orow + col] = v;
+        }
+      }
+    }
+  }
+  if ((DUAL || P.act) && __ballot(ovf) && lane == 0) atomicOr(flag, flag_out);
+}
+
 // One work item: rows [row0, row0 + rows) (rows <= 16 MT) of expert e's
 // weights, column group ng. MT (the 16-row tiles the rows fill) fixes how
 // many row pieces each wave moves per unit, so the pass's rows are moved
@@ -231,146 +391,9 @@ __device__ __attribute__((always_inline)) void pf_item(const PfSet& P, int ng, i
         }
         SB[b][m] = *reinterpret_cast<const u32x2_t*>(sb + SBO + b * (NM * 128) + m * 128 + 8 * i16);
       }
-    if constexpr (F16) {
-      // every activation operand of the unit is read up front (one LDS round
-      // trip per unit, not one per k-slice)
-      f16x8_t A[4][MT];
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          A[q][mt] = *reinterpret_cast<const f16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
-      f16x2_t sc[NB][NM][2], bs[NB][NM][2];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          if (P.io_f16) {  // float16 scales and biases: the values as they are
-            sc[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] & 0xffffu) * 0x10001u);
-            sc[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][0] >> 16) * 0x10001u);
-            bs[b][m][0] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] & 0xffffu) * 0x10001u);
-            bs[b][m][1] = __builtin_bit_cast(f16x2_t, (SB[b][m][1] >> 16) * 0x10001u);
-          } else {
-            sc[b][m][0] = f16_splat(__uint_as_float(SB[b][m][0] << 16));
-            sc[b][m][1] = f16_splat(__uint_as_float(SB[b][m][0] & 0xffff0000u));
-            bs[b][m][0] = f16_splat(__uint_as_float(SB[b][m][1] << 16));
-            bs[b][m][1] = f16_splat(__uint_as_float(SB[b][m][1] & 0xffff0000u));
-          }
-        }
-      __builtin_amdgcn_sched_barrier(0);
-      // k-slice q (32 k) of quantisation group q / 2: the weights dequantised
-      // once, multiplied against every 16-row tile of the pass
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            const f16x8_t B = dq8_f16(W[b][m][q], sc[b][m][q >> 1], bs[b][m][q >> 1]);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[mt][b][m] = mfma_f16(A[q][mt], B, acc[mt][b][m]);
-          }
-    } else {
-      float sc[NB][NM][2], cb[NB][NM][2];
-#pragma unroll
-      for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-          sc[b][m][0] = __uint_as_float(SB[b][m][0] << 16);
-          sc[b][m][1] = __uint_as_float(SB[b][m][0] & 0xffff0000u);
-          cb[b][m][0] = __builtin_fmaf(-128.0f, sc[b][m][0], __uint_as_float(SB[b][m][1] << 16));
-          cb[b][m][1] = __builtin_fmaf(-128.0f, sc[b][m][1], __uint_as_float(SB[b][m][1] & 0xffff0000u));
-        }
-      // exact dequantisation, one quantisation group (two k-slices) at a time:
-      // P = x.(128+q) and X = x.1 by MFMA, then acc += s P + (b - 128 s) X
-      // (the group's activation operands only are held, which keeps this
-      // path within the register budget of the fp16 path)
-      const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-      const u32x4_t ones_u = {0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};
-      const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, ones_u);
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        bf16x8_t A[4][MT];
-#pragma unroll
-        for (int q = 2 * g; q < 2 * g + 2; ++q)
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-            A[q][mt] = *reinterpret_cast<const bf16x8_t*>(sa + (16 * mt + i16) * 256 + (((4 * q + j) ^ i16) << 4));
-        f32x4_t X[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) X[mt] = mfma_bf16(A[2 * g + 1][mt], ones, mfma_bf16(A[2 * g][mt], ones, zero));
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            const bf16x8_t B0 = nib8(W[b][m][2 * g]), B1 = nib8(W[b][m][2 * g + 1]);
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              const f32x4_t Pg = mfma_bf16(A[2 * g + 1][mt], B1, mfma_bf16(A[2 * g][mt], B0, zero));
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                acc[mt][b][m][i] = __builtin_fmaf(sc[b][m][g], Pg[i], acc[mt][b][m][i]);
-                acc[mt][b][m][i] = __builtin_fmaf(cb[b][m][g], X[mt][i], acc[mt][b][m][i]);
-              }
-            }
-          }
-      }
-    }
+    pf_unit<DUAL, MT, F16, MLX>(P, sa, W, SB, acc, i16, j);
   }
-
-  // ---- epilogue: lane (i16, j) holds rows 4j + r of each 16-row tile,
-  // column i16; gate/up (and a relu^2 up projection) also writes its rows
-  // in fp16 (P8 layout) for the down grid and flags values outside fp16's
-  // range
-  bool ovf = false;
-  float* const out32 = P.out32 ? P.out32 + ks * P.part_stride : nullptr;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int t = tile0 + b;
-      if (t >= P.nt) continue;
-      const int col = t * 16 + i16;
-      const int colh = (col & ~7) | p8_slot(col & 7);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * mt + 4 * j + r;
-        if (row >= rows) continue;
-        const int64_t orow =
-            static_cast<int64_t>((MLX && P.out_map) ? min(P.out_map[row0 + row], static_cast<uint32_t>(P.rows_max - 1))
-                                                    : row0 + row) * P.ldo;
-        if (DUAL && P.io_f16) {  // a float16 block: fp16 SwiGLU, both copies fp16
-          const uint16_t v = swiglu_f16(round_f16(acc[mt][b][0][r]), round_f16(acc[mt][b][NM - 1][r]));
-          P.out[orow + col] = v;
-          P.outh[orow + colh] = v;
-        } else if (DUAL) {
-          const uint16_t v = swiglu_bf16(round_bf16(acc[mt][b][0][r]), round_bf16(acc[mt][b][NM - 1][r]));
-          P.out[orow + col] = v;
-          ovf |= bf16_f16_overflow(v);
-          P.outh[orow + colh] = static_cast<uint16_t>(bf16_to_f16_bits(v));
-        } else if (out32) {
-          out32[orow + col] = acc[mt][b][0][r];
-        } else if (P.act) {
-          // relu^2 of the bf16 product (Nemotron-H, nemotron_h.cpp:54-63):
-          // exact in fp32; bf16 and fp16 copies for the down grid
-          const float hv = fmaxf(round_bf16(acc[mt][b][0][r]), 0.0f);
-          const float av = hv * hv;
-          P.out[orow + col] = f32_to_bf16(av);
-          ovf |= av >= 65504.0f;
-          P.outh[orow + colh] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(av));
-        } else if (P.io_f16) {
-          P.out[orow + col] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(acc[mt][b][0][r]));
-        } else {
-          uint16_t v = f32_to_bf16(acc[mt][b][0][r]);
-          if (P.bias) v = f32_to_bf16(bf16_to_f32(v) + bf16_to_f32(P.bias[col]));
-          if (P.res)
-            v = f32_to_bf16(bf16_to_f32(P.res[static_cast<int64_t>(row0 + row) * P.ldr + col]) + bf16_to_f32(v));
-          P.out[orow + col] = v;
-        }
-      }
-    }
-  }
-  if ((DUAL || P.act) && __ballot(ovf) && lane == 0) atomicOr(flag, flag_out);
+  pf_epilogue<DUAL, MT, MLX>(P, acc, tile0, row0, rows, ks, i16, j, lane, flag, flag_out);
 }
 
 // Block -> work item. The hardware dispatches block b to XCD b % 8, each
@@ -391,11 +414,12 @@ __device__ __attribute__((always_inline)) void pf_grid(const PfArgs& a, uint8_t*
   int pass, ng, ks = 0;
   if (P.pass_n) {
     // XCD x takes a contiguous range of the pass table, so an expert's
-    // passes (consecutive in the table) run back to back on one L2
+    // passes (consecutive in the table) run back to back on one L2; the
+    // ranges differ in length by at most one pass
     const int npass = min(static_cast<int>(*P.pass_n), P.max_pass);
-    const int per = (npass + kXcds - 1) / kXcds;
-    if (l / P.ng >= per) return;
-    pass = x * per + l / P.ng;
+    const int lo = (x * npass) / kXcds, hi = ((x + 1) * npass) / kXcds;
+    if (l / P.ng >= hi - lo) return;
+    pass = lo + l / P.ng;
     ng = l % P.ng;
   } else {
     // XCD x runs every pass and K slice of one column group back to back

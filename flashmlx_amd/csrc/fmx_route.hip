@@ -4,6 +4,8 @@
 // Reference: server/src/model.cpp:757-775 (router, softmax, argpartition
 // top-k, take_along_axis), :682-700 (switch_mlp's argsort-based sort), and
 // the renormalisation of docs/superpowers/plans/2026-04-01-moe-support-plan.md:319-322.
+#include <algorithm>
+
 #include "fmx_dev.hpp"
 
 namespace fmx {
@@ -395,13 +397,18 @@ __device__ void sort_small(const uint32_t* keys, int n, int k, int E, const Sort
 //
 // Forwards of more than a few token tiles route in two kernels with no
 // cross-workgroup handoff inside either:
-//   logits_kernel  16 tokens x 16 columns per workgroup on v_mfma_f64_16x16x4f64:
-//                  the bf16 operands are exact in fp64 and so are their
-//                  products; 8 waves take interleaved 32-element slices of H
-//                  and their partial tiles are added in wave order, the sum
-//                  rounded once to bf16 (then the logit bias, as in phase 1
-//                  of router_kernel)
-//   topk_kernel    softmax and top-k, one wave per token (router_token)
+//   logits_kernel  16 tokens x 16 columns x one of lg_split slices of H per
+//                  workgroup on v_mfma_f64_16x16x4f64: the bf16 operands
+//                  are exact in fp64 and so are their products; 8 waves
+//                  take interleaved 32-element pieces of the slice and their
+//                  partial tiles are added in wave order. One slice: the sum
+//                  is rounded once to bf16 (then the logit bias, as in
+//                  phase 1 of router_kernel); more: the fp64 partial sums go
+//                  to lg_part (about 1024 workgroups instead of 128 at 512
+//                  tokens x 61 columns)
+//   topk_kernel    the logits from the partial sums (added in slice order,
+//                  then rounded and biased as above), softmax and top-k, one
+//                  wave per token
 // The sort follows as its own launch.
 
 constexpr int kLgWaves = 8;
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   __shared__ double s_red[(kLgWaves - 1) * 4 * kWave];
   // the forward's fp16-range flag starts clear (topk_kernel and the gate/up
   // GEMMs, which run after this grid, set its bits)
-  if (a.f16_flag && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.f16_flag = 0u;
+  if (a.f16_flag && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) *a.f16_flag = 0u;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int i16 = lane & 15, kk = lane >> 4;
@@ -430,28 +437,37 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   const int64_t wrow = col < E ? col : 0;
   const int nch = H / 8;
   f64x4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-  // kLgBatch chunks per lane are loaded together (one memory latency per
-  // batch, not per chunk), then multiplied in the same chunk order
+  // steps of kLgStep chunks (one per lane); this workgroup's slice is steps
+  // [s0, s1). kLgBatch steps' chunks are loaded together (one memory
+  // latency per batch, not per chunk), then multiplied in chunk order.
   constexpr int kLgStep = 4 * kLgWaves;
-  for (int base = 0; base < nch; base += kLgStep * kLgBatch) {
+  const int kn = max(a.lg_split, 1), ks = blockIdx.z;
+  const int steps = (nch + kLgStep - 1) / kLgStep;
+  const int s0 = (steps * ks) / kn, s1 = (steps * (ks + 1)) / kn;
+  for (int st = s0; st < s1; st += kLgBatch) {
+    const int nb = min(kLgBatch, s1 - st);  // workgroup-uniform
     u32x4_t xv[kLgBatch];
     RChunk wv[kLgBatch];
 #pragma unroll
     for (int b = 0; b < kLgBatch; ++b) {
-      const int ch = min(base + kLgStep * b + 4 * wave + kk, nch - 1);
-      xv[b] = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
-      wv[b] = load_rchunk<F16>(wrows, wrow, H, ch);
+      if (b < nb) {
+        const int ch = min((st + b) * kLgStep + 4 * wave + kk, nch - 1);
+        xv[b] = *reinterpret_cast<const u32x4_t*>(xrow + ch * 8);
+        wv[b] = load_rchunk<F16>(wrows, wrow, H, ch);
+      }
     }
 #pragma unroll
     for (int b = 0; b < kLgBatch; ++b) {
-      if (base + kLgStep * b + 4 * wave + kk >= nch)  // chunks past H contribute exact zeros
-        xv[b] = u32x4_t{0u, 0u, 0u, 0u};
+      if (b < nb) {
+        if ((st + b) * kLgStep + 4 * wave + kk >= nch)  // chunks past H contribute exact zeros
+          xv[b] = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const double x0 = Act<F16>::lo(xv[b][i]), x1 = Act<F16>::hi(xv[b][i]);
-        const double w0 = wv[b].template get<F16>(2 * i), w1 = wv[b].template get<F16>(2 * i + 1);
-        acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+          const double x0 = Act<F16>::lo(xv[b][i]), x1 = Act<F16>::hi(xv[b][i]);
+          const double w0 = wv[b].template get<F16>(2 * i), w1 = wv[b].template get<F16>(2 * i + 1);
+          acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(x0, w0, acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(x1, w1, acc1, 0, 0, 0);
+        }
       }
     }
   }
@@ -474,10 +490,102 @@ __global__ __launch_bounds__(kLgThreads) void logits_kernel(RouterArgs a) {
   for (int r = 0; r < 4; ++r) {
     const int t = t0 + kk + 4 * r;
     if (t >= a.T) continue;
+    if (kn > 1) {
+      a.lg_part[(static_cast<int64_t>(ks) * a.T + t) * (E + 1) + c] = acc[r];
+      continue;
+    }
     uint16_t l = Act<F16>::from64(acc[r]);
     if (c < E && a.lbias)
       l = Act<F16>::from64(static_cast<double>(Act<F16>::ld(l)) + static_cast<double>(Act<F16>::ld(a.lbias[c])));
     a.logits[static_cast<int64_t>(t) * (E + 1) + c] = l;
+  }
+}
+
+// Logit column c of token t from logits_kernel's output: the slices' fp64
+// partial sums added in slice order, rounded once, then the logit bias (as
+// router_logits); the rounded logit is also stored for the routing
+// accessors. One slice: the logit logits_kernel rounded.
+template <bool F16>
+__device__ inline uint16_t split_logit(const RouterArgs& a, int t, int c) {
+  const int ld = a.E + 1;
+  const int64_t at = static_cast<int64_t>(t) * ld + c;
+  if (a.lg_split <= 1) return a.logits[at];
+  double v = a.lg_part[at];
+  for (int ks = 1; ks < a.lg_split; ++ks) v += a.lg_part[(static_cast<int64_t>(ks) * a.T + t) * ld + c];
+  uint16_t l = Act<F16>::from64(v);
+  if (c < a.E && a.lbias)
+    l = Act<F16>::from64(static_cast<double>(Act<F16>::ld(l)) + static_cast<double>(Act<F16>::ld(a.lbias[c])));
+  a.logits[at] = l;
+  return l;
+}
+
+// Softmax (fp64, exp_det) and top-k of token t by one wave, for
+// topk_kernel: the steps of router_token, with lane l on the experts e = r +
+// 64 i (i < NPER), r the 6-bit reverse of l, and the wave reductions as DPP
+// trees (adjacent lanes first: with lanes on bit-reversed expert classes the
+// normaliser's tree adds the partials r and r xor 32 first, r xor 16 next,
+// .., the association of router_token's butterfly, w = 32, 16, .., 1).
+template <int NPER, bool F16>
+__device__ void topk_token(const RouterArgs& a, int t, int lane) {
+  const int E = a.E;
+  const int r = static_cast<int>(__builtin_bitreverse32(static_cast<uint32_t>(lane)) >> 26);
+  float lf[NPER];
+  float mf = -__builtin_huge_valf();
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) {
+    const int e = r + 64 * i;
+    lf[i] = e < E ? Act<F16>::ld(split_logit<F16>(a, t, e)) : -__builtin_huge_valf();
+    mf = fmaxf(mf, lf[i]);
+  }
+  // the shared expert's gate logit (column E)
+  if (lane == 0 && a.wsg.w) {
+    const uint16_t g = split_logit<F16>(a, t, E);
+    if (a.sgate) a.sgate[t] = Act<F16>::sigmoid(Act<F16>::ld(g));
+  }
+  // bf16 (fp16) logits are exact in fp32: the fp32 maximum is the fp64 one
+  const double m = static_cast<double>(wave_max_f32(mf));
+  double ex[NPER], s = 0.0;
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) {
+    const int e = r + 64 * i;
+    ex[i] = e < E ? exp_det(static_cast<double>(lf[i]) - m) : 0.0;
+    s += ex[i];
+  }
+  s = wave_sum_f64(s);
+  uint32_t key[NPER];
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) {
+    const int e = r + 64 * i;
+    key[i] = 0u;
+    if (e < E) {
+      const uint16_t p = Act<F16>::from64(ex[i] / s);
+      if (a.probs) a.probs[static_cast<int64_t>(t) * E + e] = p;
+      // probabilities are >= 0: their patterns order like their values
+      key[i] = (static_cast<uint32_t>(p) << 16) | (0xffffu - static_cast<uint32_t>(e));
+    }
+  }
+  // k rounds of the largest key (prob desc, expert asc); slot j's key stays in lane j
+  float sc_sum = 0.0f;
+  uint32_t my_key = 0u;
+  for (int j = 0; j < a.k; ++j) {
+    uint32_t best = 0u;
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) best = max(best, key[i]);
+    best = wave_max_u32(best);
+#pragma unroll
+    for (int i = 0; i < NPER; ++i)
+      if (key[i] == best) key[i] = 0u;
+    sc_sum += Act<F16>::ld(static_cast<uint16_t>(best >> 16));  // fp32, slot order
+    if (lane == j) my_key = best;
+  }
+  if (lane < a.k) {
+    uint16_t sc = static_cast<uint16_t>(my_key >> 16);
+    if (a.norm) {
+      const double den = static_cast<double>(Act<F16>::rnd(sc_sum));
+      sc = Act<F16>::st(static_cast<float>(static_cast<double>(Act<F16>::ld(sc)) / den));
+    }
+    a.inds[static_cast<int64_t>(t) * a.k + lane] = 0xffffu - (my_key & 0xffffu);
+    a.scores[static_cast<int64_t>(t) * a.k + lane] = sc;
   }
 }
 
@@ -508,25 +616,56 @@ __device__ void f16_row(const RouterArgs& a, int t, int lane) {
   }
 }
 
-template <bool F16>
+// NPER: experts per lane (E <= 64 NPER); mode 1 (Nemotron-H) takes its own
+// selection on rounded logits (no slices)
+template <int NPER, bool F16>
 __global__ __launch_bounds__(kRouterThreads) void topk_kernel(RouterArgs a) {
   const int t = blockIdx.x * kRouterWaves + (threadIdx.x >> 6);
   if (t >= a.T) return;
   if (a.mode == 1)
     router_token_nh(a, t, threadIdx.x & 63);
   else
-    router_token<F16>(a, t, threadIdx.x & 63);
+    topk_token<NPER, F16>(a, t, threadIdx.x & 63);
   if (a.xh) f16_row<F16>(a, t, threadIdx.x & 63);
+}
+
+template <int NPER>
+static void launch_topk(const RouterArgs& a, hipStream_t stream) {
+  const dim3 grid((a.T + kRouterWaves - 1) / kRouterWaves), block(kRouterThreads);
+  if (a.f16)
+    hipLaunchKernelGGL((topk_kernel<NPER, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((topk_kernel<NPER, false>), grid, block, 0, stream, a);
+}
+
+int router_lg_split(int64_t T, int64_t E, int64_t cap) {
+  const int64_t tiles = ((E + 1 + 15) / 16) * ((T + 15) / 16);
+  int64_t s = std::min<int64_t>(4, std::max<int64_t>(1, 1024 / std::max<int64_t>(tiles, 1)));
+  while (s > 1 && s * T * (E + 1) > std::min(kLgPartMax, cap)) --s;
+  return static_cast<int>(s);
 }
 
 hipError_t launch_router_many(const RouterArgs& a, hipStream_t stream) {
   const int ncols = a.E + (a.wsg.w ? 1 : 0);
-  hipLaunchKernelGGL((a.f16 ? logits_kernel<true> : logits_kernel<false>), dim3((ncols + 15) / 16, (a.T + 15) / 16),
-                     dim3(kLgThreads), 0, stream, a);
+  const int kn = a.mode == 1 ? 1 : std::max(a.lg_split, 1);
+  if (kn > 1 && (kn > 4 || !a.lg_part || static_cast<int64_t>(kn) * a.T * (a.E + 1) > kLgPartMax))
+    return hipErrorInvalidValue;
+  RouterArgs b = a;
+  b.lg_split = kn;
+  hipLaunchKernelGGL((a.f16 ? logits_kernel<true> : logits_kernel<false>),
+                     dim3((ncols + 15) / 16, (a.T + 15) / 16, kn), dim3(kLgThreads), 0, stream, b);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((a.f16 ? topk_kernel<true> : topk_kernel<false>), dim3((a.T + kRouterWaves - 1) / kRouterWaves),
-                     dim3(kRouterThreads), 0, stream, a);
+  if (a.E <= 64)
+    launch_topk<1>(b, stream);
+  else if (a.E <= 128)
+    launch_topk<2>(b, stream);
+  else if (a.E <= 256)
+    launch_topk<4>(b, stream);
+  else if (a.E <= 512)
+    launch_topk<8>(b, stream);
+  else
+    launch_topk<16>(b, stream);
   return hipGetLastError();
 }
 

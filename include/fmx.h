@@ -290,7 +290,7 @@ int fmx_moe_block_forward(const fmx_moe_config* cfg, const fmx_moe_weights* w,
  * ends. Forwards whose fmx_moe_workspace_size(cfg, n_tokens) exceeds that
  * return FMX_ERR_UNSUPPORTED before launching anything (8 MiB: every decode
  * batch of up to 16 tokens, and forwards of up to 72 tokens of the
- * Qwen1.5-MoE-A2.7B shape or 103 of the Qwen3-30B-A3B shape). All calls on
+ * Qwen1.5-MoE-A2.7B shape or 104 of the Qwen3-30B-A3B shape). All calls on
  * one device share the array:
  * calls that overlap on one GPU (two streams, or two host threads) race and
  * must be ordered by the caller. Each forward leaves the array's completion
