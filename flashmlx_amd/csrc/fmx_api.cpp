@@ -159,12 +159,6 @@ hipError_t clear_counters(void* base, hipStream_t stream) {
   return e != hipSuccess ? e : launch_fill_u32(w + kEpochOffsetWords, 1, 1u, stream);
 }
 
-// The decode router's logit words and epoch back to their initial state
-hipError_t clear_lgx(uint32_t* base, hipStream_t stream) {
-  const hipError_t e = launch_fill_u32(base + kLgxOffsetWords, kLgxWords, 0u, stream);
-  return e != hipSuccess ? e : launch_fill_u32(base + kEpochOffsetWords, 1, 1u, stream);
-}
-
 // bound of the decode down workgroups' wait (fmx_set_decode_wait_limit)
 std::atomic<int> g_wait_polls{kDecWaitPolls};
 
@@ -986,10 +980,10 @@ int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint
   FMX_HIP(hipMemcpy(status, word, 4, hipMemcpyDeviceToHost));
   if (clear) {
     // after a wait that ran out, late router columns may have tagged their
-    // logit words with the next epoch: a fresh epoch and cleared words make
-    // the next forward start clean
-    FMX_HIP(launch_fill_u32(word, 1, 0u, stream));
-    FMX_HIP(clear_lgx(static_cast<uint32_t*>(const_cast<void*>(workspace)), stream));
+    // logit words with the next epoch, and late stores may have left counters
+    // and flags set: the whole counter block back to its initial state (the
+    // status word included) makes the next forward start clean
+    FMX_HIP(clear_counters(const_cast<void*>(workspace), stream));
   }
   return ok();
 }

@@ -259,18 +259,19 @@ int fmx_moe_workspace_init(void* workspace, size_t workspace_bytes, fmx_stream s
  * gate/up tiles: its products are written as NaN; or the router waiting for
  * the other router columns' logits: missing logits are read as 0). Bits
  * stay set until cleared (clear != 0 clears them after reading, in stream
- * order, and resets the router's logit exchange, which a forward whose wait
- * ran out may leave holding late logits: clear before the next forward). No
- * counterpart in the reference: MLX's graph has no in-kernel waits. */
+ * order, and resets every counter, flag and logit word of the workspace,
+ * which a forward whose wait ran out may leave set: clear before the next
+ * forward). No counterpart in the reference: MLX's graph has no in-kernel
+ * waits. */
 #define FMX_STATUS_WAIT_TIMEOUT 1u
 int fmx_moe_workspace_status(const void* workspace, size_t workspace_bytes, uint32_t* status,
                              int clear, fmx_stream stream);
 
-/* Bound of that wait, in flag reads s_sleep(16) apart (default 2^21, far
- * beyond any real wait): applies to forwards launched after the call;
- * polls = 0 gives up at once (a way to exercise the guard), polls < 0
- * restores the default. Returns the previous bound. No counterpart in the
- * reference. */
+/* Bound of those waits, in flag reads s_sleep(2) to s_sleep(16) apart
+ * (default 2^21, far beyond any real wait): applies to forwards launched
+ * after the call; polls = 0 gives up at once (a way to exercise the guard),
+ * polls < 0 restores the default. Returns the previous bound. No
+ * counterpart in the reference. */
 int64_t fmx_set_decode_wait_limit(int64_t polls);
 
 /* y [T, H] = moe_block(x [T, H]), T = B*L tokens, in the config's activation
