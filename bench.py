@@ -17,11 +17,12 @@ Qwen3-30B-A3B decode batch 1 and 8, prefill 1024), each with its own
 roofline, under "configs".
 
 Per-stage timing: graphs of the first j kernel stages of every layer give
-each stage's marginal time (HIP events on the stream the kernels run on);
-the dominant kernel's average duration (the stages it runs, together) gives
-the roofline figure. The same command under `rocprofv3 --kernel-trace
---stats` gives the per-kernel averages that the summaries under profiles/
-quote.
+each stage's marginal time inside the layer (HIP events on the stream the
+kernels run on, each timed section queued behind whole-layer graph replays
+so that it never waits for the host's launches); the dominant kernel's
+average duration (the stages it runs, together) gives the roofline figure.
+The same command under `rocprofv3 --kernel-trace --stats` gives the
+per-kernel averages that the summaries under profiles/ quote.
 
 `--copy-calibration MIB` instead runs a plain device copy of MIB MiB five
 times (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
@@ -49,6 +50,30 @@ CONFIGS = ["qwen15_decode_b1", "qwen15_decode_b4", "qwen15_prefill_512", "qwen3_
 
 def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+_SLEEP_CYCLES_PER_MS = None
+
+
+def gpu_lead(stream, ms: float = 20.0) -> None:
+    """Queues about `ms` milliseconds of GPU work on `stream` as ONE bounded
+    spin kernel (torch.cuda._sleep, calibrated once with HIP events), so
+    that the launches the host queues after it are in place before the GPU
+    reaches them: one kernel costs the host one launch, also under a tracing
+    profiler that makes every launch slow."""
+    global _SLEEP_CYCLES_PER_MS
+    import torch
+
+    with torch.cuda.stream(stream):
+        if _SLEEP_CYCLES_PER_MS is None:
+            torch.cuda._sleep(1000)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            torch.cuda._sleep(10_000_000)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            _SLEEP_CYCLES_PER_MS = 10_000_000 / max(e0.elapsed_time(e1), 1e-3)
+        torch.cuda._sleep(int(min(ms * _SLEEP_CYCLES_PER_MS, 2e9)))
 
 
 def cpu_model() -> str:
@@ -292,27 +317,42 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
 
     # ---- per-stage timing: graphs of R layers that run only the first j
     # kernel stages; stage j's marginal time inside the layer is the
-    # difference of consecutive graphs' times
+    # difference of consecutive graphs' times. Each timed section is queued
+    # behind a 20 ms spin kernel and two whole-layer replays, so that the
+    # host has queued the section's kernels before the GPU reaches them: a
+    # graph of short kernels would otherwise wait for the host's launches
+    # where launches are slow (under a tracing profiler) and inflate its own
+    # stage at the next stage's expense
     work = W.stage_work(m, T, U, wl.router_bias, packed=pack, router_quant=wl.router_quant)
     stages = [s[0] for s in work]
     reps = max(1, profile_steps // R)
     cum = [0.0]
+    host_ms = []
     for j in range(1, len(stages) + 1):
         gj = capture(lambda j=j: [blocks[i].forward_partial(x, y, j) for i in range(R)])
         with torch.cuda.stream(stream):
             gj.replay()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        with torch.cuda.stream(stream):
-            for _ in range(reps):
-                gj.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        cum.append(e0.elapsed_time(e1) / (R * reps))
+        tries = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gpu_lead(stream)
+            h0 = time.perf_counter()
+            with torch.cuda.stream(stream):
+                for _ in range(2):
+                    graphs[R].replay()
+                e0.record(stream)
+                for _ in range(reps):
+                    gj.replay()
+                e1.record(stream)
+                host_ms.append((time.perf_counter() - h0) * 1e3)
+            torch.cuda.synchronize()
+            tries.append(e0.elapsed_time(e1) / (R * reps))
+        cum.append(statistics.median(tries))
         del gj
     dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(len(stages))]
     stage_us = {s: round(dur[j] * 1e3, 2) for j, s in enumerate(stages)}
+    log(f"{wl.key}: stage timing queued {max(host_ms):.2f} ms of launches at most behind a 20 ms spin")
 
     # the dominant kernel of a whole forward: a kernel that runs several
     # stages as one grid takes their marginal times and work together
@@ -467,15 +507,38 @@ def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_secon
     ms_total = statistics.median(times)
     ms_step = ms_total / (reps * R)
 
-    # per-stage kernel times: events around each stage of eager forwards
-    n_prof = max(R, 4 * R if T <= 16 else R)
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(n_prof)]
-    with torch.cuda.stream(stream):
-        for i in range(n_prof):
-            blocks[i % R].forward_profiled(x, y, evs[i])
-    torch.cuda.synchronize()
+    # per-stage kernel times: graphs of R layers that run only the first j
+    # kernel stages, each timed section queued behind a 20 ms spin kernel
+    # and two whole-layer replays so that it never waits for the host's
+    # launches; stage j's marginal time inside the layer is the difference
+    # of consecutive graphs' times
     names = ["router_sort", "fc1_grid", "fc2_grid", "combine"]
-    stage_ms = {nm: statistics.median([e[j].elapsed_time(e[j + 1]) for e in evs]) for j, nm in enumerate(names)}
+    sreps = max(1, 96 // R)
+    cum = [0.0]
+    for j in range(1, len(names) + 1):
+        gj = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gj, stream=stream):
+            for b in blocks:
+                b.forward_partial(x, y, j)
+        with torch.cuda.stream(stream):
+            gj.replay()
+        torch.cuda.synchronize()
+        tries = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gpu_lead(stream)
+            with torch.cuda.stream(stream):
+                for _ in range(2):
+                    g.replay()
+                e0.record(stream)
+                for _ in range(sreps):
+                    gj.replay()
+                e1.record(stream)
+            torch.cuda.synchronize()
+            tries.append(e0.elapsed_time(e1) / (R * sreps))
+        cum.append(statistics.median(tries))
+        del gj
+    stage_ms = {nm: max(cum[j + 1] - cum[j], 1e-6) for j, nm in enumerate(names)}
     grid_bytes, grid_flops, layer_bytes, layer_flops = nh_bytes_flops(cfg, T, U)
     dom = max(("fc1_grid", "fc2_grid"), key=lambda nm: stage_ms[nm])
     dur_s = stage_ms[dom] * 1e-3
@@ -950,7 +1013,9 @@ def main():
     ap.add_argument("--configs", default="all",
                     help="other MoE-layer configs measured in the same run: all, none or a comma list")
     ap.add_argument("--layers", type=int, default=24, help="weight copies cycled over")
-    ap.add_argument("--profile-steps", type=int, default=480, help="steps of the per-stage timing pass")
+    ap.add_argument("--profile-steps", type=int, default=96,
+                    help="steps of each per-stage timing section (timed three times, median); small enough "
+                         "that a section's launches fit the stream's queue behind the spin kernel")
     ap.add_argument("--cpu-seconds", type=float, default=16.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-pack", action="store_true",

@@ -290,6 +290,9 @@ _SIGS = {
     "fmx_nh_moe_block_forward_profiled": (
         C.c_int, [P(FmxNhMoEConfig), P(FmxNhMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
                   C.c_size_t, C.c_void_p, P(C.c_void_p)]),
+    "fmx_nh_moe_block_forward_partial": (
+        C.c_int, [P(FmxNhMoEConfig), P(FmxNhMoEWeights), C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                  C.c_size_t, C.c_void_p, C.c_int]),
     "fmx_nh_moe_workspace_routing": (
         C.c_int, [P(FmxNhMoEConfig), C.c_int64, C.c_void_p, P(C.c_void_p), P(C.c_void_p), P(C.c_void_p)]),
 }

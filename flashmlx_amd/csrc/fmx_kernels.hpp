@@ -386,7 +386,7 @@ struct NhDecArgs {
 };
 constexpr int kNhDecMaxColBlocks = 64;  // 64-column blocks of H (D3 arrival counters)
 bool nh_decode_plan(NhDecArgs& a);
-hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks);
+hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks, int n_stages = 4);
 
 // The Nemotron-H combine: y = bf16(bf16(sum over slots, fp32 in slot order,
 // of d * score) + sd) (the add in fp32; sd null: no shared expert).

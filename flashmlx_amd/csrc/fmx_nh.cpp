@@ -264,14 +264,16 @@ int fmx_nh_moe_workspace_routing(const fmx_nh_moe_config* cfg, int64_t T, const 
   return ok();
 }
 
-int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w, const void* x,
-                             int64_t T, void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_) {
-  return fmx_nh_moe_block_forward_profiled(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr);
-}
+}  // extern "C"
 
-int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
-                                      const void* x, int64_t T, void* y, void* workspace,
-                                      size_t workspace_bytes, fmx_stream stream_, void* const* stage_events) {
+namespace {
+
+// The forward's first n_stages kernel stages (1..4: router + sort, fc1,
+// fc2, combine; the decode kernels D1, D2, D3 with D3 forming the combine),
+// recording stage_events (when given) at the stage boundaries.
+int nh_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w, const void* x, int64_t T, void* y,
+               void* workspace, size_t workspace_bytes, fmx_stream stream_, void* const* stage_events,
+               int n_stages) {
   hipStream_t stream = static_cast<hipStream_t>(stream_);
   auto mark = [&](int i) -> hipError_t {
     return stage_events ? hipEventRecord(static_cast<hipEvent_t>(stage_events[i]), stream) : hipSuccess;
@@ -356,7 +358,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       da.y = static_cast<uint16_t*>(y);
       da.counter = L.counters;
       da.cb_counter = L.cb_counter;
-      FMX_HIP(launch_nh_decode(da, stream, stage_events));
+      FMX_HIP(launch_nh_decode(da, stream, stage_events, n_stages));
       return FMX_OK;
     }
 
@@ -397,6 +399,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       FMX_HIP(launch_sort(L.inds, static_cast<int>(n), static_cast<int>(k), static_cast<int>(E), so, stream));
     }
     FMX_HIP(mark(1));
+    if (n_stages < 2) return FMX_OK;
 
     const int mp = max_passes(n, E);
     auto routed = [&](const uint8_t* wp, int64_t es, const uint16_t* xr, const uint16_t* xrh, int64_t ldx,
@@ -453,6 +456,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       FMX_HIP(launch_pf(pa, false, stream));
       FMX_HIP(mark(2));
     }
+    if (n_stages < 3) return FMX_OK;
     {  // fc2 and the shared down projection, fp32 products
       PfArgs pa{};
       pa.s1 = routed(pk + P.fc2, P.fc2_es, L.h, L.hh, P.Ip, nullptr, H, P.Ip);
@@ -471,6 +475,7 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
       FMX_HIP(launch_pf(pa, false, stream));
       FMX_HIP(mark(3));
     }
+    if (n_stages < 4) return FMX_OK;
     NhCombineArgs cb{};
     cb.d = L.d;
     cb.inv = L.inv;
@@ -488,6 +493,28 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
   rc = body();
   if (owned) (void)hipFreeAsync(base, stream);
   return rc ? rc : ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int fmx_nh_moe_block_forward(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w, const void* x,
+                             int64_t T, void* y, void* workspace, size_t workspace_bytes, fmx_stream stream_) {
+  return nh_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr, 4);
+}
+
+int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
+                                      const void* x, int64_t T, void* y, void* workspace,
+                                      size_t workspace_bytes, fmx_stream stream_, void* const* stage_events) {
+  return nh_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, stage_events, 4);
+}
+
+int fmx_nh_moe_block_forward_partial(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
+                                     const void* x, int64_t T, void* y, void* workspace,
+                                     size_t workspace_bytes, fmx_stream stream_, int n_stages) {
+  if (n_stages < 1 || n_stages > 4) return fail(FMX_ERR_ARG, "n_stages=%d (1..4)", n_stages);
+  return nh_forward(cfg, w, x, T, y, workspace, workspace_bytes, stream_, nullptr, n_stages);
 }
 
 }  // extern "C"

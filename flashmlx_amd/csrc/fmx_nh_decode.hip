@@ -533,7 +533,7 @@ bool nh_decode_plan(NhDecArgs& a) {
   return d1_lds(a) + 16 * 1024 <= 160 * 1024 && d3_lds(a) <= 160 * 1024;
 }
 
-hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks) {
+hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const* marks, int n_stages) {
   if (!a.cb_counter || !a.counter) return hipErrorInvalidValue;
   auto mark = [&](int i) -> hipError_t {
     return marks ? hipEventRecord(static_cast<hipEvent_t>(marks[i]), stream) : hipSuccess;
@@ -550,6 +550,7 @@ hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const*
     launch_d1<8>(a, stream);
   if ((err = hipGetLastError()) != hipSuccess) return err;
   if ((err = mark(1)) != hipSuccess) return err;
+  if (n_stages < 2) return hipSuccess;
   {
     const int ntile = a.Ip / 16;
     const bool two = a.max_seg * ntile >= kNhD2PairGrid;
@@ -573,6 +574,7 @@ hipError_t launch_nh_decode(const NhDecArgs& a, hipStream_t stream, void* const*
     if ((err = hipGetLastError()) != hipSuccess) return err;
   }
   if ((err = mark(2)) != hipSuccess) return err;
+  if (n_stages < 3) return hipSuccess;
   {
     const int ncb = a.H / (16 * kNhDnTiles);
     const int n = a.max_seg * ncb * kNhDnSplit + (a.Isp > 0 ? ncb * kNhDecSdSplit : 0);

@@ -133,6 +133,17 @@ class NhMoEBlock:
             self.workspace.data_ptr(), self.workspace.numel(), _stream()))
         self._last_T = T
 
+    def forward_partial(self, x: torch.Tensor, y: torch.Tensor, n_stages: int) -> None:
+        """forward_into that launches only the first n_stages (1..4) kernel
+        stages: router + sort, fc1, fc2, combine (for per-stage timing)."""
+        T = x.numel() // self.cfg.hidden_size
+        if T > self.max_tokens:
+            raise ValueError(f"{T} tokens > max_tokens {self.max_tokens}")
+        _lib.check(self.lib.fmx_nh_moe_block_forward_partial(
+            C.byref(self._c_cfg), C.byref(self._c_w), x.data_ptr(), T, y.data_ptr(),
+            self.workspace.data_ptr(), self.workspace.numel(), _stream(), n_stages))
+        self._last_T = T
+
     def forward_profiled(self, x: torch.Tensor, y: torch.Tensor, events) -> None:
         """forward_into recording 5 torch.cuda.Events at the stage
         boundaries (router+sort, fc1, fc2, combine)."""

@@ -41,6 +41,14 @@ STAGE_OF = [
     (r"dense_dec_kernel<false", "o_proj, lm_head"),
     (r"greedy_kernel", "argmax"),
     (r"rmsnorm_kernel", "norm"),
+    # the Nemotron-H block's kernels
+    (r"nh_d1", "router+shared_up (D1)"),
+    (r"nh_d2", "fc1 (D2)"),
+    (r"nh_d3", "fc2+combine (D3)"),
+    (r"nh_combine_kernel", "combine"),
+    # bench.py's timing lead: one bounded spin kernel queued before each
+    # timed per-stage section
+    (r"spin_kernel", "timing lead"),
 ]
 
 

@@ -102,6 +102,16 @@ int fmx_nh_moe_block_forward_profiled(const fmx_nh_moe_config* cfg, const fmx_nh
                                       size_t workspace_bytes, fmx_stream stream,
                                       void* const* stage_events);
 
+/* fmx_nh_moe_block_forward that launches only its first n_stages kernel
+ * stages (1..4: router + sort, fc1 (+ shared up), fc2 (+ shared down),
+ * combine; 4 = the whole forward, y complete; on the decode kernels 3
+ * already forms the combine). Timing graphs of 1, 2, 3 and 4 stages gives
+ * each stage's marginal time inside the layer. A measurement aid with no
+ * counterpart in the reference. */
+int fmx_nh_moe_block_forward_partial(const fmx_nh_moe_config* cfg, const fmx_nh_moe_weights* w,
+                                     const void* x, int64_t n_tokens, void* y, void* workspace,
+                                     size_t workspace_bytes, fmx_stream stream, int n_stages);
+
 /* Device views of the routing the latest forward of n_tokens tokens left in
  * the workspace: inds [T, k] u32, scores [T, k] fp32, logits [T, E + 1] bf16
  * (row stride E + 1); any out pointer may be NULL. */

@@ -357,3 +357,7 @@ def test_nemotron_sizes_and_validation(fmx):
     w = _lib.FmxNhMoEWeights()
     assert lib.fmx_nh_moe_block_forward(C.byref(c), C.byref(w), None, 0, None, None, 0, None) == _lib.FMX_OK
     assert lib.fmx_nh_moe_block_forward(C.byref(c), None, None, 1, None, None, 0, None) == _lib.FMX_ERR_ARG
+    for bad_n in (0, 5):
+        assert lib.fmx_nh_moe_block_forward_partial(C.byref(c), C.byref(w), None, 0, None, None, 0, None,
+                                                    bad_n) == _lib.FMX_ERR_ARG
+    assert lib.fmx_nh_moe_block_forward_partial(C.byref(c), C.byref(w), None, 0, None, None, 0, None, 2) == _lib.FMX_OK

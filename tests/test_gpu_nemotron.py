@@ -124,3 +124,30 @@ def test_nh_empty_and_refusals(gpu, fmx):
     rc = lib.fmx_nh_moe_block_forward(C.byref(c), C.byref(cw), x.data_ptr(), 4, y.data_ptr(), None, 0,
                                       torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.FMX_ERR_ARG
+
+
+@pytest.mark.parametrize("T", [3, 40])
+def test_nh_partial_forwards_leave_the_block_consistent(gpu, fmx, T):
+    """fmx_nh_moe_block_forward_partial: 4 stages give the whole forward's y
+    bit for bit, and forwards cut after 1, 2 or 3 stages (as per-stage
+    timing runs them) leave the workspace's counters and flags such that the
+    next whole forward still gives the same bits (decode kernels at 3
+    tokens, the prefill GEMMs at 40)."""
+    import torch
+    from flashmlx_amd import nemotron as N
+    cfg = N.NhMoEConfig(hidden_size=512, n_routed_experts=32, num_experts_per_tok=4,
+                        moe_intermediate_size=192, moe_shared_expert_intermediate_size=640,
+                        n_group=4, topk_group=2, routed_scaling_factor=1.5)
+    w = N.synthetic_nh_weights(cfg, 19, w_std=0.05)
+    blk = N.NhMoEBlock(cfg, w, T)
+    x = to_dev(_x((T, 512), 700 + T))
+    y_ref = blk(x)
+    y = torch.zeros_like(y_ref)
+    blk.forward_partial(x, y, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    for n in (1, 2, 3, 2, 1):
+        blk.forward_partial(x, y, n)
+        y2 = blk(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y2, y_ref), f"after a {n}-stage forward"
