@@ -121,17 +121,42 @@ __global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
         }
   }
 
+  // the wave's first batch of weight units is issued before anything waits:
+  // with the input norm, the raw rows' loads go out first and the norm is
+  // formed while the weights are in flight (loads complete in order, so the
+  // norm waits for the rows only)
+  PkUnit<false> L[kDnBatch];
+  auto load_batch = [&](int u0) {
+#pragma unroll
+    for (int d = 0; d < kDnBatch; ++d) {
+      const int u = min(u0 + 4 * d, a.nu - 1);  // units past K repeat the last and are skipped
+      L[d] = pk_load<false>(tb + static_cast<int64_t>(u) * kBlockSingle, lane);
+    }
+  };
+
   const uint16_t* xrow;
   if constexpr (NIN) {
     // the input norm of the T rows, into LDS
     const int nch = K / 8;
-    u32x4_t xv[kDenseNormMaxT][kNormMaxChunks], wv[kNormMaxChunks];
+    u32x4_t xv[kDenseNormMaxT][kNormMaxChunks], dv[kDenseNormMaxT][kNormMaxChunks], wv[kNormMaxChunks];
     double ss[kDenseNormMaxT];
+#pragma unroll
+    for (int t = 0; t < kDenseNormMaxT; ++t) {
+      if (t >= a.T) continue;
+#pragma unroll
+      for (int q = 0; q < kNormMaxChunks; ++q) {
+        const int c = tid + q * kNormThreads;
+        if (c >= nch) break;
+        xv[t][q] = reinterpret_cast<const u32x4_t*>(a.nin + static_cast<int64_t>(t) * a.ldx)[c];
+        if (a.ndelta) dv[t][q] = reinterpret_cast<const u32x4_t*>(a.ndelta + static_cast<int64_t>(t) * a.ldx)[c];
+      }
+    }
 #pragma unroll
     for (int q = 0; q < kNormMaxChunks; ++q) {
       const int c = tid + q * kNormThreads;
       if (c < nch) wv[q] = reinterpret_cast<const u32x4_t*>(a.nin_w)[c];
     }
+    load_batch(wave);
 #pragma unroll
     for (int t = 0; t < kDenseNormMaxT; ++t) {
       ss[t] = 0.0;
@@ -140,11 +165,8 @@ __global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
       for (int q = 0; q < kNormMaxChunks; ++q) {
         const int c = tid + q * kNormThreads;
         if (c >= nch) break;
-        u32x4_t x = reinterpret_cast<const u32x4_t*>(a.nin + static_cast<int64_t>(t) * a.ldx)[c];
-        if (a.ndelta)
-          x = norm_add(x, reinterpret_cast<const u32x4_t*>(a.ndelta + static_cast<int64_t>(t) * a.ldx)[c]);
-        xv[t][q] = x;
-        ss[t] = norm_sq(x, ss[t]);
+        if (a.ndelta) xv[t][q] = norm_add(xv[t][q], dv[t][q]);
+        ss[t] = norm_sq(xv[t][q], ss[t]);
       }
     }
 #pragma unroll
@@ -169,17 +191,17 @@ __global__ __launch_bounds__(256) void dense_dec_kernel(DenseArgs a) {
     __syncthreads();
     xrow = reinterpret_cast<const uint16_t*>(s_dn) + static_cast<int64_t>(min(i16, a.T - 1)) * K + 8 * j;
   } else {
+    load_batch(wave);
     xrow = a.x + static_cast<int64_t>(min(i16, a.T - 1)) * a.ldx + 8 * j;
   }
 
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f}, unused = {0.f, 0.f, 0.f, 0.f};
   for (int u0 = wave; u0 < a.nu; u0 += 4 * kDnBatch) {
-    PkUnit<false> L[kDnBatch];
+    if (u0 != wave) load_batch(u0);
     bf16x8_t A[kDnBatch][4];
 #pragma unroll
     for (int d = 0; d < kDnBatch; ++d) {
-      const int u = min(u0 + 4 * d, a.nu - 1);  // units past K repeat the last and are skipped
-      L[d] = pk_load<false>(tb + static_cast<int64_t>(u) * kBlockSingle, lane);
+      const int u = min(u0 + 4 * d, a.nu - 1);
 #pragma unroll
       for (int q = 0; q < 4; ++q) A[d][q] = *reinterpret_cast<const bf16x8_t*>(xrow + 128 * u + 32 * q);
     }
