@@ -18,8 +18,9 @@ roofline, under "configs".
 
 Per-stage timing: graphs of the first j kernel stages of every layer give
 each stage's marginal time inside the layer (HIP events on the stream the
-kernels run on, each timed section queued behind whole-layer graph replays
-so that it never waits for the host's launches); the dominant kernel's
+kernels run on, each timed section queued behind a spin kernel and
+whole-layer graph replays so that it never waits for the host's launches
+and runs at the layer's own clocks); the dominant kernel's
 average duration (the stages it runs, together) gives the roofline figure.
 The same command under `rocprofv3 --kernel-trace --stats` gives the
 per-kernel averages that the summaries under profiles/ quote.
@@ -318,14 +319,16 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
     # ---- per-stage timing: graphs of R layers that run only the first j
     # kernel stages; stage j's marginal time inside the layer is the
     # difference of consecutive graphs' times. Each timed section is queued
-    # behind a 20 ms spin kernel and two whole-layer replays, so that the
-    # host has queued the section's kernels before the GPU reaches them: a
-    # graph of short kernels would otherwise wait for the host's launches
-    # where launches are slow (under a tracing profiler) and inflate its own
-    # stage at the next stage's expense
+    # behind a 20 ms spin kernel, so that the host has queued the section's
+    # kernels before the GPU reaches them (a graph of short kernels would
+    # otherwise wait for the host's launches where launches are slow, under
+    # a tracing profiler, and inflate its own stage at the next stage's
+    # expense), and behind about 8 ms of whole-layer replays, which bring
+    # the clocks back from the spin's one busy wave to the layer's own
     work = W.stage_work(m, T, U, wl.router_bias, packed=pack, router_quant=wl.router_quant)
     stages = [s[0] for s in work]
     reps = max(1, profile_steps // R)
+    warm = max(2, int(8.0 / (R * ms_step)) + 1)
     cum = [0.0]
     host_ms = []
     for j in range(1, len(stages) + 1):
@@ -339,7 +342,7 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
             gpu_lead(stream)
             h0 = time.perf_counter()
             with torch.cuda.stream(stream):
-                for _ in range(2):
+                for _ in range(warm):
                     graphs[R].replay()
                 e0.record(stream)
                 for _ in range(reps):
@@ -352,7 +355,8 @@ def measure(wl, R: int, K: int, Wm: int, trials: int, profile_steps: int, pack: 
         del gj
     dur = [max(cum[j + 1] - cum[j], 1e-6) for j in range(len(stages))]
     stage_us = {s: round(dur[j] * 1e3, 2) for j, s in enumerate(stages)}
-    log(f"{wl.key}: stage timing queued {max(host_ms):.2f} ms of launches at most behind a 20 ms spin")
+    log(f"{wl.key}: stage timing queued {max(host_ms):.2f} ms of launches at most behind a 20 ms spin; "
+        f"stages add up to {cum[-1] * 1e3:.2f} us against {ms_step * 1e3:.2f} us per whole layer")
 
     # the dominant kernel of a whole forward: a kernel that runs several
     # stages as one grid takes their marginal times and work together
@@ -509,11 +513,13 @@ def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_secon
 
     # per-stage kernel times: graphs of R layers that run only the first j
     # kernel stages, each timed section queued behind a 20 ms spin kernel
-    # and two whole-layer replays so that it never waits for the host's
-    # launches; stage j's marginal time inside the layer is the difference
-    # of consecutive graphs' times
+    # (so that it never waits for the host's launches) and about 8 ms of
+    # whole-layer replays (the clocks back to the layer's own); stage j's
+    # marginal time inside the layer is the difference of consecutive
+    # graphs' times
     names = ["router_sort", "fc1_grid", "fc2_grid", "combine"]
     sreps = max(1, 96 // R)
+    warm = max(2, int(8.0 / (R * ms_step)) + 1)
     cum = [0.0]
     for j in range(1, len(names) + 1):
         gj = torch.cuda.CUDAGraph()
@@ -528,7 +534,7 @@ def measure_nh(key: str, T: int, R: int, K: int, Wm: int, trials: int, cpu_secon
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             gpu_lead(stream)
             with torch.cuda.stream(stream):
-                for _ in range(2):
+                for _ in range(warm):
                     g.replay()
                 e0.record(stream)
                 for _ in range(sreps):
