@@ -42,11 +42,6 @@ namespace fmx {
 namespace {
 
 constexpr int kDecK2Units = 4;  // units (of H / 128 <= 16) per wave of a gate/up tile pair
-// K1's cache warming: LDS DMA instructions per wave (1 KB each, into a
-// throwaway LDS piece), at least a shared tile pair's share of the shared
-// down weights (9 H bytes per workgroup, H <= 2048)
-constexpr int kDecWarmDma = 5;
-constexpr int kDecWarmLdsBytes = kWave * 16;
 // Gate/up tile pairs per K2 workgroup (their loads in flight together, the
 // routing tables and staged rows shared): two when the grid has at least
 // kDecK2PairGrid tile pairs (about two resident grids of one-pair
@@ -60,7 +55,7 @@ constexpr int kDecK1LpBytes = kDecWaves * kDecMaxT * 8;              // router p
 
 constexpr int kDecK1LgBytes = kDecMaxT * (kDecMaxE + 1) * 2;         // every token's logits
 // K1's LDS: the router's partials and logits, or the shared tiles' quarter
-// reduction; then the staged rows (the warming's throwaway piece follows)
+// reduction; then the staged rows
 __host__ __device__ inline int k1_lds_main(int T, int H) {
   return (kDecQuadRedBytes > kDecK1LpBytes + kDecK1LgBytes ? kDecQuadRedBytes : kDecK1LpBytes + kDecK1LgBytes) +
          T * xstride(H) * 2;
@@ -389,27 +384,12 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   const uint8_t* tb = a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair;
-  // Warming of the device's last-level cache with this workgroup's share of
-  // the shared expert's down weights, which K23 reads after the routing (K1's
-  // HBM would otherwise idle while its router chain finishes): exactly
-  // kDecWarmDma LDS DMA instructions per wave, issued right behind the tile's
-  // loads into a throwaway LDS piece (no registers held; addresses past the
-  // share re-read its last piece), drained before the workgroup ends.
-  uint8_t* s_warm = smem + k1_lds_main(T, H);
-  const int64_t total = static_cast<int64_t>(a.H / 16) * (a.Is / 128) * kBlockSingle;
-  const int64_t per = (total + a.n_sgu - 1) / a.n_sgu;
-  const int64_t b0 = min(static_cast<int64_t>(tp) * per, total - 16), b1 = min(b0 + per, total);
-  auto warm = [&]() {
-#pragma unroll
-    for (int i = 0; i < kDecWarmDma; ++i) {
-      const int64_t off = min(b0 + ((static_cast<int64_t>(wave) * kDecWarmDma + i) * kWave + lane) * 16, b1 - 16);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.sdn + off),
-                                       (__attribute__((address_space(3))) void*)s_warm, 16, 0, 0);
-    }
-  };
+  // No last-level-cache warming with the shared down weights here: that LDS
+  // DMA (6.5 MB at the Qwen1.5 shape) delays the router columns' loads,
+  // which share K1's HBM stream, more than it saves K23.
   if constexpr (NIN) {
     // the tile's loads first, then the input norm (its barrier also waits
-    // for them), then the warming, then the products
+    // for them), then the products
     __shared__ double s_nred[NT * (kNormThreads / kWave)];
     PkUnit<true> L[kDecK2Units];
     __builtin_amdgcn_sched_barrier(0);
@@ -417,7 +397,6 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
     for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
     __builtin_amdgcn_sched_barrier(0);
     norm_rows_lds<NT>(a.nin, H, a.nin_w, a.nin_eps, T, H, s_x, xs, s_nred);
-    warm();
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
       if (u0 + d < u1) {
@@ -432,11 +411,10 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) L[d] = pk_load<true>(tb + min(u0 + d, u1 - 1) * kBlockPair, lane);
-    warm();
     __builtin_amdgcn_sched_barrier(0);
     // vector memory operations complete in order: the rows' DMA, issued
-    // before the tile's loads and the warming, has landed at this count
-    wait_vmcnt<kDecK2Units * pk_load_insts<true>() + kDecWarmDma>();
+    // before the tile's loads, has landed at this count
+    wait_vmcnt<kDecK2Units * pk_load_insts<true>()>();
     lds_dma_barrier();
 #pragma unroll
     for (int d = 0; d < kDecK2Units; ++d) {
@@ -457,7 +435,6 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
         a.hs[static_cast<int64_t>(t) * Is + n] = Act<F16>::swiglu(Act<F16>::rnd(acc0[i]), Act<F16>::rnd(acc1[i]));
     }
   }
-  wait_vmcnt0();  // the warming's LDS writes land before the workgroup's LDS is released
 }
 
 // Workgroups [0, n_rt): router columns; [n_rt, n_rt + n_sgu): shared tile pairs.
@@ -825,7 +802,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_k23(DecodeArgs a) {
 
 // ---------------------------------------------------------------- host side
 
-static size_t k1_lds(const DecodeArgs& a) { return k1_lds_main(a.T, a.H) + kDecWarmLdsBytes; }
+static size_t k1_lds(const DecodeArgs& a) { return k1_lds_main(a.T, a.H); }
 
 // K2: the quarter reduction, then the staged rows
 static size_t k2_lds(const DecodeArgs& a) {
