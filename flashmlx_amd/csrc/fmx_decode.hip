@@ -384,9 +384,19 @@ __device__ void dec_shared_gu(const DecodeArgs& a, int tp, uint8_t* smem) {
   const uint16_t* xl = s_x + min(m, T - 1) * xs + 8 * j;
   f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   const uint8_t* tb = a.sgu + static_cast<int64_t>(tp) * nu * kBlockPair;
-  // No last-level-cache warming with the shared down weights here: that LDS
-  // DMA (6.5 MB at the Qwen1.5 shape) delays the router columns' loads,
-  // which share K1's HBM stream, more than it saves K23.
+  // The router columns' loads go out first: from two tokens on, the tiles
+  // hold theirs back about 0.85 us (up to 4 tokens) or 1.3 us (more), so
+  // that the columns' rows and weights are not queued behind the shared
+  // expert's (Qwen1.5 shape: batch 8 44.3 -> 43.0 us per layer, batch 16
+  // 49.5 -> 47.8, batch 4 31.6 -> 30.9). The tiles still end before the
+  // routing does; at one token (x and the weight rows land at about 1.9
+  // us) the delay would only move their end past it. No last-level-cache
+  // warming with the shared down weights either: that LDS DMA (6.5 MB at
+  // the Qwen1.5 shape) delayed the columns' loads more than it saved K23.
+  {
+    const int naps = T <= 1 ? 0 : (T <= 4 ? 2 : 3);  // s_sleep 16 = 1024 clocks each
+    for (int z = 0; z < naps; ++z) __builtin_amdgcn_s_sleep(16);
+  }
   if constexpr (NIN) {
     // the tile's loads first, then the input norm (its barrier also waits
     // for them), then the products
