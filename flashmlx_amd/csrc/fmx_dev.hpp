@@ -534,17 +534,23 @@ struct PkUnit {
 template <bool DUAL>
 constexpr int pk_load_insts() { return DUAL ? 4 : 2; }
 
+// The loads are non-temporal: a decode forward reads each weight once, and
+// without the hint the weight stream evicts from the L2 and the last-level
+// cache what the next kernels need at once (their code, the routing
+// tables, rows and flags), so every later kernel's first instructions and
+// loads went out to HBM (measured: Qwen1.5-MoE decode batch 1 21.9 -> 20.4
+// us per layer, the 24-layer stack's batch-1 step 1.25 -> 1.18 ms).
 template <bool DUAL>
 __device__ inline PkUnit<DUAL> pk_load(const uint8_t* blk, int lane) {
   PkUnit<DUAL> L;
   const int col = lane & 15;
-  L.w0 = *reinterpret_cast<const u32x4_t*>(blk + 16 * lane);
+  L.w0 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(blk + 16 * lane));
   if (DUAL) {
-    L.w1 = *reinterpret_cast<const u32x4_t*>(blk + 1024 + 16 * lane);
-    L.sb0 = *reinterpret_cast<const u32x2_t*>(blk + 2048 + 8 * col);
-    L.sb1 = *reinterpret_cast<const u32x2_t*>(blk + 2048 + 128 + 8 * col);
+    L.w1 = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(blk + 1024 + 16 * lane));
+    L.sb0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(blk + 2048 + 8 * col));
+    L.sb1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(blk + 2048 + 128 + 8 * col));
   } else {
-    L.sb0 = *reinterpret_cast<const u32x2_t*>(blk + 1024 + 8 * col);
+    L.sb0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(blk + 1024 + 8 * col));
   }
   return L;
 }

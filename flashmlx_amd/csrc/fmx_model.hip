@@ -482,22 +482,22 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
   const int rep = a.nh / a.nkv, g = h / rep;
   const int half = a.hd / 2, nch = a.hd / 8;
 
-  // 1. the rotation's inputs that do not depend on the position: thread
-  // i < hd takes pair i mod hd/2 of q (i < hd/2) or of the new key; thread
-  // d < hd the new value's element d
+  // 1. the position and the cache slot (token_pos, cache_slot): both words
+  // are loaded together, ahead of every load whose address needs them (a
+  // null pointer reads a word of the q/k/v row and discards it, so neither
+  // load waits behind a branch): one memory round trip
   const uint16_t* row = a.qkv + static_cast<int64_t>(t) * (a.nh + 2 * a.nkv) * a.hd;
-  const bool rot = tid < a.hd;
-  const int hd_i = tid % half;
-  uint16_t rx1 = 0, rx2 = 0, rv = 0;
-  if (rot) {
-    const uint16_t* src = row + (tid < half ? h : a.nh + g) * a.hd;
-    rx1 = src[hd_i];
-    rx2 = src[hd_i + half];
-    rv = row[(a.nh + a.nkv + g) * a.hd + tid];
-  }
-  const int p = token_pos(a.offs, a.off, t, 0, a.max_seq);
+  const int32_t* po = a.offs ? a.offs + t : reinterpret_cast<const int32_t*>(row);
+  const int32_t* ps = a.slots ? a.slots + t : reinterpret_cast<const int32_t*>(row);
+  // both addresses formed before either load (scalar loads complete out of
+  // order: a wait for one pointer argument would wait for the other word)
+  asm volatile("" : "+s"(po), "+s"(ps));
+  const int32_t ow = *po, sw = *ps;
+  const int64_t p64 = a.offs ? static_cast<int64_t>(ow) : static_cast<int64_t>(a.off);
+  const int p = static_cast<int>(p64 < 0 ? 0 : (p64 >= a.max_seq ? a.max_seq - 1 : p64));
+  const int64_t slot = a.slots ? (sw < 0 ? 0 : (sw >= a.n_slots ? a.n_slots - 1 : sw)) : t;
   const int nk = p + 1, S = attn_splits(nk);
-  const int64_t cbase = (cache_slot(a.slots, a.n_slots, t) * a.nkv + g) * a.max_seq * a.hd;
+  const int64_t cbase = (slot * a.nkv + g) * a.max_seq * a.hd;
   uint16_t* kb = a.kc + cbase;
   uint16_t* vb = a.vc + cbase;
   // this wave's range; keys before jg come from the cache (p, the last key
@@ -508,12 +508,6 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
   const bool last = wave == S - 1;
   const int jg = last ? j1 - 1 : j1;
   const int jclamp = max(jg - 1, 0);  // loads past the range re-read its last cached key
-  float rc = 0.0f, rsn = 0.0f;
-  if (rot) {
-    const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
-    rc = cs[2 * hd_i];
-    rsn = cs[2 * hd_i + 1];
-  }
   // 2. the first key round (32 keys: instruction c brings keys c * kpi +
   // lane / nch, chunk lane mod nch) and value batch (lane (c, i): keys j0 +
   // c + 4u, chunk i)
@@ -541,6 +535,22 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
     load_keys(j0);
     load_values(j0);
   }
+  // and, in the same round trip, the rotation's inputs: thread i < hd takes
+  // pair i mod hd/2 of q (i < hd/2) or of the new key and the table's
+  // (cos, sin) at p; thread d < hd the new value's element d
+  const bool rot = tid < a.hd;
+  const int hd_i = tid % half;
+  uint16_t rx1 = 0, rx2 = 0, rv = 0;
+  float rc = 0.0f, rsn = 0.0f;
+  if (rot) {
+    const uint16_t* src = row + (tid < half ? h : a.nh + g) * a.hd;
+    const float* cs = a.cs + static_cast<int64_t>(p) * half * 2;
+    rx1 = src[hd_i];
+    rx2 = src[hd_i + half];
+    rv = row[(a.nh + a.nkv + g) * a.hd + tid];
+    rc = cs[2 * hd_i];
+    rsn = cs[2 * hd_i + 1];
+  }
 
   // 3. rotation (one rounding of the fp64 value), the new value
   if (rot) {
@@ -558,10 +568,6 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
     s_vnew[tid] = rv;
   }
   __syncthreads();
-  if (h % rep == 0 && tid < a.hd) {
-    kb[static_cast<int64_t>(p) * a.hd + tid] = s_knew[tid];
-    vb[static_cast<int64_t>(p) * a.hd + tid] = s_vnew[tid];
-  }
 
   // 4. scores (LDS per wave: the range's fp64 weights, its fp32 scores,
   // and the chunk sums of one 32-key round)
@@ -699,6 +705,12 @@ __global__ __launch_bounds__(kWave * kAttnSplitMax) void attn_split_kernel(AttnA
     }
   }
   if (a.outh && __ballot(ovf) && lane == 0) atomicOr(a.flag, 1u);
+  // the new key and value into the caches, last: nothing after them waits
+  // for the stores
+  if (h % rep == 0 && tid < a.hd) {
+    kb[static_cast<int64_t>(p) * a.hd + tid] = s_knew[tid];
+    vb[static_cast<int64_t>(p) * a.hd + tid] = s_vnew[tid];
+  }
 }
 
 // ------------------------------------------------------------------ greedy
